@@ -1,0 +1,400 @@
+"""Benchmark of the Mamba mixer hot path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--only scan|decode|quant|shard|prefill|all]
+
+Headline (`value`): fused selective-scan prefill throughput, fp32, on the
+isolated-op workload u, delta, z [32, 1536, 1024], B, C [32, 16, 1024],
+A [1536, 16] = -(1..16), D = 1 (one step = one scan over the whole batch =
+32,768 tokens), with `roofline` for the scan kernel (algorithmic bytes /
+HIP-event kernel time vs 8 TB/s) and `cpu_baseline` (the numpy oracle's
+materialize-then-loop scan on the host cores, same workload).
+
+Reported beside it in the same JSON line, each with its own parity check:
+  decode_us_per_token  hipGraph-replayed MambaLM.step, 130m shape b=1 and
+                       1.4b shape b=1 / b=32 (random-init fp32 weights)
+  prefill_tok_s        MambaLM.prefill, 130m shape (b=1 x 64, b=32 x 1024)
+  quant                per-token int8 and fp16 quantize->dequantize-sum of
+                       two [32768, 768] fp32 partials (GB/s)
+  shard_bf16           one TP rank's 1.4b channel shard (D=2048), bf16
+                       activations, b=32 x 2048: conv and scan+gate kernels
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for _p in (ROOT, os.path.join(ROOT, "mamba-tp-lite_amd")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+METRIC = "prefill tok/s + scan HBM GB/s (% peak); decode µs/token, 130m & 1.4b shape"
+HBM_PEAK_GBPS = 8000.0
+
+# isolated selective-scan workload
+SCAN_B, SCAN_D, SCAN_L, SCAN_N = 32, 1536, 1024, 16
+SCAN_BYTES = 4 * (4 * SCAN_B * SCAN_D * SCAN_L + 2 * SCAN_B * SCAN_N * SCAN_L + SCAN_D * SCAN_N + 2 * SCAN_D
+                  + SCAN_B * SCAN_D * SCAN_N)  # u, delta, z, y + B, C + A + D, dt_bias + h_out = 812,756,992
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def _timed(fn, iters, warmup, stream=None):
+    """Mean ms per call of fn() over `iters` back-to-back calls, bracketed by
+    HIP events on the stream the work is enqueued on."""
+    import torch
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    s = torch.cuda.Event(enable_timing=True)
+    e = torch.cuda.Event(enable_timing=True)
+    s.record(stream)
+    for _ in range(iters):
+        fn()
+    e.record(stream)
+    e.synchronize()
+    return s.elapsed_time(e) / iters
+
+
+def _median_trials(fn, iters, warmup, trials=5):
+    import statistics
+    vals = [_timed(fn, iters, warmup if i == 0 else 1) for i in range(trials)]
+    return statistics.median(vals), vals
+
+
+# --------------------------------------------------------------------------- scan (headline)
+def make_scan_inputs(dev, seed=0):
+    import numpy as np
+    import torch
+    from oracle.mixer import inv_softplus
+    g = torch.Generator(device=dev).manual_seed(seed)
+    b, D, L, N = SCAN_B, SCAN_D, SCAN_L, SCAN_N
+    rng = np.random.default_rng(seed)
+    bias = torch.from_numpy(inv_softplus(np.exp(rng.uniform(np.log(1e-3), np.log(0.1), D))).astype(np.float32))
+    return dict(
+        u=torch.randn(b, D, L, device=dev, generator=g),
+        delta=0.5 * torch.randn(b, D, L, device=dev, generator=g),
+        z=torch.randn(b, D, L, device=dev, generator=g),
+        B=torch.randn(b, N, L, device=dev, generator=g),
+        C=torch.randn(b, N, L, device=dev, generator=g),
+        A=-torch.arange(1, N + 1, device=dev, dtype=torch.float32).repeat(D, 1).contiguous(),
+        D=torch.ones(D, device=dev),
+        delta_bias=bias.to(dev),
+    )
+
+
+def bench_scan(dev, steps, warmup):
+    import numpy as np
+    import torch
+    from mamba_lite import ops
+    from oracle import mixer as om
+    x = make_scan_inputs(dev)
+    y = torch.empty_like(x["u"])
+    h = torch.empty(SCAN_B, SCAN_D, SCAN_N, device=dev)
+
+    def step():
+        ops.selective_scan(x["u"], x["delta"], x["A"], x["B"], x["C"], D=x["D"], z=x["z"],
+                           delta_bias=x["delta_bias"], y=y, h_out=h)
+
+    ms, trials = _median_trials(step, steps, warmup)
+    # parity gate on two sampled (batch, 64-channel) blocks vs the float64 oracle
+    torch.cuda.synchronize()
+    err = 0.0
+    for bi, c0 in ((0, 0), (29, 1408)):
+        sl = slice(c0, c0 + 64)
+        yr, hr = om.selective_scan_bnl(*(x[k][bi:bi + 1, sl].cpu().numpy() for k in ("u", "delta")),
+                                       x["A"][sl].cpu().numpy(), x["B"][bi:bi + 1].cpu().numpy(),
+                                       x["C"][bi:bi + 1].cpu().numpy(), x["D"][sl].cpu().numpy(),
+                                       x["z"][bi:bi + 1, sl].cpu().numpy(), x["delta_bias"][sl].cpu().numpy(),
+                                       None, dtype=np.float64)
+        for got, ref in ((y[bi:bi + 1, sl], yr), (h[bi:bi + 1, sl], hr)):
+            d = np.abs(got.cpu().numpy() - ref)
+            err = max(err, float((d / (np.abs(ref) + np.sqrt(np.mean(ref ** 2)))).max()))
+    return ms, trials, err
+
+
+def cpu_baseline_scan(workers):
+    """The oracle's materialize-then-loop scan (numpy, float32) on the host:
+    the whole isolated-op workload, one batch row per task."""
+    import multiprocessing as mp
+    t0 = time.perf_counter()
+    with mp.get_context("spawn").Pool(workers) as pool:
+        pool.map(_cpu_scan_row, range(SCAN_B))
+    return time.perf_counter() - t0
+
+
+def _cpu_scan_row(bi):
+    import numpy as np
+    from oracle import mixer as om
+    rng = np.random.default_rng(1000 + bi)
+    D, L, N = SCAN_D, SCAN_L, SCAN_N
+    u = rng.standard_normal((1, D, L), dtype=np.float32)
+    delta = (0.5 * rng.standard_normal((1, D, L), dtype=np.float32))
+    z = rng.standard_normal((1, D, L), dtype=np.float32)
+    B = rng.standard_normal((1, N, L), dtype=np.float32)
+    C = rng.standard_normal((1, N, L), dtype=np.float32)
+    A = -np.tile(np.arange(1, N + 1, dtype=np.float32), (D, 1))
+    bias = om.inv_softplus(np.exp(rng.uniform(np.log(1e-3), np.log(0.1), D))).astype(np.float32)
+    om.selective_scan_bnl(u, delta, A, B, C, np.ones(D, np.float32), z, bias, None, dtype=np.float32)
+    return bi
+
+
+def traffic_from_profiles(key):
+    """HBM bytes per launch measured by rocprofv3 FETCH_SIZE + WRITE_SIZE
+    (calibrated against a copy kernel) for `key`, if recorded."""
+    path = os.path.join(ROOT, "profiles", "traffic.json")
+    try:
+        with open(path) as f:
+            return json.load(f).get(key, {}).get("bytes_per_launch")
+    except (OSError, ValueError):
+        return None
+
+
+# --------------------------------------------------------------------------- model decode / prefill
+def build_lm(cfg, dev, seed=0):
+    import numpy as np
+    import torch
+    from mamba_lite.model import MambaLM, MambaMixer
+    from oracle.mixer import inv_softplus
+    torch.manual_seed(seed)
+    with torch.device(dev):
+        model = MambaLM(cfg)
+    rng = np.random.default_rng(seed)
+    with torch.no_grad():
+        for m in model.modules():
+            if isinstance(m, MambaMixer):
+                D = m.dt_proj.bias.shape[0]
+                m.dt_proj.bias.copy_(torch.from_numpy(
+                    inv_softplus(np.exp(rng.uniform(np.log(1e-3), np.log(0.1), D))).astype(np.float32)))
+    return model.eval()
+
+
+def bench_decode(model, batch, prompt, n_tokens, dev):
+    import torch
+    from mamba_lite.cuda_graph import GraphedStepper
+    g = torch.Generator(device=dev).manual_seed(1234)
+    ids = torch.randint(0, model.cfg.vocab_size, (batch, prompt), device=dev, generator=g)
+    nxt = torch.zeros(batch, 1, dtype=torch.long, device=dev)
+    with torch.no_grad():
+        _, cache_e = model.prefill(ids)
+        eager = [model.step(nxt, cache_e).clone() for _ in range(3)]
+        _, cache = model.prefill(ids)
+        st = GraphedStepper(model, cache, batch, "cuda")
+        st.capture()
+        ok = all(torch.equal(st.replay(nxt), e) for e in eager)   # graph == eager, bit for bit
+        ms = _timed(lambda: st.replay(nxt), n_tokens, 3)
+    return ms * 1000.0, ok
+
+
+def bench_prefill(model, batch, seqlen, dev, iters=3):
+    import torch
+    g = torch.Generator(device=dev).manual_seed(7)
+    ids = torch.randint(0, model.cfg.vocab_size, (batch, seqlen), device=dev, generator=g)
+    with torch.no_grad():
+        ms = _timed(lambda: model.prefill(ids), iters, 1)
+    return batch * seqlen / (ms / 1000.0)
+
+
+# --------------------------------------------------------------------------- quant / shard
+def bench_quant(dev, iters=20):
+    import numpy as np
+    import torch
+    from mamba_lite import ops
+    from oracle import quant as oq
+    rows, cols = 32 * 1024, 768
+    g = torch.Generator(device=dev).manual_seed(3)
+    # Student-t(3) * 0.5 partials drawn on the host (seeded), then resident in HBM
+    rng = np.random.default_rng(3)
+    parts = [torch.from_numpy((rng.standard_t(3, (rows, cols)) * 0.5).astype(np.float32)).to(dev) for _ in range(2)]
+    out = torch.empty_like(parts[0])
+    pays = [torch.empty(rows * (cols + 4), dtype=torch.uint8, device=dev) for _ in range(2)]
+    ms8 = _timed(lambda: ops.quant_dequant_sum_int8_tok(parts, payloads=pays, out=out), iters, 3)
+    sl = slice(1000, 1256)
+    ref_out, ref_pays = oq.quant_dequant_sum_int8_tok([p[sl].cpu().numpy() for p in parts])
+    exact = bool(np.array_equal(out[sl].cpu().numpy(), ref_out))
+    s, q = oq.unpack_payload(pays[0].cpu().numpy(), rows, cols)
+    rs, rq = oq.unpack_payload(ref_pays[0], 256, cols)
+    exact = exact and bool(np.array_equal(s[sl], rs) and np.array_equal(q[sl], rq))
+    bytes8 = 2 * rows * cols * 4 + 2 * rows * (cols + 4) + rows * cols * 4
+    p16 = [torch.empty(rows, cols, dtype=torch.float16, device=dev) for _ in range(2)]
+    ms16 = _timed(lambda: ops.quant_dequant_sum_fp16(parts, payloads=p16, out=out), iters, 3)
+    ref16, _ = oq.fp16_sum([p[sl].cpu().numpy() for p in parts])
+    exact16 = bool(np.array_equal(out[sl].cpu().numpy(), ref16))
+    bytes16 = 2 * rows * cols * 4 + 2 * rows * cols * 2 + rows * cols * 4
+    return {"int8_us": ms8 * 1e3, "int8_gbps": bytes8 / ms8 / 1e6, "int8_bit_exact": exact,
+            "fp16_us": ms16 * 1e3, "fp16_gbps": bytes16 / ms16 / 1e6, "fp16_bit_exact": exact16,
+            "algorithmic_bytes": {"int8": bytes8, "fp16": bytes16}}
+
+
+def bench_shard(dev, iters=10):
+    """One TP rank's channel shard of the 1.4b mixer (D = 2048 of 4096),
+    bf16 activations with fp32 state, b=32 x l=2048, token-major layout as
+    the mixer produces it."""
+    import numpy as np
+    import torch
+    from mamba_lite import ops
+    from oracle import mixer as om
+    from oracle.mixer import inv_softplus
+    b, L, D, N, R = 32, 2048, 2048, 16, 128
+    g = torch.Generator(device=dev).manual_seed(5)
+    bf = torch.bfloat16
+    xz = torch.randn(b, L, 2 * D, device=dev, generator=g).to(bf)
+    xdbl = torch.randn(b, L, R + 2 * N, device=dev, generator=g).to(bf)
+    delta = (0.5 * torch.randn(b, L, D, device=dev, generator=g)).to(bf)
+    rng = np.random.default_rng(5)
+    bias = torch.from_numpy(inv_softplus(np.exp(rng.uniform(np.log(1e-3), np.log(0.1), D))).astype(np.float32)).to(dev)
+    w = torch.randn(D, 4, device=dev, generator=g) * 0.5
+    cb = torch.randn(D, device=dev, generator=g) * 0.1
+    A_log = torch.log(torch.arange(1, N + 1, device=dev, dtype=torch.float32)).repeat(D, 1).contiguous()
+    Dv = torch.ones(D, device=dev)
+    u = torch.empty(b, L, D, device=dev, dtype=bf)
+    y = torch.empty(b, L, D, device=dev, dtype=bf)
+    fs = torch.empty(b, D, 3, device=dev, dtype=bf)
+    h = torch.empty(b, D, N, device=dev)
+    xs, z = xz[..., :D].transpose(1, 2), xz[..., D:].transpose(1, 2)
+    Bv, Cv = xdbl[..., R:R + N].transpose(1, 2), xdbl[..., R + N:].transpose(1, 2)
+    conv = lambda: ops.causal_conv1d(xs, w, cb, out=u.transpose(1, 2), final_state=fs)
+    scan = lambda: ops.selective_scan(u.transpose(1, 2), delta.transpose(1, 2), A_log, Bv, Cv, D=Dv, z=z,
+                                      delta_bias=bias, a_is_log=True, y=y.transpose(1, 2), h_out=h)
+    ms_conv = _timed(conv, iters, 2)
+    ms_scan = _timed(scan, iters, 2)
+    torch.cuda.synchronize()
+    # parity gate: one batch row, 64 channels, vs the oracle on the same bf16 inputs
+    sl = slice(640, 704)
+    f = lambda t: t.float().cpu().numpy()
+    cref, _ = om.causal_conv1d(f(xs[0:1, sl]), f(w[sl]), f(cb[sl]), None, dtype=np.float64)
+    e_conv = float(np.abs(f(u[0:1, :, sl]).transpose(0, 2, 1) - om.silu(cref)).max() / np.abs(om.silu(cref)).max())
+    yr, hr = om.selective_scan(f(u[0:1, :, sl]).transpose(0, 2, 1), f(delta[0:1, :, sl]).transpose(0, 2, 1),
+                               -np.exp(f(A_log[sl]).astype(np.float64)), f(xdbl[0:1, :, R:R + N]),
+                               f(xdbl[0:1, :, R + N:]), f(Dv[sl]), f(z[0:1, sl]), f(bias[sl]), None,
+                               dtype=np.float64)
+    e_scan = float(np.abs(f(y[0:1, :, sl]).transpose(0, 2, 1) - yr).max() / np.abs(yr).max())
+    conv_bytes = 2 * b * L * D * 2 + 2 * b * D * 3 * 2 + D * 4 * 4 + D * 4
+    scan_bytes = 4 * b * L * D * 2 + 2 * b * N * L * 2 + b * D * N * 4 + D * N * 4 + 2 * D * 4
+    return {"conv_us": ms_conv * 1e3, "conv_gbps": conv_bytes / ms_conv / 1e6,
+            "scan_us": ms_scan * 1e3, "scan_gbps": scan_bytes / ms_scan / 1e6,
+            "scan_frac_hbm_peak": scan_bytes / ms_scan / 1e6 / HBM_PEAK_GBPS,
+            "tok_s": b * L / ((ms_conv + ms_scan) / 1000.0),
+            "max_rel_err": {"conv": e_conv, "scan": e_scan},
+            "algorithmic_bytes": {"conv": conv_bytes, "scan": scan_bytes}}
+
+
+# --------------------------------------------------------------------------- main
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--only", default="all", choices=["all", "scan", "decode", "quant", "shard", "prefill"])
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}); "
+              "run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    from mamba_lite import _lib
+    from mamba_lite.model import MambaConfig
+    _lib.load()
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    result = {"metric": METRIC}
+    extra = {}
+
+    want = lambda s: args.only in ("all", s)
+    if want("scan"):
+        log("scan: isolated selective scan fp32 [32,1536,1024]")
+        t0 = time.perf_counter()
+        ms, trials, err = bench_scan(dev, args.steps, args.warmup)
+        wall = time.perf_counter() - t0
+        gbps = SCAN_BYTES / ms / 1e6
+        result.update({
+            "value": SCAN_B * SCAN_L / (ms / 1000.0), "unit": "tok/s", "n_gpus": 1, "steps": args.steps,
+            "warmup": args.warmup, "ms_per_step": ms, "higher_is_better": True, "scaling": "weak",
+            "vs_baseline": None, "dtype": "f32", "data": "synthetic (seeded torch.Generator / numpy)",
+            "config": {"workload": "isolated selective scan fp32: u, delta, z [32,1536,1024]; B, C [32,16,1024]; "
+                                   "A [1536,16] = -(1..16); D = 1; y and final state h [32,1536,16]",
+                       "batch": SCAN_B, "dim": SCAN_D, "seqlen": SCAN_L, "dstate": SCAN_N},
+            "roofline": {"bound": "hbm", "achieved": gbps, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                         "frac": gbps / HBM_PEAK_GBPS,
+                         "traffic": traffic_from_profiles("scan_fp32_b32_d1536_l1024"),
+                         "kernel": "scan_fwd_kernel<float,4,16,true>", "algorithmic_bytes": SCAN_BYTES},
+        })
+        extra["scan_trials_ms"] = trials
+        extra["scan_max_rel_err"] = err
+        log(f"scan: {ms*1000:.1f} us/call, {gbps:.0f} GB/s ({gbps/HBM_PEAK_GBPS:.1%} of peak), err {err:.2e}, "
+            f"{wall:.1f}s")
+        if not args.no_cpu_baseline:
+            workers = max(1, min(16, os.cpu_count() or 1))
+            log(f"cpu baseline: oracle scan, {workers} processes")
+            secs = cpu_baseline_scan(workers)
+            result["cpu_baseline"] = {
+                "value": SCAN_B * SCAN_L / secs, "unit": "tok/s", "cores": workers, "kind": "port",
+                "sample": f"the full isolated-scan workload (32 rows x 1536 ch x 1024 steps x 16 states), numpy "
+                          f"float32 materialize-then-loop, one batch row per process over {workers} processes; "
+                          f"{secs:.1f} s wall",
+                "cpu_count": os.cpu_count()}
+            log(f"cpu baseline: {secs:.1f}s")
+
+    if want("decode"):
+        dec = {}
+        for name, cfg_kw, batches, prompt, ntok in (
+                ("130m", dict(d_model=768, n_layer=24, vocab_size=50280), (1,), 64, 64),
+                ("1.4b", dict(d_model=2048, n_layer=48, vocab_size=50280), (1, 32), 1024, 64)):
+            try:
+                log(f"decode {name}: building model")
+                model = build_lm(MambaConfig(**cfg_kw), dev)
+                for bsz in batches:
+                    us, ok = bench_decode(model, bsz, prompt, ntok, dev)
+                    dec[f"{name}_b{bsz}"] = {"us_per_step": us, "us_per_token": us / bsz, "graph_equals_eager": ok,
+                                             "prompt": prompt, "tokens_timed": ntok}
+                    log(f"decode {name} b={bsz}: {us:.1f} us/step (graph==eager {ok})")
+                del model
+                torch.cuda.empty_cache()
+            except Exception as e:  # report, keep the headline line
+                dec[name] = {"error": repr(e)}
+                log(f"decode {name} failed: {e!r}")
+        extra["decode_us_per_token"] = dec
+
+    if want("prefill"):
+        try:
+            model = build_lm(MambaConfig(d_model=768, n_layer=24, vocab_size=50280), dev)
+            extra["prefill_tok_s"] = {"130m_b1_l64": bench_prefill(model, 1, 64, dev),
+                                      "130m_b32_l1024": bench_prefill(model, 32, 1024, dev)}
+            log(f"prefill: {extra['prefill_tok_s']}")
+            del model
+            torch.cuda.empty_cache()
+        except Exception as e:
+            extra["prefill_tok_s"] = {"error": repr(e)}
+
+    if want("quant"):
+        try:
+            extra["quant"] = bench_quant(dev)
+            log(f"quant: {extra['quant']}")
+        except Exception as e:
+            extra["quant"] = {"error": repr(e)}
+
+    if want("shard"):
+        try:
+            extra["shard_bf16"] = bench_shard(dev)
+            log(f"shard: {extra['shard_bf16']}")
+        except Exception as e:
+            extra["shard_bf16"] = {"error": repr(e)}
+
+    if "value" not in result:
+        result.update({"value": None, "unit": "tok/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+                       "ms_per_step": None, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+                       "dtype": "f32", "data": "synthetic", "config": {"workload": f"partial run: {args.only}"}})
+    result.update(extra)
+    result["device"] = torch.cuda.get_device_name(dev)
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,186 @@
+/*
+ * mtl.h -- C ABI of the MI355X (gfx950) Mamba mixer hot-path library
+ * (libmtl.so, built from mamba-tp-lite_amd/csrc).
+ *
+ * The reference (mamba-tp-lite) has no FFI: its operator surface is the
+ * Python method set of mamba_lite/model.py and mamba_lite/tp_utils.py.  Each
+ * entry point below replaces the named span of that Python code; the Python
+ * package mamba_lite (mamba-tp-lite_amd/mamba_lite) binds them with ctypes.
+ *
+ * Conventions
+ *   - Every buffer is device memory owned by the caller.  No entry point
+ *     allocates, frees, synchronizes or reads host memory behind a device
+ *     pointer, so every call can be captured into a hipGraph.
+ *   - Work is enqueued on `stream` (a hipStream_t; NULL = legacy default).
+ *   - Return 0 on success, a nonzero MTL_E* code otherwise; the message is in
+ *     mtl_last_error() (thread-local).  No C++ exception crosses the ABI.
+ *   - Strides are in ELEMENTS of the tensor they describe.
+ *   - Activations are fp32 or bf16 (`dtype`); weights, A, D, biases and the
+ *     SSM state are always fp32.
+ *   - Calls are stateless and re-entrant; calls on one stream are ordered.
+ */
+#ifndef MTL_H
+#define MTL_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum mtl_status { MTL_OK = 0, MTL_EINVAL = 1, MTL_EHIP = 2, MTL_EUNSUPPORTED = 3 };
+enum mtl_dtype { MTL_F32 = 0, MTL_BF16 = 1 };
+
+typedef void* mtl_stream_t; /* hipStream_t */
+
+/* Thread-local text of the last failure ("" if none). */
+const char* mtl_last_error(void);
+/* ABI version, bumped on any signature change. */
+int mtl_abi_version(void);
+
+/* ------------------------------------------------------------------------
+ * Selective scan, prefill.
+ * Replaces model.py:216-238 (dt bias + softplus, dA = exp(dt*A),
+ * dBx = dt*B*x, the per-token recurrence loop 231-236, y = C.h, the D skip
+ * 237 and the silu(z) gate 238) and returns the final state (model.py:241).
+ * Also the same span of the TP shard, tp_model.py:110-129.
+ *
+ *   dt[b,d,t] = delta[b,d,t] + delta_bias[d]     (delta_bias may be NULL)
+ *   dt        = softplus(dt)                      (if delta_softplus)
+ *   h[b,d,:]  = h0[b,d,:] or 0
+ *   for t:  h[n] = exp(dt*A[d,n]) * h[n] + dt * B[b,n,t] * u[b,d,t]
+ *           y[b,d,t] = sum_n C[b,n,t] h[n]  (+ D[d]*u)  (* silu(z))
+ *   h_out[b,d,:] = h                               (fp32, contiguous [b,D,N])
+ *
+ * A is the negated continuous-time matrix [D,N] (A = -exp(A_log)); with
+ * a_is_log != 0 the pointer holds A_log and the kernel forms -exp(A_log).
+ * u, delta, z, y: 3-D [b, D, l] with strides (sb, sd, sl) -- either
+ * channel-major (sl == 1) or token-major (sd == 1) is fast, any other
+ * stride pattern is rejected.  B, C: [b, N, l] with strides (sb, sn, sl).
+ * h0 (nullable) and h_out (nullable): contiguous fp32 [b, D, N].
+ * Limits: 1 <= N <= 32, l >= 0.
+ * ---------------------------------------------------------------------- */
+typedef struct {
+    const void* u;     int64_t u_sb, u_sd, u_sl;
+    const void* delta; int64_t delta_sb, delta_sd, delta_sl;
+    const void* z;     int64_t z_sb, z_sd, z_sl;        /* nullable */
+    const void* B;     int64_t B_sb, B_sn, B_sl;
+    const void* C;     int64_t C_sb, C_sn, C_sl;
+    void* y;           int64_t y_sb, y_sd, y_sl;
+    const float* A;            /* [D, N] contiguous */
+    const float* D;            /* [D] nullable */
+    const float* delta_bias;   /* [D] nullable */
+    const float* h0;           /* [b, D, N] nullable */
+    float* h_out;              /* [b, D, N] nullable */
+    int64_t batch, seqlen, dim, dstate;
+    int32_t dtype;             /* mtl_dtype of u, delta, z, B, C, y */
+    int32_t delta_softplus;
+    int32_t a_is_log;
+    int32_t reserved;
+} mtl_scan_params;
+
+int mtl_selective_scan_fwd(const mtl_scan_params* p, mtl_stream_t stream);
+
+/* ------------------------------------------------------------------------
+ * Causal depthwise conv1d (+ optional SiLU), prefill.
+ * Replaces model.py:201-212 (left-pad with cache.conv_state or zeros,
+ * F.conv1d(groups=D) + bias, [..., :l], F.silu, final_conv_state =
+ * x_padded[..., -(K-1):]); tp_model.py:95-103 on a channel shard.
+ *
+ *   xp = concat(conv_state_in or 0 [b,D,K-1], x [b,D,l]) along l
+ *   out[b,d,t] = act( sum_k w[d,k] * xp[b,d,t+k] + bias[d] )
+ *   conv_state_out[b,d,:] = xp[b,d, l : l+K-1]       (pre-activation inputs)
+ *
+ * x, out: [b, D, l] strided (sb, sd, sl); w: [D, K] fp32 contiguous;
+ * bias: [D] fp32 nullable; conv_state_in/out: contiguous [b, D, K-1] in the
+ * activation dtype, nullable, must not alias each other.  2 <= K <= 8.
+ * ---------------------------------------------------------------------- */
+typedef struct {
+    const void* x;   int64_t x_sb, x_sd, x_sl;
+    void* out;       int64_t out_sb, out_sd, out_sl;
+    const float* w;
+    const float* bias;
+    const void* conv_state_in;
+    void* conv_state_out;
+    int64_t batch, seqlen, dim;
+    int32_t width;    /* K = d_conv */
+    int32_t dtype;    /* mtl_dtype of x, out, conv states */
+    int32_t silu;
+    int32_t reserved;
+} mtl_conv_params;
+
+int mtl_causal_conv1d_fwd(const mtl_conv_params* p, mtl_stream_t stream);
+
+/* ------------------------------------------------------------------------
+ * Single-token conv step, in place.
+ * Replaces model.py:264-277 (conv_in = cat(conv_state, x), sum(conv_in*w)
+ * + bias, conv_state.copy_(conv_in[..., 1:]), F.silu); tp_model.py:145-157.
+ *
+ * conv_state: [b, D, K-1] contiguous (activation dtype), updated in place.
+ * x: [b, D] with batch stride x_sb (channel stride 1); out: [b, D] with
+ * batch stride out_sb.  w: [D, K] fp32; bias: [D] fp32 nullable.
+ * ---------------------------------------------------------------------- */
+int mtl_conv_step(void* conv_state, const void* x, int64_t x_sb, const float* w, const float* bias,
+                  void* out, int64_t out_sb, int64_t batch, int64_t dim, int32_t width,
+                  int32_t dtype, int32_t silu, mtl_stream_t stream);
+
+/* ------------------------------------------------------------------------
+ * Single-token selective state update, in place.
+ * Replaces model.py:280-292 after x_proj (dt = softplus(F.linear(dt_low,
+ * W_dt, b_dt)), dA = exp(dt*A), dBx = dt*B*x, ssm_state.copy_(h*dA + dBx),
+ * y = einsum(h_new, C) + x*D, y *= silu(z)); tp_model.py:161-173.
+ *
+ * ssm_state: fp32 [b, D, N] contiguous, updated in place.
+ * x, z, y: [b, D] with batch strides (channel stride 1).  x_dbl: [b, R+2N]
+ * with batch stride xdbl_sb holding [dt_low | B | C] (model.py:280).
+ * W_dt: [D, R] fp32; b_dt: [D] fp32; A: [D, N] (a_is_log as in the scan);
+ * Dvec: [D] nullable.  1 <= N <= 16.
+ * ---------------------------------------------------------------------- */
+int mtl_selective_state_update(float* ssm_state, const void* x, int64_t x_sb, const void* z, int64_t z_sb,
+                               const void* x_dbl, int64_t xdbl_sb, const float* W_dt, const float* b_dt,
+                               const float* A, const float* Dvec, void* y, int64_t y_sb,
+                               int64_t batch, int64_t dim, int64_t dstate, int64_t dt_rank,
+                               int32_t dtype, int32_t a_is_log, mtl_stream_t stream);
+
+/* ------------------------------------------------------------------------
+ * Residual add + RMSNorm (fp32).
+ * Replaces MambaBlock's residual (model.py:306, 311) fused with the next
+ * RMSNorm (model.py:130-135): x_out = x + y (if y != NULL), then
+ * normed = w * (x_out * rsqrt(mean(x_out^2) + eps)).  x_out may alias x.
+ * All [rows, cols] contiguous fp32.
+ * ---------------------------------------------------------------------- */
+int mtl_add_rmsnorm(const float* x, const float* y, float* x_out, const float* w, float* normed,
+                    int64_t rows, int64_t cols, float eps, mtl_stream_t stream);
+
+/* ------------------------------------------------------------------------
+ * Per-token int8 quantize -> dequantize-sum of an AllReduce payload,
+ * local (the collective replaced by nparts partials resident on one GPU).
+ * Replaces tp_utils.py:103-131 (_int8_gather, per_token=True, reached via
+ * all_reduce_sum_int8_gather_tok 145-149).  For each part r (rank order):
+ *   s_r[i] = max(max_j |part_r[i,j]|, 1e-8f) / 127.0f        (IEEE fp32 div)
+ *   q_r[i,j] = clamp(rint(part_r[i,j] / s_r[i]), -127, 127)  (half-even)
+ *   payload_r = [s_r as 4*rows LE bytes || q_r row-major int8]  (nullable)
+ *   out = ((0 + q_0*s_0) + q_1*s_1) + ...  (fp32, no FMA contraction)
+ * parts: host array of nparts device pointers to contiguous fp32
+ * [rows, cols]; payloads: host array of nparts device pointers (each
+ * rows*(cols+4) bytes) or NULL.  1 <= nparts <= 8.  Codes and scales are
+ * bit-identical to the reference's torch CPU arithmetic.
+ * ---------------------------------------------------------------------- */
+int mtl_quant_dequant_sum_int8_tok(const float* const* parts, int32_t nparts, int64_t rows, int64_t cols,
+                                   uint8_t* const* payloads, float* out, mtl_stream_t stream);
+
+/* ------------------------------------------------------------------------
+ * fp16 cast -> sum -> cast back, local.  Replaces tp_utils.py:31-42
+ * (all_reduce_sum_fp16): low_r = fp16_rne(part_r); acc = low_0;
+ * acc = fp16_rne(acc + low_r) for r = 1.. (rank order); out = fp32(acc).
+ * payloads: host array of nparts device pointers to n fp16 values each
+ * (the materialized wire payload) or NULL.  1 <= nparts <= 8.
+ * ---------------------------------------------------------------------- */
+int mtl_quant_dequant_sum_fp16(const float* const* parts, int32_t nparts, int64_t n,
+                               uint16_t* const* payloads, float* out, mtl_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MTL_H */

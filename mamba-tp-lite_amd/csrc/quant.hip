@@ -1,0 +1,165 @@
+// AllReduce payload quantizers, run locally on one GPU (gfx950).
+//
+// int8 per token replaces mamba-tp-lite tp_utils.py:103-131 (_int8_gather,
+// per_token=True): per row scale = max(amax, 1e-8) / 127, codes =
+// clamp(round_half_even(x / scale), +-127), payload = [scales || codes],
+// then the rank-ordered dequantize-sum out = (0 + q0*s0) + q1*s1 + ...
+// fp16 replaces tp_utils.py:31-42: cast each partial to fp16, sum in fp16,
+// cast back.
+//
+// Bit-exactness: the division is IEEE binary32 (hipcc's default correctly
+// rounded fp32 divide; this file must never be built with fast-math), rint
+// is round-half-to-even, and the dequantize-sum runs with FP contraction off
+// so every q*s and every + rounds once, as torch's separate CPU ops do.
+// amax is a max of absolute values: order-independent, hence exact.
+
+#include "common.h"
+
+namespace mtl {
+namespace {
+
+constexpr int kMaxParts = 8;
+constexpr int kQThreads = 256;          // 4 wavefronts, one row each
+constexpr int kRowsPerBlock = kQThreads / 64;
+constexpr int kMaxColsPerLane = 32;     // cols <= 2048 keeps the row in registers
+
+struct PartPtrs {
+    const float* p[kMaxParts];
+    uint8_t* pay[kMaxParts];
+    uint16_t* pay16[kMaxParts];
+};
+
+template <int PER_LANE>
+__global__ void __launch_bounds__(kQThreads)
+quant_int8_tok_kernel(PartPtrs pp, int nparts, int64_t rows, int cols, float* __restrict__ out) {
+#pragma clang fp contract(off)
+    const int lane = threadIdx.x & 63;
+    const int64_t row = (int64_t)blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
+    if (row >= rows) return;  // uniform over the wavefront
+    const int64_t base = row * cols;
+
+    float acc[PER_LANE];
+#pragma unroll
+    for (int j = 0; j < PER_LANE; ++j) acc[j] = 0.f;
+
+    for (int r = 0; r < nparts; ++r) {
+        const float* src = pp.p[r] + base;
+        float v[PER_LANE];
+        float amax = 0.f;
+#pragma unroll
+        for (int j = 0; j < PER_LANE; ++j) {
+            const int col = lane + 64 * j;
+            v[j] = col < cols ? src[col] : 0.f;
+            amax = fmaxf(amax, fabsf(v[j]));
+        }
+        amax = group_max<64>(amax);
+        const float scale = fmaxf(amax, 1e-8f) / 127.0f;
+        uint8_t* pay = pp.pay[r];
+        if (pay && lane == 0) reinterpret_cast<float*>(pay)[row] = scale;  // 4*rows scale bytes first
+#pragma unroll
+        for (int j = 0; j < PER_LANE; ++j) {
+            const int col = lane + 64 * j;
+            const float q = fminf(fmaxf(rintf(v[j] / scale), -127.f), 127.f);
+            if (col < cols) {
+                if (pay) pay[4 * rows + base + col] = (uint8_t)(int8_t)q;
+                acc[j] = acc[j] + q * scale;
+            }
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < PER_LANE; ++j) {
+        const int col = lane + 64 * j;
+        if (col < cols) out[base + col] = acc[j];
+    }
+}
+
+// Rows wider than the register tile: the row is re-read from HBM (L2) for
+// every pass instead of held in registers.
+__global__ void __launch_bounds__(kQThreads)
+quant_int8_tok_wide_kernel(PartPtrs pp, int nparts, int64_t rows, int cols, float* __restrict__ out) {
+#pragma clang fp contract(off)
+    const int lane = threadIdx.x & 63;
+    const int64_t row = (int64_t)blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
+    if (row >= rows) return;
+    const int64_t base = row * cols;
+    for (int r = 0; r < nparts; ++r) {
+        const float* src = pp.p[r] + base;
+        float amax = 0.f;
+        for (int col = lane; col < cols; col += 64) amax = fmaxf(amax, fabsf(src[col]));
+        amax = group_max<64>(amax);
+        const float scale = fmaxf(amax, 1e-8f) / 127.0f;
+        uint8_t* pay = pp.pay[r];
+        if (pay && lane == 0) reinterpret_cast<float*>(pay)[row] = scale;
+        for (int col = lane; col < cols; col += 64) {
+            const float q = fminf(fmaxf(rintf(src[col] / scale), -127.f), 127.f);
+            if (pay) pay[4 * rows + base + col] = (uint8_t)(int8_t)q;
+            const float prev = r == 0 ? 0.f : out[base + col];
+            out[base + col] = prev + q * scale;
+        }
+    }
+}
+
+__global__ void __launch_bounds__(256)
+fp16_sum_kernel(PartPtrs pp, int nparts, int64_t n, float* __restrict__ out) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    _Float16 acc = (_Float16)pp.p[0][i];
+    if (pp.pay16[0]) reinterpret_cast<_Float16*>(pp.pay16[0])[i] = acc;
+    for (int r = 1; r < nparts; ++r) {
+        const _Float16 lo = (_Float16)pp.p[r][i];
+        if (pp.pay16[r]) reinterpret_cast<_Float16*>(pp.pay16[r])[i] = lo;
+        acc = (_Float16)((float)acc + (float)lo);
+    }
+    out[i] = (float)acc;
+}
+
+}  // namespace
+}  // namespace mtl
+
+extern "C" int mtl_quant_dequant_sum_int8_tok(const float* const* parts, int32_t nparts, int64_t rows, int64_t cols,
+                                              uint8_t* const* payloads, float* out, mtl_stream_t stream) {
+    using namespace mtl;
+    clear_error();
+    MTL_REQUIRE(parts != nullptr, "null parts array");
+    MTL_REQUIRE(nparts >= 1 && nparts <= kMaxParts, "nparts must be in [1, 8]");
+    MTL_REQUIRE(rows >= 0 && cols >= 0 && cols < (int64_t(1) << 31), "size out of range");
+    MTL_REQUIRE((rows + kRowsPerBlock - 1) / kRowsPerBlock < (int64_t(1) << 31), "too many rows");
+    if (rows == 0 || cols == 0) return MTL_OK;
+    MTL_REQUIRE(out != nullptr, "null out");
+    PartPtrs pp{};
+    for (int r = 0; r < nparts; ++r) {
+        MTL_REQUIRE(parts[r] != nullptr, "null part pointer");
+        pp.p[r] = parts[r];
+        pp.pay[r] = payloads ? payloads[r] : nullptr;
+    }
+    hipStream_t st = as_stream(stream);
+    dim3 grid((unsigned)((rows + kRowsPerBlock - 1) / kRowsPerBlock));
+    const int c = (int)cols;
+    const int per_lane = (c + 63) / 64;
+    if (per_lane <= 4) hipLaunchKernelGGL((quant_int8_tok_kernel<4>), grid, dim3(kQThreads), 0, st, pp, nparts, rows, c, out);
+    else if (per_lane <= 8) hipLaunchKernelGGL((quant_int8_tok_kernel<8>), grid, dim3(kQThreads), 0, st, pp, nparts, rows, c, out);
+    else if (per_lane <= 16) hipLaunchKernelGGL((quant_int8_tok_kernel<16>), grid, dim3(kQThreads), 0, st, pp, nparts, rows, c, out);
+    else if (per_lane <= kMaxColsPerLane) hipLaunchKernelGGL((quant_int8_tok_kernel<kMaxColsPerLane>), grid, dim3(kQThreads), 0, st, pp, nparts, rows, c, out);
+    else hipLaunchKernelGGL(quant_int8_tok_wide_kernel, grid, dim3(kQThreads), 0, st, pp, nparts, rows, c, out);
+    return check_launch("quant_dequant_sum_int8_tok");
+}
+
+extern "C" int mtl_quant_dequant_sum_fp16(const float* const* parts, int32_t nparts, int64_t n,
+                                          uint16_t* const* payloads, float* out, mtl_stream_t stream) {
+    using namespace mtl;
+    clear_error();
+    MTL_REQUIRE(parts != nullptr, "null parts array");
+    MTL_REQUIRE(nparts >= 1 && nparts <= kMaxParts, "nparts must be in [1, 8]");
+    MTL_REQUIRE(n >= 0 && (n + 255) / 256 < (int64_t(1) << 31), "size out of range");
+    if (n == 0) return MTL_OK;
+    MTL_REQUIRE(out != nullptr, "null out");
+    PartPtrs pp{};
+    for (int r = 0; r < nparts; ++r) {
+        MTL_REQUIRE(parts[r] != nullptr, "null part pointer");
+        pp.p[r] = parts[r];
+        pp.pay16[r] = payloads ? payloads[r] : nullptr;
+    }
+    hipLaunchKernelGGL(fp16_sum_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, as_stream(stream), pp, nparts,
+                       n, out);
+    return check_launch("quant_dequant_sum_fp16");
+}

@@ -1,0 +1,79 @@
+"""hipGraph-captured decode step (same API as mamba-tp-lite's
+mamba_lite/cuda_graph.py:29-131).
+
+On ROCm, torch.cuda.graph / torch.cuda.CUDAGraph record a hipGraph.  The
+whole MambaLM.step -- embedding, fused add+RMSNorm, the in_proj / x_proj /
+out_proj / lm_head GEMMs and the libmtl conv-step and SSM-update kernels --
+is captured once and replayed with one launch per token.  The step kernels
+update the cache in place and never allocate, synchronize or touch host
+memory, which is what makes the capture valid.
+"""
+from __future__ import annotations
+
+import torch
+
+
+class CUDAGraphUnsupported(RuntimeError):
+    """Capture cannot proceed; the caller should fall back to eager decode
+    (reference cuda_graph.py:29-30)."""
+
+
+def _clone_cache(cache):
+    """Disposable copy of a MambaCache for the warmup steps, so warmup does
+    not advance the cache that gets captured (reference cuda_graph.py:34-48)."""
+    from .model import LayerCache, MambaCache
+
+    return MambaCache([LayerCache(conv_state=l.conv_state.clone(), ssm_state=l.ssm_state.clone())
+                       for l in cache.layers])
+
+
+class GraphedStepper:
+    """Captures `model.step(static_ids, cache)` once, then replays it.
+
+        stepper = GraphedStepper(model, cache, batch_size=1, device="cuda")
+        stepper.capture()
+        for _ in range(n_new_tokens):
+            logits = stepper.replay(next_id)   # next_id: [batch, 1] int64
+    """
+
+    def __init__(self, model, cache, batch_size: int, device: str, n_warmup: int = 3):
+        if device != "cuda" or not torch.cuda.is_available():
+            raise CUDAGraphUnsupported("graph capture needs a GPU device ('cuda'); there is no CPU fallback.")
+        allreduce_dtype = getattr(model, "allreduce_dtype", "fp32")
+        names = {allreduce_dtype} if isinstance(allreduce_dtype, str) else set(allreduce_dtype.values())
+        if "int8_legacy" in names:
+            raise CUDAGraphUnsupported("int8_legacy synchronizes its scale through the host (.item()), "
+                                       "which cannot be captured.")
+        self.model = model
+        self.cache = cache
+        self.device = device
+        self.static_ids = torch.zeros((batch_size, 1), dtype=torch.long, device=device)
+        self.static_logits = None
+        self.graph = None
+        self.n_warmup = n_warmup
+
+    def capture(self):
+        # warmup on a side stream against a clone of the cache: settles the
+        # caching allocator and the GEMM libraries' lazy initialization
+        warm = _clone_cache(self.cache)
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side), torch.no_grad():
+            for _ in range(self.n_warmup):
+                self.model.step(self.static_ids, warm)
+        torch.cuda.current_stream().wait_stream(side)
+        torch.cuda.synchronize()
+        del warm
+
+        self.graph = torch.cuda.CUDAGraph()
+        try:
+            with torch.cuda.graph(self.graph), torch.no_grad():
+                self.static_logits = self.model.step(self.static_ids, self.cache)
+        except RuntimeError as e:
+            self.graph = None
+            raise CUDAGraphUnsupported(f"graph capture failed: {e}") from e
+
+    def replay(self, next_id: torch.Tensor) -> torch.Tensor:
+        self.static_ids.copy_(next_id)
+        self.graph.replay()
+        return self.static_logits

@@ -1,0 +1,329 @@
+"""Drop-in Mamba (v1) model API backed by the MI355X kernels.
+
+Same public surface as mamba-tp-lite's mamba_lite/model.py:
+  MambaConfig, LayerCache, MambaCache.allocate, RMSNorm, MambaMixer
+  (.prefill / .step / .forward), MambaBlock, MambaLM (.prefill / .step /
+  .generate / .from_pretrained), load_hf_state_dict.
+Parameter names and shapes match the reference, so its state dicts (and HF
+`state-spaces/mamba-*-hf` checkpoints through from_pretrained) load as is.
+
+What runs where: in_proj / x_proj / dt_proj / out_proj / lm_head are torch
+GEMMs (hipBLASLt / rocBLAS); the causal conv + SiLU, the selective scan
+(with dt bias, softplus, D skip and SiLU gate fused), the single-token conv
+and SSM updates and the residual + RMSNorm are the libmtl HIP kernels.  The
+model runs on the GPU only.
+
+Deliberate deviation: with bfloat16 activations the SSM state stays float32
+(the cache allocates it in float32 and prefill returns it in float32);
+the reference casts it to the activation dtype (model.py:241).
+"""
+from __future__ import annotations
+
+import json
+import os
+from dataclasses import dataclass
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from . import ops
+
+
+def load_hf_state_dict(hf_path: str) -> dict[str, torch.Tensor]:
+    """Reads a HF checkpoint directory: model.safetensors, or the shards named
+    by model.safetensors.index.json (reference model.py:28-47)."""
+    from safetensors.torch import load_file
+
+    single = os.path.join(hf_path, "model.safetensors")
+    index = os.path.join(hf_path, "model.safetensors.index.json")
+    if os.path.exists(single):
+        return load_file(single)
+    if os.path.exists(index):
+        with open(index) as f:
+            shards = sorted(set(json.load(f)["weight_map"].values()))
+        merged: dict[str, torch.Tensor] = {}
+        for name in shards:
+            merged.update(load_file(os.path.join(hf_path, name)))
+        return merged
+    raise FileNotFoundError(f"no model.safetensors or model.safetensors.index.json under {hf_path}")
+
+
+@dataclass
+class MambaConfig:
+    """Shape source of the model (reference model.py:50-93)."""
+
+    d_model: int
+    n_layer: int
+    vocab_size: int
+    d_state: int = 16
+    d_conv: int = 4
+    expand: int = 2
+    dt_rank: int | None = None
+    conv_bias: bool = True
+    bias: bool = False
+    pad_vocab_size_multiple: int = 8
+    layer_norm_epsilon: float = 1e-5
+
+    @property
+    def d_inner(self) -> int:
+        return self.expand * self.d_model
+
+    def __post_init__(self):
+        if self.dt_rank is None:
+            self.dt_rank = max(1, self.d_model // 16)
+        rem = self.vocab_size % self.pad_vocab_size_multiple
+        if rem:
+            self.vocab_size += self.pad_vocab_size_multiple - rem
+
+    @classmethod
+    def from_hf_config(cls, config_path: str) -> "MambaConfig":
+        with open(config_path) as f:
+            c = json.load(f)
+        return cls(d_model=c["hidden_size"], n_layer=c["num_hidden_layers"], vocab_size=c["vocab_size"],
+                   d_state=c["state_size"], d_conv=c["conv_kernel"], expand=c["expand"],
+                   dt_rank=c["time_step_rank"], conv_bias=c["use_conv_bias"], bias=c["use_bias"],
+                   pad_vocab_size_multiple=c.get("pad_vocab_size_multiple", 8),
+                   layer_norm_epsilon=c.get("layer_norm_epsilon", 1e-5))
+
+
+@dataclass
+class LayerCache:
+    """Per-layer recurrent state (reference model.py:96-101)."""
+
+    conv_state: torch.Tensor  # [batch, d_inner, d_conv - 1]
+    ssm_state: torch.Tensor   # [batch, d_inner, d_state], float32
+
+
+def _state_dtype(dtype):
+    return torch.float32 if dtype in (torch.bfloat16, torch.float16) else dtype
+
+
+class MambaCache:
+    """List of LayerCache (reference model.py:104-121).  step() mutates the
+    tensors in place, so their addresses stay fixed for graph replay."""
+
+    def __init__(self, layers: list[LayerCache]):
+        self.layers = layers
+
+    @staticmethod
+    def allocate(config: MambaConfig, batch_size: int, device, dtype) -> "MambaCache":
+        return MambaCache([
+            LayerCache(
+                conv_state=torch.zeros(batch_size, config.d_inner, config.d_conv - 1, device=device, dtype=dtype),
+                ssm_state=torch.zeros(batch_size, config.d_inner, config.d_state, device=device,
+                                      dtype=_state_dtype(dtype)),
+            )
+            for _ in range(config.n_layer)
+        ])
+
+
+def _f32(t: torch.Tensor | None) -> torch.Tensor | None:
+    if t is None:
+        return None
+    return t if t.dtype == torch.float32 and t.is_contiguous() else t.float().contiguous()
+
+
+class RMSNorm(nn.Module):
+    """w * x * rsqrt(mean(x^2) + eps) in float32 (reference model.py:124-135),
+    one fused kernel per call."""
+
+    def __init__(self, d_model: int, eps: float = 1e-5):
+        super().__init__()
+        self.eps = eps
+        self.weight = nn.Parameter(torch.ones(d_model))
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        dtype = x.dtype
+        out = ops.add_rmsnorm(x.float().contiguous(), _f32(self.weight), self.eps)
+        return out.to(dtype)
+
+
+class MambaMixer(nn.Module):
+    """One Mamba mixer (reference model.py:138-294):
+    in_proj -> causal conv1d + SiLU -> x_proj -> dt_proj -> selective scan
+    (+ D skip, * SiLU(z)) -> out_proj."""
+
+    def __init__(self, cfg: MambaConfig, layer_idx: int):
+        super().__init__()
+        self.cfg = cfg
+        self.layer_idx = layer_idx
+        d_inner, d_model, d_state, dt_rank, d_conv = cfg.d_inner, cfg.d_model, cfg.d_state, cfg.dt_rank, cfg.d_conv
+        self.in_proj = nn.Linear(d_model, 2 * d_inner, bias=cfg.bias)
+        self.conv1d = nn.Conv1d(d_inner, d_inner, kernel_size=d_conv, groups=d_inner, padding=d_conv - 1,
+                                bias=cfg.conv_bias)
+        self.x_proj = nn.Linear(d_inner, dt_rank + 2 * d_state, bias=False)
+        self.dt_proj = nn.Linear(dt_rank, d_inner, bias=True)
+        self.A_log = nn.Parameter(torch.empty(d_inner, d_state))
+        self.D = nn.Parameter(torch.empty(d_inner))
+        self.out_proj = nn.Linear(d_inner, d_model, bias=cfg.bias)
+        self._reset_ssm_params()
+
+    def _reset_ssm_params(self):
+        """S4D-real init A_log = log(1..N) per channel, D = 1 (reference
+        model.py:172-181)."""
+        with torch.no_grad():
+            n = self.A_log.shape[1]
+            self.A_log.copy_(torch.log(torch.arange(1, n + 1, dtype=torch.float32)).expand_as(self.A_log))
+            self.D.fill_(1.0)
+
+    # small per-channel parameters are consumed in float32 by the kernels
+    def _conv_w(self):
+        w = self.conv1d.weight
+        return _f32(w.reshape(w.shape[0], w.shape[-1]))
+
+    def prefill(self, x: torch.Tensor, cache: LayerCache | None = None):
+        """x: [b, l, d_model] -> (out [b, l, d_model], conv_state [b, D, K-1],
+        ssm_state [b, D, N]) -- reference model.py:184-241.  The cache is read
+        as the initial state and never written; new state tensors are returned."""
+        b, l, _ = x.shape
+        Dm, N, R, K = self.cfg.d_inner, self.cfg.d_state, self.cfg.dt_rank, self.cfg.d_conv
+        xz = self.in_proj(x)                                     # [b, l, 2D]
+        xs = xz[..., :Dm].transpose(1, 2)                        # [b, D, l] view, D-stride 1
+        z = xz[..., Dm:].transpose(1, 2)
+        conv_in_state = cache.conv_state if cache is not None else None
+        if conv_in_state is not None and conv_in_state.dtype != x.dtype:
+            conv_in_state = conv_in_state.to(x.dtype)
+        u_store = torch.empty(b, l, Dm, device=x.device, dtype=x.dtype)
+        u, conv_state = ops.causal_conv1d(xs, self._conv_w(), _f32(self.conv1d.bias),
+                                          conv_state=None if conv_in_state is None else conv_in_state.contiguous(),
+                                          silu=True, out=u_store.transpose(1, 2))
+        x_dbl = F.linear(u_store, self.x_proj.weight)            # [b, l, R+2N]
+        dt = F.linear(x_dbl[..., :R], self.dt_proj.weight)        # [b, l, D]; bias fused in the scan
+        B = x_dbl[..., R:R + N].transpose(1, 2)                   # [b, N, l] view
+        C = x_dbl[..., R + N:].transpose(1, 2)
+        h0 = None
+        if cache is not None:
+            h0 = cache.ssm_state.float().contiguous()
+        y_store = torch.empty(b, l, Dm, device=x.device, dtype=x.dtype)
+        _, h = ops.selective_scan(u, dt.transpose(1, 2), _f32(self.A_log), B, C, D=_f32(self.D), z=z,
+                                  delta_bias=_f32(self.dt_proj.bias), h0=h0, delta_softplus=True, a_is_log=True,
+                                  y=y_store.transpose(1, 2))
+        out = self.out_proj(y_store)
+        return out, conv_state, h.to(_state_dtype(x.dtype))
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        """No-cache forward (reference model.py:243-246)."""
+        out, _, _ = self.prefill(x, cache=None)
+        return out
+
+    def step(self, x_t: torch.Tensor, cache: LayerCache):
+        """x_t: [b, d_model] -> out [b, d_model]; updates cache.conv_state and
+        cache.ssm_state in place (reference model.py:249-294).  No host sync,
+        no allocation outside torch's caching allocator: graph-capturable."""
+        Dm, R = self.cfg.d_inner, self.cfg.dt_rank
+        xz = self.in_proj(x_t)                                   # [b, 2D]
+        xc = ops.conv_step(cache.conv_state, xz[:, :Dm], self._conv_w(), _f32(self.conv1d.bias), silu=True)
+        x_dbl = F.linear(xc, self.x_proj.weight)                 # [b, R+2N]
+        y = ops.selective_state_update(cache.ssm_state, xc, xz[:, Dm:], x_dbl, _f32(self.dt_proj.weight),
+                                       _f32(self.dt_proj.bias), _f32(self.A_log), _f32(self.D), a_is_log=True)
+        return self.out_proj(y)
+
+
+class MambaBlock(nn.Module):
+    """RMSNorm -> mixer -> residual (reference model.py:297-311)."""
+
+    def __init__(self, cfg: MambaConfig, layer_idx: int):
+        super().__init__()
+        self.norm = RMSNorm(cfg.d_model, eps=cfg.layer_norm_epsilon)
+        self.mixer = MambaMixer(cfg, layer_idx)
+
+    def prefill(self, x, cache: LayerCache | None):
+        y, conv_state, ssm_state = self.mixer.prefill(self.norm(x), cache)
+        return x + y, conv_state, ssm_state
+
+    def step(self, x_t, cache: LayerCache):
+        return x_t + self.mixer.step(self.norm(x_t), cache)
+
+
+class MambaLM(nn.Module):
+    """Embedding -> n_layer MambaBlocks -> RMSNorm -> lm_head tied to the
+    embedding (reference model.py:314-365).  Between blocks the residual add
+    and the next block's RMSNorm run as one fused kernel."""
+
+    def __init__(self, cfg: MambaConfig):
+        super().__init__()
+        self.cfg = cfg
+        self.embedding = nn.Embedding(cfg.vocab_size, cfg.d_model)
+        self.layers = nn.ModuleList([MambaBlock(cfg, i) for i in range(cfg.n_layer)])
+        self.norm_f = RMSNorm(cfg.d_model, eps=cfg.layer_norm_epsilon)
+
+    def lm_head(self, x: torch.Tensor) -> torch.Tensor:
+        return F.linear(x, self.embedding.weight)
+
+    def _norm_weight(self, i: int) -> torch.Tensor:
+        mod = self.layers[i].norm if i < len(self.layers) else self.norm_f
+        return _f32(mod.weight)
+
+    def _eps(self, i: int) -> float:
+        return (self.layers[i].norm if i < len(self.layers) else self.norm_f).eps
+
+    def _run(self, x: torch.Tensor, per_layer):
+        """Residual stream in float32: h_{i+1} = h_i + mixer_i(norm_i(h_i)),
+        with each add fused into the following norm."""
+        act = x.dtype
+        h = x.float().contiguous()
+        normed = ops.add_rmsnorm(h, self._norm_weight(0), self._eps(0))
+        for i in range(len(self.layers)):
+            y = per_layer(i, normed.to(act) if act != torch.float32 else normed)
+            normed = ops.add_rmsnorm(h, self._norm_weight(i + 1), self._eps(i + 1), y=y.float().contiguous(),
+                                     x_out=h)
+        return normed.to(act) if act != torch.float32 else normed
+
+    def prefill(self, input_ids: torch.Tensor, cache: MambaCache | None = None):
+        """input_ids [b, l] -> (logits [b, l, vocab], new MambaCache)
+        (reference model.py:328-341)."""
+        x = self.embedding(input_ids)
+        new_layers: list[LayerCache] = []
+
+        def layer(i, xn):
+            lc = cache.layers[i] if cache is not None else None
+            y, cs, hs = self.layers[i].mixer.prefill(xn, lc)
+            new_layers.append(LayerCache(conv_state=cs, ssm_state=hs))
+            return y
+
+        xf = self._run(x, layer)
+        return self.lm_head(xf), MambaCache(new_layers)
+
+    def step(self, input_ids: torch.Tensor, cache: MambaCache):
+        """input_ids [b, 1] -> logits [b, 1, vocab]; cache updated in place
+        (reference model.py:343-353)."""
+        x = self.embedding(input_ids).squeeze(1)
+        xf = self._run(x, lambda i, xn: self.layers[i].mixer.step(xn, cache.layers[i]))
+        return self.lm_head(xf).unsqueeze(1)
+
+    @torch.no_grad()
+    def generate(self, input_ids: torch.Tensor, max_new_tokens: int, greedy: bool = True):
+        """Prefill once, then greedy decode through the cache (reference
+        model.py:355-365).  Returns the full token sequence."""
+        logits, cache = self.prefill(input_ids)
+        next_id = logits[:, -1:].argmax(dim=-1)
+        tokens = [input_ids, next_id]
+        for _ in range(max_new_tokens - 1):
+            logits = self.step(next_id, cache)
+            next_id = logits[:, -1, :].argmax(dim=-1, keepdim=True)
+            tokens.append(next_id)
+        return torch.cat(tokens, dim=1)
+
+    @classmethod
+    def from_pretrained(cls, hf_path: str, dtype=torch.float32) -> "MambaLM":
+        """Local HF `state-spaces/mamba-*-hf` snapshot -> MambaLM (reference
+        model.py:367-397): `backbone.` prefix and `embeddings` renamed, strict
+        load."""
+        cfg = MambaConfig.from_hf_config(os.path.join(hf_path, "config.json"))
+        model = cls(cfg).to(dtype)
+        sd = load_hf_state_dict(hf_path)
+        remapped = {"embedding.weight": sd["backbone.embeddings.weight"],
+                    "norm_f.weight": sd["backbone.norm_f.weight"]}
+        names = ["norm.weight", "mixer.in_proj.weight", "mixer.conv1d.weight", "mixer.x_proj.weight",
+                 "mixer.dt_proj.weight", "mixer.dt_proj.bias", "mixer.A_log", "mixer.D", "mixer.out_proj.weight"]
+        if cfg.conv_bias:
+            names.append("mixer.conv1d.bias")
+        if cfg.bias:
+            names += ["mixer.in_proj.bias", "mixer.out_proj.bias"]
+        for i in range(cfg.n_layer):
+            for n in names:
+                remapped[f"layers.{i}.{n}"] = sd[f"backbone.layers.{i}.{n}"]
+        missing, unexpected = model.load_state_dict({k: v.to(dtype) for k, v in remapped.items()}, strict=True)
+        assert not missing and not unexpected, (missing, unexpected)
+        return model

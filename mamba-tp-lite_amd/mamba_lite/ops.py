@@ -1,0 +1,338 @@
+"""torch-facing wrappers of the libmtl HIP kernels.
+
+Each function validates shapes, dtypes, devices and strides on the host
+(so a kernel never sees operands that disagree with its grid), then calls
+the C ABI on torch's current stream.  Inputs must be GPU tensors: there is
+no CPU path, a CPU tensor raises.
+
+Shape conventions follow the reference mixer (mamba_lite/model.py):
+  u, delta, z, y : [b, D, l]  (any view whose l-stride or D-stride is 1)
+  B, C           : [b, N, l]  (strided views of x_dbl are fine)
+  A / A_log      : [D, N];  D, delta_bias : [D];  ssm state [b, D, N] fp32
+"""
+from __future__ import annotations
+
+import contextlib
+import ctypes
+
+import torch
+
+from . import _lib
+
+_ACT_DTYPES = {torch.float32: _lib.MTL_F32, torch.bfloat16: _lib.MTL_BF16}
+
+
+def _dev_guard(t: torch.Tensor):
+    if t.device.type != "cuda":
+        raise RuntimeError(f"mamba_lite kernels need GPU tensors, got a tensor on {t.device} "
+                           "(there is no CPU fallback)")
+    if t.device.index is not None and t.device.index != torch.cuda.current_device():
+        return torch.cuda.device(t.device)
+    return contextlib.nullcontext()
+
+
+def _stream(t: torch.Tensor) -> ctypes.c_void_p:
+    return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
+
+
+def _ptr(t):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _act_code(*ts) -> int:
+    dts = {t.dtype for t in ts if t is not None}
+    if len(dts) != 1:
+        raise TypeError(f"activations must share one dtype, got {sorted(map(str, dts))}")
+    dt = dts.pop()
+    if dt not in _ACT_DTYPES:
+        raise TypeError(f"activation dtype must be float32 or bfloat16, got {dt}")
+    return _ACT_DTYPES[dt]
+
+
+def _same_device(ref: torch.Tensor, *ts):
+    for t in ts:
+        if t is not None and t.device != ref.device:
+            raise RuntimeError(f"all operands must be on {ref.device}, got {t.device}")
+
+
+def _f32_vec(t, n, name):
+    if t is None:
+        return None
+    if t.dtype != torch.float32 or t.dim() != 1 or t.shape[0] != n or not t.is_contiguous():
+        raise ValueError(f"{name} must be a contiguous float32 vector of length {n}, got "
+                         f"{tuple(t.shape)} {t.dtype}")
+    return t
+
+
+def _f32_mat(t, shape, name):
+    if t.dtype != torch.float32 or tuple(t.shape) != tuple(shape) or not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous float32 {tuple(shape)}, got {tuple(t.shape)} {t.dtype}"
+                         f"{'' if t.is_contiguous() else ' (non-contiguous)'}")
+    return t
+
+
+def _bdl_layout_ok(*ts):
+    """True if every [b,D,l] operand is channel-major (l-stride 1) or every one
+    is token-major (D-stride 1)."""
+    ts = [t for t in ts if t is not None]
+    return all(t.stride(2) == 1 for t in ts) or all(t.stride(1) == 1 for t in ts)
+
+
+# --------------------------------------------------------------------------- selective scan
+def selective_scan(u, delta, A, B, C, D=None, z=None, delta_bias=None, h0=None, delta_softplus=True,
+                   a_is_log=False, y=None, h_out=None, return_last_state=True):
+    """Fused selective scan (mtl_selective_scan_fwd); see include/mtl.h.
+
+    Returns (y [b,D,l] in the activation dtype, h_last [b,D,N] fp32) -- the
+    pair MambaMixer.prefill gets from its scan loop (model.py:226-241).
+    `y` / `h_out` may be preallocated (y with the same layout rules as u)."""
+    if u.dim() != 3:
+        raise ValueError(f"u must be [b, D, l], got {tuple(u.shape)}")
+    b, Dm, L = u.shape
+    if A.dim() != 2 or A.shape[0] != Dm:
+        raise ValueError(f"A must be [D={Dm}, N], got {tuple(A.shape)}")
+    N = A.shape[1]
+    _f32_mat(A, (Dm, N), "A")
+    for name, t in (("delta", delta), ("z", z)):
+        if t is not None and tuple(t.shape) != (b, Dm, L):
+            raise ValueError(f"{name} must be {(b, Dm, L)}, got {tuple(t.shape)}")
+    for name, t in (("B", B), ("C", C)):
+        if tuple(t.shape) != (b, N, L):
+            raise ValueError(f"{name} must be {(b, N, L)}, got {tuple(t.shape)}")
+    _f32_vec(D, Dm, "D")
+    _f32_vec(delta_bias, Dm, "delta_bias")
+    if h0 is not None:
+        _f32_mat(h0, (b, Dm, N), "h0")
+    code = _act_code(u, delta, z, B, C)
+    _same_device(u, delta, z, B, C, A, D, delta_bias, h0, y, h_out)
+    if not _bdl_layout_ok(u, delta, z, y):
+        u, delta = u.contiguous(), delta.contiguous()
+        z = z.contiguous() if z is not None else None
+    if y is None:
+        if u.stride(1) == 1 and L > 1:
+            y = torch.empty(b, L, Dm, device=u.device, dtype=u.dtype).transpose(1, 2)
+        else:
+            y = torch.empty(b, Dm, L, device=u.device, dtype=u.dtype)
+    elif tuple(y.shape) != (b, Dm, L) or y.dtype != u.dtype:
+        raise ValueError(f"y must be {(b, Dm, L)} {u.dtype}, got {tuple(y.shape)} {y.dtype}")
+    if not _bdl_layout_ok(u, delta, z, y):
+        raise ValueError("u, delta, z and y must all have l-stride 1 or all have D-stride 1")
+    if h_out is None and return_last_state:
+        h_out = torch.empty(b, Dm, N, device=u.device, dtype=torch.float32)
+    elif h_out is not None:
+        _f32_mat(h_out, (b, Dm, N), "h_out")
+
+    p = _lib.ScanParams()
+    p.u, (p.u_sb, p.u_sd, p.u_sl) = u.data_ptr(), u.stride()
+    p.delta, (p.delta_sb, p.delta_sd, p.delta_sl) = delta.data_ptr(), delta.stride()
+    if z is not None:
+        p.z, (p.z_sb, p.z_sd, p.z_sl) = z.data_ptr(), z.stride()
+    p.B, (p.B_sb, p.B_sn, p.B_sl) = B.data_ptr(), B.stride()
+    p.C, (p.C_sb, p.C_sn, p.C_sl) = C.data_ptr(), C.stride()
+    p.y, (p.y_sb, p.y_sd, p.y_sl) = y.data_ptr(), y.stride()
+    p.A = A.data_ptr()
+    p.D = D.data_ptr() if D is not None else None
+    p.delta_bias = delta_bias.data_ptr() if delta_bias is not None else None
+    p.h0 = h0.data_ptr() if h0 is not None else None
+    p.h_out = h_out.data_ptr() if h_out is not None else None
+    p.batch, p.seqlen, p.dim, p.dstate = b, L, Dm, N
+    p.dtype, p.delta_softplus, p.a_is_log = code, int(bool(delta_softplus)), int(bool(a_is_log))
+    with _dev_guard(u):
+        _lib.check(_lib.load().mtl_selective_scan_fwd(ctypes.byref(p), _stream(u)), "selective_scan_fwd")
+    return y, h_out
+
+
+# --------------------------------------------------------------------------- conv
+def causal_conv1d(x, weight, bias=None, conv_state=None, silu=True, out=None, final_state=None,
+                  return_final_state=True):
+    """Fused causal depthwise conv (+SiLU) over x [b,D,l] (mtl_causal_conv1d_fwd).
+    weight: [D,K] or [D,1,K] fp32; conv_state: [b,D,K-1] incoming history.
+    Returns (out [b,D,l], final conv state [b,D,K-1]) as model.py:206-212."""
+    if x.dim() != 3:
+        raise ValueError(f"x must be [b, D, l], got {tuple(x.shape)}")
+    b, Dm, L = x.shape
+    w = weight.reshape(weight.shape[0], weight.shape[-1]) if weight.dim() == 3 else weight
+    if w.shape[0] != Dm:
+        raise ValueError(f"weight must be [D={Dm}, K], got {tuple(weight.shape)}")
+    K = w.shape[1]
+    _f32_mat(w, (Dm, K), "weight")
+    _f32_vec(bias, Dm, "bias")
+    code = _act_code(x, out, conv_state, final_state)
+    _same_device(x, w, bias, conv_state, out, final_state)
+    if conv_state is not None and (tuple(conv_state.shape) != (b, Dm, K - 1) or not conv_state.is_contiguous()):
+        raise ValueError(f"conv_state must be contiguous {(b, Dm, K - 1)}, got {tuple(conv_state.shape)}")
+    if out is None:
+        if x.stride(1) == 1 and L > 1:
+            out = torch.empty(b, L, Dm, device=x.device, dtype=x.dtype).transpose(1, 2)
+        else:
+            out = torch.empty(b, Dm, L, device=x.device, dtype=x.dtype)
+    elif tuple(out.shape) != (b, Dm, L):
+        raise ValueError(f"out must be {(b, Dm, L)}, got {tuple(out.shape)}")
+    if final_state is None and return_final_state:
+        final_state = torch.empty(b, Dm, K - 1, device=x.device, dtype=x.dtype)
+    elif final_state is not None and (tuple(final_state.shape) != (b, Dm, K - 1) or not final_state.is_contiguous()):
+        raise ValueError(f"final_state must be contiguous {(b, Dm, K - 1)}")
+    if final_state is not None and conv_state is not None and final_state.data_ptr() == conv_state.data_ptr():
+        raise ValueError("final_state must not alias conv_state")
+
+    p = _lib.ConvParams()
+    p.x, (p.x_sb, p.x_sd, p.x_sl) = x.data_ptr(), x.stride()
+    p.out, (p.out_sb, p.out_sd, p.out_sl) = out.data_ptr(), out.stride()
+    p.w = w.data_ptr()
+    p.bias = bias.data_ptr() if bias is not None else None
+    p.conv_state_in = conv_state.data_ptr() if conv_state is not None else None
+    p.conv_state_out = final_state.data_ptr() if final_state is not None else None
+    p.batch, p.seqlen, p.dim, p.width = b, L, Dm, K
+    p.dtype, p.silu = code, int(bool(silu))
+    with _dev_guard(x):
+        _lib.check(_lib.load().mtl_causal_conv1d_fwd(ctypes.byref(p), _stream(x)), "causal_conv1d_fwd")
+    return out, final_state
+
+
+def conv_step(conv_state, x, weight, bias=None, silu=True, out=None):
+    """In-place single-token conv (mtl_conv_step).  conv_state: [b,D,K-1]
+    contiguous, updated in place; x: [b,D] with channel stride 1."""
+    b, Dm = x.shape
+    w = weight.reshape(weight.shape[0], weight.shape[-1]) if weight.dim() == 3 else weight
+    K = w.shape[1]
+    _f32_mat(w, (Dm, K), "weight")
+    _f32_vec(bias, Dm, "bias")
+    if tuple(conv_state.shape) != (b, Dm, K - 1) or not conv_state.is_contiguous():
+        raise ValueError(f"conv_state must be contiguous {(b, Dm, K - 1)}, got {tuple(conv_state.shape)}")
+    if x.stride(1) != 1:
+        raise ValueError("x must have channel stride 1")
+    if out is None:
+        out = torch.empty(b, Dm, device=x.device, dtype=x.dtype)
+    elif tuple(out.shape) != (b, Dm) or out.stride(1) != 1:
+        raise ValueError(f"out must be {(b, Dm)} with channel stride 1")
+    code = _act_code(x, conv_state, out)
+    _same_device(x, conv_state, w, bias, out)
+    with _dev_guard(x):
+        _lib.check(_lib.load().mtl_conv_step(_ptr(conv_state), _ptr(x), x.stride(0), _ptr(w), _ptr(bias), _ptr(out),
+                                             out.stride(0), b, Dm, K, code, int(bool(silu)), _stream(x)),
+                   "conv_step")
+    return out
+
+
+# --------------------------------------------------------------------------- step
+def selective_state_update(ssm_state, x, z, x_dbl, W_dt, b_dt, A, D=None, a_is_log=False, out=None):
+    """In-place single-token SSM update (mtl_selective_state_update).
+    ssm_state: fp32 [b,D,N] contiguous; x, z: [b,D]; x_dbl: [b, R+2N] holding
+    [dt_low | B | C]; W_dt: [D,R]; b_dt: [D]; A or A_log: [D,N].  Returns y [b,D]."""
+    b, Dm = x.shape
+    N = A.shape[1]
+    R = W_dt.shape[1]
+    _f32_mat(ssm_state, (b, Dm, N), "ssm_state")
+    _f32_mat(W_dt, (Dm, R), "W_dt")
+    _f32_mat(A, (Dm, N), "A")
+    _f32_vec(b_dt, Dm, "b_dt")
+    _f32_vec(D, Dm, "D")
+    if N > 16:
+        raise ValueError("selective_state_update supports d_state <= 16")
+    if tuple(x_dbl.shape) != (b, R + 2 * N) or x_dbl.stride(1) != 1:
+        raise ValueError(f"x_dbl must be {(b, R + 2 * N)} with unit column stride, got {tuple(x_dbl.shape)}")
+    for name, t in (("x", x), ("z", z)):
+        if t is not None and (tuple(t.shape) != (b, Dm) or t.stride(1) != 1):
+            raise ValueError(f"{name} must be {(b, Dm)} with channel stride 1")
+    if out is None:
+        out = torch.empty(b, Dm, device=x.device, dtype=x.dtype)
+    elif tuple(out.shape) != (b, Dm) or out.stride(1) != 1:
+        raise ValueError(f"out must be {(b, Dm)} with channel stride 1")
+    code = _act_code(x, z, x_dbl, out)
+    _same_device(x, ssm_state, z, x_dbl, W_dt, b_dt, A, D, out)
+    with _dev_guard(x):
+        _lib.check(_lib.load().mtl_selective_state_update(
+            _ptr(ssm_state), _ptr(x), x.stride(0), _ptr(z), z.stride(0) if z is not None else 0,
+            _ptr(x_dbl), x_dbl.stride(0), _ptr(W_dt), _ptr(b_dt), _ptr(A), _ptr(D), _ptr(out), out.stride(0),
+            b, Dm, N, R, code, int(bool(a_is_log)), _stream(x)), "selective_state_update")
+    return out
+
+
+# --------------------------------------------------------------------------- norm
+def add_rmsnorm(x, weight, eps, y=None, x_out=None, out=None):
+    """normed = weight * rmsnorm(x + y) (fp32, rows = all leading dims);
+    x_out (may alias x) receives x + y."""
+    if x.dtype != torch.float32 or not x.is_contiguous():
+        raise ValueError("x must be contiguous float32")
+    cols = x.shape[-1]
+    rows = x.numel() // cols if cols else 0
+    _f32_vec(weight, cols, "weight")
+    for name, t in (("y", y), ("x_out", x_out)):
+        if t is not None and (t.shape != x.shape or t.dtype != torch.float32 or not t.is_contiguous()):
+            raise ValueError(f"{name} must be contiguous float32 {tuple(x.shape)}")
+    if out is None:
+        out = torch.empty_like(x)
+    elif out.shape != x.shape or out.dtype != torch.float32 or not out.is_contiguous():
+        raise ValueError("out must be contiguous float32 like x")
+    _same_device(x, weight, y, x_out, out)
+    with _dev_guard(x):
+        _lib.check(_lib.load().mtl_add_rmsnorm(_ptr(x), _ptr(y), _ptr(x_out), _ptr(weight), _ptr(out), rows, cols,
+                                               float(eps), _stream(x)), "add_rmsnorm")
+    return out
+
+
+# --------------------------------------------------------------------------- payload quantizers
+def _parts_array(parts):
+    arr = (ctypes.c_void_p * len(parts))(*[p.data_ptr() for p in parts])
+    return ctypes.cast(arr, ctypes.POINTER(ctypes.c_void_p)), arr
+
+
+def quant_dequant_sum_int8_tok(parts, payloads=None, out=None, return_payloads=True):
+    """Per-token int8 quantize -> dequantize-sum of `parts` (rank order),
+    mtl_quant_dequant_sum_int8_tok.  parts: list of same-shape float32
+    tensors (rows = leading dims, cols = last dim).  Returns (out, payloads)
+    with payload r = [scales (4*rows bytes) || int8 codes] as uint8."""
+    if not 1 <= len(parts) <= 8:
+        raise ValueError("between 1 and 8 parts")
+    p0 = parts[0]
+    for p in parts:
+        if p.shape != p0.shape or p.dtype != torch.float32 or not p.is_contiguous():
+            raise ValueError("parts must be contiguous float32 tensors of one shape")
+    cols = p0.shape[-1] if p0.dim() else 1
+    rows = p0.numel() // cols if cols else 0
+    if out is None:
+        out = torch.empty_like(p0)
+    elif out.shape != p0.shape or out.dtype != torch.float32 or not out.is_contiguous():
+        raise ValueError("out must be contiguous float32 like the parts")
+    nbytes = rows * (cols + 4)
+    if payloads is None and return_payloads:
+        payloads = [torch.empty(nbytes, dtype=torch.uint8, device=p0.device) for _ in parts]
+    if payloads is not None:
+        if len(payloads) != len(parts) or any(q.dtype != torch.uint8 or q.numel() != nbytes or not q.is_contiguous()
+                                              for q in payloads):
+            raise ValueError(f"payloads must be {len(parts)} contiguous uint8 tensors of {nbytes} bytes")
+    _same_device(p0, *parts, out, *(payloads or []))
+    parr, keep1 = _parts_array(parts)
+    qarr, keep2 = _parts_array(payloads) if payloads is not None else (None, None)
+    with _dev_guard(p0):
+        _lib.check(_lib.load().mtl_quant_dequant_sum_int8_tok(parr, len(parts), rows, cols, qarr, _ptr(out),
+                                                              _stream(p0)), "quant_dequant_sum_int8_tok")
+    return out, payloads
+
+
+def quant_dequant_sum_fp16(parts, payloads=None, out=None, return_payloads=False):
+    """fp16 cast -> sum (rank order) -> fp32 of `parts`
+    (mtl_quant_dequant_sum_fp16).  Returns (out, payloads or None)."""
+    if not 1 <= len(parts) <= 8:
+        raise ValueError("between 1 and 8 parts")
+    p0 = parts[0]
+    for p in parts:
+        if p.shape != p0.shape or p.dtype != torch.float32 or not p.is_contiguous():
+            raise ValueError("parts must be contiguous float32 tensors of one shape")
+    if out is None:
+        out = torch.empty_like(p0)
+    elif out.shape != p0.shape or out.dtype != torch.float32 or not out.is_contiguous():
+        raise ValueError("out must be contiguous float32 like the parts")
+    if payloads is None and return_payloads:
+        payloads = [torch.empty(p0.shape, dtype=torch.float16, device=p0.device) for _ in parts]
+    if payloads is not None:
+        if len(payloads) != len(parts) or any(q.dtype != torch.float16 or q.shape != p0.shape or not q.is_contiguous()
+                                              for q in payloads):
+            raise ValueError("payloads must be contiguous float16 tensors shaped like the parts")
+    _same_device(p0, *parts, out, *(payloads or []))
+    parr, keep1 = _parts_array(parts)
+    qarr, keep2 = _parts_array(payloads) if payloads is not None else (None, None)
+    with _dev_guard(p0):
+        _lib.check(_lib.load().mtl_quant_dequant_sum_fp16(parr, len(parts), p0.numel(), qarr, _ptr(out),
+                                                          _stream(p0)), "quant_dequant_sum_fp16")
+    return out, payloads

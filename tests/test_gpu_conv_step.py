@@ -1,0 +1,168 @@
+"""Conv (prefill + step), single-token SSM update and add+RMSNorm kernels vs
+the oracle, on the GPU.  fp32 within 1e-4 relative; bf16 activations within
+1e-2 of the oracle on bf16-rounded inputs."""
+import numpy as np
+import pytest
+import torch
+
+from _util import assert_rel, bf16_round
+from mamba_lite import ops
+from oracle import mixer as om
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _t(a, dtype=torch.float32):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(DEV, dtype)
+
+
+@pytest.mark.parametrize("layout", ["cm", "tm"])
+@pytest.mark.parametrize("L", [1, 2, 3, 4, 37, 100])
+@pytest.mark.parametrize("with_state", [False, True])
+def test_conv_fp32(layout, L, with_state):
+    rng = np.random.default_rng(L * 10 + with_state)
+    b, D, K = 2, 300, 4
+    x = rng.standard_normal((b, D, L)).astype(np.float32)
+    w = rng.standard_normal((D, K)).astype(np.float32)
+    bias = rng.standard_normal(D).astype(np.float32)
+    st = rng.standard_normal((b, D, K - 1)).astype(np.float32) if with_state else None
+    X = _t(x) if layout == "cm" else _t(x.transpose(0, 2, 1)).transpose(1, 2)
+    out, fs = ops.causal_conv1d(X, _t(w), _t(bias), conv_state=_t(st) if st is not None else None, silu=True)
+    ref, ref_fs = om.causal_conv1d(x, w, bias, st, dtype=np.float64)
+    assert_rel(out.cpu().numpy(), om.silu(ref), 1e-4, "conv out")
+    assert np.array_equal(fs.cpu().numpy(), ref_fs.astype(np.float32)), "final conv state must be exact copies"
+
+
+def test_conv_no_activation_and_widths():
+    rng = np.random.default_rng(3)
+    for K in (2, 3, 4, 5, 8):
+        x = rng.standard_normal((1, 65, 19)).astype(np.float32)
+        w = rng.standard_normal((65, K)).astype(np.float32)
+        out, fs = ops.causal_conv1d(_t(x), _t(w), None, silu=False)
+        ref, ref_fs = om.causal_conv1d(x, w, None, None, dtype=np.float64)
+        assert_rel(out.cpu().numpy(), ref, 1e-4, f"K={K}")
+        assert np.array_equal(fs.cpu().numpy(), ref_fs.astype(np.float32))
+
+
+def test_conv_zero_length_passes_state_through():
+    st = torch.randn(2, 64, 3, device=DEV)
+    x = torch.empty(2, 64, 0, device=DEV)
+    out, fs = ops.causal_conv1d(x, torch.randn(64, 4, device=DEV), conv_state=st)
+    assert out.shape == (2, 64, 0) and torch.equal(fs, st)
+
+
+def test_conv_bf16():
+    rng = np.random.default_rng(4)
+    x = rng.standard_normal((2, 256, 50)).astype(np.float32)
+    w = rng.standard_normal((256, 4)).astype(np.float32)
+    bias = rng.standard_normal(256).astype(np.float32)
+    X = _t(x.transpose(0, 2, 1), torch.bfloat16).transpose(1, 2)
+    out, fs = ops.causal_conv1d(X, _t(w), _t(bias))
+    ref, ref_fs = om.causal_conv1d(bf16_round(x), w, bias, None, dtype=np.float64)
+    assert out.dtype == torch.bfloat16
+    assert_rel(out.float().cpu().numpy(), om.silu(ref), 1e-2, "conv bf16")
+    assert np.array_equal(fs.float().cpu().numpy(), ref_fs.astype(np.float32))
+
+
+def test_conv_step_in_place():
+    rng = np.random.default_rng(5)
+    b, D, K = 3, 200, 4
+    st = rng.standard_normal((b, D, K - 1)).astype(np.float32)
+    xz = rng.standard_normal((b, 2 * D)).astype(np.float32)
+    w = rng.standard_normal((D, K)).astype(np.float32)
+    bias = rng.standard_normal(D).astype(np.float32)
+    S = _t(st)
+    ptr = S.data_ptr()
+    XZ = _t(xz)
+    out = ops.conv_step(S, XZ[:, :D], _t(w), _t(bias))
+    ref, ref_st = om.conv_step(st, xz[:, :D], w, bias, dtype=np.float64)
+    assert S.data_ptr() == ptr
+    assert_rel(out.cpu().numpy(), om.silu(ref), 1e-4, "conv step")
+    assert np.array_equal(S.cpu().numpy(), ref_st.astype(np.float32))
+
+
+@pytest.mark.parametrize("N,R", [(16, 48), (16, 128), (8, 2), (4, 5)])
+@pytest.mark.parametrize("b", [1, 4])
+def test_selective_state_update(N, R, b):
+    rng = np.random.default_rng(N * 100 + R + b)
+    D = 200
+    h = rng.standard_normal((b, D, N)).astype(np.float32)
+    x = rng.standard_normal((b, D)).astype(np.float32)
+    z = rng.standard_normal((b, D)).astype(np.float32)
+    xdbl = rng.standard_normal((b, R + 2 * N)).astype(np.float32)
+    W = (rng.standard_normal((D, R)) / np.sqrt(R)).astype(np.float32)
+    bdt = om.inv_softplus(np.exp(rng.uniform(np.log(1e-3), np.log(0.1), D))).astype(np.float32)
+    A_log = np.log(np.tile(np.arange(1, N + 1, dtype=np.float32), (D, 1)))
+    Dv = rng.standard_normal(D).astype(np.float32)
+    H = _t(h)
+    y = ops.selective_state_update(H, _t(x), _t(z), _t(xdbl), _t(W), _t(bdt), _t(A_log), _t(Dv), a_is_log=True)
+    y_ref, h_ref = om.selective_state_update(h, x, xdbl[:, :R], W, bdt, -np.exp(A_log.astype(np.float64)),
+                                             xdbl[:, R:R + N], xdbl[:, R + N:], Dv, z, dtype=np.float64)
+    assert_rel(y.cpu().numpy(), y_ref, 1e-4, "y")
+    assert_rel(H.cpu().numpy(), h_ref, 1e-4, "state")
+
+
+def test_selective_state_update_bf16():
+    rng = np.random.default_rng(9)
+    b, D, N, R = 2, 256, 16, 48
+    h = rng.standard_normal((b, D, N)).astype(np.float32)
+    x = rng.standard_normal((b, D)).astype(np.float32)
+    z = rng.standard_normal((b, D)).astype(np.float32)
+    xdbl = rng.standard_normal((b, R + 2 * N)).astype(np.float32)
+    W = (rng.standard_normal((D, R)) / np.sqrt(R)).astype(np.float32)
+    bdt = om.inv_softplus(np.exp(rng.uniform(np.log(1e-3), np.log(0.1), D))).astype(np.float32)
+    A = -np.tile(np.arange(1, N + 1, dtype=np.float32), (D, 1))
+    Dv = np.ones(D, np.float32)
+    H = _t(h)
+    y = ops.selective_state_update(H, _t(x, torch.bfloat16), _t(z, torch.bfloat16), _t(xdbl, torch.bfloat16),
+                                   _t(W), _t(bdt), _t(A), _t(Dv))
+    xr, zr, dr = bf16_round(x), bf16_round(z), bf16_round(xdbl)
+    y_ref, h_ref = om.selective_state_update(h, xr, dr[:, :R], W, bdt, A, dr[:, R:R + N], dr[:, R + N:], Dv, zr,
+                                             dtype=np.float64)
+    assert_rel(y.float().cpu().numpy(), y_ref, 1e-2, "y bf16")
+    assert_rel(H.cpu().numpy(), h_ref, 1e-2, "state bf16")
+
+
+def test_step_matches_one_token_prefill():
+    """A single conv+SSM step from a given state equals a length-1 prefill
+    through the conv and scan kernels from the same state."""
+    rng = np.random.default_rng(10)
+    b, D, N, R, K = 2, 192, 16, 12, 4
+    cs = rng.standard_normal((b, D, K - 1)).astype(np.float32)
+    hs = rng.standard_normal((b, D, N)).astype(np.float32)
+    xz = rng.standard_normal((b, 2 * D)).astype(np.float32)
+    w = rng.standard_normal((D, K)).astype(np.float32)
+    cb = rng.standard_normal(D).astype(np.float32)
+    xdbl = rng.standard_normal((b, R + 2 * N)).astype(np.float32)
+    W = (rng.standard_normal((D, R)) / np.sqrt(R)).astype(np.float32)
+    bdt = rng.standard_normal(D).astype(np.float32) - 3
+    A = -np.tile(np.arange(1, N + 1, dtype=np.float32), (D, 1))
+    Dv = rng.standard_normal(D).astype(np.float32)
+    XZ = _t(xz)
+    CS, HS = _t(cs), _t(hs)
+    xc = ops.conv_step(CS, XZ[:, :D], _t(w), _t(cb))
+    y = ops.selective_state_update(HS, xc, XZ[:, D:], _t(xdbl), _t(W), _t(bdt), _t(A), _t(Dv))
+    u, fs = ops.causal_conv1d(_t(xz[:, :D, None]), _t(w), _t(cb), conv_state=_t(cs))
+    dt = _t(xdbl[:, :R] @ W.T)[:, :, None]
+    yp, hp = ops.selective_scan(u, dt, _t(A), _t(xdbl[:, R:R + N, None]), _t(xdbl[:, R + N:, None]), D=_t(Dv),
+                                z=_t(xz[:, D:, None]), delta_bias=_t(bdt), h0=_t(hs))
+    torch.cuda.synchronize()
+    assert torch.equal(CS, fs)
+    assert_rel(xc.cpu().numpy(), u[..., 0].cpu().numpy(), 1e-6, "conv")
+    assert_rel(y.cpu().numpy(), yp[..., 0].cpu().numpy(), 1e-5, "y")
+    assert_rel(HS.cpu().numpy(), hp.cpu().numpy(), 1e-5, "h")
+
+
+@pytest.mark.parametrize("rows,cols", [(1, 768), (7, 2048), (64, 33)])
+def test_add_rmsnorm(rows, cols):
+    rng = np.random.default_rng(rows + cols)
+    x = rng.standard_normal((rows, cols)).astype(np.float32)
+    y = rng.standard_normal((rows, cols)).astype(np.float32)
+    w = (1 + 0.1 * rng.standard_normal(cols)).astype(np.float32)
+    X = _t(x)
+    out = ops.add_rmsnorm(X, _t(w), 1e-5, y=_t(y), x_out=X)
+    assert_rel(X.cpu().numpy(), x.astype(np.float64) + y, 1e-6, "x_out")
+    assert_rel(out.cpu().numpy(), om.rmsnorm(x.astype(np.float64) + y, w, 1e-5, np.float64), 1e-5, "normed")
+    out2 = ops.add_rmsnorm(_t(x), _t(w), 1e-5)
+    assert_rel(out2.cpu().numpy(), om.rmsnorm(x, w, 1e-5, np.float64), 1e-5, "norm only")

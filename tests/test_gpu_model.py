@@ -1,0 +1,217 @@
+"""Drop-in model API on the GPU: MambaMixer.prefill/step and MambaLM vs the
+oracle, the reference's invariants (chunked continuation, teacher-forced
+step == prefill, fresh prefill states vs in-place step), and hipGraph
+replay == eager, bit for bit."""
+import numpy as np
+import pytest
+import torch
+
+from _util import assert_rel
+from mamba_lite.cuda_graph import GraphedStepper
+from mamba_lite.model import LayerCache, MambaCache, MambaConfig, MambaLM, MambaMixer
+from oracle import mixer as om
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _np(t):
+    return t.detach().float().cpu().numpy()
+
+
+def _mixer_weights(m):
+    d = {"in_proj_w": _np(m.in_proj.weight), "conv_w": _np(m.conv1d.weight)[:, 0, :],
+         "conv_b": _np(m.conv1d.bias) if m.conv1d.bias is not None else None, "x_proj_w": _np(m.x_proj.weight),
+         "dt_proj_w": _np(m.dt_proj.weight), "dt_proj_b": _np(m.dt_proj.bias), "A_log": _np(m.A_log),
+         "D": _np(m.D), "out_proj_w": _np(m.out_proj.weight)}
+    if m.in_proj.bias is not None:
+        d["in_proj_b"] = _np(m.in_proj.bias)
+    if m.out_proj.bias is not None:
+        d["out_proj_b"] = _np(m.out_proj.bias)
+    return d
+
+
+def _lm_weights(model):
+    return {"embedding": _np(model.embedding.weight), "norm_f": _np(model.norm_f.weight),
+            "layers": [dict(_mixer_weights(b.mixer), norm=_np(b.norm.weight)) for b in model.layers]}
+
+
+def _init_dt_bias(module, seed):
+    """dt_proj.bias = inv_softplus(log-uniform[1e-3, 0.1]) as HF Mamba inits it."""
+    rng = np.random.default_rng(seed)
+    with torch.no_grad():
+        for m in module.modules():
+            if isinstance(m, MambaMixer):
+                D = m.dt_proj.bias.shape[0]
+                m.dt_proj.bias.copy_(torch.from_numpy(
+                    om.inv_softplus(np.exp(rng.uniform(np.log(1e-3), np.log(0.1), D))).astype(np.float32)))
+
+
+@pytest.fixture(scope="module")
+def small_mixer():
+    torch.manual_seed(0)
+    cfg = MambaConfig(d_model=64, n_layer=1, vocab_size=100, d_state=16)
+    m = MambaMixer(cfg, 0)
+    _init_dt_bias(m, 0)
+    return m.to(DEV).eval()
+
+
+@pytest.mark.parametrize("bias", [False, True])
+def test_mixer_prefill_vs_oracle(bias):
+    torch.manual_seed(1)
+    cfg = MambaConfig(d_model=64, n_layer=1, vocab_size=100, d_state=16, bias=bias)
+    m = MambaMixer(cfg, 0)
+    _init_dt_bias(m, 1)
+    m = m.to(DEV).eval()
+    x = torch.randn(2, 37, 64, device=DEV)
+    with torch.no_grad():
+        out, cs, hs = m.prefill(x)
+    ref, rcs, rhs = om.mixer_prefill(_mixer_weights(m), _np(x), dtype=np.float64)
+    assert_rel(_np(out), ref, 1e-4, "out")
+    assert np.array_equal(_np(cs), rcs.astype(np.float32)) or np.allclose(_np(cs), rcs, rtol=1e-6, atol=1e-6)
+    assert_rel(_np(hs), rhs, 1e-4, "ssm_state")
+
+
+def test_mixer_reference_test_config():
+    """The reference TP tests' config: d_model 32, d_state 8, x [2,5,32]
+    (test_tp_correctness.py:28-30, 47-48)."""
+    torch.manual_seed(0)
+    cfg = MambaConfig(d_model=32, n_layer=1, vocab_size=100, d_state=8, d_conv=4, expand=2)
+    m = MambaMixer(cfg, 0).to(DEV).eval()
+    torch.manual_seed(123)
+    x = torch.randn(2, 5, 32).to(DEV)
+    with torch.no_grad():
+        out = m(x)
+    ref, _, _ = om.mixer_prefill(_mixer_weights(m), _np(x), dtype=np.float64)
+    assert_rel(_np(out), ref, 1e-4, "forward")
+
+
+def test_mixer_chunked_continuation(small_mixer):
+    m = small_mixer
+    x = torch.randn(2, 50, 64, device=DEV)
+    with torch.no_grad():
+        out, cs, hs = m.prefill(x)
+        o1, c1, h1 = m.prefill(x[:, :21])
+        o2, c2, h2 = m.prefill(x[:, 21:], LayerCache(c1, h1))
+    assert_rel(_np(torch.cat([o1, o2], 1)), _np(out), 1e-5, "out")
+    assert torch.equal(c2, cs)
+    assert_rel(_np(h2), _np(hs), 1e-5, "h")
+
+
+def test_mixer_step_vs_oracle_and_in_place(small_mixer):
+    m = small_mixer
+    cfg = m.cfg
+    cache = MambaCache.allocate(cfg, 3, DEV, torch.float32).layers[0]
+    ptrs = (cache.conv_state.data_ptr(), cache.ssm_state.data_ptr())
+    W = _mixer_weights(m)
+    rcs = np.zeros((3, cfg.d_inner, 3))
+    rhs = np.zeros((3, cfg.d_inner, cfg.d_state))
+    for t in range(6):
+        x = torch.randn(3, 64, device=DEV)
+        with torch.no_grad():
+            out = m.step(x, cache)
+        ref = om.mixer_step(W, _np(x), rcs, rhs, dtype=np.float64)
+        assert_rel(_np(out), ref, 1e-4, f"step {t}")
+    assert (cache.conv_state.data_ptr(), cache.ssm_state.data_ptr()) == ptrs
+    assert_rel(_np(cache.ssm_state), rhs, 1e-4, "ssm_state")
+    assert_rel(_np(cache.conv_state), rcs, 1e-5, "conv_state")
+
+
+def test_prefill_returns_fresh_state_and_leaves_cache(small_mixer):
+    """model.py:334-341: prefill reads the cache but returns new tensors."""
+    m = small_mixer
+    cache = MambaCache.allocate(m.cfg, 1, DEV, torch.float32).layers[0]
+    cache.ssm_state.normal_()
+    before = cache.ssm_state.clone()
+    with torch.no_grad():
+        _, cs, hs = m.prefill(torch.randn(1, 9, 64, device=DEV), cache)
+    assert torch.equal(cache.ssm_state, before)
+    assert hs.data_ptr() != cache.ssm_state.data_ptr() and cs.data_ptr() != cache.conv_state.data_ptr()
+
+
+@pytest.fixture(scope="module")
+def small_lm():
+    torch.manual_seed(2)
+    cfg = MambaConfig(d_model=64, n_layer=3, vocab_size=203, d_state=16)
+    model = MambaLM(cfg)
+    _init_dt_bias(model, 2)
+    return model.to(DEV).eval()
+
+
+def test_lm_prefill_vs_oracle(small_lm):
+    ids = torch.randint(0, small_lm.cfg.vocab_size, (2, 19), device=DEV)
+    with torch.no_grad():
+        logits, cache = small_lm.prefill(ids)
+    ref, rcache = om.lm_prefill(_lm_weights(small_lm), ids.cpu().numpy(), dtype=np.float64)
+    assert logits.shape == (2, 19, small_lm.cfg.vocab_size)
+    assert_rel(_np(logits), ref, 1e-4, "logits")
+    for lc, (rc, rh) in zip(cache.layers, rcache):
+        assert_rel(_np(lc.ssm_state), rh, 1e-4, "ssm")
+
+
+def test_lm_teacher_forced_step_matches_prefill(small_lm):
+    """test_correctness.py:49-72 restated on random weights."""
+    ids = torch.randint(0, small_lm.cfg.vocab_size, (1, 12), device=DEV)
+    with torch.no_grad():
+        full, _ = small_lm.prefill(ids)
+        first, cache = small_lm.prefill(ids[:, :1])
+        got = [first]
+        for t in range(1, 12):
+            got.append(small_lm.step(ids[:, t:t + 1], cache))
+    assert_rel(_np(torch.cat(got, 1)), _np(full), 1e-4, "cached vs full")
+
+
+def test_lm_generate_matches_eager_loop(small_lm):
+    ids = torch.randint(0, small_lm.cfg.vocab_size, (2, 5), device=DEV)
+    with torch.no_grad():
+        toks = small_lm.generate(ids, max_new_tokens=6)
+        logits, cache = small_lm.prefill(ids)
+        nxt = logits[:, -1:].argmax(-1)
+        seq = [ids, nxt]
+        for _ in range(5):
+            nxt = small_lm.step(nxt, cache)[:, -1, :].argmax(-1, keepdim=True)
+            seq.append(nxt)
+    assert torch.equal(toks, torch.cat(seq, 1))
+
+
+@pytest.mark.parametrize("batch", [1, 4])
+def test_graph_replay_bit_identical_to_eager(small_lm, batch):
+    """run_tp.py:111-141 restated with a stricter bar: every replay's logits
+    and the carried cache equal eager's bit for bit; eager work and syncs run
+    between replays."""
+    torch.manual_seed(3)
+    ids = torch.randint(0, small_lm.cfg.vocab_size, (batch, 8), device=DEV)
+    steps = [torch.randint(0, small_lm.cfg.vocab_size, (batch, 1), device=DEV) for _ in range(5)]
+    with torch.no_grad():
+        _, cache_e = small_lm.prefill(ids)
+        eager = [small_lm.step(s, cache_e).clone() for s in steps]
+        _, cache_g = small_lm.prefill(ids)
+        st = GraphedStepper(small_lm, cache_g, batch, "cuda")
+        st.capture()
+        for i, s in enumerate(steps):
+            g = st.replay(s).clone()
+            torch.cuda.synchronize()
+            _ = small_lm.prefill(ids[:, :3])   # unrelated eager work between replays
+            assert torch.equal(g, eager[i]), f"replay {i} differs"
+    for le, lg in zip(cache_e.layers, cache_g.layers):
+        assert torch.equal(le.ssm_state, lg.ssm_state) and torch.equal(le.conv_state, lg.conv_state)
+
+
+def test_bf16_mixer_shard_shape():
+    """bf16 activations, fp32 scan state, through conv + scan + gate at a
+    reduced TP-rank shard shape; vs the oracle on bf16-rounded mixer inputs."""
+    torch.manual_seed(4)
+    cfg = MambaConfig(d_model=128, n_layer=1, vocab_size=100, d_state=16)
+    m = MambaMixer(cfg, 0)
+    _init_dt_bias(m, 4)
+    m = m.to(DEV)
+    x = torch.randn(2, 40, 128, device=DEV)
+    with torch.no_grad():
+        m32 = m
+        out32, _, h32 = m32.prefill(x)
+        mb = MambaMixer(cfg, 0).to(DEV)
+        mb.load_state_dict(m.state_dict())
+        mb = mb.to(torch.bfloat16)
+        outb, _, hb = mb.prefill(x.bfloat16())
+    assert outb.dtype == torch.bfloat16 and hb.dtype == torch.float32
+    assert_rel(_np(outb), _np(out32), 5e-2, "bf16 out vs fp32 out")

@@ -1,0 +1,89 @@
+"""Payload quantizer kernels vs the oracle, on the GPU: int8 codes, per-token
+scales, payload bytes and the dequantize-sum output are BIT-EXACT; the fp16
+cast-sum output is bit-exact too."""
+import numpy as np
+import pytest
+import torch
+
+from mamba_lite import ops, tp_utils
+from oracle import quant as oq
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _student(rng, shape):
+    return (rng.standard_t(3, shape) * 0.5).astype(np.float32)
+
+
+@pytest.mark.parametrize("rows,cols", [(1024, 768), (1000, 80), (33, 160), (5, 2048), (3, 4097), (17, 1)])
+@pytest.mark.parametrize("nparts", [2, 1, 3])
+def test_int8_tok_bit_exact(rows, cols, nparts):
+    rng = np.random.default_rng(rows * 7 + cols + nparts)
+    parts = [_student(rng, (rows, cols)) for _ in range(nparts)]
+    out, pays = ops.quant_dequant_sum_int8_tok([torch.from_numpy(p).to(DEV) for p in parts])
+    ref_out, ref_pays = oq.quant_dequant_sum_int8_tok(parts)
+    for r in range(nparts):
+        assert np.array_equal(pays[r].cpu().numpy(), ref_pays[r]), f"payload {r} differs"
+    assert np.array_equal(out.cpu().numpy(), ref_out), "dequantized sum differs"
+
+
+def test_int8_edge_rows():
+    rows = np.zeros((6, 64), np.float32)
+    rows[1, :9] = [2.5, 3.5, -2.5, -0.5, 0.5, 1.5, 127.0, -127.0, 126.5]   # scale exactly 1: ties to even
+    rows[2, 5] = -3.0e-12                                                  # tiny: clamps to the 1e-8 floor
+    rows[3] = np.linspace(-1e30, 1e30, 64, dtype=np.float32)              # huge magnitudes
+    rows[4, ::2] = 7.0                                                     # exact +-amax -> +-127
+    rows[4, 1::2] = -7.0
+    rows[5] = np.float32(1e-38) * np.arange(64, dtype=np.float32)         # subnormal-range values
+    b = np.flip(rows, 0).copy()
+    out, pays = ops.quant_dequant_sum_int8_tok([torch.from_numpy(rows).to(DEV), torch.from_numpy(b).to(DEV)])
+    ref_out, ref_pays = oq.quant_dequant_sum_int8_tok([rows, b])
+    for r in range(2):
+        assert np.array_equal(pays[r].cpu().numpy(), ref_pays[r])
+    assert np.array_equal(out.cpu().numpy(), ref_out)
+    s, q = oq.unpack_payload(pays[0].cpu().numpy(), 6, 64)
+    assert q[1, :9].tolist() == [2, 4, -2, 0, 0, 2, 127, -127, 126]
+    assert (np.abs(q[4]) == 127).all()
+
+
+def test_int8_full_payload_shape():
+    """The quantize->dequantize-sum workload: two [32*1024, 768] partials."""
+    g = torch.Generator(device=DEV).manual_seed(1)
+    rows, cols = 32 * 1024, 768
+    parts = [torch.randn(rows, cols, device=DEV, generator=g) * 0.5 for _ in range(2)]
+    out, pays = ops.quant_dequant_sum_int8_tok(parts)
+    assert pays[0].numel() == tp_utils.int8_tok_payload_nbytes(rows, cols) == 25_296_896
+    # bit-exact on a sampled block of rows, error bound everywhere
+    sl = slice(12345, 12345 + 257)
+    ref_out, ref_pays = oq.quant_dequant_sum_int8_tok([p[sl].cpu().numpy() for p in parts])
+    assert np.array_equal(out[sl].cpu().numpy(), ref_out)
+    s0, q0 = oq.unpack_payload(pays[0].cpu().numpy(), rows, cols)
+    rs, rq = oq.unpack_payload(ref_pays[0], 257, cols)
+    assert np.array_equal(s0[sl], rs) and np.array_equal(q0[sl], rq)
+    dense = (parts[0] + parts[1]).cpu().numpy()
+    assert np.abs(out.cpu().numpy() - dense).max() < 0.15 * np.abs(dense).max()
+
+
+@pytest.mark.parametrize("n", [1, 1000, 65536 + 3])
+@pytest.mark.parametrize("nparts", [2, 3])
+def test_fp16_bit_exact(n, nparts):
+    rng = np.random.default_rng(n + nparts)
+    parts = [_student(rng, (n,)) for _ in range(nparts)]
+    if n >= 4:
+        parts[0][:4] = [32768.0, 1.0, -65504.0, 70000.0]
+        parts[1][:4] = [2.0 ** -24, 2.0 ** -24, 65504.0, 1.0]
+    out, pays = ops.quant_dequant_sum_fp16([torch.from_numpy(p).to(DEV) for p in parts], return_payloads=True)
+    ref_out, ref_lows = oq.fp16_sum(parts)
+    for r in range(nparts):
+        assert np.array_equal(pays[r].cpu().numpy().view(np.uint16), ref_lows[r].view(np.uint16))
+    assert np.array_equal(out.cpu().numpy(), ref_out)
+
+
+def test_tp_utils_wrappers_count_bytes():
+    c = tp_utils.CommCounter()
+    a = torch.randn(10, 80, device=DEV)
+    b = torch.randn(10, 80, device=DEV)
+    tp_utils.quant_dequant_sum_int8_tok([a, b], counter=c)
+    tp_utils.quant_dequant_sum_fp16([a, b], counter=c)
+    assert c.count == 2 and c.bytes == 10 * 84 + 10 * 80 * 2

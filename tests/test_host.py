@@ -1,0 +1,117 @@
+"""Host-side logic of the drop-in API (CPU only)."""
+import numpy as np
+import pytest
+import torch
+
+from mamba_lite import ops, tp_utils
+from mamba_lite.cuda_graph import CUDAGraphUnsupported, GraphedStepper
+from mamba_lite.model import LayerCache, MambaCache, MambaConfig, MambaLM, MambaMixer
+
+
+def test_config_defaults_and_padding():
+    """reference model.py:64-76"""
+    c = MambaConfig(d_model=768, n_layer=24, vocab_size=50277)
+    assert c.d_inner == 1536 and c.dt_rank == 48 and c.vocab_size == 50280
+    c2 = MambaConfig(d_model=2048, n_layer=48, vocab_size=50280)
+    assert c2.d_inner == 4096 and c2.dt_rank == 128 and c2.vocab_size == 50280
+    assert MambaConfig(d_model=8, n_layer=1, vocab_size=8).dt_rank == 1
+
+
+def test_from_hf_config(tmp_path):
+    import json
+    p = tmp_path / "config.json"
+    p.write_text(json.dumps({"hidden_size": 768, "num_hidden_layers": 24, "vocab_size": 50280, "state_size": 16,
+                             "conv_kernel": 4, "expand": 2, "time_step_rank": 48, "use_conv_bias": True,
+                             "use_bias": False}))
+    c = MambaConfig.from_hf_config(str(p))
+    assert (c.d_model, c.n_layer, c.d_inner, c.dt_rank, c.layer_norm_epsilon) == (768, 24, 1536, 48, 1e-5)
+
+
+def test_cache_allocate_shapes_and_dtypes():
+    cfg = MambaConfig(d_model=32, n_layer=3, vocab_size=100, d_state=8)
+    cache = MambaCache.allocate(cfg, 2, "cpu", torch.float32)
+    assert len(cache.layers) == 3
+    assert cache.layers[0].conv_state.shape == (2, 64, 3) and cache.layers[0].ssm_state.shape == (2, 64, 8)
+    assert all(float(l.ssm_state.abs().sum()) == 0 for l in cache.layers)
+    c16 = MambaCache.allocate(cfg, 1, "cpu", torch.bfloat16)
+    assert c16.layers[0].conv_state.dtype == torch.bfloat16
+    assert c16.layers[0].ssm_state.dtype == torch.float32   # fp32 SSM state with bf16 activations
+
+
+def test_parameter_names_match_reference_state_dict():
+    """Same keys as reference MambaLM (model.py:148-170, 317-322) so its state
+    dicts load strictly."""
+    cfg = MambaConfig(d_model=32, n_layer=1, vocab_size=100, d_state=8)
+    keys = set(MambaLM(cfg).state_dict())
+    expect = {"embedding.weight", "norm_f.weight", "layers.0.norm.weight", "layers.0.mixer.in_proj.weight",
+              "layers.0.mixer.conv1d.weight", "layers.0.mixer.conv1d.bias", "layers.0.mixer.x_proj.weight",
+              "layers.0.mixer.dt_proj.weight", "layers.0.mixer.dt_proj.bias", "layers.0.mixer.A_log",
+              "layers.0.mixer.D", "layers.0.mixer.out_proj.weight"}
+    assert keys == expect
+
+
+def test_ssm_param_init():
+    """reference model.py:172-181: A_log = log(1..N) per channel, D = 1."""
+    m = MambaMixer(MambaConfig(d_model=32, n_layer=1, vocab_size=100, d_state=8), 0)
+    np.testing.assert_allclose(m.A_log.detach().numpy(), np.log(np.tile(np.arange(1, 9), (64, 1))), rtol=1e-7)
+    assert torch.equal(m.D.detach(), torch.ones(64))
+
+
+def test_cpu_tensors_raise_instead_of_falling_back():
+    m = MambaMixer(MambaConfig(d_model=32, n_layer=1, vocab_size=100, d_state=8), 0)
+    with pytest.raises(RuntimeError, match="GPU"):
+        m.prefill(torch.randn(1, 3, 32))
+    with pytest.raises(RuntimeError, match="GPU"):
+        ops.quant_dequant_sum_int8_tok([torch.randn(4, 8), torch.randn(4, 8)])
+
+
+def test_shape_validation_before_launch():
+    with pytest.raises(ValueError):
+        ops.selective_scan(torch.randn(1, 8, 4), torch.randn(1, 8, 5), torch.randn(8, 4), torch.randn(1, 4, 4),
+                           torch.randn(1, 4, 4))
+    with pytest.raises(ValueError):
+        ops.causal_conv1d(torch.randn(1, 8, 4), torch.randn(7, 4))
+
+
+def test_graphed_stepper_rejects_cpu():
+    """reference cuda_graph.py:62-65"""
+    cfg = MambaConfig(d_model=32, n_layer=1, vocab_size=100, d_state=8)
+    with pytest.raises(CUDAGraphUnsupported):
+        GraphedStepper(MambaLM(cfg), MambaCache.allocate(cfg, 1, "cpu", torch.float32), 1, "cpu")
+
+
+def test_graphed_stepper_rejects_int8_legacy():
+    class M:
+        allreduce_dtype = {(0, "x_proj"): "int8_legacy"}
+    if not torch.cuda.is_available():
+        pytest.skip("the device check fires first without a GPU")
+    with pytest.raises(CUDAGraphUnsupported):
+        GraphedStepper(M(), None, 1, "cuda")
+
+
+def test_channel_slice_and_payload_bytes():
+    assert tp_utils.channel_slice(1, 2, 4096) == slice(2048, 4096)
+    with pytest.raises(AssertionError):
+        tp_utils.channel_slice(0, 3, 4096)
+    assert tp_utils.int8_tok_payload_nbytes(32768, 768) == 25_296_896
+
+
+def test_shard_params_partition_the_dense_mixer():
+    torch.manual_seed(0)
+    cfg = MambaConfig(d_model=32, n_layer=1, vocab_size=100, d_state=8, bias=True)
+    dense = MambaMixer(cfg, 0)
+    s0 = tp_utils.shard_mixer_params(dense, 0, 2)
+    s1 = tp_utils.shard_mixer_params(dense, 1, 2)
+    Di = cfg.d_inner
+    w = dense.in_proj.weight.detach()
+    # x rows and z rows are split separately (reference tp_model.py:194-197)
+    assert torch.equal(torch.cat([s0["in_proj.weight"][:Di // 2], s1["in_proj.weight"][:Di // 2]]), w[:Di])
+    assert torch.equal(torch.cat([s0["in_proj.weight"][Di // 2:], s1["in_proj.weight"][Di // 2:]]), w[Di:])
+    assert torch.equal(torch.cat([s0["x_proj.weight"], s1["x_proj.weight"]], 1), dense.x_proj.weight.detach())
+    assert torch.equal(s1["out_proj.bias"], torch.zeros_like(dense.out_proj.bias))
+    assert torch.equal(s0["out_proj.bias"], dense.out_proj.bias.detach())
+
+
+def test_layer_cache_is_a_dataclass_pair():
+    lc = LayerCache(conv_state=torch.zeros(1, 2, 3), ssm_state=torch.zeros(1, 2, 4))
+    assert lc.conv_state.shape == (1, 2, 3) and lc.ssm_state.shape == (1, 2, 4)
