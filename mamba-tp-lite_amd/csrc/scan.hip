@@ -23,14 +23,12 @@
 // ops (mul, mul, fma, fma); exp(x) is exp2(x * log2 e) with log2 e folded
 // into A once per launch.
 
+#include <type_traits>
+
 #include "common.h"
 
 namespace mtl {
 namespace {
-
-constexpr int kCH = 64;                 // channels per workgroup
-constexpr int kWaves = 4;               // state groups per workgroup
-constexpr int kThreads = kCH * kWaves;  // 256
 
 struct ScanArgs {
     const void* u; const void* delta; const void* z; const void* B; const void* C; void* y;
@@ -45,48 +43,104 @@ struct ScanArgs {
     int softplus, a_is_log;
 };
 
-// CM = channel-major (stride along l is 1), else token-major (stride along d is 1).
-template <typename T, int SPW, int TT, bool CM>
-__global__ void __launch_bounds__(kThreads) scan_fwd_kernel(const ScanArgs a) {
-    constexpr int E = TT * kCH / kThreads;               // (channel, t) elements per thread per tile
-    constexpr int NP = kWaves * SPW;                     // padded state count
-    constexpr int BCE = (NP * TT + kThreads - 1) / kThreads;
-    static_assert(TT % 4 == 0, "tile must split over 4 threads per channel");
+// E contiguous activations <-> floats (E a multiple of 4; 16-byte (fp32) or
+// 8-byte (bf16) aligned when VEC).
+template <typename T, int E, bool VEC>
+__device__ __forceinline__ void load_run(const T* p, float* v) {
+    if constexpr (VEC && sizeof(T) == 4) {
+#pragma unroll
+        for (int q = 0; q < E / 4; ++q) {
+            const float4 x = reinterpret_cast<const float4*>(p)[q];
+            v[4 * q] = x.x; v[4 * q + 1] = x.y; v[4 * q + 2] = x.z; v[4 * q + 3] = x.w;
+        }
+    } else if constexpr (VEC && sizeof(T) == 2) {
+#pragma unroll
+        for (int q = 0; q < E / 4; ++q) {
+            const uint2 x = reinterpret_cast<const uint2*>(p)[q];
+            v[4 * q] = __uint_as_float(x.x << 16); v[4 * q + 1] = __uint_as_float(x.x & 0xffff0000u);
+            v[4 * q + 2] = __uint_as_float(x.y << 16); v[4 * q + 3] = __uint_as_float(x.y & 0xffff0000u);
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < E; ++j) v[j] = Act<T>::load(p + j);
+    }
+}
+template <typename T, int E, bool VEC>
+__device__ __forceinline__ void store_run(T* p, const float* v) {
+    if constexpr (VEC && sizeof(T) == 4) {
+#pragma unroll
+        for (int q = 0; q < E / 4; ++q)
+            reinterpret_cast<float4*>(p)[q] = make_float4(v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]);
+    } else if constexpr (VEC && sizeof(T) == 2) {
+#pragma unroll
+        for (int q = 0; q < E / 4; ++q) {
+            uint2 x;
+            x.x = uint32_t(f32_to_bf16(v[4 * q])) | (uint32_t(f32_to_bf16(v[4 * q + 1])) << 16);
+            x.y = uint32_t(f32_to_bf16(v[4 * q + 2])) | (uint32_t(f32_to_bf16(v[4 * q + 3])) << 16);
+            reinterpret_cast<uint2*>(p)[q] = x;
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < E; ++j) Act<T>::store(p + j, v[j]);
+    }
+}
 
-    __shared__ float s_dt[TT][kCH + 1];
-    __shared__ float s_dtx[TT][kCH + 1];
-    __shared__ float s_y[kWaves][TT][kCH + 1];
-    __shared__ float s_B[TT][NP];
-    __shared__ float s_C[TT][NP];
+template <bool B> using Full = std::integral_constant<bool, B>;
+
+// NW wavefronts per workgroup = NW state groups of SPW states over the same
+// 64 channels.  CM: channel-major [b,D,l] rows (l-stride 1); otherwise
+// token-major (D-stride 1).  VEC: CM rows are aligned for vector access.
+template <typename T, int NW, int SPW, int TT, bool CM, bool VEC>
+__global__ void __launch_bounds__(NW * 64) scan_fwd_kernel(const ScanArgs a) {
+    constexpr int NT = NW * 64;
+    constexpr int E = TT * 64 / NT;            // consecutive timesteps one thread stages per tile
+    constexpr int NP = NW * SPW;               // padded state count
+    constexpr int BCE = (NP * TT + NT - 1) / NT;
+    constexpr int TS = TT + 4;                 // [c][t] LDS row stride: 16B aligned, b128 conflict-free
+    static_assert(E % 4 == 0 && SPW % 1 == 0, "tile shape");
+
+    __shared__ __align__(16) float s_dt[64][TS];
+    __shared__ __align__(16) float s_dx[64][TS];
+    __shared__ __align__(16) float s_y[NW][64][TS];
+    constexpr int BS = NP + 4;                 // padded B/C rows: staging writes spread over banks
+    __shared__ __align__(16) float s_B[TT][BS];
+    __shared__ __align__(16) float s_C[TT][BS];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
     const int b = blockIdx.y;
-    const int c0 = blockIdx.x * kCH;
+    const int c0 = blockIdx.x * 64;
     const int L = a.L, D = a.D, N = a.N;
 
-    // loader mapping: every thread owns ONE channel and E timesteps of a tile
-    const int my_c = CM ? (tid >> 2) : lane;
-    auto my_t = [&](int j) { return CM ? ((tid & 3) * E + j) : (wave + 4 * j); };
-    const bool c_ok = c0 + my_c < D;
-    const int cg = c_ok ? c0 + my_c : 0;
+    // staging ownership: channel oc, timesteps [ot, ot + E) of each tile.
+    // Token-major puts 64 channels on the 64 lanes.  Channel-major gives each
+    // wavefront 64/NW channels x all NW row segments of the tile (the same
+    // addresses per load instruction as any other split), with the channel
+    // fastest across lanes so 8 adjacent lanes hit distinct LDS bank groups.
+    constexpr int CPW = 64 / NW;               // channels per wavefront (CM)
+    const int oc = CM ? wave * CPW + lane % CPW : lane;
+    const int ot = CM ? (lane / CPW) * E : wave * E;
+    const bool c_ok = c0 + oc < D;
+    const int cl = c_ok ? c0 + oc : D - 1;     // loads of a tail channel block read a valid row
 
-    const T* __restrict__ up = static_cast<const T*>(a.u) + b * a.u_sb + (int64_t)cg * (CM ? a.u_sd : 1);
-    const T* __restrict__ dp = static_cast<const T*>(a.delta) + b * a.d_sb + (int64_t)cg * (CM ? a.d_sd : 1);
-    const T* __restrict__ zp = a.z ? static_cast<const T*>(a.z) + b * a.z_sb + (int64_t)cg * (CM ? a.z_sd : 1)
-                                   : nullptr;
-    T* __restrict__ yp = static_cast<T*>(a.y) + b * a.y_sb + (int64_t)cg * (CM ? a.y_sd : 1);
-    const int64_t u_st = CM ? 1 : a.u_sl, d_st = CM ? 1 : a.d_sl, z_st = CM ? 1 : a.z_sl,
-                  y_st = CM ? 1 : a.y_sl;
+    const T* __restrict__ up = static_cast<const T*>(a.u) + b * a.u_sb + (int64_t)cl * (CM ? a.u_sd : 1);
+    const T* __restrict__ dp = static_cast<const T*>(a.delta) + b * a.d_sb + (int64_t)cl * (CM ? a.d_sd : 1);
+    const bool has_z = a.z != nullptr;
+    // without a gate z aliases u: its loads stay unconditional (a branch
+    // around them would merge registers through copies that wait for loads)
+    const T* __restrict__ zp = has_z ? static_cast<const T*>(a.z) + b * a.z_sb + (int64_t)cl * (CM ? a.z_sd : 1)
+                                     : up;
+    const int64_t z_sl = has_z ? a.z_sl : a.u_sl;
+    T* __restrict__ yp = static_cast<T*>(a.y) + b * a.y_sb + (int64_t)cl * (CM ? a.y_sd : 1);
     const T* __restrict__ Bp = static_cast<const T*>(a.B) + b * a.B_sb;
     const T* __restrict__ Cp = static_cast<const T*>(a.C) + b * a.C_sb;
-    const bool bc_t_fast = (a.B_sl == 1);
+    const bool bc_t_fast = a.B_sl == 1;
 
-    const float bias_c = a.dbias ? a.dbias[cg] : 0.f;
-    const float D_c = a.Dv ? a.Dv[cg] : 0.f;
+    const float bias_c = a.dbias ? a.dbias[cl] : 0.f;
+    const float D_c = a.Dv ? a.Dv[cl] : 0.f;
 
-    // scan registers: this wavefront's states of channel c0 + lane
+    // scan registers: states [wave*SPW, wave*SPW + SPW) of channel c0 + lane
     const bool lane_ok = c0 + lane < D;
     float h[SPW], a2[SPW];
 #pragma unroll
@@ -99,92 +153,172 @@ __global__ void __launch_bounds__(kThreads) scan_fwd_kernel(const ScanArgs a) {
         h[k] = (ok && a.h0) ? a.h0[((int64_t)b * D + c0 + lane) * N + n] : 0.f;
     }
 
-    float ru[E], rd[E], rz[E], rB[BCE], rC[BCE];
+    // raw tile registers: two sets, so the loads of tiles k+1 and k+2 are in
+    // flight while tile k is scanned (prefetch distance 2)
+    struct Raw { float u[E], d[E], z[E], B[BCE], C[BCE]; };
+    Raw r0, r1;
     float du[E], gz[E];
 
-    auto load_tile = [&](int tb) {
+    // B/C staging slots of this thread (loop invariant): element e = tid + NT*k
+    // of the [TT x NP] tile.  Loads always read a valid address (state and
+    // time clamped); out-of-range slots are zeroed when staged.  No select
+    // consumes a loaded register before the stage, so the prefetch stays in
+    // flight across the scan (a select right after a load would force a wait
+    // for every outstanding load).
+    int bc_off[BCE], bc_t[BCE], bc_slot[BCE];
+    bool bc_ok[BCE];
 #pragma unroll
-        for (int j = 0; j < E; ++j) {
-            const int t = tb + my_t(j);
-            const bool ok = c_ok && t < L;
-            ru[j] = ok ? Act<T>::load(up + t * u_st) : 0.f;
-            rd[j] = ok ? Act<T>::load(dp + t * d_st) : 0.f;
-            rz[j] = (ok && zp) ? Act<T>::load(zp + t * z_st) : 0.f;
-        }
-#pragma unroll
-        for (int k = 0; k < BCE; ++k) {
-            const int e = tid + kThreads * k;
-            const int n = bc_t_fast ? e / TT : e % NP;
-            const int t = bc_t_fast ? e % TT : e / NP;
-            const bool ok = n < N && t < TT && tb + t < L;
-            rB[k] = ok ? Act<T>::load(Bp + n * a.B_sn + (int64_t)(tb + t) * a.B_sl) : 0.f;
-            rC[k] = ok ? Act<T>::load(Cp + n * a.C_sn + (int64_t)(tb + t) * a.C_sl) : 0.f;
-        }
-    };
+    for (int k = 0; k < BCE; ++k) {
+        const int e = tid + NT * k;
+        const int n = bc_t_fast ? e / TT : e % NP;
+        const int t = bc_t_fast ? e % TT : e / NP;
+        bc_ok[k] = e < NP * TT && n < N;
+        const int nc = min(n, N - 1);
+        bc_t[k] = min(t, TT - 1);
+        bc_off[k] = nc;
+        bc_slot[k] = (e < NP * TT) ? bc_t[k] * BS + n : -1;
+    }
 
-    auto stage_tile = [&](int tb) {
-#pragma unroll
-        for (int j = 0; j < E; ++j) {
-            const int tl = my_t(j);
-            const bool ok = c_ok && tb + tl < L;
-            float dt = rd[j] + bias_c;
-            if (a.softplus) dt = softplus_f(dt);
-            dt = ok ? dt : 0.f;  // a zero step leaves the state untouched past the end
-            s_dt[tl][my_c] = dt;
-            s_dtx[tl][my_c] = dt * ru[j];
-            du[j] = D_c * ru[j];
-            gz[j] = zp ? silu_f(rz[j]) : 1.f;
-        }
-#pragma unroll
-        for (int k = 0; k < BCE; ++k) {
-            const int e = tid + kThreads * k;
-            const int n = bc_t_fast ? e / TT : e % NP;
-            const int t = bc_t_fast ? e % TT : e / NP;
-            if (n < NP && t < TT) {
-                s_B[t][n] = rB[k];
-                s_C[t][n] = rC[k];
-            }
-        }
-    };
-
-    auto scan_step = [&](int tt) {
-        const float dt = s_dt[tt][lane];
-        const float dtx = s_dtx[tt][lane];
-        float acc = 0.f;
-#pragma unroll
-        for (int k = 0; k < SPW; ++k) {
-            const float bk = s_B[tt][wave * SPW + k];
-            const float ck = s_C[tt][wave * SPW + k];
-            h[k] = fmaf(__builtin_amdgcn_exp2f(dt * a2[k]), h[k], dtx * bk);
-            acc = fmaf(h[k], ck, acc);
-        }
-        s_y[wave][tt][lane] = acc;
-    };
-
-    load_tile(0);
-    for (int tb = 0; tb < L; tb += TT) {
-        stage_tile(tb);
-        __syncthreads();
-        if (tb + TT < L) load_tile(tb + TT);
-        const int steps = min(TT, L - tb);
-        if (steps == TT) {
-#pragma unroll
-            for (int tt = 0; tt < TT; ++tt) scan_step(tt);
+    auto load_tile = [&](Raw& r, int tb, auto full) {
+        constexpr bool F = decltype(full)::value;
+        if constexpr (CM && F) {
+            load_run<T, E, VEC>(up + tb + ot, r.u);
+            load_run<T, E, VEC>(dp + tb + ot, r.d);
+            load_run<T, E, VEC>(zp + tb + ot, r.z);
         } else {
-            for (int tt = 0; tt < steps; ++tt) scan_step(tt);
-        }
-        __syncthreads();
+            const int64_t su = CM ? 1 : a.u_sl, sd = CM ? 1 : a.d_sl, sz = CM ? 1 : z_sl;
 #pragma unroll
-        for (int j = 0; j < E; ++j) {
-            const int tl = my_t(j);
-            const int t = tb + tl;
-            if (c_ok && t < L) {
-                float yv = s_y[0][tl][my_c];
-#pragma unroll
-                for (int w = 1; w < kWaves; ++w) yv += s_y[w][tl][my_c];
-                Act<T>::store(yp + t * y_st, (yv + du[j]) * gz[j]);
+            for (int j = 0; j < E; ++j) {
+                const int t = F ? tb + ot + j : min(tb + ot + j, L - 1);
+                r.u[j] = Act<T>::load(up + t * su);
+                r.d[j] = Act<T>::load(dp + t * sd);
+                r.z[j] = Act<T>::load(zp + t * sz);
             }
         }
+#pragma unroll
+        for (int k = 0; k < BCE; ++k) {
+            const int t = F ? tb + bc_t[k] : min(tb + bc_t[k], L - 1);
+            r.B[k] = Act<T>::load(Bp + bc_off[k] * a.B_sn + (int64_t)t * a.B_sl);
+            r.C[k] = Act<T>::load(Cp + bc_off[k] * a.C_sn + (int64_t)t * a.C_sl);
+        }
+    };
+    auto stage_tile = [&](const Raw& r, int tb, auto full) {
+        constexpr bool F = decltype(full)::value;
+        float vdt[E], vdx[E];
+#pragma unroll
+        for (int j = 0; j < E; ++j) {
+            const bool ok = F || tb + ot + j < L;
+            float dt = r.d[j] + bias_c;
+            if (a.softplus) dt = softplus_f(dt);
+            const float uv = ok ? r.u[j] : 0.f;
+            dt = ok ? dt : 0.f;                 // zero steps leave the state untouched past the end
+            vdt[j] = dt;
+            vdx[j] = dt * uv;
+            du[j] = D_c * uv;
+            gz[j] = has_z ? silu_f(r.z[j]) : 1.f;
+        }
+#pragma unroll
+        for (int q = 0; q < E / 4; ++q) {
+            *reinterpret_cast<float4*>(&s_dt[oc][ot + 4 * q]) =
+                make_float4(vdt[4 * q], vdt[4 * q + 1], vdt[4 * q + 2], vdt[4 * q + 3]);
+            *reinterpret_cast<float4*>(&s_dx[oc][ot + 4 * q]) =
+                make_float4(vdx[4 * q], vdx[4 * q + 1], vdx[4 * q + 2], vdx[4 * q + 3]);
+        }
+#pragma unroll
+        for (int k = 0; k < BCE; ++k) {
+            if (bc_slot[k] >= 0) {
+                const bool ok = bc_ok[k] && (F || tb + bc_t[k] < L);
+                (&s_B[0][0])[bc_slot[k]] = ok ? r.B[k] : 0.f;
+                (&s_C[0][0])[bc_slot[k]] = ok ? r.C[k] : 0.f;
+            }
+        }
+    };
+
+    // TT recurrence steps; padded steps past the end have dt = dt*u = 0 and
+    // leave h unchanged, so the loop never needs a bound check
+    auto scan_tile = [&]() {
+#pragma unroll
+        for (int tt = 0; tt < TT; tt += 4) {
+            const float4 dt4 = *reinterpret_cast<const float4*>(&s_dt[lane][tt]);
+            const float4 dx4 = *reinterpret_cast<const float4*>(&s_dx[lane][tt]);
+            const float dts[4] = {dt4.x, dt4.y, dt4.z, dt4.w};
+            const float dxs[4] = {dx4.x, dx4.y, dx4.z, dx4.w};
+            float yq[4];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                float acc = 0.f;
+#pragma unroll
+                for (int k = 0; k < SPW; ++k) {
+                    const float bk = s_B[tt + q][wave * SPW + k];
+                    const float ck = s_C[tt + q][wave * SPW + k];
+                    h[k] = fmaf(__builtin_amdgcn_exp2f(dts[q] * a2[k]), h[k], dxs[q] * bk);
+                    acc = fmaf(h[k], ck, acc);
+                }
+                yq[q] = acc;
+            }
+            *reinterpret_cast<float4*>(&s_y[wave][lane][tt]) = make_float4(yq[0], yq[1], yq[2], yq[3]);
+        }
+    };
+
+    auto finish_tile = [&](int tb, auto full) {
+        constexpr bool F = decltype(full)::value;
+        float out[E];
+#pragma unroll
+        for (int q = 0; q < E / 4; ++q) {
+            float4 acc = *reinterpret_cast<const float4*>(&s_y[0][oc][ot + 4 * q]);
+#pragma unroll
+            for (int w = 1; w < NW; ++w) {
+                const float4 p = *reinterpret_cast<const float4*>(&s_y[w][oc][ot + 4 * q]);
+                acc.x += p.x; acc.y += p.y; acc.z += p.z; acc.w += p.w;
+            }
+            out[4 * q] = (acc.x + du[4 * q]) * gz[4 * q];
+            out[4 * q + 1] = (acc.y + du[4 * q + 1]) * gz[4 * q + 1];
+            out[4 * q + 2] = (acc.z + du[4 * q + 2]) * gz[4 * q + 2];
+            out[4 * q + 3] = (acc.w + du[4 * q + 3]) * gz[4 * q + 3];
+        }
+        if (!c_ok) return;
+        if constexpr (CM && F) {
+            store_run<T, E, VEC>(yp + tb + ot, out);
+        } else {
+            const int64_t sy = CM ? 1 : a.y_sl;
+#pragma unroll
+            for (int j = 0; j < E; ++j)
+                if (F || tb + ot + j < L) Act<T>::store(yp + (int64_t)(tb + ot + j) * sy, out[j]);
+        }
+    };
+
+    // one full tile: stage it from r, refill r with the full tile two ahead
+    // (if any), scan, write y.  Only full tiles pass through this pipeline, so
+    // the loads have a single code path (two paths would merge through
+    // register copies that wait for the loads).
+    const int nfull = L / TT;
+    auto run_full = [&](Raw& r, int i) {
+        stage_tile(r, i * TT, Full<true>{});
+        __syncthreads();
+        // unconditional refill (the last two tiles re-read tile nfull-1):
+        // a conditional one would again merge registers through copies
+        load_tile(r, min(i + 2, nfull - 1) * TT, Full<true>{});
+        scan_tile();
+        __syncthreads();
+        finish_tile(i * TT, Full<true>{});
+    };
+
+    if (nfull > 0) load_tile(r0, 0, Full<true>{});
+    if (nfull > 1) load_tile(r1, TT, Full<true>{});
+    int i = 0;
+    for (; i + 1 < nfull; i += 2) {
+        run_full(r0, i);
+        run_full(r1, i + 1);
+    }
+    if (i < nfull) run_full(r0, i);
+    if (nfull * TT < L) {  // the partial last tile, outside the pipeline
+        const int tb = nfull * TT;
+        load_tile(r0, tb, Full<false>{});
+        stage_tile(r0, tb, Full<false>{});
+        __syncthreads();
+        scan_tile();
+        __syncthreads();
+        finish_tile(tb, Full<false>{});
     }
 
     if (a.h_out) {
@@ -196,19 +330,30 @@ __global__ void __launch_bounds__(kThreads) scan_fwd_kernel(const ScanArgs a) {
     }
 }
 
-template <typename T, int SPW, bool CM>
+template <typename T, int NW, int SPW, int TT, bool CM, bool VEC>
 void launch_scan(const ScanArgs& a, int64_t batch, hipStream_t st) {
-    constexpr int TT = 16;
-    dim3 grid((unsigned)((a.D + kCH - 1) / kCH), (unsigned)batch);
-    hipLaunchKernelGGL((scan_fwd_kernel<T, SPW, TT, CM>), grid, dim3(kThreads), 0, st, a);
+    dim3 grid((unsigned)((a.D + 63) / 64), (unsigned)batch);
+    hipLaunchKernelGGL((scan_fwd_kernel<T, NW, SPW, TT, CM, VEC>), grid, dim3(NW * 64), 0, st, a);
 }
 
-template <typename T, bool CM>
+// 4 state groups of ceil(N/4) states: 4 wavefronts of 64 channels
+template <typename T, bool CM, bool VEC>
 void dispatch_spw(const ScanArgs& a, int64_t batch, hipStream_t st) {
-    if (a.N <= 4) launch_scan<T, 1, CM>(a, batch, st);
-    else if (a.N <= 8) launch_scan<T, 2, CM>(a, batch, st);
-    else if (a.N <= 16) launch_scan<T, 4, CM>(a, batch, st);
-    else launch_scan<T, 8, CM>(a, batch, st);
+    if (a.N <= 4) launch_scan<T, 4, 1, 16, CM, VEC>(a, batch, st);
+    else if (a.N <= 8) launch_scan<T, 4, 2, 16, CM, VEC>(a, batch, st);
+    else if (a.N <= 16) launch_scan<T, 4, 4, 16, CM, VEC>(a, batch, st);
+    else launch_scan<T, 4, 8, 16, CM, VEC>(a, batch, st);
+}
+
+template <typename T>
+bool rows_aligned(const ScanArgs& a, int64_t batch) {
+    const uintptr_t al = sizeof(T) == 4 ? 16 : 8;
+    auto ok = [&](const void* p, int64_t sb, int64_t sd) {
+        return p == nullptr || ((uintptr_t)p % al == 0 && (batch == 1 || (sb * (int64_t)sizeof(T)) % al == 0) &&
+                                (sd * (int64_t)sizeof(T)) % al == 0);
+    };
+    return ok(a.u, a.u_sb, a.u_sd) && ok(a.delta, a.d_sb, a.d_sd) && ok(a.z, a.z_sb, a.z_sd) &&
+           ok(a.y, a.y_sb, a.y_sd);
 }
 
 }  // namespace
@@ -224,7 +369,10 @@ extern "C" int mtl_selective_scan_fwd(const mtl_scan_params* p, mtl_stream_t str
     MTL_REQUIRE(p->seqlen < (int64_t(1) << 31) && p->dim < (int64_t(1) << 31), "size overflows int32");
     MTL_REQUIRE(p->dtype == MTL_F32 || p->dtype == MTL_BF16, "dtype must be MTL_F32 or MTL_BF16");
     if (p->batch == 0 || p->dim == 0) return MTL_OK;
-    MTL_REQUIRE(p->u && p->delta && p->B && p->C && p->y && p->A, "null required pointer");
+    MTL_REQUIRE(p->A != nullptr, "null A");
+    // an empty sequence only carries h0 (or zeros) through to h_out; torch
+    // hands out null data pointers for empty tensors
+    MTL_REQUIRE(p->seqlen == 0 || (p->u && p->delta && p->B && p->C && p->y), "null required pointer");
 
     const bool has_z = p->z != nullptr;
     const bool cm = p->u_sl == 1 && p->delta_sl == 1 && p->y_sl == 1 && (!has_z || p->z_sl == 1);
@@ -248,11 +396,13 @@ extern "C" int mtl_selective_scan_fwd(const mtl_scan_params* p, mtl_stream_t str
     // seqlen <= 1 has no meaningful l-stride; the channel-major path handles it.
     const bool use_cm = cm || (!tm);
     if (p->dtype == MTL_F32) {
-        if (use_cm) dispatch_spw<float, true>(a, p->batch, st);
-        else dispatch_spw<float, false>(a, p->batch, st);
+        if (!use_cm) dispatch_spw<float, false, false>(a, p->batch, st);
+        else if (rows_aligned<float>(a, p->batch)) dispatch_spw<float, true, true>(a, p->batch, st);
+        else dispatch_spw<float, true, false>(a, p->batch, st);
     } else {
-        if (use_cm) dispatch_spw<uint16_t, true>(a, p->batch, st);
-        else dispatch_spw<uint16_t, false>(a, p->batch, st);
+        if (!use_cm) dispatch_spw<uint16_t, false, false>(a, p->batch, st);
+        else if (rows_aligned<uint16_t>(a, p->batch)) dispatch_spw<uint16_t, true, true>(a, p->batch, st);
+        else dispatch_spw<uint16_t, true, false>(a, p->batch, st);
     }
     return check_launch("selective_scan_fwd");
 }

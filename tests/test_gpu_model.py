@@ -94,7 +94,9 @@ def test_mixer_chunked_continuation(small_mixer):
         o1, c1, h1 = m.prefill(x[:, :21])
         o2, c2, h2 = m.prefill(x[:, 21:], LayerCache(c1, h1))
     assert_rel(_np(torch.cat([o1, o2], 1)), _np(out), 1e-5, "out")
-    assert torch.equal(c2, cs)
+    # the carried conv history holds in_proj outputs; the GEMM library may pick
+    # different kernels for different row counts, so equality holds to rounding
+    assert_rel(_np(c2), _np(cs), 1e-5, "conv_state")
     assert_rel(_np(h2), _np(hs), 1e-5, "h")
 
 
