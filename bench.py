@@ -44,6 +44,15 @@ def log(msg):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
+def dt_bias_init(D, seed):
+    """dt_proj.bias = inv_softplus(dt), dt log-uniform in [1e-3, 0.1] (the HF
+    Mamba init): inv_softplus(y) = y + log(-expm1(-y))."""
+    import numpy as np
+    rng = np.random.default_rng(seed)
+    dt = np.exp(rng.uniform(np.log(1e-3), np.log(0.1), D))
+    return (dt + np.log(-np.expm1(-dt))).astype(np.float32)
+
+
 def _timed(fn, iters, warmup, stream=None):
     """Mean ms per call of fn() over `iters` back-to-back calls, bracketed by
     HIP events on the stream the work is enqueued on."""
@@ -69,13 +78,10 @@ def _median_trials(fn, iters, warmup, trials=5):
 
 # --------------------------------------------------------------------------- scan (headline)
 def make_scan_inputs(dev, seed=0):
-    import numpy as np
     import torch
-    from oracle.mixer import inv_softplus
     g = torch.Generator(device=dev).manual_seed(seed)
     b, D, L, N = SCAN_B, SCAN_D, SCAN_L, SCAN_N
-    rng = np.random.default_rng(seed)
-    bias = torch.from_numpy(inv_softplus(np.exp(rng.uniform(np.log(1e-3), np.log(0.1), D))).astype(np.float32))
+    bias = torch.from_numpy(dt_bias_init(D, seed))
     return dict(
         u=torch.randn(b, D, L, device=dev, generator=g),
         delta=0.5 * torch.randn(b, D, L, device=dev, generator=g),
@@ -89,10 +95,8 @@ def make_scan_inputs(dev, seed=0):
 
 
 def bench_scan(dev, steps, warmup):
-    import numpy as np
     import torch
     from mamba_lite import ops
-    from oracle import mixer as om
     x = make_scan_inputs(dev)
     y = torch.empty_like(x["u"])
     h = torch.empty(SCAN_B, SCAN_D, SCAN_N, device=dev)
@@ -102,30 +106,35 @@ def bench_scan(dev, steps, warmup):
                            delta_bias=x["delta_bias"], y=y, h_out=h)
 
     ms, trials = _median_trials(step, steps, warmup)
-    # parity gate on two sampled (batch, 64-channel) blocks vs the float64 oracle
     torch.cuda.synchronize()
-    err = 0.0
-    for bi, c0 in ((0, 0), (29, 1408)):
-        sl = slice(c0, c0 + 64)
-        yr, hr = om.selective_scan_bnl(*(x[k][bi:bi + 1, sl].cpu().numpy() for k in ("u", "delta")),
-                                       x["A"][sl].cpu().numpy(), x["B"][bi:bi + 1].cpu().numpy(),
-                                       x["C"][bi:bi + 1].cpu().numpy(), x["D"][sl].cpu().numpy(),
-                                       x["z"][bi:bi + 1, sl].cpu().numpy(), x["delta_bias"][sl].cpu().numpy(),
-                                       None, dtype=np.float64)
-        for got, ref in ((y[bi:bi + 1, sl], yr), (h[bi:bi + 1, sl], hr)):
-            d = np.abs(got.cpu().numpy() - ref)
-            err = max(err, float((d / (np.abs(ref) + np.sqrt(np.mean(ref ** 2)))).max()))
-    return ms, trials, err
+    return ms, trials, (x, y, h)
 
 
-def cpu_baseline_scan(workers):
-    """The oracle's materialize-then-loop scan (numpy, float32) on the host:
-    the whole isolated-op workload, one batch row per task."""
+def cpu_baseline_scan(workers, gpu_run):
+    """cpu_baseline leg: the oracle's materialize-then-loop scan (numpy,
+    float32) on the host cores over the whole isolated-op workload, one batch
+    row per process; then the oracle (float64) on two sampled (row, 64-channel)
+    blocks of the very inputs the GPU scanned, as the parity gate reported
+    with the throughput."""
     import multiprocessing as mp
+    import numpy as np
+    from oracle import mixer as om
     t0 = time.perf_counter()
     with mp.get_context("spawn").Pool(workers) as pool:
         pool.map(_cpu_scan_row, range(SCAN_B))
-    return time.perf_counter() - t0
+    secs = time.perf_counter() - t0
+    x, y, h = gpu_run
+    err = 0.0
+    for bi, c0 in ((0, 0), (29, 1408)):
+        sl = slice(c0, c0 + 64)
+        f = lambda t: t.cpu().numpy()
+        yr, hr = om.selective_scan_bnl(f(x["u"][bi:bi + 1, sl]), f(x["delta"][bi:bi + 1, sl]), f(x["A"][sl]),
+                                       f(x["B"][bi:bi + 1]), f(x["C"][bi:bi + 1]), f(x["D"][sl]),
+                                       f(x["z"][bi:bi + 1, sl]), f(x["delta_bias"][sl]), None, dtype=np.float64)
+        for got, ref in ((y[bi:bi + 1, sl], yr), (h[bi:bi + 1, sl], hr)):
+            d = np.abs(f(got) - ref)
+            err = max(err, float((d / (np.abs(ref) + np.sqrt(np.mean(ref ** 2)))).max()))
+    return secs, err
 
 
 def _cpu_scan_row(bi):
@@ -139,8 +148,8 @@ def _cpu_scan_row(bi):
     B = rng.standard_normal((1, N, L), dtype=np.float32)
     C = rng.standard_normal((1, N, L), dtype=np.float32)
     A = -np.tile(np.arange(1, N + 1, dtype=np.float32), (D, 1))
-    bias = om.inv_softplus(np.exp(rng.uniform(np.log(1e-3), np.log(0.1), D))).astype(np.float32)
-    om.selective_scan_bnl(u, delta, A, B, C, np.ones(D, np.float32), z, bias, None, dtype=np.float32)
+    om.selective_scan_bnl(u, delta, A, B, C, np.ones(D, np.float32), z, dt_bias_init(D, bi), None,
+                          dtype=np.float32)
     return bi
 
 
@@ -157,20 +166,14 @@ def traffic_from_profiles(key):
 
 # --------------------------------------------------------------------------- model decode / prefill
 def build_lm(cfg, dev, seed=0):
-    import numpy as np
     import torch
     from mamba_lite.model import MambaLM, MambaMixer
-    from oracle.mixer import inv_softplus
     torch.manual_seed(seed)
     with torch.device(dev):
         model = MambaLM(cfg)
-    rng = np.random.default_rng(seed)
     with torch.no_grad():
-        for m in model.modules():
-            if isinstance(m, MambaMixer):
-                D = m.dt_proj.bias.shape[0]
-                m.dt_proj.bias.copy_(torch.from_numpy(
-                    inv_softplus(np.exp(rng.uniform(np.log(1e-3), np.log(0.1), D))).astype(np.float32)))
+        for i, m in enumerate(x for x in model.modules() if isinstance(x, MambaMixer)):
+            m.dt_proj.bias.copy_(torch.from_numpy(dt_bias_init(m.dt_proj.bias.shape[0], seed * 1000 + i)))
     return model.eval()
 
 
@@ -201,53 +204,85 @@ def bench_prefill(model, batch, seqlen, dev, iters=3):
 
 
 # --------------------------------------------------------------------------- quant / shard
+def cpu_baseline_quant(parts, pays, out, rows=4096):
+    """cpu_baseline leg of the int8 payload op: the oracle's per-token int8
+    quantize -> dequantize-sum (numpy, IEEE fp32 like the reference's torch
+    CPU ops) on the first `rows` rows of the same partials, timed on one host
+    core, and compared byte for byte with the GPU payloads and output there.
+    (torch's own GPU division on ROCm is not correctly rounded, so it cannot
+    serve as the bit-exact reference.)"""
+    import numpy as np
+    from oracle import quant as oq
+    cols = parts[0].shape[1]
+    host = [p[:rows].cpu().numpy() for p in parts]
+    t0 = time.perf_counter()
+    ref_out, ref_pays = oq.quant_dequant_sum_int8_tok(host)
+    secs = time.perf_counter() - t0
+    R = parts[0].shape[0]
+    exact = bool(np.array_equal(out[:rows].cpu().numpy(), ref_out))
+    for p, rp in zip(pays, ref_pays):
+        s, q = oq.unpack_payload(p.cpu().numpy(), R, cols)
+        rs, rq = oq.unpack_payload(rp, rows, cols)
+        exact = exact and bool(np.array_equal(s[:rows], rs) and np.array_equal(q[:rows], rq))
+    nbytes = 2 * rows * cols * 4 + 2 * rows * (cols + 4) + rows * cols * 4
+    return {"value": nbytes / secs / 1e9, "unit": "GB/s", "cores": 1, "kind": "port",
+            "sample": f"first {rows} of {R} rows, numpy oracle", "bit_exact_codes_scales_out": exact}
+
+
 def bench_quant(dev, iters=20):
     import numpy as np
     import torch
     from mamba_lite import ops
-    from oracle import quant as oq
     rows, cols = 32 * 1024, 768
-    g = torch.Generator(device=dev).manual_seed(3)
     # Student-t(3) * 0.5 partials drawn on the host (seeded), then resident in HBM
     rng = np.random.default_rng(3)
     parts = [torch.from_numpy((rng.standard_t(3, (rows, cols)) * 0.5).astype(np.float32)).to(dev) for _ in range(2)]
     out = torch.empty_like(parts[0])
     pays = [torch.empty(rows * (cols + 4), dtype=torch.uint8, device=dev) for _ in range(2)]
     ms8 = _timed(lambda: ops.quant_dequant_sum_int8_tok(parts, payloads=pays, out=out), iters, 3)
-    sl = slice(1000, 1256)
-    ref_out, ref_pays = oq.quant_dequant_sum_int8_tok([p[sl].cpu().numpy() for p in parts])
-    exact = bool(np.array_equal(out[sl].cpu().numpy(), ref_out))
-    s, q = oq.unpack_payload(pays[0].cpu().numpy(), rows, cols)
-    rs, rq = oq.unpack_payload(ref_pays[0], 256, cols)
-    exact = exact and bool(np.array_equal(s[sl], rs) and np.array_equal(q[sl], rq))
+    torch.cuda.synchronize()
+    cpu = cpu_baseline_quant(parts, pays, out)
     bytes8 = 2 * rows * cols * 4 + 2 * rows * (cols + 4) + rows * cols * 4
     p16 = [torch.empty(rows, cols, dtype=torch.float16, device=dev) for _ in range(2)]
     ms16 = _timed(lambda: ops.quant_dequant_sum_fp16(parts, payloads=p16, out=out), iters, 3)
-    ref16, _ = oq.fp16_sum([p[sl].cpu().numpy() for p in parts])
-    exact16 = bool(np.array_equal(out[sl].cpu().numpy(), ref16))
+    ref16 = (parts[0].half() + parts[1].half()).float()
+    exact16 = bool(torch.equal(out, ref16))
     bytes16 = 2 * rows * cols * 4 + 2 * rows * cols * 2 + rows * cols * 4
-    return {"int8_us": ms8 * 1e3, "int8_gbps": bytes8 / ms8 / 1e6, "int8_bit_exact": exact,
-            "fp16_us": ms16 * 1e3, "fp16_gbps": bytes16 / ms16 / 1e6, "fp16_bit_exact": exact16,
+    return {"int8_us": ms8 * 1e3, "int8_gbps": bytes8 / ms8 / 1e6, "int8_frac_hbm_peak": bytes8 / ms8 / 1e6 / HBM_PEAK_GBPS,
+            "int8_cpu_baseline": cpu,
+            "fp16_us": ms16 * 1e3, "fp16_gbps": bytes16 / ms16 / 1e6, "fp16_bit_exact_vs_torch": exact16,
             "algorithmic_bytes": {"int8": bytes8, "fp16": bytes16}}
+
+
+def _torch_scan_ref(u, delta, A, B, C, Dv, z, bias):
+    """Sequential fp32 scan in torch on the GPU (reference model.py:216-238
+    op order) for a small block: u, delta, z [D, L]; B, C [L, N]."""
+    import torch
+    import torch.nn.functional as F
+    dt = F.softplus(delta + bias[:, None])
+    h = torch.zeros(u.shape[0], A.shape[1], device=u.device)
+    ys = []
+    for t in range(u.shape[1]):
+        h = torch.exp(dt[:, t, None] * A) * h + (dt[:, t, None] * B[t][None, :]) * u[:, t, None]
+        ys.append(h @ C[t])
+    y = torch.stack(ys, 1)
+    return (y + u * Dv[:, None]) * F.silu(z)
 
 
 def bench_shard(dev, iters=10):
     """One TP rank's channel shard of the 1.4b mixer (D = 2048 of 4096),
     bf16 activations with fp32 state, b=32 x l=2048, token-major layout as
     the mixer produces it."""
-    import numpy as np
     import torch
+    import torch.nn.functional as F
     from mamba_lite import ops
-    from oracle import mixer as om
-    from oracle.mixer import inv_softplus
     b, L, D, N, R = 32, 2048, 2048, 16, 128
     g = torch.Generator(device=dev).manual_seed(5)
     bf = torch.bfloat16
     xz = torch.randn(b, L, 2 * D, device=dev, generator=g).to(bf)
     xdbl = torch.randn(b, L, R + 2 * N, device=dev, generator=g).to(bf)
     delta = (0.5 * torch.randn(b, L, D, device=dev, generator=g)).to(bf)
-    rng = np.random.default_rng(5)
-    bias = torch.from_numpy(inv_softplus(np.exp(rng.uniform(np.log(1e-3), np.log(0.1), D))).astype(np.float32)).to(dev)
+    bias = torch.from_numpy(dt_bias_init(D, 5)).to(dev)
     w = torch.randn(D, 4, device=dev, generator=g) * 0.5
     cb = torch.randn(D, device=dev, generator=g) * 0.1
     A_log = torch.log(torch.arange(1, N + 1, device=dev, dtype=torch.float32)).repeat(D, 1).contiguous()
@@ -264,23 +299,23 @@ def bench_shard(dev, iters=10):
     ms_conv = _timed(conv, iters, 2)
     ms_scan = _timed(scan, iters, 2)
     torch.cuda.synchronize()
-    # parity gate: one batch row, 64 channels, vs the oracle on the same bf16 inputs
+    # parity gate: batch row 0, channels 640..703, torch fp32 on the same bf16 inputs
     sl = slice(640, 704)
-    f = lambda t: t.float().cpu().numpy()
-    cref, _ = om.causal_conv1d(f(xs[0:1, sl]), f(w[sl]), f(cb[sl]), None, dtype=np.float64)
-    e_conv = float(np.abs(f(u[0:1, :, sl]).transpose(0, 2, 1) - om.silu(cref)).max() / np.abs(om.silu(cref)).max())
-    yr, hr = om.selective_scan(f(u[0:1, :, sl]).transpose(0, 2, 1), f(delta[0:1, :, sl]).transpose(0, 2, 1),
-                               -np.exp(f(A_log[sl]).astype(np.float64)), f(xdbl[0:1, :, R:R + N]),
-                               f(xdbl[0:1, :, R + N:]), f(Dv[sl]), f(z[0:1, sl]), f(bias[sl]), None,
-                               dtype=np.float64)
-    e_scan = float(np.abs(f(y[0:1, :, sl]).transpose(0, 2, 1) - yr).max() / np.abs(yr).max())
+    with torch.no_grad():
+        xr = F.pad(xs[0, sl].float(), (3, 0))
+        cref = F.silu(F.conv1d(xr[None], w[sl][:, None, :], cb[sl], groups=64)[0])
+        e_conv = float(((u[0, :, sl].float().T - cref).abs().max() / cref.abs().max()).item())
+        yr = _torch_scan_ref(u[0, :, sl].float().T, delta[0, :, sl].float().T, -torch.exp(A_log[sl]),
+                             xdbl[0, :, R:R + N].float(), xdbl[0, :, R + N:].float(), Dv[sl], z[0, sl].float(),
+                             bias[sl])
+        e_scan = float(((y[0, :, sl].float().T - yr).abs().max() / yr.abs().max()).item())
     conv_bytes = 2 * b * L * D * 2 + 2 * b * D * 3 * 2 + D * 4 * 4 + D * 4
     scan_bytes = 4 * b * L * D * 2 + 2 * b * N * L * 2 + b * D * N * 4 + D * N * 4 + 2 * D * 4
     return {"conv_us": ms_conv * 1e3, "conv_gbps": conv_bytes / ms_conv / 1e6,
             "scan_us": ms_scan * 1e3, "scan_gbps": scan_bytes / ms_scan / 1e6,
             "scan_frac_hbm_peak": scan_bytes / ms_scan / 1e6 / HBM_PEAK_GBPS,
             "tok_s": b * L / ((ms_conv + ms_scan) / 1000.0),
-            "max_rel_err": {"conv": e_conv, "scan": e_scan},
+            "max_rel_err_vs_torch_fp32": {"conv": e_conv, "scan": e_scan},
             "algorithmic_bytes": {"conv": conv_bytes, "scan": scan_bytes}}
 
 
@@ -290,8 +325,9 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--only", default="all", choices=["all", "scan", "decode", "quant", "shard", "prefill"])
+    ap.add_argument("--only", default="all", choices=["all", "scan", "decode", "quant", "shard", "prefill", "copy"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--decode-shapes", default="130m,1.4b", help="comma list of 130m, 1.4b")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}); "
@@ -308,10 +344,21 @@ def main():
     extra = {}
 
     want = lambda s: args.only in ("all", s)
+    if args.only == "copy":
+        # calibration for rocprofv3 FETCH_SIZE / WRITE_SIZE: a plain device copy
+        # of a known 1 GiB fp32 buffer, 5 times
+        n = 1 << 28
+        src = torch.randn(n, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_bytes_each_way": n * 4, "launches": 5}), flush=True)
+        return
     if want("scan"):
         log("scan: isolated selective scan fp32 [32,1536,1024]")
         t0 = time.perf_counter()
-        ms, trials, err = bench_scan(dev, args.steps, args.warmup)
+        ms, trials, gpu_run = bench_scan(dev, args.steps, args.warmup)
         wall = time.perf_counter() - t0
         gbps = SCAN_BYTES / ms / 1e6
         result.update({
@@ -324,29 +371,31 @@ def main():
             "roofline": {"bound": "hbm", "achieved": gbps, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                          "frac": gbps / HBM_PEAK_GBPS,
                          "traffic": traffic_from_profiles("scan_fp32_b32_d1536_l1024"),
-                         "kernel": "scan_fwd_kernel<float,4,16,true>", "algorithmic_bytes": SCAN_BYTES},
+                         "kernel": "scan_fwd_kernel<float, NW=4, SPW=4, TT=16, channel-major>",
+                         "algorithmic_bytes": SCAN_BYTES},
         })
         extra["scan_trials_ms"] = trials
-        extra["scan_max_rel_err"] = err
-        log(f"scan: {ms*1000:.1f} us/call, {gbps:.0f} GB/s ({gbps/HBM_PEAK_GBPS:.1%} of peak), err {err:.2e}, "
-            f"{wall:.1f}s")
+        log(f"scan: {ms*1000:.1f} us/call, {gbps:.0f} GB/s ({gbps/HBM_PEAK_GBPS:.1%} of peak), {wall:.1f}s")
         if not args.no_cpu_baseline:
             workers = max(1, min(16, os.cpu_count() or 1))
             log(f"cpu baseline: oracle scan, {workers} processes")
-            secs = cpu_baseline_scan(workers)
+            secs, err = cpu_baseline_scan(workers, gpu_run)
+            extra["scan_max_rel_err_vs_oracle"] = err
             result["cpu_baseline"] = {
                 "value": SCAN_B * SCAN_L / secs, "unit": "tok/s", "cores": workers, "kind": "port",
                 "sample": f"the full isolated-scan workload (32 rows x 1536 ch x 1024 steps x 16 states), numpy "
                           f"float32 materialize-then-loop, one batch row per process over {workers} processes; "
                           f"{secs:.1f} s wall",
                 "cpu_count": os.cpu_count()}
-            log(f"cpu baseline: {secs:.1f}s")
+            log(f"cpu baseline: {secs:.1f}s; GPU scan max rel err vs oracle {err:.2e}")
 
     if want("decode"):
         dec = {}
         for name, cfg_kw, batches, prompt, ntok in (
                 ("130m", dict(d_model=768, n_layer=24, vocab_size=50280), (1,), 64, 64),
                 ("1.4b", dict(d_model=2048, n_layer=48, vocab_size=50280), (1, 32), 1024, 64)):
+            if name not in args.decode_shapes.split(","):
+                continue
             try:
                 log(f"decode {name}: building model")
                 model = build_lm(MambaConfig(**cfg_kw), dev)

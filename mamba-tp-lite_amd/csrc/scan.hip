@@ -90,21 +90,29 @@ template <bool B> using Full = std::integral_constant<bool, B>;
 // NW wavefronts per workgroup = NW state groups of SPW states over the same
 // 64 channels.  CM: channel-major [b,D,l] rows (l-stride 1); otherwise
 // token-major (D-stride 1).  VEC: CM rows are aligned for vector access.
+//
+// A load tile is KC sub-tiles of TT steps: channel-major rows are read KC*TT
+// steps at a time (a whole 128-byte line per row for fp32 when KC*TT = 32,
+// both halves requested back to back) and y is written the same way, while
+// the scan works through LDS one TT-step sub-tile at a time.  Token-major
+// reads are full lines at any tile length, so there KC = 1.
 template <typename T, int NW, int SPW, int TT, bool CM, bool VEC>
-__global__ void __launch_bounds__(NW * 64) scan_fwd_kernel(const ScanArgs a) {
+__global__ void __launch_bounds__(NW * 64, 3) scan_fwd_kernel(const ScanArgs a) {
     constexpr int NT = NW * 64;
-    constexpr int E = TT * 64 / NT;            // consecutive timesteps one thread stages per tile
+    constexpr int E = TT * 64 / NT;            // consecutive steps one thread stages per sub-tile
+    constexpr int KC = CM ? 2 : 1;             // sub-tiles per load tile
+    constexpr int LT = KC * TT;                // steps per load tile
     constexpr int NP = NW * SPW;               // padded state count
-    constexpr int BCE = (NP * TT + NT - 1) / NT;
+    constexpr int BCE = (NP * LT + NT - 1) / NT;
     constexpr int TS = TT + 4;                 // [c][t] LDS row stride: 16B aligned, b128 conflict-free
-    static_assert(E % 4 == 0 && SPW % 1 == 0, "tile shape");
+    constexpr int BS = NP + 4;                 // padded B/C rows: staging writes spread over banks
+    static_assert(E % 4 == 0, "tile shape");
 
     __shared__ __align__(16) float s_dt[64][TS];
     __shared__ __align__(16) float s_dx[64][TS];
     __shared__ __align__(16) float s_y[NW][64][TS];
-    constexpr int BS = NP + 4;                 // padded B/C rows: staging writes spread over banks
-    __shared__ __align__(16) float s_B[TT][BS];
-    __shared__ __align__(16) float s_C[TT][BS];
+    __shared__ __align__(16) float s_B[LT][BS];
+    __shared__ __align__(16) float s_C[LT][BS];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -113,11 +121,12 @@ __global__ void __launch_bounds__(NW * 64) scan_fwd_kernel(const ScanArgs a) {
     const int c0 = blockIdx.x * 64;
     const int L = a.L, D = a.D, N = a.N;
 
-    // staging ownership: channel oc, timesteps [ot, ot + E) of each tile.
-    // Token-major puts 64 channels on the 64 lanes.  Channel-major gives each
-    // wavefront 64/NW channels x all NW row segments of the tile (the same
-    // addresses per load instruction as any other split), with the channel
-    // fastest across lanes so 8 adjacent lanes hit distinct LDS bank groups.
+    // staging ownership: channel oc and, in sub-tile kc, steps
+    // [kc*TT + ot, kc*TT + ot + E).  Token-major puts 64 channels on the 64
+    // lanes.  Channel-major gives each wavefront 64/NW channels x all NW row
+    // segments (the same addresses per load instruction as any other split),
+    // with the channel fastest across lanes so 8 adjacent lanes hit distinct
+    // LDS bank groups.
     constexpr int CPW = 64 / NW;               // channels per wavefront (CM)
     const int oc = CM ? wave * CPW + lane % CPW : lane;
     const int ot = CM ? (lane / CPW) * E : wave * E;
@@ -153,14 +162,16 @@ __global__ void __launch_bounds__(NW * 64) scan_fwd_kernel(const ScanArgs a) {
         h[k] = (ok && a.h0) ? a.h0[((int64_t)b * D + c0 + lane) * N + n] : 0.f;
     }
 
-    // raw tile registers: two sets, so the loads of tiles k+1 and k+2 are in
-    // flight while tile k is scanned (prefetch distance 2)
-    struct Raw { float u[E], d[E], z[E], B[BCE], C[BCE]; };
-    Raw r0, r1;
+    // raw load-tile registers: two sets, so the next load tile is in flight
+    // while the current one is scanned
+    struct Raw { float u[KC][E], d[KC][E], z[KC][E], B[BCE], C[BCE]; };
+    Raw r0;
+    [[maybe_unused]] Raw r1;
     float du[E], gz[E];
+    float yout[KC][E];
 
     // B/C staging slots of this thread (loop invariant): element e = tid + NT*k
-    // of the [TT x NP] tile.  Loads always read a valid address (state and
+    // of the [LT x NP] tile.  Loads always read a valid address (state and
     // time clamped); out-of-range slots are zeroed when staged.  No select
     // consumes a loaded register before the stage, so the prefetch stays in
     // flight across the scan (a select right after a load would force a wait
@@ -170,29 +181,32 @@ __global__ void __launch_bounds__(NW * 64) scan_fwd_kernel(const ScanArgs a) {
 #pragma unroll
     for (int k = 0; k < BCE; ++k) {
         const int e = tid + NT * k;
-        const int n = bc_t_fast ? e / TT : e % NP;
-        const int t = bc_t_fast ? e % TT : e / NP;
-        bc_ok[k] = e < NP * TT && n < N;
-        const int nc = min(n, N - 1);
-        bc_t[k] = min(t, TT - 1);
-        bc_off[k] = nc;
-        bc_slot[k] = (e < NP * TT) ? bc_t[k] * BS + n : -1;
+        const int n = bc_t_fast ? e / LT : e % NP;
+        const int t = bc_t_fast ? e % LT : e / NP;
+        bc_ok[k] = e < NP * LT && n < N;
+        bc_t[k] = min(t, LT - 1);
+        bc_off[k] = min(n, N - 1);
+        bc_slot[k] = (e < NP * LT) ? bc_t[k] * BS + n : -1;
     }
 
     auto load_tile = [&](Raw& r, int tb, auto full) {
         constexpr bool F = decltype(full)::value;
-        if constexpr (CM && F) {
-            load_run<T, E, VEC>(up + tb + ot, r.u);
-            load_run<T, E, VEC>(dp + tb + ot, r.d);
-            load_run<T, E, VEC>(zp + tb + ot, r.z);
-        } else {
-            const int64_t su = CM ? 1 : a.u_sl, sd = CM ? 1 : a.d_sl, sz = CM ? 1 : z_sl;
 #pragma unroll
-            for (int j = 0; j < E; ++j) {
-                const int t = F ? tb + ot + j : min(tb + ot + j, L - 1);
-                r.u[j] = Act<T>::load(up + t * su);
-                r.d[j] = Act<T>::load(dp + t * sd);
-                r.z[j] = Act<T>::load(zp + t * sz);
+        for (int kc = 0; kc < KC; ++kc) {
+            const int t0 = tb + kc * TT + ot;
+            if constexpr (CM && F) {
+                load_run<T, E, VEC>(up + t0, r.u[kc]);
+                load_run<T, E, VEC>(dp + t0, r.d[kc]);
+                load_run<T, E, VEC>(zp + t0, r.z[kc]);
+            } else {
+                const int64_t su = CM ? 1 : a.u_sl, sd = CM ? 1 : a.d_sl, sz = CM ? 1 : z_sl;
+#pragma unroll
+                for (int j = 0; j < E; ++j) {
+                    const int t = F ? t0 + j : min(t0 + j, L - 1);
+                    r.u[kc][j] = Act<T>::load(up + t * su);
+                    r.d[kc][j] = Act<T>::load(dp + t * sd);
+                    r.z[kc][j] = Act<T>::load(zp + t * sz);
+                }
             }
         }
 #pragma unroll
@@ -202,20 +216,23 @@ __global__ void __launch_bounds__(NW * 64) scan_fwd_kernel(const ScanArgs a) {
             r.C[k] = Act<T>::load(Cp + bc_off[k] * a.C_sn + (int64_t)t * a.C_sl);
         }
     };
-    auto stage_tile = [&](const Raw& r, int tb, auto full) {
+
+    // stage sub-tile kc of the load tile at tb (B/C of the whole load tile
+    // are staged with sub-tile 0)
+    auto stage_tile = [&](const Raw& r, int tb, int kc, auto full) {
         constexpr bool F = decltype(full)::value;
         float vdt[E], vdx[E];
 #pragma unroll
         for (int j = 0; j < E; ++j) {
-            const bool ok = F || tb + ot + j < L;
-            float dt = r.d[j] + bias_c;
+            const bool ok = F || tb + kc * TT + ot + j < L;
+            float dt = r.d[kc][j] + bias_c;
             if (a.softplus) dt = softplus_f(dt);
-            const float uv = ok ? r.u[j] : 0.f;
+            const float uv = ok ? r.u[kc][j] : 0.f;
             dt = ok ? dt : 0.f;                 // zero steps leave the state untouched past the end
             vdt[j] = dt;
             vdx[j] = dt * uv;
             du[j] = D_c * uv;
-            gz[j] = has_z ? silu_f(r.z[j]) : 1.f;
+            gz[j] = has_z ? silu_f(r.z[kc][j]) : 1.f;
         }
 #pragma unroll
         for (int q = 0; q < E / 4; ++q) {
@@ -224,19 +241,21 @@ __global__ void __launch_bounds__(NW * 64) scan_fwd_kernel(const ScanArgs a) {
             *reinterpret_cast<float4*>(&s_dx[oc][ot + 4 * q]) =
                 make_float4(vdx[4 * q], vdx[4 * q + 1], vdx[4 * q + 2], vdx[4 * q + 3]);
         }
+        if (kc == 0) {
 #pragma unroll
-        for (int k = 0; k < BCE; ++k) {
-            if (bc_slot[k] >= 0) {
-                const bool ok = bc_ok[k] && (F || tb + bc_t[k] < L);
-                (&s_B[0][0])[bc_slot[k]] = ok ? r.B[k] : 0.f;
-                (&s_C[0][0])[bc_slot[k]] = ok ? r.C[k] : 0.f;
+            for (int k = 0; k < BCE; ++k) {
+                if (bc_slot[k] >= 0) {
+                    const bool ok = bc_ok[k] && (F || tb + bc_t[k] < L);
+                    (&s_B[0][0])[bc_slot[k]] = ok ? r.B[k] : 0.f;
+                    (&s_C[0][0])[bc_slot[k]] = ok ? r.C[k] : 0.f;
+                }
             }
         }
     };
 
-    // TT recurrence steps; padded steps past the end have dt = dt*u = 0 and
-    // leave h unchanged, so the loop never needs a bound check
-    auto scan_tile = [&]() {
+    // TT recurrence steps of sub-tile kc; padded steps past the end have
+    // dt = dt*u = 0 and leave h unchanged, so the loop never needs a bound check
+    auto scan_tile = [&](int kc) {
 #pragma unroll
         for (int tt = 0; tt < TT; tt += 4) {
             const float4 dt4 = *reinterpret_cast<const float4*>(&s_dt[lane][tt]);
@@ -249,8 +268,8 @@ __global__ void __launch_bounds__(NW * 64) scan_fwd_kernel(const ScanArgs a) {
                 float acc = 0.f;
 #pragma unroll
                 for (int k = 0; k < SPW; ++k) {
-                    const float bk = s_B[tt + q][wave * SPW + k];
-                    const float ck = s_C[tt + q][wave * SPW + k];
+                    const float bk = s_B[kc * TT + tt + q][wave * SPW + k];
+                    const float ck = s_C[kc * TT + tt + q][wave * SPW + k];
                     h[k] = fmaf(__builtin_amdgcn_exp2f(dts[q] * a2[k]), h[k], dxs[q] * bk);
                     acc = fmaf(h[k], ck, acc);
                 }
@@ -260,9 +279,10 @@ __global__ void __launch_bounds__(NW * 64) scan_fwd_kernel(const ScanArgs a) {
         }
     };
 
-    auto finish_tile = [&](int tb, auto full) {
+    // y of sub-tile kc into registers; the whole load tile is stored after
+    // its last sub-tile
+    auto finish_tile = [&](int tb, int kc, auto full) {
         constexpr bool F = decltype(full)::value;
-        float out[E];
 #pragma unroll
         for (int q = 0; q < E / 4; ++q) {
             float4 acc = *reinterpret_cast<const float4*>(&s_y[0][oc][ot + 4 * q]);
@@ -271,54 +291,70 @@ __global__ void __launch_bounds__(NW * 64) scan_fwd_kernel(const ScanArgs a) {
                 const float4 p = *reinterpret_cast<const float4*>(&s_y[w][oc][ot + 4 * q]);
                 acc.x += p.x; acc.y += p.y; acc.z += p.z; acc.w += p.w;
             }
-            out[4 * q] = (acc.x + du[4 * q]) * gz[4 * q];
-            out[4 * q + 1] = (acc.y + du[4 * q + 1]) * gz[4 * q + 1];
-            out[4 * q + 2] = (acc.z + du[4 * q + 2]) * gz[4 * q + 2];
-            out[4 * q + 3] = (acc.w + du[4 * q + 3]) * gz[4 * q + 3];
+            yout[kc][4 * q] = (acc.x + du[4 * q]) * gz[4 * q];
+            yout[kc][4 * q + 1] = (acc.y + du[4 * q + 1]) * gz[4 * q + 1];
+            yout[kc][4 * q + 2] = (acc.z + du[4 * q + 2]) * gz[4 * q + 2];
+            yout[kc][4 * q + 3] = (acc.w + du[4 * q + 3]) * gz[4 * q + 3];
         }
-        if (!c_ok) return;
-        if constexpr (CM && F) {
-            store_run<T, E, VEC>(yp + tb + ot, out);
-        } else {
-            const int64_t sy = CM ? 1 : a.y_sl;
+        if (kc != KC - 1 || !c_ok) return;
 #pragma unroll
-            for (int j = 0; j < E; ++j)
-                if (F || tb + ot + j < L) Act<T>::store(yp + (int64_t)(tb + ot + j) * sy, out[j]);
+        for (int k2 = 0; k2 < KC; ++k2) {
+            const int t0 = tb + k2 * TT + ot;
+            if constexpr (CM && F) {
+                store_run<T, E, VEC>(yp + t0, yout[k2]);
+            } else {
+                const int64_t sy = CM ? 1 : a.y_sl;
+#pragma unroll
+                for (int j = 0; j < E; ++j)
+                    if (F || t0 + j < L) Act<T>::store(yp + (int64_t)(t0 + j) * sy, yout[k2][j]);
+            }
         }
     };
 
-    // one full tile: stage it from r, refill r with the full tile two ahead
-    // (if any), scan, write y.  Only full tiles pass through this pipeline, so
-    // the loads have a single code path (two paths would merge through
-    // register copies that wait for the loads).
-    const int nfull = L / TT;
-    auto run_full = [&](Raw& r, int i) {
-        stage_tile(r, i * TT, Full<true>{});
-        __syncthreads();
-        // unconditional refill (the last two tiles re-read tile nfull-1):
-        // a conditional one would again merge registers through copies
-        load_tile(r, min(i + 2, nfull - 1) * TT, Full<true>{});
-        scan_tile();
-        __syncthreads();
-        finish_tile(i * TT, Full<true>{});
+    auto run_subtiles = [&](Raw& r, int tb, auto full, auto refill) {
+#pragma unroll
+        for (int kc = 0; kc < KC; ++kc) {
+            stage_tile(r, tb, kc, full);
+            __syncthreads();
+            if (kc == KC - 1) refill();
+            scan_tile(kc);
+            __syncthreads();
+            finish_tile(tb, kc, full);
+        }
     };
 
-    if (nfull > 0) load_tile(r0, 0, Full<true>{});
-    if (nfull > 1) load_tile(r1, TT, Full<true>{});
-    int i = 0;
-    for (; i + 1 < nfull; i += 2) {
-        run_full(r0, i);
-        run_full(r1, i + 1);
+    // Only full load tiles pass through the pipeline, so the loads have a
+    // single code path (two paths would merge through register copies that
+    // wait for the loads).  The refill is unconditional: the last tiles
+    // re-read tile nfull-1 rather than branch.  Token-major keeps two raw
+    // sets (the tile two ahead in flight); channel-major load tiles are
+    // twice as long, so one set refilled right after its last sub-tile is
+    // staged keeps the next tile in flight across two sub-tile scans within
+    // the 3-waves-per-SIMD register budget.
+    const int nfull = L / LT;
+    if constexpr (KC == 1) {
+        auto run_full = [&](Raw& r, int i) {
+            run_subtiles(r, i * LT, Full<true>{},
+                         [&]() { load_tile(r, min(i + 2, nfull - 1) * LT, Full<true>{}); });
+        };
+        if (nfull > 0) load_tile(r0, 0, Full<true>{});
+        if (nfull > 1) load_tile(r1, LT, Full<true>{});
+        int i = 0;
+        for (; i + 1 < nfull; i += 2) {
+            run_full(r0, i);
+            run_full(r1, i + 1);
+        }
+        if (i < nfull) run_full(r0, i);
+    } else {
+        if (nfull > 0) load_tile(r0, 0, Full<true>{});
+        for (int i = 0; i < nfull; ++i)
+            run_subtiles(r0, i * LT, Full<true>{},
+                         [&]() { load_tile(r0, min(i + 1, nfull - 1) * LT, Full<true>{}); });
     }
-    if (i < nfull) run_full(r0, i);
-    if (nfull * TT < L) {  // the partial last tile, outside the pipeline
-        const int tb = nfull * TT;
+    if (nfull * LT < L) {  // the partial last load tile, outside the pipeline
+        const int tb = nfull * LT;
         load_tile(r0, tb, Full<false>{});
-        stage_tile(r0, tb, Full<false>{});
-        __syncthreads();
-        scan_tile();
-        __syncthreads();
-        finish_tile(tb, Full<false>{});
+        run_subtiles(r0, tb, Full<false>{}, []() {});
     }
 
     if (a.h_out) {
