@@ -179,6 +179,43 @@ int mtl_quant_dequant_sum_int8_tok(const float* const* parts, int32_t nparts, in
 int mtl_quant_dequant_sum_fp16(const float* const* parts, int32_t nparts, int64_t n,
                                uint16_t* const* payloads, float* out, mtl_stream_t stream);
 
+/* ------------------------------------------------------------------------
+ * Fused single-token decode step, fp32, batch 1, 2 or 4.
+ * Together these replace one MambaBlock.step (model.py:308-311) around
+ * MambaMixer.step (model.py:249-294): 3 launches per layer (4 when x_proj
+ * runs as its own row GEMV) instead of one per ATen op, every weight byte
+ * read once.  Deterministic: no atomics, fixed summation orders.
+ *
+ * mtl_decode_in: x [b, M] (or, for the first layer, emb [V, M] + ids [b],
+ *   with resid_out [b, M] receiving the gathered rows, model.py:348) ->
+ *   RMSNorm (norm_w, eps; model.py:130-135) -> in_proj rows W_in [2D, M]
+ *   (+ b_in) of channel blocks of `channels_per_block` (must be 8: one
+ *   workgroup per 8 channels, 4 in_proj rows per wavefront; model.py:261) ->
+ *   conv step with the in-place history shift of conv_state [b, D, K-1]
+ *   (conv_w [D, K], conv_b; model.py:264-274) -> xc = SiLU(conv)
+ *   (model.py:277), gz = SiLU(z) [b, D] -> if W_xT (x_proj transposed
+ *   [D, J], J = R + 2N) is given, the split-K partial x_proj sums of each
+ *   block into xpart [nblk, b, J] (model.py:279), nblk = ceil(D / cpb).
+ * mtl_decode_gemv: out [b, rows] = W [rows, cols] . v [b, cols] (+ bias)
+ *   (+ x_in, the residual add of model.py:311): the out_proj rows
+ *   (model.py:293) and, in the 4-launch form, the x_proj rows (279).
+ * mtl_decode_ssm: x_dbl [b, J] = sum over nblk of xpart (block order) ->
+ *   dt = softplus(W_dt [D, R] . dt_low + b_dt) (model.py:281-282) ->
+ *   ssm_state [b, D, N] updated in place with A = -exp(A_log) (284-289) ->
+ *   y [b, D] = (C . h + D x) * gz (model.py:290-292).  N <= 16.
+ * All pointers are device memory; W_in, W and v must be 16-byte aligned.
+ * ---------------------------------------------------------------------- */
+int mtl_decode_in(const float* x, const float* emb, const int64_t* ids, float* resid_out, const float* norm_w,
+                  float eps, const float* W_in, const float* b_in, float* conv_state, const float* conv_w,
+                  const float* conv_b, const float* W_xT, float* xc, float* gz, float* xpart, int32_t batch,
+                  int32_t d_model, int32_t d_inner, int32_t d_conv, int32_t xdbl_cols, int32_t channels_per_block,
+                  mtl_stream_t stream);
+int mtl_decode_gemv(const float* v, const float* W, const float* bias, const float* x_in, float* out, int32_t batch,
+                    int32_t rows, int32_t cols, mtl_stream_t stream);
+int mtl_decode_ssm(const float* xpart, int32_t nblk, const float* xc, const float* gz, const float* W_dt,
+                   const float* b_dt, const float* A_log, const float* Dv, float* ssm_state, float* y,
+                   int32_t batch, int32_t d_inner, int32_t d_state, int32_t dt_rank, mtl_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

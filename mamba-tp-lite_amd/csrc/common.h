@@ -4,6 +4,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <algorithm>
 #include <string>
 
 #include "mtl.h"
@@ -70,18 +71,41 @@ __device__ __forceinline__ float silu_f(float x) {
     return x * __builtin_amdgcn_rcpf(1.f + fast_exp(-x));
 }
 
-// Butterfly reductions inside a wavefront (64 lanes) or a power-of-two
-// group of lanes; __shfl_xor lowers to ds_swizzle / DPP on gfx950.
+// Reductions over a 16-lane DPP row or a whole 64-lane wavefront, in DPP
+// lane moves instead of LDS permutes.  Within a row: butterfly over
+// quad_perm [1,0,3,2], quad_perm [2,3,0,1], row_half_mirror, row_mirror --
+// each step combines two values that the partner lane combines in the other
+// order, so (with + and max commutative) every lane ends with the same bits.
+// Across rows: lanes 0, 16, 32, 48 are read out and combined as
+// (r0 + r1) + (r2 + r3).  Callers keep whole rows (whole wavefronts for the
+// 64-wide forms) active.
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float lane_read(float v, int lane) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
+}
+constexpr int kDppXor1 = 0xB1, kDppXor2 = 0x4E, kDppRowMirror = 0x140, kDppHalfMirror = 0x141;
+
 template <int WIDTH>
 __device__ __forceinline__ float group_sum(float v) {
-#pragma unroll
-    for (int o = WIDTH / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, WIDTH);
+    static_assert(WIDTH == 16 || WIDTH == 64, "16 or 64 lanes");
+    v += dpp_mov<kDppXor1>(v);
+    v += dpp_mov<kDppXor2>(v);
+    v += dpp_mov<kDppHalfMirror>(v);
+    v += dpp_mov<kDppRowMirror>(v);
+    if constexpr (WIDTH == 64) v = (lane_read(v, 0) + lane_read(v, 16)) + (lane_read(v, 32) + lane_read(v, 48));
     return v;
 }
 template <int WIDTH>
 __device__ __forceinline__ float group_max(float v) {
-#pragma unroll
-    for (int o = WIDTH / 2; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, WIDTH));
+    static_assert(WIDTH == 16 || WIDTH == 64, "16 or 64 lanes");
+    v = fmaxf(v, dpp_mov<kDppXor1>(v));
+    v = fmaxf(v, dpp_mov<kDppXor2>(v));
+    v = fmaxf(v, dpp_mov<kDppHalfMirror>(v));
+    v = fmaxf(v, dpp_mov<kDppRowMirror>(v));
+    if constexpr (WIDTH == 64) v = fmaxf(fmaxf(lane_read(v, 0), lane_read(v, 16)), fmaxf(lane_read(v, 32), lane_read(v, 48)));
     return v;
 }
 

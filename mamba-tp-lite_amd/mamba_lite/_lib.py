@@ -65,6 +65,11 @@ SIGNATURES = {
     "mtl_quant_dequant_sum_int8_tok": (ctypes.c_int, [ctypes.POINTER(_vp), _i32, _i64, _i64,
                                                       ctypes.POINTER(_vp), _fp, _vp]),
     "mtl_quant_dequant_sum_fp16": (ctypes.c_int, [ctypes.POINTER(_vp), _i32, _i64, ctypes.POINTER(_vp), _fp, _vp]),
+    "mtl_decode_in": (ctypes.c_int, [_fp, _fp, _vp, _fp, _fp, ctypes.c_float, _fp, _fp, _fp, _fp, _fp, _fp, _fp, _fp,
+                                     _fp, _i32, _i32, _i32, _i32, _i32, _i32, _vp]),
+    "mtl_decode_gemv": (ctypes.c_int, [_fp, _fp, _fp, _fp, _fp, _i32, _i32, _i32, _vp]),
+    "mtl_decode_ssm": (ctypes.c_int, [_fp, _i32, _fp, _fp, _fp, _fp, _fp, _fp, _fp, _fp, _i32, _i32, _i32, _i32,
+                                      _vp]),
 }
 
 _lib = None

@@ -287,10 +287,92 @@ class MambaLM(nn.Module):
 
     def step(self, input_ids: torch.Tensor, cache: MambaCache):
         """input_ids [b, 1] -> logits [b, 1, vocab]; cache updated in place
-        (reference model.py:343-353)."""
+        (reference model.py:343-353).  fp32 models at batch 1, 2 or 4 take
+        the fused decode path (3-4 launches per layer); others run the
+        per-op path (GEMMs + conv-step and SSM-update kernels)."""
+        if self._fused_step_ok(input_ids, cache):
+            return self._step_fused(input_ids, cache)
         x = self.embedding(input_ids).squeeze(1)
         xf = self._run(x, lambda i, xn: self.layers[i].mixer.step(xn, cache.layers[i]))
         return self.lm_head(xf).unsqueeze(1)
+
+    # ---- fused decode step ----
+    def _fused_step_ok(self, input_ids, cache) -> bool:
+        cfg = self.cfg
+        b = input_ids.shape[0]
+        if b not in (1, 2, 4) or cfg.d_state > 16 or cfg.d_model % 4 or cfg.d_inner % 4 or \
+                b * cfg.d_model > 15 * 1024 or cfg.d_inner > 4096 or cfg.dt_rank > 256 or cfg.d_conv > 8:
+            return False
+        if self.embedding.weight.dtype != torch.float32 or not input_ids.is_cuda:
+            return False
+        lc = cache.layers[0]
+        return lc.conv_state.dtype == torch.float32 and lc.ssm_state.dtype == torch.float32 and \
+            lc.conv_state.is_contiguous() and lc.ssm_state.is_contiguous()
+
+    def _decode_plan(self):
+        """Per-layer tensors of the fused step: x_proj transposed [D, J] for the
+        split-K partials, conv weights as [D, K].  Rebuilt whenever a source
+        parameter changes (tracked by tensor version and address)."""
+        key = tuple((m.mixer.x_proj.weight.data_ptr(), m.mixer.x_proj.weight._version,
+                     m.mixer.conv1d.weight.data_ptr(), m.mixer.conv1d.weight._version) for m in self.layers)
+        plan = getattr(self, "_plan", None)
+        if plan is not None and plan["key"] == key:
+            return plan
+        cfg = self.cfg
+        J = cfg.dt_rank + 2 * cfg.d_state
+        cpb = 8  # channels per decode_in workgroup (fixed by the kernel)
+        nblk = (cfg.d_inner + cpb - 1) // cpb
+        # every decode_ssm workgroup sums the x_proj partials with Q threads
+        # per (j, batch) pair and one batch of <= 64 loads per thread; when
+        # that does not cover nblk, x_proj runs as its own row GEMV instead
+        def _fits(b):
+            q = max(1, min(256 // (J * b), 8))
+            return -(-nblk // q) <= 64
+        split_k_max_b = max([b for b in (1, 2, 4) if _fits(b)], default=0)
+        split_k = split_k_max_b > 0
+        layers = []
+        with torch.no_grad():
+            for m in self.layers:
+                mx = m.mixer
+                w = mx.conv1d.weight
+                layers.append({
+                    "W_xT": mx.x_proj.weight.detach().t().contiguous() if split_k else None,
+                    "conv_w": w.detach().reshape(w.shape[0], w.shape[-1]).contiguous(),
+                })
+        self._plan = {"key": key, "layers": layers, "cpb": cpb, "nblk": nblk, "J": J,
+                      "split_k_max_b": split_k_max_b}
+        return self._plan
+
+    def _step_fused(self, input_ids, cache):
+        cfg = self.cfg
+        plan = self._decode_plan()
+        b, M, D, J = input_ids.shape[0], cfg.d_model, cfg.d_inner, plan["J"]
+        split_k = b <= plan["split_k_max_b"]
+        dev = input_ids.device
+        ids = input_ids.reshape(-1)
+        f32 = dict(device=dev, dtype=torch.float32)
+        xc = torch.empty(b, D, **f32)
+        gz = torch.empty(b, D, **f32)
+        y = torch.empty(b, D, **f32)
+        xs = [torch.empty(b, M, **f32) for _ in range(3)]
+        xpart = torch.empty(plan["nblk"] if split_k else 1, b, J, **f32)
+        x_cur = None
+        for i, blk in enumerate(self.layers):
+            mx, lp, lc = blk.mixer, plan["layers"][i], cache.layers[i]
+            resid = xs[2] if i == 0 else x_cur
+            ops.decode_in(blk.norm.weight, blk.norm.eps, mx.in_proj.weight, lc.conv_state, lp["conv_w"], xc, gz,
+                          x=x_cur, emb=self.embedding.weight if i == 0 else None, ids=ids if i == 0 else None,
+                          resid_out=xs[2] if i == 0 else None, b_in=mx.in_proj.bias, conv_b=mx.conv1d.bias,
+                          W_xT=lp["W_xT"] if split_k else None, xpart=xpart if split_k else None,
+                          channels_per_block=plan["cpb"])
+            if not split_k:
+                ops.decode_gemv(xc, mx.x_proj.weight, xpart[0])
+            ops.decode_ssm(xpart, xc, gz, mx.dt_proj.weight, mx.dt_proj.bias, mx.A_log, mx.D, lc.ssm_state, y)
+            x_next = xs[i % 2]
+            ops.decode_gemv(y, mx.out_proj.weight, x_next, bias=mx.out_proj.bias, x_in=resid)
+            x_cur = x_next
+        normed = ops.add_rmsnorm(x_cur, _f32(self.norm_f.weight), self.norm_f.eps)
+        return self.lm_head(normed).unsqueeze(1)
 
     @torch.no_grad()
     def generate(self, input_ids: torch.Tensor, max_new_tokens: int, greedy: bool = True):

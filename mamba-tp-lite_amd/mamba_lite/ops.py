@@ -336,3 +336,75 @@ def quant_dequant_sum_fp16(parts, payloads=None, out=None, return_payloads=False
         _lib.check(_lib.load().mtl_quant_dequant_sum_fp16(parr, len(parts), p0.numel(), qarr, _ptr(out),
                                                           _stream(p0)), "quant_dequant_sum_fp16")
     return out, payloads
+
+
+# --------------------------------------------------------------------------- fused decode step
+def _f32c(t, name):
+    if t is None:
+        return None
+    if t.dtype != torch.float32 or not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous float32")
+    return t
+
+
+def decode_in(norm_w, eps, W_in, conv_state, conv_w, xc, gz, *, x=None, emb=None, ids=None, resid_out=None,
+              b_in=None, conv_b=None, W_xT=None, xpart=None, channels_per_block=8):
+    """mtl_decode_in: RMSNorm -> in_proj rows -> conv step (conv_state in
+    place) -> xc = SiLU(conv), gz = SiLU(z), and optionally the x_proj split-K
+    partials into xpart [nblk, b, J].  x [b, M] or (emb [V, M], ids [b])."""
+    b, D = xc.shape
+    M = norm_w.shape[0]
+    K = conv_w.shape[1]
+    for name, t in (("norm_w", norm_w), ("W_in", W_in), ("conv_state", conv_state), ("conv_w", conv_w),
+                    ("xc", xc), ("gz", gz), ("x", x), ("emb", emb), ("resid_out", resid_out), ("b_in", b_in),
+                    ("conv_b", conv_b), ("W_xT", W_xT), ("xpart", xpart)):
+        _f32c(t, name)
+    if tuple(W_in.shape) != (2 * D, M) or tuple(conv_state.shape) != (b, D, K - 1) or tuple(gz.shape) != (b, D):
+        raise ValueError("decode_in: W_in [2D, M], conv_state [b, D, K-1], xc/gz [b, D] expected")
+    if x is not None and tuple(x.shape) != (b, M):
+        raise ValueError(f"x must be {(b, M)}")
+    if ids is not None and (ids.dtype != torch.int64 or ids.numel() != b or not ids.is_contiguous()):
+        raise ValueError("ids must be contiguous int64 with b entries")
+    J = W_xT.shape[1] if W_xT is not None else 1
+    if W_xT is not None:
+        nblk = (D + channels_per_block - 1) // channels_per_block
+        if tuple(W_xT.shape) != (D, J) or xpart is None or tuple(xpart.shape) != (nblk, b, J):
+            raise ValueError("decode_in: W_xT [D, J] and xpart [nblk, b, J] expected")
+    with _dev_guard(xc):
+        _lib.check(_lib.load().mtl_decode_in(_ptr(x), _ptr(emb), _ptr(ids), _ptr(resid_out), _ptr(norm_w), float(eps),
+                                             _ptr(W_in), _ptr(b_in), _ptr(conv_state), _ptr(conv_w), _ptr(conv_b),
+                                             _ptr(W_xT), _ptr(xc), _ptr(gz), _ptr(xpart), b, M, D, K, J,
+                                             channels_per_block, _stream(xc)), "decode_in")
+
+
+def decode_gemv(v, W, out, bias=None, x_in=None):
+    """mtl_decode_gemv: out [b, rows] = W [rows, cols] . v [b, cols] (+ bias)
+    (+ x_in)."""
+    for name, t in (("v", v), ("W", W), ("out", out), ("bias", bias), ("x_in", x_in)):
+        _f32c(t, name)
+    b, cols = v.shape
+    rows = W.shape[0]
+    if W.shape[1] != cols or tuple(out.shape) != (b, rows):
+        raise ValueError("decode_gemv: W [rows, cols], v [b, cols], out [b, rows] expected")
+    with _dev_guard(v):
+        _lib.check(_lib.load().mtl_decode_gemv(_ptr(v), _ptr(W), _ptr(bias), _ptr(x_in), _ptr(out), b, rows, cols,
+                                               _stream(v)), "decode_gemv")
+    return out
+
+
+def decode_ssm(xpart, xc, gz, W_dt, b_dt, A_log, Dv, ssm_state, y):
+    """mtl_decode_ssm: reduce x_proj partials [nblk, b, J] -> dt_proj +
+    softplus -> ssm_state update in place -> y = (C.h + D x) * gz."""
+    for name, t in (("xpart", xpart), ("xc", xc), ("gz", gz), ("W_dt", W_dt), ("b_dt", b_dt), ("A_log", A_log),
+                    ("Dv", Dv), ("ssm_state", ssm_state), ("y", y)):
+        _f32c(t, name)
+    b, D = xc.shape
+    N = A_log.shape[1]
+    R = W_dt.shape[1]
+    if xpart.dim() != 3 or xpart.shape[1:] != (b, R + 2 * N) or tuple(ssm_state.shape) != (b, D, N):
+        raise ValueError("decode_ssm: xpart [nblk, b, R+2N], ssm_state [b, D, N] expected")
+    with _dev_guard(xc):
+        _lib.check(_lib.load().mtl_decode_ssm(_ptr(xpart), xpart.shape[0], _ptr(xc), _ptr(gz), _ptr(W_dt),
+                                              _ptr(b_dt), _ptr(A_log), _ptr(Dv), _ptr(ssm_state), _ptr(y), b, D, N,
+                                              R, _stream(xc)), "decode_ssm")
+    return y

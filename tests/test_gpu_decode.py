@@ -1,0 +1,118 @@
+"""Fused decode step (mtl_decode_in / mtl_decode_gemv / mtl_decode_ssm) on
+the GPU: against the per-op step path and the oracle, at the 130m width
+(d_model 768: register-blocked rows, x_proj as split-K partials) and the
+1.4b width (d_model 2048: x_proj as its own row GEMV), batch 1, 2 and 4.
+fp32 within 1e-4 relative; the in-place cache and graph replay checks are
+bit-exact."""
+import numpy as np
+import pytest
+import torch
+
+from _util import assert_rel
+from mamba_lite.cuda_graph import GraphedStepper
+from mamba_lite.model import MambaConfig, MambaLM, MambaMixer
+from oracle import mixer as om
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _np(t):
+    return t.detach().float().cpu().numpy()
+
+
+def _model(d_model, n_layer, vocab, seed):
+    torch.manual_seed(seed)
+    cfg = MambaConfig(d_model=d_model, n_layer=n_layer, vocab_size=vocab, d_state=16)
+    with torch.device(DEV):
+        m = MambaLM(cfg)
+    rng = np.random.default_rng(seed)
+    with torch.no_grad():
+        for mx in m.modules():
+            if isinstance(mx, MambaMixer):
+                D = mx.dt_proj.bias.shape[0]
+                mx.dt_proj.bias.copy_(torch.from_numpy(
+                    om.inv_softplus(np.exp(rng.uniform(np.log(1e-3), np.log(0.1), D))).astype(np.float32)))
+    return m.eval()
+
+
+def _per_op_step(model, ids, cache):
+    """The unfused step: GEMMs + conv-step and SSM-update kernels."""
+    x = model.embedding(ids).squeeze(1)
+    xf = model._run(x, lambda i, xn: model.layers[i].mixer.step(xn, cache.layers[i]))
+    return model.lm_head(xf).unsqueeze(1)
+
+
+@pytest.mark.parametrize("d_model,split_max_b", [(768, 1), (2048, 0), (64, 4)])
+@pytest.mark.parametrize("b", [1, 2, 4])
+def test_fused_step_matches_per_op_step(d_model, split_max_b, b):
+    """split_max_b: the largest batch whose x_proj runs as split-K partials
+    (1 at the 130m width, never at the 1.4b width)."""
+    print(f"fused decode d_model={d_model} b={b}", flush=True)
+    model = _model(d_model, 2, 512, seed=d_model + b)
+    assert model._decode_plan()["split_k_max_b"] == split_max_b
+    ids = torch.randint(0, 512, (b, 6), device=DEV)
+    with torch.no_grad():
+        _, c1 = model.prefill(ids)
+        _, c2 = model.prefill(ids)
+        assert model._fused_step_ok(ids[:, :1], c1)
+        ptrs = [(l.conv_state.data_ptr(), l.ssm_state.data_ptr()) for l in c1.layers]
+        for t in range(3):
+            nxt = torch.randint(0, 512, (b, 1), device=DEV)
+            got = model.step(nxt, c1)
+            ref = _per_op_step(model, nxt, c2)
+            assert_rel(_np(got), _np(ref), 1e-4, f"logits step {t}")
+        for l1, l2 in zip(c1.layers, c2.layers):
+            assert_rel(_np(l1.ssm_state), _np(l2.ssm_state), 1e-4, "ssm_state")
+            assert_rel(_np(l1.conv_state), _np(l2.conv_state), 1e-5, "conv_state")
+        assert ptrs == [(l.conv_state.data_ptr(), l.ssm_state.data_ptr()) for l in c1.layers]
+
+
+def test_fused_step_vs_oracle():
+    model = _model(768, 2, 256, seed=11)
+    W = {"embedding": _np(model.embedding.weight), "norm_f": _np(model.norm_f.weight), "layers": []}
+    for blk in model.layers:
+        m = blk.mixer
+        W["layers"].append({"norm": _np(blk.norm.weight), "in_proj_w": _np(m.in_proj.weight),
+                            "conv_w": _np(m.conv1d.weight)[:, 0, :], "conv_b": _np(m.conv1d.bias),
+                            "x_proj_w": _np(m.x_proj.weight), "dt_proj_w": _np(m.dt_proj.weight),
+                            "dt_proj_b": _np(m.dt_proj.bias), "A_log": _np(m.A_log), "D": _np(m.D),
+                            "out_proj_w": _np(m.out_proj.weight)})
+    ids = torch.randint(0, 256, (1, 5), device=DEV)
+    with torch.no_grad():
+        _, cache = model.prefill(ids[:, :4])
+        got = model.step(ids[:, 4:5], cache)
+    _, rc = om.lm_prefill(W, ids[:, :4].cpu().numpy(), dtype=np.float64)
+    ref = om.lm_step(W, ids[:, 4:5].cpu().numpy(), rc, dtype=np.float64)
+    assert_rel(_np(got), ref, 1e-4, "fused step vs oracle")
+
+
+def test_fused_step_graph_replay_bit_identical():
+    model = _model(768, 3, 1024, seed=5)
+    ids = torch.randint(0, 1024, (1, 8), device=DEV)
+    steps = [torch.randint(0, 1024, (1, 1), device=DEV) for _ in range(4)]
+    with torch.no_grad():
+        _, ce = model.prefill(ids)
+        eager = [model.step(s, ce).clone() for s in steps]
+        _, cg = model.prefill(ids)
+        st = GraphedStepper(model, cg, 1, "cuda")
+        st.capture()
+        for i, s in enumerate(steps):
+            g = st.replay(s).clone()
+            torch.cuda.synchronize()
+            assert torch.equal(g, eager[i]), f"replay {i}"
+    for a, b in zip(ce.layers, cg.layers):
+        assert torch.equal(a.ssm_state, b.ssm_state) and torch.equal(a.conv_state, b.conv_state)
+
+
+def test_plan_refreshes_after_weight_change():
+    model = _model(64, 1, 128, seed=3)
+    ids = torch.randint(0, 128, (1, 3), device=DEV)
+    with torch.no_grad():
+        _, c1 = model.prefill(ids)
+        model.step(ids[:, :1], c1)
+        p1 = model._decode_plan()
+        model.layers[0].mixer.x_proj.weight.mul_(0.5)
+        p2 = model._decode_plan()
+        assert p2 is not p1
+        assert torch.equal(p2["layers"][0]["W_xT"], model.layers[0].mixer.x_proj.weight.t().contiguous())
