@@ -324,7 +324,7 @@ def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=100)
-    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--only", default="all", choices=["all", "scan", "decode", "quant", "shard", "prefill", "copy"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--decode-shapes", default="130m,1.4b", help="comma list of 130m, 1.4b")

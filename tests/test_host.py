@@ -115,3 +115,21 @@ def test_shard_params_partition_the_dense_mixer():
 def test_layer_cache_is_a_dataclass_pair():
     lc = LayerCache(conv_state=torch.zeros(1, 2, 3), ssm_state=torch.zeros(1, 2, 4))
     assert lc.conv_state.shape == (1, 2, 3) and lc.ssm_state.shape == (1, 2, 4)
+
+
+def test_product_package_never_imports_the_oracle():
+    """The oracle is test infrastructure: nothing under the package may import
+    or load it (no CPU fallback path)."""
+    import os
+    import re
+    pkg = os.path.join(os.path.dirname(__file__), "..", "mamba-tp-lite_amd")
+    pat = re.compile(r"^\s*(from\s+oracle\b|import\s+oracle\b)|['\"]oracle[/'\"]", re.M)
+    hits = []
+    for dirpath, _, files in os.walk(pkg):
+        for f in files:
+            if f.endswith((".py", ".hip", ".cpp", ".h")):
+                path = os.path.join(dirpath, f)
+                with open(path, encoding="utf-8") as fh:
+                    if pat.search(fh.read()):
+                        hits.append(path)
+    assert hits == []
