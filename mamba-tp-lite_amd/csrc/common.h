@@ -109,4 +109,25 @@ __device__ __forceinline__ float group_max(float v) {
     return v;
 }
 
+// Fixed-count register blocking: kernels that hold RUNS values per lane are
+// instantiated for these counts; a size needing `need` runs uses the
+// smallest instantiated count >= need (the extra runs are masked).
+constexpr int kMaxRuns = 16;
+inline int round_runs(int need) {
+    for (int p : {1, 2, 3, 4, 6, 8, 12})
+        if (p >= need) return p;
+    return kMaxRuns;
+}
+#define MTL_DISPATCH_RUNS(NAME, VALUE, ...)                          \
+    switch (VALUE) {                                                 \
+        case 1: { constexpr int NAME = 1; __VA_ARGS__; } break;      \
+        case 2: { constexpr int NAME = 2; __VA_ARGS__; } break;      \
+        case 3: { constexpr int NAME = 3; __VA_ARGS__; } break;      \
+        case 4: { constexpr int NAME = 4; __VA_ARGS__; } break;      \
+        case 6: { constexpr int NAME = 6; __VA_ARGS__; } break;      \
+        case 8: { constexpr int NAME = 8; __VA_ARGS__; } break;      \
+        case 12: { constexpr int NAME = 12; __VA_ARGS__; } break;    \
+        default: { constexpr int NAME = 16; __VA_ARGS__; } break;    \
+    }
+
 }  // namespace mtl

@@ -34,7 +34,7 @@ namespace {
 
 constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / 64;
-constexpr int kMaxPL = 16;                         // float4 runs per lane: rows of up to 4096 floats
+constexpr int kMaxPL = kMaxRuns;                   // float4 runs per lane: rows of up to 4096 floats
 static_assert(kWaves == 4, "the block reductions below add 4 wavefront sums");
 
 template <int B>
@@ -303,6 +303,62 @@ __global__ void __launch_bounds__(kThreads) decode_gemv_kernel(const GemvArgs a)
     }
 }
 
+// Few long rows (x_proj at d_inner 4096: 160 rows): one workgroup per row,
+// the 4 wavefronts take quarters of it (PLW float4 runs per lane each,
+// K <= 1024 PLW) and their sums are added in wavefront order.
+template <int B, int PLW>
+__global__ void __launch_bounds__(kThreads) decode_gemv_split_kernel(const GemvArgs a) {
+    extern __shared__ __align__(16) float s_v[];      // [B][K], then the [kWaves][B] wavefront sums
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int K = a.K, K4 = K >> 2;
+    const int m = blockIdx.x;
+    const float4* row = reinterpret_cast<const float4*>(a.W + (int64_t)m * K);
+    float4 w[PLW];
+#pragma unroll
+    for (int p = 0; p < PLW; ++p) w[p] = row[min((wave * PLW + p) * 64 + lane, K4 - 1)];
+    const float bias = a.bias ? a.bias[m] : 0.f;
+    float xin[B];
+#pragma unroll
+    for (int bi = 0; bi < B; ++bi) xin[bi] = a.x_in ? a.x_in[(int64_t)bi * a.Mrows + m] : 0.f;
+    constexpr int PL = kWaves * PLW;
+    float vv[B][PL];
+#pragma unroll
+    for (int q = 0; q < PL; ++q)
+#pragma unroll
+        for (int bi = 0; bi < B; ++bi) vv[bi][q] = a.v[(int64_t)bi * K + min(tid + q * kThreads, K - 1)];
+#pragma unroll
+    for (int q = 0; q < PL; ++q)
+        if (tid + q * kThreads < K)
+#pragma unroll
+            for (int bi = 0; bi < B; ++bi) s_v[bi * K + tid + q * kThreads] = vv[bi][q];
+    __syncthreads();
+
+    float acc[B];
+#pragma unroll
+    for (int bi = 0; bi < B; ++bi) acc[bi] = 0.f;
+#pragma unroll
+    for (int p = 0; p < PLW; ++p) {
+        const int k4 = (wave * PLW + p) * 64 + lane;
+        const bool ok = k4 < K4;
+#pragma unroll
+        for (int bi = 0; bi < B; ++bi) {
+            const float4 x4 = reinterpret_cast<const float4*>(s_v + (size_t)bi * K)[min(k4, K4 - 1)];
+            const float t = dot4(w[p], x4, acc[bi]);
+            acc[bi] = ok ? t : acc[bi];
+        }
+    }
+    wave_sum<B>(acc);
+    __syncthreads();                                  // every wavefront is done reading s_v
+    if (lane == 0)
+#pragma unroll
+        for (int bi = 0; bi < B; ++bi) s_v[wave * B + bi] = acc[bi];
+    __syncthreads();
+    if (tid < B) {
+        const float o = ((s_v[tid] + s_v[B + tid]) + (s_v[2 * B + tid] + s_v[3 * B + tid])) + bias;
+        a.out[(int64_t)tid * a.Mrows + m] = a.x_in ? xin[tid] + o : o;
+    }
+}
+
 // ---------------------------------------------------------------- decode_ssm
 struct SsmArgs {
     const float* xpart;      // [nblk, b, J]
@@ -404,42 +460,12 @@ __global__ void __launch_bounds__(kThreads) decode_ssm_kernel(const SsmArgs a) {
     }
 }
 
-// smallest instantiated run count >= need (need in 1..kMaxPL)
-inline int round_pl(int need) {
-    for (int p : {1, 2, 3, 4, 6, 8, 12})
-        if (p >= need) return p;
-    return 16;
-}
-
-#define MTL_DISPATCH_PL(PLV, ...)                                  \
-    switch (PLV) {                                                 \
-        case 1: { constexpr int PL = 1; __VA_ARGS__; } break;      \
-        case 2: { constexpr int PL = 2; __VA_ARGS__; } break;      \
-        case 3: { constexpr int PL = 3; __VA_ARGS__; } break;      \
-        case 4: { constexpr int PL = 4; __VA_ARGS__; } break;      \
-        case 6: { constexpr int PL = 6; __VA_ARGS__; } break;      \
-        case 8: { constexpr int PL = 8; __VA_ARGS__; } break;      \
-        case 12: { constexpr int PL = 12; __VA_ARGS__; } break;    \
-        default: { constexpr int PL = 16; __VA_ARGS__; } break;    \
-    }
 #define MTL_DISPATCH_B(BV, ...)                                    \
     switch (BV) {                                                  \
         case 1: { constexpr int B = 1; __VA_ARGS__; } break;       \
         case 2: { constexpr int B = 2; __VA_ARGS__; } break;       \
         default: { constexpr int B = 4; __VA_ARGS__; } break;      \
     }
-#define MTL_DISPATCH_RQ(RQV, ...)                                  \
-    switch (RQV) {                                                 \
-        case 1: { constexpr int RQ = 1; __VA_ARGS__; } break;      \
-        case 2: { constexpr int RQ = 2; __VA_ARGS__; } break;      \
-        case 3: { constexpr int RQ = 3; __VA_ARGS__; } break;      \
-        case 4: { constexpr int RQ = 4; __VA_ARGS__; } break;      \
-        case 6: { constexpr int RQ = 6; __VA_ARGS__; } break;      \
-        case 8: { constexpr int RQ = 8; __VA_ARGS__; } break;      \
-        case 12: { constexpr int RQ = 12; __VA_ARGS__; } break;    \
-        default: { constexpr int RQ = 16; __VA_ARGS__; } break;    \
-    }
-
 }  // namespace
 }  // namespace mtl
 
@@ -465,8 +491,8 @@ extern "C" int mtl_decode_in(const float* x, const float* emb, const int64_t* id
              d_model, d_inner, d_conv, xdbl_cols, eps};
     const dim3 grid((unsigned)((d_inner + kCB - 1) / kCB));
     hipStream_t st = as_stream(stream);
-    const int plv = round_pl((d_model / 4 + 63) / 64);
-    MTL_DISPATCH_B(batch, MTL_DISPATCH_PL(plv, hipLaunchKernelGGL((decode_in_kernel<B, PL>), grid, dim3(kThreads),
+    const int plv = round_runs((d_model / 4 + 63) / 64);
+    MTL_DISPATCH_B(batch, MTL_DISPATCH_RUNS(PL, plv, hipLaunchKernelGGL((decode_in_kernel<B, PL>), grid, dim3(kThreads),
                                                                   smem, st, a)));
     return check_launch("decode_in");
 }
@@ -484,11 +510,20 @@ extern "C" int mtl_decode_gemv(const float* v, const float* W, const float* bias
     const size_t smem = sizeof(float) * (size_t)batch * cols;
     MTL_REQUIRE(smem <= 64 * 1024, "batch * cols too large for the decode LDS tile");
     GemvArgs a{v, W, bias, x_in, out, rows, cols};
-    const dim3 grid((unsigned)((rows + kWaves - 1) / kWaves));
     hipStream_t st = as_stream(stream);
-    const int plv = round_pl((cols / 4 + 63) / 64);
-    MTL_DISPATCH_B(batch, MTL_DISPATCH_PL(plv, hipLaunchKernelGGL((decode_gemv_kernel<B, PL>), grid,
-                                                                  dim3(kThreads), smem, st, a)));
+    const int runs = (cols / 4 + 63) / 64;
+    if (rows < 128 * kWaves && runs >= 2 * kWaves) {
+        // few long rows: a workgroup per row, split four ways
+        const int plw = round_runs((runs + kWaves - 1) / kWaves);
+        MTL_REQUIRE(plw * kWaves <= kMaxPL, "internal: split GEMV run count");
+        MTL_DISPATCH_B(batch, MTL_DISPATCH_RUNS(PLW, plw,
+            if constexpr (PLW * kWaves <= kMaxPL) hipLaunchKernelGGL((decode_gemv_split_kernel<B, PLW>),
+                dim3((unsigned)rows), dim3(kThreads), smem, st, a)));
+    } else {
+        const dim3 grid((unsigned)((rows + kWaves - 1) / kWaves));
+        MTL_DISPATCH_B(batch, MTL_DISPATCH_RUNS(PL, round_runs(runs), hipLaunchKernelGGL((decode_gemv_kernel<B, PL>),
+                                                                  grid, dim3(kThreads), smem, st, a)));
+    }
     return check_launch("decode_gemv");
 }
 
@@ -510,8 +545,8 @@ extern "C" int mtl_decode_ssm(const float* xpart, int32_t nblk, const float* xc,
     SsmArgs a{xpart, nblk, xc, gz, W_dt, b_dt, A_log, Dv, ssm_state, y, d_inner, d_state, dt_rank, J};
     const dim3 grid((unsigned)((d_inner + kSsmChannels - 1) / kSsmChannels));
     hipStream_t st = as_stream(stream);
-    const int rqv = round_pl((dt_rank + 15) / 16);
-    MTL_DISPATCH_B(batch, MTL_DISPATCH_RQ(rqv, hipLaunchKernelGGL((decode_ssm_kernel<B, RQ>), grid, dim3(kThreads),
+    const int rqv = round_runs((dt_rank + 15) / 16);
+    MTL_DISPATCH_B(batch, MTL_DISPATCH_RUNS(RQ, rqv, hipLaunchKernelGGL((decode_ssm_kernel<B, RQ>), grid, dim3(kThreads),
                                                                   smem, st, a)));
     return check_launch("decode_ssm");
 }

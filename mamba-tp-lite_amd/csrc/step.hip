@@ -5,8 +5,9 @@
 //   h <- h*dA + (dt*B)*x (in place, the graph-stable cache buffer, 289);
 //   y = sum_n h*C + D*x; y *= silu(z).
 // Sixteen lanes serve one channel: lane n owns state n and a 1/16 slice of
-// the dt_proj dot product; both the dot product and y are 16-lane butterfly
-// sums, so a single wavefront updates four channels with no LDS traffic.
+// the dt_proj dot product; both the dot product and y are 16-lane DPP
+// butterfly sums, so a single wavefront updates four channels with no LDS
+// traffic.  A workgroup serves 16 channels of up to 8 batch rows.
 //
 // mtl_add_rmsnorm replaces the residual add of MambaBlock (model.py:306,
 // 311) fused with the following RMSNorm (model.py:130-135).
@@ -20,56 +21,125 @@ constexpr int kLanesPerChannel = 16;
 constexpr int kStepThreads = 256;
 constexpr int kChPerBlock = kStepThreads / kLanesPerChannel;
 
-template <typename T>
+// RQ = dt_proj columns per lane (R <= 16 RQ); BB = batch rows per workgroup,
+// so W_dt, A, D and the biases are read once per BB rows.  Every operand is
+// loaded up front with clamped addresses, then the BB rows are updated.
+template <typename T, int RQ, int BB>
 __global__ void __launch_bounds__(kStepThreads)
 ssm_step_kernel(float* __restrict__ state, const T* __restrict__ x, int64_t x_sb, const T* __restrict__ z,
                 int64_t z_sb, const T* __restrict__ xdbl, int64_t xdbl_sb, const float* __restrict__ Wdt,
                 const float* __restrict__ bdt, const float* __restrict__ A, const float* __restrict__ Dv,
-                T* __restrict__ y, int64_t y_sb, int D, int N, int R, int a_is_log) {
+                T* __restrict__ y, int64_t y_sb, int D, int N, int R, int batch, int a_is_log) {
     const int g = threadIdx.x / kLanesPerChannel;
     const int n = threadIdx.x % kLanesPerChannel;
     const int c = blockIdx.x * kChPerBlock + g;
-    const int b = blockIdx.y;
-    if (c >= D) return;  // uniform over the 16-lane group
+    const int cc = min(c, D - 1), nn = min(n, N - 1);
+    const int b0 = blockIdx.y * BB;
 
-    const T* xd = xdbl + b * xdbl_sb;
-    float acc = 0.f;
-    for (int r = n; r < R; r += kLanesPerChannel)
-        acc = fmaf(Wdt[(int64_t)c * R + r], Act<T>::load(xd + r), acc);
-    acc = group_sum<kLanesPerChannel>(acc);
-    const float dt = softplus_f(acc + bdt[c]);
-    const float xv = Act<T>::load(x + b * x_sb + c);
-
-    float yv = 0.f;
-    if (n < N) {
-        float av = A[(int64_t)c * N + n];
-        if (a_is_log) av = -expf(av);
-        const float dA = __builtin_amdgcn_exp2f(dt * (av * kLog2e));
-        const float Bn = Act<T>::load(xd + R + n);
-        const float Cn = Act<T>::load(xd + R + N + n);
-        float* sp = state + ((int64_t)b * D + c) * N + n;
-        const float hv = fmaf(*sp, dA, (dt * Bn) * xv);
-        *sp = hv;
-        yv = hv * Cn;
+    float wdt[RQ];
+#pragma unroll
+    for (int q = 0; q < RQ; ++q) wdt[q] = Wdt[(int64_t)cc * R + min(n + 16 * q, R - 1)];
+    float av = A[(int64_t)cc * N + nn];
+    const float bd = bdt[cc];
+    const float Dc = Dv ? Dv[cc] : 0.f;
+    float hs[BB], xv[BB], zv[BB], Bn[BB], Cn[BB], dl[BB][RQ];
+#pragma unroll
+    for (int i = 0; i < BB; ++i) {
+        const int64_t b = min(b0 + i, batch - 1);
+        hs[i] = state[(b * D + cc) * N + nn];
+        xv[i] = Act<T>::load(x + b * x_sb + cc);
+        zv[i] = z ? Act<T>::load(z + b * z_sb + cc) : 0.f;
+        const T* xd = xdbl + b * xdbl_sb;
+#pragma unroll
+        for (int q = 0; q < RQ; ++q) dl[i][q] = Act<T>::load(xd + min(n + 16 * q, R - 1));
+        Bn[i] = Act<T>::load(xd + R + nn);
+        Cn[i] = Act<T>::load(xd + R + N + nn);
     }
-    yv = group_sum<kLanesPerChannel>(yv);
-    if (n == 0) {
-        if (Dv) yv += xv * Dv[c];
-        if (z) yv *= silu_f(Act<T>::load(z + b * z_sb + c));
-        Act<T>::store(y + b * y_sb + c, yv);
+    if (c >= D) return;  // whole 16-lane row
+    if (a_is_log) av = -expf(av);
+
+#pragma unroll
+    for (int i = 0; i < BB; ++i) {
+        const int64_t b = b0 + i;
+        if (b >= batch) break;  // uniform over the workgroup
+        float acc = 0.f;
+#pragma unroll
+        for (int q = 0; q < RQ; ++q) {
+            const float t = fmaf(wdt[q], dl[i][q], acc);
+            acc = n + 16 * q < R ? t : acc;
+        }
+        acc = group_sum<kLanesPerChannel>(acc);
+        const float dt = softplus_f(acc + bd);
+        float yv = 0.f;
+        if (n < N) {
+            const float dA = __builtin_amdgcn_exp2f(dt * (av * kLog2e));
+            const float hv = fmaf(hs[i], dA, (dt * Bn[i]) * xv[i]);
+            state[(b * D + c) * N + n] = hv;
+            yv = hv * Cn[i];
+        }
+        yv = group_sum<kLanesPerChannel>(yv);
+        if (n == 0) {
+            if (Dv) yv += xv[i] * Dc;
+            if (z) yv *= silu_f(zv[i]);
+            Act<T>::store(y + b * y_sb + c, yv);
+        }
     }
 }
 
 constexpr int kNormThreads = 256;
 
+// One workgroup per row.  RUNS elements per thread (cols <= 256 RUNS),
+// loaded up front with clamped addresses.
+template <int RUNS>
 __global__ void __launch_bounds__(kNormThreads)
 add_rmsnorm_kernel(const float* __restrict__ x, const float* __restrict__ y, float* x_out,
                    const float* __restrict__ w, float* __restrict__ normed, int cols, float eps) {
     __shared__ float s_part[kNormThreads / 64];
     const int64_t row = blockIdx.x;
+    const int tid = threadIdx.x;
     const float* xr = x + row * cols;
     const float* yr = y ? y + row * cols : nullptr;
-    float* xo = x_out ? x_out + row * cols : nullptr;
+    float v[RUNS], wv[RUNS];
+#pragma unroll
+    for (int q = 0; q < RUNS; ++q) {
+        const int i = min(tid + q * kNormThreads, cols - 1);
+        v[q] = xr[i];
+        wv[q] = w[i];
+    }
+    if (yr) {
+        float yv[RUNS];
+#pragma unroll
+        for (int q = 0; q < RUNS; ++q) yv[q] = yr[min(tid + q * kNormThreads, cols - 1)];
+#pragma unroll
+        for (int q = 0; q < RUNS; ++q) v[q] += yv[q];
+    }
+    float ss = 0.f;
+#pragma unroll
+    for (int q = 0; q < RUNS; ++q)
+        if (tid + q * kNormThreads < cols) ss = fmaf(v[q], v[q], ss);
+    ss = group_sum<64>(ss);
+    if ((tid & 63) == 0) s_part[tid >> 6] = ss;
+    __syncthreads();
+    const float tot = (s_part[0] + s_part[1]) + (s_part[2] + s_part[3]);
+    const float r = rsqrtf(tot / (float)cols + eps);
+#pragma unroll
+    for (int q = 0; q < RUNS; ++q) {
+        const int i = tid + q * kNormThreads;
+        if (i < cols) {
+            if (x_out) x_out[row * cols + i] = v[q];
+            normed[row * cols + i] = wv[q] * (v[q] * r);
+        }
+    }
+}
+
+// rows longer than 256 * kMaxRuns
+__global__ void __launch_bounds__(kNormThreads)
+add_rmsnorm_long_kernel(const float* __restrict__ x, const float* __restrict__ y, float* x_out,
+                        const float* __restrict__ w, float* __restrict__ normed, int cols, float eps) {
+    __shared__ float s_part[kNormThreads / 64];
+    const int64_t row = blockIdx.x;
+    const float* xr = x + row * cols;
+    const float* yr = y ? y + row * cols : nullptr;
     float ss = 0.f;
     for (int i = threadIdx.x; i < cols; i += kNormThreads) {
         float v = xr[i];
@@ -79,16 +149,35 @@ add_rmsnorm_kernel(const float* __restrict__ x, const float* __restrict__ y, flo
     ss = group_sum<64>(ss);
     if ((threadIdx.x & 63) == 0) s_part[threadIdx.x >> 6] = ss;
     __syncthreads();
-    float tot = 0.f;
-#pragma unroll
-    for (int i = 0; i < kNormThreads / 64; ++i) tot += s_part[i];
+    const float tot = (s_part[0] + s_part[1]) + (s_part[2] + s_part[3]);
     const float r = rsqrtf(tot / (float)cols + eps);
     for (int i = threadIdx.x; i < cols; i += kNormThreads) {
         float v = xr[i];
         if (yr) v += yr[i];
-        if (xo) xo[i] = v;
+        if (x_out) x_out[row * cols + i] = v;
         normed[row * cols + i] = w[i] * (v * r);
     }
+}
+
+#define MTL_DISPATCH_BB(BBV, ...)                                  \
+    switch (BBV) {                                                 \
+        case 1: { constexpr int BB = 1; __VA_ARGS__; } break;      \
+        case 2: { constexpr int BB = 2; __VA_ARGS__; } break;      \
+        case 4: { constexpr int BB = 4; __VA_ARGS__; } break;      \
+        default: { constexpr int BB = 8; __VA_ARGS__; } break;     \
+    }
+
+template <typename T>
+void launch_ssm_step(float* state, const void* x, int64_t x_sb, const void* z, int64_t z_sb, const void* xdbl,
+                     int64_t xdbl_sb, const float* Wdt, const float* bdt, const float* A, const float* Dv, void* y,
+                     int64_t y_sb, int64_t batch, int D, int N, int R, int a_is_log, hipStream_t st) {
+    const int bb = batch >= 8 ? 8 : batch >= 4 ? 4 : batch >= 2 ? 2 : 1;
+    const int rq = round_runs((R + 15) / 16);
+    dim3 grid((unsigned)((D + kChPerBlock - 1) / kChPerBlock), (unsigned)((batch + bb - 1) / bb));
+    MTL_DISPATCH_BB(bb, MTL_DISPATCH_RUNS(RQ, rq, hipLaunchKernelGGL((ssm_step_kernel<T, RQ, BB>), grid,
+        dim3(kStepThreads), 0, st, state, static_cast<const T*>(x), x_sb, static_cast<const T*>(z), z_sb,
+        static_cast<const T*>(xdbl), xdbl_sb, Wdt, bdt, A, Dv, static_cast<T*>(y), y_sb, D, N, R, (int)batch,
+        a_is_log)));
 }
 
 }  // namespace
@@ -107,18 +196,14 @@ extern "C" int mtl_selective_state_update(float* ssm_state, const void* x, int64
     MTL_REQUIRE(dtype == MTL_F32 || dtype == MTL_BF16, "dtype must be MTL_F32 or MTL_BF16");
     if (batch == 0 || dim == 0) return MTL_OK;
     MTL_REQUIRE(ssm_state && x && x_dbl && W_dt && b_dt && A && y, "null required pointer");
+    MTL_REQUIRE(dt_rank >= 1 && dt_rank <= 16 * kMaxRuns, "dt_rank must be in [1, 256]");
     hipStream_t st = as_stream(stream);
-    dim3 grid((unsigned)((dim + kChPerBlock - 1) / kChPerBlock), (unsigned)batch);
     if (dtype == MTL_F32)
-        hipLaunchKernelGGL((ssm_step_kernel<float>), grid, dim3(kStepThreads), 0, st, ssm_state,
-                           static_cast<const float*>(x), x_sb, static_cast<const float*>(z), z_sb,
-                           static_cast<const float*>(x_dbl), xdbl_sb, W_dt, b_dt, A, Dvec, static_cast<float*>(y),
-                           y_sb, (int)dim, (int)dstate, (int)dt_rank, a_is_log);
+        launch_ssm_step<float>(ssm_state, x, x_sb, z, z_sb, x_dbl, xdbl_sb, W_dt, b_dt, A, Dvec, y, y_sb, batch,
+                               (int)dim, (int)dstate, (int)dt_rank, a_is_log, st);
     else
-        hipLaunchKernelGGL((ssm_step_kernel<uint16_t>), grid, dim3(kStepThreads), 0, st, ssm_state,
-                           static_cast<const uint16_t*>(x), x_sb, static_cast<const uint16_t*>(z), z_sb,
-                           static_cast<const uint16_t*>(x_dbl), xdbl_sb, W_dt, b_dt, A, Dvec,
-                           static_cast<uint16_t*>(y), y_sb, (int)dim, (int)dstate, (int)dt_rank, a_is_log);
+        launch_ssm_step<uint16_t>(ssm_state, x, x_sb, z, z_sb, x_dbl, xdbl_sb, W_dt, b_dt, A, Dvec, y, y_sb, batch,
+                                  (int)dim, (int)dstate, (int)dt_rank, a_is_log, st);
     return check_launch("selective_state_update");
 }
 
@@ -130,7 +215,14 @@ extern "C" int mtl_add_rmsnorm(const float* x, const float* y, float* x_out, con
     MTL_REQUIRE(rows < (int64_t(1) << 31), "too many rows");
     if (rows == 0) return MTL_OK;
     MTL_REQUIRE(x && w && normed, "null required pointer");
-    hipLaunchKernelGGL(add_rmsnorm_kernel, dim3((unsigned)rows), dim3(kNormThreads), 0, as_stream(stream), x, y,
-                       x_out, w, normed, (int)cols, eps);
+    hipStream_t st = as_stream(stream);
+    const int runs = (int)((cols + kNormThreads - 1) / kNormThreads);
+    if (runs > kMaxRuns)
+        hipLaunchKernelGGL(add_rmsnorm_long_kernel, dim3((unsigned)rows), dim3(kNormThreads), 0, st, x, y, x_out, w,
+                           normed, (int)cols, eps);
+    else
+        MTL_DISPATCH_RUNS(RUNS, round_runs(runs), hipLaunchKernelGGL((add_rmsnorm_kernel<RUNS>), dim3((unsigned)rows),
+                                                                     dim3(kNormThreads), 0, st, x, y, x_out, w,
+                                                                     normed, (int)cols, eps));
     return check_launch("add_rmsnorm");
 }
