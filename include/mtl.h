@@ -153,6 +153,15 @@ int mtl_add_rmsnorm(const float* x, const float* y, float* x_out, const float* w
                     int64_t rows, int64_t cols, float eps, mtl_stream_t stream);
 
 /* ------------------------------------------------------------------------
+ * Sum of split-K partial products, in part order:
+ *   out[i] = ((parts[0*n + i] + parts[1*n + i]) + ...) + parts[(nparts-1)*n + i]
+ * The x_proj of the batched step (model.py:279, x_dbl = x_proj(x)) runs as
+ * nparts GEMMs over channel chunks on hipBLASLt; this adds their outputs.
+ * parts: contiguous fp32 [nparts, n]; out: fp32 [n].  1 <= nparts <= 64.
+ * ---------------------------------------------------------------------- */
+int mtl_sum_parts(const float* parts, int32_t nparts, int64_t n, float* out, mtl_stream_t stream);
+
+/* ------------------------------------------------------------------------
  * Per-token int8 quantize -> dequantize-sum of an AllReduce payload,
  * local (the collective replaced by nparts partials resident on one GPU).
  * Replaces tp_utils.py:103-131 (_int8_gather, per_token=True, reached via

@@ -22,19 +22,26 @@ constexpr int kStepThreads = 256;
 constexpr int kChPerBlock = kStepThreads / kLanesPerChannel;
 
 // RQ = dt_proj columns per lane (R <= 16 RQ); BB = batch rows per workgroup,
-// so W_dt, A, D and the biases are read once per BB rows.  Every operand is
-// loaded up front with clamped addresses, then the BB rows are updated.
+// so W_dt, A, D and the biases are read once per BB rows.  The BB rows of
+// x_dbl and the block's x, z are staged in LDS by all threads; every other
+// operand is loaded up front with clamped addresses.
 template <typename T, int RQ, int BB>
 __global__ void __launch_bounds__(kStepThreads)
 ssm_step_kernel(float* __restrict__ state, const T* __restrict__ x, int64_t x_sb, const T* __restrict__ z,
                 int64_t z_sb, const T* __restrict__ xdbl, int64_t xdbl_sb, const float* __restrict__ Wdt,
                 const float* __restrict__ bdt, const float* __restrict__ A, const float* __restrict__ Dv,
                 T* __restrict__ y, int64_t y_sb, int D, int N, int R, int batch, int a_is_log) {
-    const int g = threadIdx.x / kLanesPerChannel;
-    const int n = threadIdx.x % kLanesPerChannel;
+    constexpr int kJMax = 16 * RQ + 2 * kLanesPerChannel;          // R + 2N <= 16 RQ + 32
+    constexpr int kStage = (BB * kJMax + kStepThreads - 1) / kStepThreads;
+    __shared__ float s_xd[BB * kJMax];
+    __shared__ float s_x[BB][kChPerBlock], s_z[BB][kChPerBlock];
+    const int tid = threadIdx.x;
+    const int g = tid / kLanesPerChannel;
+    const int n = tid % kLanesPerChannel;
     const int c = blockIdx.x * kChPerBlock + g;
     const int cc = min(c, D - 1), nn = min(n, N - 1);
     const int b0 = blockIdx.y * BB;
+    const int J = R + 2 * N;
 
     float wdt[RQ];
 #pragma unroll
@@ -42,19 +49,31 @@ ssm_step_kernel(float* __restrict__ state, const T* __restrict__ x, int64_t x_sb
     float av = A[(int64_t)cc * N + nn];
     const float bd = bdt[cc];
     const float Dc = Dv ? Dv[cc] : 0.f;
-    float hs[BB], xv[BB], zv[BB], Bn[BB], Cn[BB], dl[BB][RQ];
+    float hs[BB];
 #pragma unroll
-    for (int i = 0; i < BB; ++i) {
-        const int64_t b = min(b0 + i, batch - 1);
-        hs[i] = state[(b * D + cc) * N + nn];
-        xv[i] = Act<T>::load(x + b * x_sb + cc);
-        zv[i] = z ? Act<T>::load(z + b * z_sb + cc) : 0.f;
-        const T* xd = xdbl + b * xdbl_sb;
+    for (int i = 0; i < BB; ++i) hs[i] = state[((int64_t)min(b0 + i, batch - 1) * D + cc) * N + nn];
+    // staging: x_dbl rows (element e = i*J + j of the block), and x, z of the block's channels
+    float st[kStage];
 #pragma unroll
-        for (int q = 0; q < RQ; ++q) dl[i][q] = Act<T>::load(xd + min(n + 16 * q, R - 1));
-        Bn[i] = Act<T>::load(xd + R + nn);
-        Cn[i] = Act<T>::load(xd + R + N + nn);
+    for (int q = 0; q < kStage; ++q) {
+        const int e = min(tid + q * kStepThreads, BB * J - 1);
+        const int i = e / J, j = e - i * J;
+        st[q] = Act<T>::load(xdbl + (int64_t)min(b0 + i, batch - 1) * xdbl_sb + j);
     }
+    const bool xz_t = tid < BB * kChPerBlock;
+    const int xi = min(tid / kChPerBlock, BB - 1), xch = tid % kChPerBlock;
+    const int64_t xb = min(b0 + xi, batch - 1);
+    const int xc_ = min((int)blockIdx.x * kChPerBlock + xch, D - 1);
+    const float xs = Act<T>::load(x + xb * x_sb + xc_);
+    const float zs = z ? Act<T>::load(z + xb * z_sb + xc_) : 0.f;
+#pragma unroll
+    for (int q = 0; q < kStage; ++q)
+        if (tid + q * kStepThreads < BB * J) s_xd[tid + q * kStepThreads] = st[q];
+    if (xz_t) {
+        s_x[xi][xch] = xs;
+        s_z[xi][xch] = zs;
+    }
+    __syncthreads();
     if (c >= D) return;  // whole 16-lane row
     if (a_is_log) av = -expf(av);
 
@@ -62,28 +81,45 @@ ssm_step_kernel(float* __restrict__ state, const T* __restrict__ x, int64_t x_sb
     for (int i = 0; i < BB; ++i) {
         const int64_t b = b0 + i;
         if (b >= batch) break;  // uniform over the workgroup
+        const float* xd = s_xd + i * J;
         float acc = 0.f;
 #pragma unroll
         for (int q = 0; q < RQ; ++q) {
-            const float t = fmaf(wdt[q], dl[i][q], acc);
+            const float t = fmaf(wdt[q], xd[min(n + 16 * q, R - 1)], acc);
             acc = n + 16 * q < R ? t : acc;
         }
         acc = group_sum<kLanesPerChannel>(acc);
         const float dt = softplus_f(acc + bd);
+        const float xv = s_x[i][g];
         float yv = 0.f;
         if (n < N) {
             const float dA = __builtin_amdgcn_exp2f(dt * (av * kLog2e));
-            const float hv = fmaf(hs[i], dA, (dt * Bn[i]) * xv[i]);
+            const float hv = fmaf(hs[i], dA, (dt * xd[R + n]) * xv);
             state[(b * D + c) * N + n] = hv;
-            yv = hv * Cn[i];
+            yv = hv * xd[R + N + n];
         }
         yv = group_sum<kLanesPerChannel>(yv);
         if (n == 0) {
-            if (Dv) yv += xv[i] * Dc;
-            if (z) yv *= silu_f(zv[i]);
+            if (Dv) yv += xv * Dc;
+            if (z) yv *= silu_f(s_z[i][g]);
             Act<T>::store(y + b * y_sb + c, yv);
         }
     }
+}
+
+// out[i] = parts[0][i] + parts[1][i] + ... in part order (split-K partials)
+template <int P>
+__global__ void __launch_bounds__(256) sum_parts_kernel(const float* __restrict__ parts, int nparts, int64_t n,
+                                                        float* __restrict__ out) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const int64_t ii = min(i, n - 1);
+    float v[P];
+#pragma unroll
+    for (int p = 0; p < P; ++p) v[p] = parts[(int64_t)min(p, nparts - 1) * n + ii];
+    float s = v[0];
+#pragma unroll
+    for (int p = 1; p < P; ++p) s = p < nparts ? s + v[p] : s;
+    if (i < n) out[i] = s;
 }
 
 constexpr int kNormThreads = 256;
@@ -225,4 +261,20 @@ extern "C" int mtl_add_rmsnorm(const float* x, const float* y, float* x_out, con
                                                                      dim3(kNormThreads), 0, st, x, y, x_out, w,
                                                                      normed, (int)cols, eps));
     return check_launch("add_rmsnorm");
+}
+
+extern "C" int mtl_sum_parts(const float* parts, int32_t nparts, int64_t n, float* out, mtl_stream_t stream) {
+    using namespace mtl;
+    clear_error();
+    MTL_REQUIRE(nparts >= 1 && nparts <= 64 && n >= 0, "nparts must be in [1, 64]");
+    if (n == 0) return MTL_OK;
+    MTL_REQUIRE(parts && out, "null required pointer");
+    MTL_REQUIRE(n < (int64_t(1) << 31), "n too large");
+    const dim3 grid((unsigned)((n + 255) / 256));
+    hipStream_t st = as_stream(stream);
+    if (nparts <= 8) hipLaunchKernelGGL((sum_parts_kernel<8>), grid, dim3(256), 0, st, parts, nparts, n, out);
+    else if (nparts <= 16) hipLaunchKernelGGL((sum_parts_kernel<16>), grid, dim3(256), 0, st, parts, nparts, n, out);
+    else if (nparts <= 32) hipLaunchKernelGGL((sum_parts_kernel<32>), grid, dim3(256), 0, st, parts, nparts, n, out);
+    else hipLaunchKernelGGL((sum_parts_kernel<64>), grid, dim3(256), 0, st, parts, nparts, n, out);
+    return check_launch("sum_parts");
 }

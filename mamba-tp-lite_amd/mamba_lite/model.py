@@ -214,10 +214,36 @@ class MambaMixer(nn.Module):
         Dm, R = self.cfg.d_inner, self.cfg.dt_rank
         xz = self.in_proj(x_t)                                   # [b, 2D]
         xc = ops.conv_step(cache.conv_state, xz[:, :Dm], self._conv_w(), _f32(self.conv1d.bias), silu=True)
-        x_dbl = F.linear(xc, self.x_proj.weight)                 # [b, R+2N]
+        x_dbl = self._x_proj_step(xc)                            # [b, R+2N]
         y = ops.selective_state_update(cache.ssm_state, xc, xz[:, Dm:], x_dbl, _f32(self.dt_proj.weight),
                                        _f32(self.dt_proj.bias), _f32(self.A_log), _f32(self.D), a_is_log=True)
         return self.out_proj(y)
+
+
+    # x_proj of a batched step: [b, D] x [D, R+2N] has too few output tiles
+    # for one GEMM to fill the GPU, so it runs as D/128 GEMMs over channel
+    # chunks (one batched call) whose outputs are added in chunk order
+    _XPROJ_CHUNK = 128
+
+    def _xproj_chunks(self) -> torch.Tensor:
+        w = self.x_proj.weight
+        key = (w.data_ptr(), w._version, w.dtype)
+        cached = getattr(self, "_xproj_cache", None)
+        if cached is None or cached[0] != key:
+            D, J = w.shape[1], w.shape[0]
+            with torch.no_grad():
+                wt = w.detach().t().contiguous().view(D // self._XPROJ_CHUNK, self._XPROJ_CHUNK, J)
+            cached = (key, wt)
+            self._xproj_cache = cached
+        return cached[1]
+
+    def _x_proj_step(self, xc: torch.Tensor) -> torch.Tensor:
+        b, D = xc.shape
+        if b >= 8 and D >= 1024 and D % self._XPROJ_CHUNK == 0 and xc.dtype == torch.float32 and xc.is_cuda:
+            wt = self._xproj_chunks()
+            parts = torch.bmm(xc.view(b, wt.shape[0], self._XPROJ_CHUNK).transpose(0, 1), wt)   # [D/128, b, J]
+            return ops.sum_parts(parts)
+        return F.linear(xc, self.x_proj.weight)
 
 
 class MambaBlock(nn.Module):

@@ -272,6 +272,23 @@ def add_rmsnorm(x, weight, eps, y=None, x_out=None, out=None):
 
 
 # --------------------------------------------------------------------------- payload quantizers
+def sum_parts(parts, out=None):
+    """mtl_sum_parts: parts [P, ...] fp32 contiguous -> out [...] =
+    parts[0] + parts[1] + ... in part order."""
+    _f32c(parts, "parts")
+    if parts.dim() < 2:
+        raise ValueError("parts must be [P, ...]")
+    if out is None:
+        out = torch.empty(parts.shape[1:], device=parts.device, dtype=torch.float32)
+    _f32c(out, "out")
+    if tuple(out.shape) != tuple(parts.shape[1:]):
+        raise ValueError("out must have the shape of one part")
+    with _dev_guard(parts):
+        _lib.check(_lib.load().mtl_sum_parts(_ptr(parts), parts.shape[0], out.numel(), _ptr(out), _stream(parts)),
+                   "sum_parts")
+    return out
+
+
 def _parts_array(parts):
     arr = (ctypes.c_void_p * len(parts))(*[p.data_ptr() for p in parts])
     return ctypes.cast(arr, ctypes.POINTER(ctypes.c_void_p)), arr

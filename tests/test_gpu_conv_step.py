@@ -82,9 +82,11 @@ def test_conv_step_in_place():
     assert np.array_equal(S.cpu().numpy(), ref_st.astype(np.float32))
 
 
-@pytest.mark.parametrize("N,R", [(16, 48), (16, 128), (8, 2), (4, 5)])
-@pytest.mark.parametrize("b", [1, 4])
+@pytest.mark.parametrize("N,R", [(16, 48), (16, 128), (8, 2), (4, 5), (16, 256)])
+@pytest.mark.parametrize("b", [1, 4, 11, 32])
 def test_selective_state_update(N, R, b):
+    """b = 11 and 32 cover the 8-row batch blocks (with a ragged last block)."""
+    print(f"state update N={N} R={R} b={b}", flush=True)
     rng = np.random.default_rng(N * 100 + R + b)
     D = 200
     h = rng.standard_normal((b, D, N)).astype(np.float32)
@@ -154,7 +156,7 @@ def test_step_matches_one_token_prefill():
     assert_rel(HS.cpu().numpy(), hp.cpu().numpy(), 1e-5, "h")
 
 
-@pytest.mark.parametrize("rows,cols", [(1, 768), (7, 2048), (64, 33)])
+@pytest.mark.parametrize("rows,cols", [(1, 768), (7, 2048), (64, 33), (3, 4096), (2, 5000)])
 def test_add_rmsnorm(rows, cols):
     rng = np.random.default_rng(rows + cols)
     x = rng.standard_normal((rows, cols)).astype(np.float32)
@@ -166,3 +168,17 @@ def test_add_rmsnorm(rows, cols):
     assert_rel(out.cpu().numpy(), om.rmsnorm(x.astype(np.float64) + y, w, 1e-5, np.float64), 1e-5, "normed")
     out2 = ops.add_rmsnorm(_t(x), _t(w), 1e-5)
     assert_rel(out2.cpu().numpy(), om.rmsnorm(x, w, 1e-5, np.float64), 1e-5, "norm only")
+
+
+@pytest.mark.parametrize("nparts,n", [(1, 5), (3, 1000), (16, 5120), (32, 257), (64, 300)])
+def test_sum_parts_in_part_order(nparts, n):
+    """mtl_sum_parts adds the parts left to right in float32, bit for bit."""
+    rng = np.random.default_rng(nparts * 7 + n)
+    scale = 10.0 ** rng.integers(-3, 4, (nparts, 1))
+    parts = (rng.standard_normal((nparts, n)) * scale).astype(np.float32)
+    assert parts.dtype == np.float32
+    got = ops.sum_parts(_t(parts)).cpu().numpy()
+    ref = parts[0].copy()
+    for p in range(1, nparts):
+        ref = (ref + parts[p]).astype(np.float32)
+    assert np.array_equal(got, ref)

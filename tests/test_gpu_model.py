@@ -217,3 +217,30 @@ def test_bf16_mixer_shard_shape():
         outb, _, hb = mb.prefill(x.bfloat16())
     assert outb.dtype == torch.bfloat16 and hb.dtype == torch.float32
     assert_rel(_np(outb), _np(out32), 5e-2, "bf16 out vs fp32 out")
+
+
+@pytest.mark.parametrize("b", [8, 32])
+def test_mixer_step_batched_x_proj_chunks(b):
+    """At b >= 8 and d_inner >= 1024 the step's x_proj runs as chunked GEMMs
+    plus mtl_sum_parts; the step still matches the oracle mixer step."""
+    print(f"batched mixer step b={b}", flush=True)
+    torch.manual_seed(b)
+    cfg = MambaConfig(d_model=512, n_layer=1, vocab_size=64, d_state=16)
+    mx = MambaMixer(cfg, 0)
+    _init_dt_bias(mx, b)
+    mx = mx.to(DEV).eval()
+    p = _mixer_weights(mx)
+    rng = np.random.default_rng(b)
+    D = cfg.d_inner
+    cs = rng.standard_normal((b, D, cfg.d_conv - 1)).astype(np.float32)
+    hs = (0.1 * rng.standard_normal((b, D, cfg.d_state))).astype(np.float32)
+    x = rng.standard_normal((b, cfg.d_model)).astype(np.float32)
+    lc = LayerCache(conv_state=torch.from_numpy(cs).to(DEV), ssm_state=torch.from_numpy(hs).to(DEV))
+    with torch.no_grad():
+        y = mx.step(torch.from_numpy(x).to(DEV), lc)
+    cs_r, hs_r = cs.astype(np.float64), hs.astype(np.float64)
+    y_ref = om.mixer_step(p, x.astype(np.float64), cs_r, hs_r, dtype=np.float64)
+    assert mx._xproj_cache is not None
+    assert_rel(y.cpu().numpy(), y_ref, 1e-4, "y")
+    assert_rel(lc.ssm_state.cpu().numpy(), hs_r, 1e-4, "ssm_state")
+    assert_rel(lc.conv_state.cpu().numpy(), cs_r, 1e-5, "conv_state")
