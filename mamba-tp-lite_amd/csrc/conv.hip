@@ -6,11 +6,14 @@
 // (conv_in = cat(conv_state, x), sum(conv_in * w) + bias, in-place history
 // shift, F.silu).
 //
-// Prefill mapping: a thread owns one channel and a run of kTC consecutive
-// timesteps and slides a K-wide window along l, so each input element is
-// read once from HBM (plus a K-1 halo per run).  For the token-major
-// layout of the mixer (x a strided view of in_proj's output, stride 1 along
-// d) consecutive lanes read consecutive channels: fully coalesced.
+// Prefill mapping: a thread owns 4 adjacent channels (one vector) and a run
+// of kTC consecutive timesteps; it loads the kTC + K - 1 inputs of its
+// window up front and forms the outputs from registers, so each input
+// element is read once from HBM (plus a K-1 halo per run, which the
+// neighbouring run has just pulled into L2).  For the token-major layout of
+// the mixer (x a strided view of in_proj's output, stride 1 along d)
+// consecutive lanes read consecutive vectors: fully coalesced.  Layouts
+// without unit channel stride use one channel per thread.
 
 #include "common.h"
 
@@ -18,7 +21,7 @@ namespace mtl {
 namespace {
 
 constexpr int kConvThreads = 256;
-constexpr int kTC = 32;      // timesteps per thread
+constexpr int kTC = 16;      // timesteps per thread
 constexpr int kMaxK = 8;
 
 struct ConvArgs {
@@ -28,52 +31,104 @@ struct ConvArgs {
     int L, D, K, silu;
 };
 
-template <typename T, int K>
+// VC adjacent channels as one vector (VC > 1 needs unit channel stride and
+// VC-aligned rows), TC timesteps per thread.
+template <typename T, int VC> struct Vec;
+template <> struct Vec<float, 1> {
+    __device__ __forceinline__ static void load(const float* p, float* v) { v[0] = *p; }
+    __device__ __forceinline__ static void store(float* p, const float* v) { *p = v[0]; }
+};
+template <> struct Vec<uint16_t, 1> {
+    __device__ __forceinline__ static void load(const uint16_t* p, float* v) { v[0] = bf16_to_f32(*p); }
+    __device__ __forceinline__ static void store(uint16_t* p, const float* v) { *p = f32_to_bf16(v[0]); }
+};
+template <> struct Vec<float, 4> {
+    __device__ __forceinline__ static void load(const float* p, float* v) {
+        const float4 x = *reinterpret_cast<const float4*>(p);
+        v[0] = x.x; v[1] = x.y; v[2] = x.z; v[3] = x.w;
+    }
+    __device__ __forceinline__ static void store(float* p, const float* v) {
+        *reinterpret_cast<float4*>(p) = make_float4(v[0], v[1], v[2], v[3]);
+    }
+};
+template <> struct Vec<uint16_t, 4> {
+    __device__ __forceinline__ static void load(const uint16_t* p, float* v) {
+        const uint2 x = *reinterpret_cast<const uint2*>(p);
+        v[0] = __uint_as_float(x.x << 16); v[1] = __uint_as_float(x.x & 0xffff0000u);
+        v[2] = __uint_as_float(x.y << 16); v[3] = __uint_as_float(x.y & 0xffff0000u);
+    }
+    __device__ __forceinline__ static void store(uint16_t* p, const float* v) {
+        uint2 x;
+        x.x = (uint32_t)f32_to_bf16(v[0]) | ((uint32_t)f32_to_bf16(v[1]) << 16);
+        x.y = (uint32_t)f32_to_bf16(v[2]) | ((uint32_t)f32_to_bf16(v[3]) << 16);
+        *reinterpret_cast<uint2*>(p) = x;
+    }
+};
+
+// A thread owns VC channels x TC timesteps.  The TC + K - 1 padded inputs
+// it needs are loaded up front (clamped addresses; positions before the
+// sequence come from the carried history or are zero), then the TC outputs
+// are formed from registers.
+template <typename T, int K, int VC, int TC>
 __global__ void __launch_bounds__(kConvThreads) conv_fwd_kernel(const ConvArgs a) {
-    const int c = blockIdx.x * kConvThreads + threadIdx.x;
+    constexpr int W = TC + K - 1;
+    const int c0 = (blockIdx.x * kConvThreads + threadIdx.x) * VC;
     const int b = blockIdx.z;
-    const int t0 = blockIdx.y * kTC;
-    if (c >= a.D || t0 >= a.L) return;
+    const int t0 = blockIdx.y * TC;
+    if (c0 >= a.D) return;
 
-    const T* __restrict__ xp = static_cast<const T*>(a.x) + b * a.x_sb + (int64_t)c * a.x_sd;
-    T* __restrict__ op = static_cast<T*>(a.out) + b * a.o_sb + (int64_t)c * a.o_sd;
-    const T* __restrict__ sin = a.st_in ? static_cast<const T*>(a.st_in) + ((int64_t)b * a.D + c) * (K - 1)
-                                        : nullptr;
+    const T* __restrict__ xp = static_cast<const T*>(a.x) + b * a.x_sb + (int64_t)c0 * a.x_sd;
+    T* __restrict__ op = static_cast<T*>(a.out) + b * a.o_sb + (int64_t)c0 * a.o_sd;
 
-    float w[K];
+    // v[j] = padded input at position t0 + j, i.e. x[t0 + j - (K-1)]
+    float v[W][VC];
 #pragma unroll
-    for (int k = 0; k < K; ++k) w[k] = a.w[(int64_t)c * K + k];
-    const float bias = a.bias ? a.bias[c] : 0.f;
-
-    // padded input xp_pad[i] = state[i] for i < K-1, x[i-(K-1)] otherwise;
-    // out[t] needs xp_pad[t .. t+K-1].  win[k] holds xp_pad[t + k].
-    auto padded = [&](int i) -> float {
-        if (i >= K - 1) return Act<T>::load(xp + (int64_t)(i - (K - 1)) * a.x_sl);
-        return sin ? Act<T>::load(sin + i) : 0.f;
-    };
-    float win[K];
+    for (int j = 0; j < W; ++j) {
+        const int t = min(max(t0 + j - (K - 1), 0), a.L - 1);
+        Vec<T, VC>::load(xp + (int64_t)t * a.x_sl, v[j]);
+    }
+    float w[K][VC], bias[VC];
 #pragma unroll
-    for (int k = 0; k < K - 1; ++k) win[k] = padded(t0 + k);
-
-    const int t1 = min(t0 + kTC, a.L);
-    for (int t = t0; t < t1; ++t) {
-        win[K - 1] = Act<T>::load(xp + (int64_t)t * a.x_sl);
-        float acc = 0.f;
+    for (int ci = 0; ci < VC; ++ci) {
 #pragma unroll
-        for (int k = 0; k < K; ++k) acc = fmaf(w[k], win[k], acc);
-        acc += bias;
-        if (a.silu) acc = silu_f(acc);
-        Act<T>::store(op + (int64_t)t * a.o_sl, acc);
+        for (int k = 0; k < K; ++k) w[k][ci] = a.w[(int64_t)(c0 + ci) * K + k];
+        bias[ci] = a.bias ? a.bias[c0 + ci] : 0.f;
+    }
+    if (t0 == 0) {  // the first K-1 padded positions: carried history or zeros (uniform per block)
+        const T* __restrict__ sin = a.st_in ? static_cast<const T*>(a.st_in) : nullptr;
 #pragma unroll
-        for (int k = 0; k < K - 1; ++k) win[k] = win[k + 1];
+        for (int j = 0; j < K - 1; ++j)
+#pragma unroll
+            for (int ci = 0; ci < VC; ++ci)
+                v[j][ci] = sin ? Act<T>::load(sin + ((int64_t)b * a.D + c0 + ci) * (K - 1) + j) : 0.f;
     }
 
-    // final conv state: padded positions L .. L+K-2, written by the run that
-    // holds the last timestep
-    if (a.st_out && t1 == a.L) {
-        T* so = static_cast<T*>(a.st_out) + ((int64_t)b * a.D + c) * (K - 1);
 #pragma unroll
-        for (int k = 0; k < K - 1; ++k) Act<T>::store(so + k, padded(a.L + k));
+    for (int tt = 0; tt < TC; ++tt) {
+        if (t0 + tt >= a.L) break;  // uniform per block
+        float o[VC];
+#pragma unroll
+        for (int ci = 0; ci < VC; ++ci) {
+            float acc = 0.f;
+#pragma unroll
+            for (int k = 0; k < K; ++k) acc = fmaf(w[k][ci], v[tt + k][ci], acc);
+            acc += bias[ci];
+            o[ci] = a.silu ? silu_f(acc) : acc;
+        }
+        Vec<T, VC>::store(op + (int64_t)(t0 + tt) * a.o_sl, o);
+    }
+
+    // final conv state = padded positions L .. L+K-2, held by the block with the last timestep
+    if (a.st_out && t0 + TC >= a.L) {
+        T* so = static_cast<T*>(a.st_out) + ((int64_t)b * a.D + c0) * (K - 1);
+        const int j0 = a.L - t0;  // v index of padded position L
+#pragma unroll
+        for (int j = 0; j < W; ++j) {
+            const int k = j - j0;
+            if (k >= 0 && k < K - 1)
+#pragma unroll
+                for (int ci = 0; ci < VC; ++ci) Act<T>::store(so + (int64_t)ci * (K - 1) + k, v[j][ci]);
+        }
     }
 }
 
@@ -107,20 +162,33 @@ __global__ void __launch_bounds__(256) conv_step_kernel(T* __restrict__ state, c
     Act<T>::store(out + b * o_sb + c, silu ? silu_f(acc) : acc);
 }
 
-template <typename T>
-int launch_conv(const ConvArgs& a, int64_t batch, hipStream_t st) {
+template <typename T, int VC, int TC>
+int launch_conv_vc(const ConvArgs& a, int64_t batch, hipStream_t st) {
     dim3 block(kConvThreads);
-    dim3 grid((unsigned)((a.D + kConvThreads - 1) / kConvThreads), (unsigned)((a.L + kTC - 1) / kTC),
+    dim3 grid((unsigned)((a.D / VC + kConvThreads - 1) / kConvThreads), (unsigned)((a.L + TC - 1) / TC),
               (unsigned)batch);
     switch (a.K) {
 #define MTL_CONV_CASE(KK) \
-    case KK: hipLaunchKernelGGL((conv_fwd_kernel<T, KK>), grid, block, 0, st, a); break;
+    case KK: hipLaunchKernelGGL((conv_fwd_kernel<T, KK, VC, TC>), grid, block, 0, st, a); break;
         MTL_CONV_CASE(2) MTL_CONV_CASE(3) MTL_CONV_CASE(4) MTL_CONV_CASE(5)
         MTL_CONV_CASE(6) MTL_CONV_CASE(7) MTL_CONV_CASE(8)
 #undef MTL_CONV_CASE
         default: set_error("conv width unsupported"); return MTL_EINVAL;
     }
     return check_launch("causal_conv1d_fwd");
+}
+
+// 4-channel vectors when channels are unit-stride and every row start is
+// vector-aligned; one channel per thread otherwise.
+template <typename T>
+int launch_conv(const ConvArgs& a, int64_t batch, hipStream_t st) {
+    constexpr int kVC = 4;
+    const uintptr_t al = kVC * sizeof(T);
+    const bool vec = a.x_sd == 1 && a.o_sd == 1 && a.D % kVC == 0 && (uintptr_t)a.x % al == 0 &&
+                     (uintptr_t)a.out % al == 0 && (a.x_sl * (int64_t)sizeof(T)) % al == 0 &&
+                     (a.o_sl * (int64_t)sizeof(T)) % al == 0 &&
+                     (batch == 1 || ((a.x_sb * (int64_t)sizeof(T)) % al == 0 && (a.o_sb * (int64_t)sizeof(T)) % al == 0));
+    return vec ? launch_conv_vc<T, kVC, kTC>(a, batch, st) : launch_conv_vc<T, 1, kTC>(a, batch, st);
 }
 
 template <typename T>

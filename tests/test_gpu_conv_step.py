@@ -34,6 +34,34 @@ def test_conv_fp32(layout, L, with_state):
     assert np.array_equal(fs.cpu().numpy(), ref_fs.astype(np.float32)), "final conv state must be exact copies"
 
 
+@pytest.mark.parametrize("D,offset", [(301, 0), (300, 1), (256, 0)])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("with_state", [False, True])
+def test_conv_token_major_views(D, offset, dtype, with_state):
+    """Token-major views as the mixer passes them (the x half of in_proj's
+    [b, l, 2D] output): vector path when channels are unit-stride and
+    aligned, one channel per thread when D is odd or the view starts off a
+    vector boundary; L = 70 spans five 16-step runs with a ragged last one."""
+    rng = np.random.default_rng(D + offset + with_state)
+    b, L, K = 3, 70, 4
+    xz = rng.standard_normal((b, L, 2 * D + offset)).astype(np.float32)
+    w = rng.standard_normal((D, K)).astype(np.float32)
+    bias = rng.standard_normal(D).astype(np.float32)
+    st = rng.standard_normal((b, D, K - 1)).astype(np.float32) if with_state else None
+    XZ = _t(xz, dtype)
+    X = XZ[..., offset:offset + D].transpose(1, 2)
+    st_t = _t(st, dtype) if st is not None else None
+    out, fs = ops.causal_conv1d(X, _t(w), _t(bias), conv_state=st_t, silu=True)
+    xr = xz[..., offset:offset + D].transpose(0, 2, 1)
+    if dtype == torch.bfloat16:
+        xr = bf16_round(xr)
+        st = bf16_round(st) if st is not None else None
+    ref, ref_fs = om.causal_conv1d(np.ascontiguousarray(xr), w, bias, st, dtype=np.float64)
+    tol = 1e-4 if dtype == torch.float32 else 1e-2
+    assert_rel(out.float().cpu().numpy(), om.silu(ref), tol, "conv out")
+    assert np.array_equal(fs.float().cpu().numpy(), ref_fs.astype(np.float32))
+
+
 def test_conv_no_activation_and_widths():
     rng = np.random.default_rng(3)
     for K in (2, 3, 4, 5, 8):
