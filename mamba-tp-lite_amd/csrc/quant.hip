@@ -113,6 +113,30 @@ fp16_sum_kernel(PartPtrs pp, int nparts, int64_t n, float* __restrict__ out) {
     out[i] = (float)acc;
 }
 
+// Four elements per thread: float4 loads of every part issued first, 8-byte
+// fp16 payload stores, float4 output.  Same roundings as fp16_sum_kernel.
+template <int P>
+__global__ void __launch_bounds__(256) fp16_sum_vec_kernel(PartPtrs pp, int64_t n4, float* __restrict__ out) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n4) return;
+    float4 v[P];
+#pragma unroll
+    for (int r = 0; r < P; ++r) v[r] = reinterpret_cast<const float4*>(pp.p[r])[i];
+    _Float16 acc[4];
+#pragma unroll
+    for (int r = 0; r < P; ++r) {
+        const _Float16 lo[4] = {(_Float16)v[r].x, (_Float16)v[r].y, (_Float16)v[r].z, (_Float16)v[r].w};
+        if (pp.pay16[r]) {
+            typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+            half4 h = {lo[0], lo[1], lo[2], lo[3]};
+            reinterpret_cast<half4*>(pp.pay16[r])[i] = h;
+        }
+#pragma unroll
+        for (int q = 0; q < 4; ++q) acc[q] = r == 0 ? lo[q] : (_Float16)((float)acc[q] + (float)lo[q]);
+    }
+    reinterpret_cast<float4*>(out)[i] = make_float4((float)acc[0], (float)acc[1], (float)acc[2], (float)acc[3]);
+}
+
 }  // namespace
 }  // namespace mtl
 
@@ -159,7 +183,22 @@ extern "C" int mtl_quant_dequant_sum_fp16(const float* const* parts, int32_t npa
         pp.p[r] = parts[r];
         pp.pay16[r] = payloads ? payloads[r] : nullptr;
     }
-    hipLaunchKernelGGL(fp16_sum_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, as_stream(stream), pp, nparts,
-                       n, out);
+    bool vec = n % 4 == 0 && (uintptr_t)out % 16 == 0;
+    for (int r = 0; r < nparts; ++r)
+        vec = vec && (uintptr_t)pp.p[r] % 16 == 0 && (uintptr_t)pp.pay16[r] % 8 == 0;
+    hipStream_t st = as_stream(stream);
+    if (vec) {
+        const int64_t n4 = n / 4;
+        const dim3 grid((unsigned)((n4 + 255) / 256));
+        switch (nparts) {
+#define MTL_FP16_CASE(PP) \
+    case PP: hipLaunchKernelGGL((fp16_sum_vec_kernel<PP>), grid, dim3(256), 0, st, pp, n4, out); break;
+            MTL_FP16_CASE(1) MTL_FP16_CASE(2) MTL_FP16_CASE(3) MTL_FP16_CASE(4)
+            MTL_FP16_CASE(5) MTL_FP16_CASE(6) MTL_FP16_CASE(7) MTL_FP16_CASE(8)
+#undef MTL_FP16_CASE
+        }
+    } else {
+        hipLaunchKernelGGL(fp16_sum_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, pp, nparts, n, out);
+    }
     return check_launch("quant_dequant_sum_fp16");
 }

@@ -65,18 +65,28 @@ def test_int8_full_payload_shape():
     assert np.abs(out.cpu().numpy() - dense).max() < 0.15 * np.abs(dense).max()
 
 
-@pytest.mark.parametrize("n", [1, 1000, 65536 + 3])
-@pytest.mark.parametrize("nparts", [2, 3])
+@pytest.mark.parametrize("n", [1, 1000, 65536 + 3, 4096])
+@pytest.mark.parametrize("nparts", [1, 2, 3, 8])
 def test_fp16_bit_exact(n, nparts):
+    """n % 4 == 0 takes the 4-wide path, other n the scalar one."""
     rng = np.random.default_rng(n + nparts)
     parts = [_student(rng, (n,)) for _ in range(nparts)]
-    if n >= 4:
+    if n >= 4 and nparts >= 2:
         parts[0][:4] = [32768.0, 1.0, -65504.0, 70000.0]
         parts[1][:4] = [2.0 ** -24, 2.0 ** -24, 65504.0, 1.0]
     out, pays = ops.quant_dequant_sum_fp16([torch.from_numpy(p).to(DEV) for p in parts], return_payloads=True)
     ref_out, ref_lows = oq.fp16_sum(parts)
     for r in range(nparts):
         assert np.array_equal(pays[r].cpu().numpy().view(np.uint16), ref_lows[r].view(np.uint16))
+    assert np.array_equal(out.cpu().numpy(), ref_out)
+
+
+def test_fp16_without_payloads_matches():
+    rng = np.random.default_rng(77)
+    parts = [_student(rng, (4096,)) for _ in range(2)]
+    out, pays = ops.quant_dequant_sum_fp16([torch.from_numpy(p).to(DEV) for p in parts], return_payloads=False)
+    assert pays is None
+    ref_out, _ = oq.fp16_sum(parts)
     assert np.array_equal(out.cpu().numpy(), ref_out)
 
 
