@@ -96,8 +96,10 @@ template <bool B> using Full = std::integral_constant<bool, B>;
 // both halves requested back to back) and y is written the same way, while
 // the scan works through LDS one TT-step sub-tile at a time.  Token-major
 // reads are full lines at any tile length, so there KC = 1.
+// Channel-major tiles hold twice the raw registers (3 waves per SIMD);
+// token-major ones fit 128 VGPRs, so 4 workgroups share a CU.
 template <typename T, int NW, int SPW, int TT, bool CM, bool VEC>
-__global__ void __launch_bounds__(NW * 64, 3) scan_fwd_kernel(const ScanArgs a) {
+__global__ void __launch_bounds__(NW * 64, CM ? 3 : 4) scan_fwd_kernel(const ScanArgs a) {
     constexpr int NT = NW * 64;
     constexpr int E = TT * 64 / NT;            // consecutive steps one thread stages per sub-tile
     constexpr int KC = CM ? 2 : 1;             // sub-tiles per load tile
