@@ -57,7 +57,8 @@ int mtl_abi_version(void);
  * u, delta, z, y: 3-D [b, D, l] with strides (sb, sd, sl) -- either
  * channel-major (sl == 1) or token-major (sd == 1) is fast, any other
  * stride pattern is rejected.  B, C: [b, N, l] with strides (sb, sn, sl).
- * h0 (nullable) and h_out (nullable): contiguous fp32 [b, D, N].
+ * h0 (nullable) and h_out (nullable): contiguous fp32 [b, D, N]; h_out may
+ * be h0 (a state is read before it is overwritten, by the same thread).
  * Limits: 1 <= N <= 32, l >= 0.
  * ---------------------------------------------------------------------- */
 typedef struct {

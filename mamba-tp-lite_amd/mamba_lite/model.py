@@ -172,22 +172,35 @@ class MambaMixer(nn.Module):
         w = self.conv1d.weight
         return _f32(w.reshape(w.shape[0], w.shape[-1]))
 
-    def prefill(self, x: torch.Tensor, cache: LayerCache | None = None):
+    def prefill(self, x: torch.Tensor, cache: LayerCache | None = None, out: LayerCache | None = None):
         """x: [b, l, d_model] -> (out [b, l, d_model], conv_state [b, D, K-1],
         ssm_state [b, D, N]) -- reference model.py:184-241.  The cache is read
-        as the initial state and never written; new state tensors are returned."""
+        as the initial state and never written; new state tensors are returned,
+        or, with `out` (a preallocated LayerCache, which may be `cache` itself),
+        the final states are written into out's tensors and those are returned."""
         b, l, _ = x.shape
         Dm, N, R, K = self.cfg.d_inner, self.cfg.d_state, self.cfg.dt_rank, self.cfg.d_conv
+        if out is not None:
+            if tuple(out.conv_state.shape) != (b, Dm, K - 1) or out.conv_state.dtype != x.dtype or \
+                    not out.conv_state.is_contiguous():
+                raise ValueError(f"out.conv_state must be contiguous {(b, Dm, K - 1)} {x.dtype}")
+            if tuple(out.ssm_state.shape) != (b, Dm, N) or out.ssm_state.dtype != torch.float32 or \
+                    not out.ssm_state.is_contiguous():
+                raise ValueError(f"out.ssm_state must be contiguous float32 {(b, Dm, N)}")
         xz = self.in_proj(x)                                     # [b, l, 2D]
         xs = xz[..., :Dm].transpose(1, 2)                        # [b, D, l] view, D-stride 1
         z = xz[..., Dm:].transpose(1, 2)
         conv_in_state = cache.conv_state if cache is not None else None
         if conv_in_state is not None and conv_in_state.dtype != x.dtype:
             conv_in_state = conv_in_state.to(x.dtype)
+        if conv_in_state is not None:
+            conv_in_state = conv_in_state.contiguous()
+            if out is not None and conv_in_state.data_ptr() == out.conv_state.data_ptr():
+                conv_in_state = conv_in_state.clone()            # the conv reads and writes different runs
         u_store = torch.empty(b, l, Dm, device=x.device, dtype=x.dtype)
-        u, conv_state = ops.causal_conv1d(xs, self._conv_w(), _f32(self.conv1d.bias),
-                                          conv_state=None if conv_in_state is None else conv_in_state.contiguous(),
-                                          silu=True, out=u_store.transpose(1, 2))
+        u, conv_state = ops.causal_conv1d(xs, self._conv_w(), _f32(self.conv1d.bias), conv_state=conv_in_state,
+                                          silu=True, out=u_store.transpose(1, 2),
+                                          final_state=out.conv_state if out is not None else None)
         x_dbl = F.linear(u_store, self.x_proj.weight)            # [b, l, R+2N]
         dt = F.linear(x_dbl[..., :R], self.dt_proj.weight)        # [b, l, D]; bias fused in the scan
         B = x_dbl[..., R:R + N].transpose(1, 2)                   # [b, N, l] view
@@ -196,11 +209,12 @@ class MambaMixer(nn.Module):
         if cache is not None:
             h0 = cache.ssm_state.float().contiguous()
         y_store = torch.empty(b, l, Dm, device=x.device, dtype=x.dtype)
+        # h_out may be h0: each state is read and written by the same thread
         _, h = ops.selective_scan(u, dt.transpose(1, 2), _f32(self.A_log), B, C, D=_f32(self.D), z=z,
                                   delta_bias=_f32(self.dt_proj.bias), h0=h0, delta_softplus=True, a_is_log=True,
-                                  y=y_store.transpose(1, 2))
-        out = self.out_proj(y_store)
-        return out, conv_state, h.to(_state_dtype(x.dtype))
+                                  y=y_store.transpose(1, 2), h_out=out.ssm_state if out is not None else None)
+        y_out = self.out_proj(y_store)
+        return y_out, conv_state, h if out is not None else h.to(_state_dtype(x.dtype))
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         """No-cache forward (reference model.py:243-246)."""
@@ -254,8 +268,8 @@ class MambaBlock(nn.Module):
         self.norm = RMSNorm(cfg.d_model, eps=cfg.layer_norm_epsilon)
         self.mixer = MambaMixer(cfg, layer_idx)
 
-    def prefill(self, x, cache: LayerCache | None):
-        y, conv_state, ssm_state = self.mixer.prefill(self.norm(x), cache)
+    def prefill(self, x, cache: LayerCache | None, out: LayerCache | None = None):
+        y, conv_state, ssm_state = self.mixer.prefill(self.norm(x), cache, out)
         return x + y, conv_state, ssm_state
 
     def step(self, x_t, cache: LayerCache):
@@ -296,20 +310,27 @@ class MambaLM(nn.Module):
                                      x_out=h)
         return normed.to(act) if act != torch.float32 else normed
 
-    def prefill(self, input_ids: torch.Tensor, cache: MambaCache | None = None):
+    def prefill(self, input_ids: torch.Tensor, cache: MambaCache | None = None,
+                out_cache: MambaCache | None = None):
         """input_ids [b, l] -> (logits [b, l, vocab], new MambaCache)
-        (reference model.py:328-341)."""
+        (reference model.py:328-341).  With `out_cache` (e.g. the cache a
+        GraphedStepper captured, or `cache` itself) the final states are
+        written into its tensors in place and out_cache is returned, so a
+        captured decode graph can serve the next prompt without re-capture."""
         x = self.embedding(input_ids)
         new_layers: list[LayerCache] = []
+        if out_cache is not None and len(out_cache.layers) != len(self.layers):
+            raise ValueError("out_cache has the wrong number of layers")
 
         def layer(i, xn):
             lc = cache.layers[i] if cache is not None else None
-            y, cs, hs = self.layers[i].mixer.prefill(xn, lc)
+            oc = out_cache.layers[i] if out_cache is not None else None
+            y, cs, hs = self.layers[i].mixer.prefill(xn, lc, oc)
             new_layers.append(LayerCache(conv_state=cs, ssm_state=hs))
             return y
 
         xf = self._run(x, layer)
-        return self.lm_head(xf), MambaCache(new_layers)
+        return self.lm_head(xf), (out_cache if out_cache is not None else MambaCache(new_layers))
 
     def step(self, input_ids: torch.Tensor, cache: MambaCache):
         """input_ids [b, 1] -> logits [b, 1, vocab]; cache updated in place

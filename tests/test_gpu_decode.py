@@ -116,3 +116,41 @@ def test_plan_refreshes_after_weight_change():
         p2 = model._decode_plan()
         assert p2 is not p1
         assert torch.equal(p2["layers"][0]["W_xT"], model.layers[0].mixer.x_proj.weight.t().contiguous())
+
+
+@pytest.mark.parametrize("kw", [dict(d_state=8, d_conv=3, bias=True, conv_bias=False),
+                                dict(d_state=4, d_conv=2, dt_rank=5),
+                                dict(d_state=16, d_conv=8, bias=True)])
+@pytest.mark.parametrize("b", [1, 4])
+def test_fused_step_config_variants(kw, b):
+    """Fused step with in/out_proj biases, no conv bias, N < 16, d_conv 2, 3
+    and 8, and a dt_rank that is not a multiple of 16: vs the per-op step."""
+    print(f"fused decode variant {kw} b={b}", flush=True)
+    torch.manual_seed(b)
+    cfg = MambaConfig(d_model=96, n_layer=2, vocab_size=200, **kw)
+    with torch.device(DEV):
+        model = MambaLM(cfg)
+    rng = np.random.default_rng(b)
+    with torch.no_grad():
+        for mx in model.modules():
+            if isinstance(mx, MambaMixer):
+                D = mx.dt_proj.bias.shape[0]
+                mx.dt_proj.bias.copy_(torch.from_numpy(
+                    om.inv_softplus(np.exp(rng.uniform(np.log(1e-3), np.log(0.1), D))).astype(np.float32)))
+                if mx.in_proj.bias is not None:
+                    mx.in_proj.bias.normal_(0, 0.1)
+                    mx.out_proj.bias.normal_(0, 0.1)
+    model.eval()
+    ids = torch.randint(0, 200, (b, 5), device=DEV)
+    with torch.no_grad():
+        _, c1 = model.prefill(ids)
+        _, c2 = model.prefill(ids)
+        assert model._fused_step_ok(ids[:, :1], c1)
+        for t in range(3):
+            nxt = torch.randint(0, 200, (b, 1), device=DEV)
+            got = model.step(nxt, c1)
+            ref = _per_op_step(model, nxt, c2)
+            assert_rel(_np(got), _np(ref), 1e-4, f"logits step {t}")
+        for l1, l2 in zip(c1.layers, c2.layers):
+            assert_rel(_np(l1.ssm_state), _np(l2.ssm_state), 1e-4, "ssm_state")
+            assert_rel(_np(l1.conv_state), _np(l2.conv_state), 1e-5, "conv_state")

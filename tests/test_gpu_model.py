@@ -244,3 +244,60 @@ def test_mixer_step_batched_x_proj_chunks(b):
     assert_rel(y.cpu().numpy(), y_ref, 1e-4, "y")
     assert_rel(lc.ssm_state.cpu().numpy(), hs_r, 1e-4, "ssm_state")
     assert_rel(lc.conv_state.cpu().numpy(), cs_r, 1e-5, "conv_state")
+
+
+def test_prefill_into_preallocated_cache():
+    """prefill(..., out_cache=) writes the final states into the given
+    tensors: bit-identical to a fresh prefill, addresses unchanged; and a
+    chunked continuation can target its own input cache."""
+    torch.manual_seed(21)
+    cfg = MambaConfig(d_model=64, n_layer=2, vocab_size=128, d_state=16)
+    with torch.device(DEV):
+        model = MambaLM(cfg)
+    _init_dt_bias(model, 21)
+    model.eval()
+    ids = torch.randint(0, 128, (2, 40), device=DEV)
+    with torch.no_grad():
+        ref_logits, ref_cache = model.prefill(ids)
+        pre = MambaCache.allocate(cfg, 2, DEV, torch.float32)
+        ptrs = [(l.conv_state.data_ptr(), l.ssm_state.data_ptr()) for l in pre.layers]
+        logits, got = model.prefill(ids, out_cache=pre)
+        assert got is pre
+        assert ptrs == [(l.conv_state.data_ptr(), l.ssm_state.data_ptr()) for l in pre.layers]
+        assert torch.equal(logits, ref_logits)
+        for a, r in zip(pre.layers, ref_cache.layers):
+            assert torch.equal(a.conv_state, r.conv_state) and torch.equal(a.ssm_state, r.ssm_state)
+        # continuation written over its own input state
+        _, c = model.prefill(ids[:, :25])
+        _, c2 = model.prefill(ids[:, 25:], cache=c, out_cache=c)
+        assert c2 is c
+        for a, r in zip(c.layers, ref_cache.layers):
+            assert_rel(_np(a.ssm_state), _np(r.ssm_state), 1e-5, "ssm_state")
+            assert_rel(_np(a.conv_state), _np(r.conv_state), 1e-5, "conv_state")
+
+
+@pytest.mark.parametrize("b", [1, 4])
+def test_graph_serves_a_second_prompt_after_prefill_into_its_cache(b):
+    """Capture once; prefill a new prompt into the captured cache; replays
+    then equal eager steps from a fresh prefill of that prompt, bit for bit."""
+    torch.manual_seed(22 + b)
+    cfg = MambaConfig(d_model=64, n_layer=2, vocab_size=128, d_state=16)
+    with torch.device(DEV):
+        model = MambaLM(cfg)
+    _init_dt_bias(model, 22)
+    model.eval()
+    p1 = torch.randint(0, 128, (b, 12), device=DEV)
+    p2 = torch.randint(0, 128, (b, 9), device=DEV)
+    steps = [torch.randint(0, 128, (b, 1), device=DEV) for _ in range(3)]
+    with torch.no_grad():
+        _, cache = model.prefill(p1)
+        st = GraphedStepper(model, cache, b, "cuda")
+        st.capture()
+        st.replay(steps[0])
+        model.prefill(p2, out_cache=cache)
+        _, ce = model.prefill(p2)
+        for s in steps:
+            g = st.replay(s).clone()
+            e = model.step(s, ce)
+            torch.cuda.synchronize()
+            assert torch.equal(g, e)
