@@ -309,8 +309,8 @@ def bench_shard(dev, iters=10):
                              xdbl[0, :, R:R + N].float(), xdbl[0, :, R + N:].float(), Dv[sl], z[0, sl].float(),
                              bias[sl])
         e_scan = float(((y[0, :, sl].float().T - yr).abs().max() / yr.abs().max()).item())
-    conv_bytes = 2 * b * L * D * 2 + 2 * b * D * 3 * 2 + D * 4 * 4 + D * 4
-    scan_bytes = 4 * b * L * D * 2 + 2 * b * N * L * 2 + b * D * N * 4 + D * N * 4 + 2 * D * 4
+    conv_bytes = 2 * b * L * D * 2 + b * D * 3 * 2 + D * 4 * 4 + D * 4   # x, u; final state out; w, bias
+    scan_bytes = 4 * b * L * D * 2 + 2 * b * N * L * 2 + b * D * N * 4 + D * N * 4 + 2 * D * 4   # u,delta,z,y; B,C; h; A; D,bias
     return {"conv_us": ms_conv * 1e3, "conv_gbps": conv_bytes / ms_conv / 1e6,
             "scan_us": ms_scan * 1e3, "scan_gbps": scan_bytes / ms_scan / 1e6,
             "scan_frac_hbm_peak": scan_bytes / ms_scan / 1e6 / HBM_PEAK_GBPS,
