@@ -194,6 +194,57 @@ def bench_decode(model, batch, prompt, n_tokens, dev):
     return ms * 1000.0, ok
 
 
+def _oracle_lm_weights(model):
+    f = lambda p: p.detach().float().cpu().numpy()
+    layers = []
+    for blk in model.layers:
+        m = blk.mixer
+        d = {"norm": f(blk.norm.weight), "in_proj_w": f(m.in_proj.weight), "conv_w": f(m.conv1d.weight)[:, 0, :],
+             "conv_b": f(m.conv1d.bias) if m.conv1d.bias is not None else None, "x_proj_w": f(m.x_proj.weight),
+             "dt_proj_w": f(m.dt_proj.weight), "dt_proj_b": f(m.dt_proj.bias), "A_log": f(m.A_log), "D": f(m.D),
+             "out_proj_w": f(m.out_proj.weight)}
+        layers.append(d)
+    return {"embedding": f(model.embedding.weight), "norm_f": f(model.norm_f.weight), "layers": layers}
+
+
+def cpu_baseline_decode(model, dev, prompt=64, steps=8):
+    """cpu_baseline leg of the decode metric at the 130m shape, batch 1: the
+    oracle's LM (numpy float32, the reference's materialize-then-loop prefill
+    and its step) on the host, `prompt` ids then `steps` timed greedy steps
+    (ms/token), with the GPU's fused step logits compared to the oracle's on
+    the same weights and tokens."""
+    import numpy as np
+    import torch
+    from oracle import mixer as om
+    W = _oracle_lm_weights(model)
+    g = torch.Generator(device=dev).manual_seed(99)
+    ids = torch.randint(0, model.cfg.vocab_size, (1, prompt), device=dev, generator=g)
+    _, cache = om.lm_prefill(W, ids.cpu().numpy(), dtype=np.float32)
+    with torch.no_grad():
+        logits, gcache = model.prefill(ids)
+    nxt = ids[:, -1:].cpu().numpy()
+    err = 0.0
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        ref = om.lm_step(W, nxt, cache, dtype=np.float32)
+        nxt = ref[:, -1].argmax(-1)[:, None]
+    secs = time.perf_counter() - t0
+    # parity of the fused GPU step on the same tokens (teacher-forced)
+    _, cache = om.lm_prefill(W, ids.cpu().numpy(), dtype=np.float64)
+    tok = ids[:, -1:]
+    with torch.no_grad():
+        for _ in range(3):
+            got = model.step(tok, gcache)
+            ref = om.lm_step(W, tok.cpu().numpy(), cache, dtype=np.float64)
+            err = max(err, float(np.abs(got.cpu().numpy() - ref).max() / np.abs(ref).max()))
+            tok = got[:, -1].argmax(-1, keepdim=True)
+    cores = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    return {"value": secs / steps * 1e6, "unit": "us/token", "cores": cores, "kind": "port",
+            "sample": f"130m shape b=1: {prompt}-token prefill, then {steps} greedy steps timed (numpy float32 oracle; "
+                      f"BLAS threads up to {cores})",
+            "gpu_step_max_rel_err_vs_oracle_f64": err}
+
+
 def bench_prefill(model, batch, seqlen, dev, iters=3):
     import torch
     g = torch.Generator(device=dev).manual_seed(7)
@@ -404,6 +455,11 @@ def main():
                     dec[f"{name}_b{bsz}"] = {"us_per_step": us, "us_per_token": us / bsz, "graph_equals_eager": ok,
                                              "prompt": prompt, "tokens_timed": ntok}
                     log(f"decode {name} b={bsz}: {us:.1f} us/step (graph==eager {ok})")
+                if name == "130m" and not args.no_cpu_baseline:
+                    cb = cpu_baseline_decode(model, dev)
+                    dec["130m_b1"]["cpu_baseline"] = cb
+                    log(f"decode cpu baseline: {cb['value']:.0f} us/token; GPU step rel err vs oracle "
+                        f"{cb['gpu_step_max_rel_err_vs_oracle_f64']:.2e}")
                 del model
                 torch.cuda.empty_cache()
             except Exception as e:  # report, keep the headline line
