@@ -62,3 +62,58 @@ def test_invalid_arguments_are_rejected_without_a_gpu():
     c.batch, c.seqlen, c.dim, c.width = 1, 4, 8, 9     # width > 8
     assert lib.mtl_causal_conv1d_fwd(ctypes.byref(c), None) == 1
     assert b"width" in lib.mtl_last_error()
+
+
+@pytest.mark.parametrize("case", [
+    ("mtl_decode_in", dict(batch=3), b"batch must be 1, 2 or 4"),
+    ("mtl_decode_in", dict(d_model=6), b"d_model"),
+    ("mtl_decode_in", dict(channels_per_block=16), b"channels_per_block"),
+    ("mtl_decode_in", dict(d_conv=9), b"bad sizes"),
+    ("mtl_decode_gemv", dict(batch=8), b"batch must be 1, 2 or 4"),
+    ("mtl_decode_gemv", dict(cols=8192), b"cols"),
+    ("mtl_decode_ssm", dict(d_state=17), b"d_state"),
+    ("mtl_decode_ssm", dict(dt_rank=300), b"dt_rank"),
+    ("mtl_decode_ssm", dict(nblk=1000), b"partial blocks"),
+    ("mtl_sum_parts", dict(nparts=0), b"nparts"),
+    ("mtl_sum_parts", dict(nparts=65), b"nparts"),
+    ("mtl_selective_state_update", dict(dstate=17), b"dstate"),
+    ("mtl_selective_state_update", dict(dt_rank=257), b"dt_rank"),
+    ("mtl_conv_step", dict(width=9), b"width"),
+])
+def test_entry_points_validate_sizes_on_the_host(case):
+    """Each entry point rejects sizes its kernels do not cover, with a message,
+    before any launch (the pointers below are never dereferenced)."""
+    from mamba_lite import _lib
+
+    lib = _lib.load()
+    name, over, msg = case
+    P = ctypes.c_void_p(16)     # a non-null, 16-byte aligned placeholder that is never used
+    if name == "mtl_decode_in":
+        a = dict(batch=1, d_model=64, d_inner=128, d_conv=4, xdbl_cols=36, channels_per_block=8)
+        a.update(over)
+        rc = lib.mtl_decode_in(P, None, None, None, P, 1e-5, P, None, P, P, None, None, P, P, None, a["batch"],
+                               a["d_model"], a["d_inner"], a["d_conv"], a["xdbl_cols"], a["channels_per_block"], None)
+    elif name == "mtl_decode_gemv":
+        a = dict(batch=1, rows=8, cols=64)
+        a.update(over)
+        rc = lib.mtl_decode_gemv(P, P, None, None, P, a["batch"], a["rows"], a["cols"], None)
+    elif name == "mtl_decode_ssm":
+        a = dict(nblk=4, batch=1, d_inner=64, d_state=16, dt_rank=4)
+        a.update(over)
+        rc = lib.mtl_decode_ssm(P, a["nblk"], P, P, P, P, P, None, P, P, a["batch"], a["d_inner"], a["d_state"],
+                                a["dt_rank"], None)
+    elif name == "mtl_sum_parts":
+        a = dict(nparts=2)
+        a.update(over)
+        rc = lib.mtl_sum_parts(P, a["nparts"], 16, P, None)
+    elif name == "mtl_selective_state_update":
+        a = dict(dstate=16, dt_rank=4)
+        a.update(over)
+        rc = lib.mtl_selective_state_update(P, P, 64, None, 0, P, 36, P, P, P, None, P, 64, 1, 64, a["dstate"],
+                                            a["dt_rank"], 0, 0, None)
+    else:
+        a = dict(width=4)
+        a.update(over)
+        rc = lib.mtl_conv_step(P, P, 64, P, None, P, 64, 1, 64, a["width"], 0, 1, None)
+    assert rc == 1, (name, over)
+    assert msg in lib.mtl_last_error(), lib.mtl_last_error()
