@@ -97,3 +97,12 @@ def test_tp_utils_wrappers_count_bytes():
     tp_utils.quant_dequant_sum_int8_tok([a, b], counter=c)
     tp_utils.quant_dequant_sum_fp16([a, b], counter=c)
     assert c.count == 2 and c.bytes == 10 * 84 + 10 * 80 * 2
+
+
+def test_zero_rows_are_a_no_op():
+    a = torch.empty(0, 768, device=DEV)
+    out, pays = ops.quant_dequant_sum_int8_tok([a, a.clone()], return_payloads=True)
+    assert out.shape == (0, 768)
+    out16, _ = ops.quant_dequant_sum_fp16([a, a.clone()])
+    assert out16.shape == (0, 768)
+    torch.cuda.synchronize()

@@ -162,3 +162,15 @@ def test_scan_channel_shard_equals_dense_slice():
            for k, v in c.items()}
     ys, hs = _run(sub)
     assert np.array_equal(ys, y[:, 1024:]) and np.array_equal(hs, h[:, 1024:])
+
+
+def test_zero_batch_and_zero_channels_are_no_ops():
+    for b, D in ((0, 64), (2, 0)):
+        u = torch.randn(b, D, 8, device=DEV)
+        B = torch.randn(b, 16, 8, device=DEV)
+        A = -torch.ones(D, 16, device=DEV)
+        y, h = ops.selective_scan(u, u, A, B, B)
+        assert y.shape == (b, D, 8) and h.shape == (b, D, 16)
+        out, fs = ops.causal_conv1d(u, torch.randn(D, 4, device=DEV))
+        assert out.shape == (b, D, 8) and fs.shape == (b, D, 3)
+    torch.cuda.synchronize()
