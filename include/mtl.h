@@ -126,6 +126,21 @@ int mtl_conv_step(void* conv_state, const void* x, int64_t x_sb, const float* w,
                   int32_t dtype, int32_t silu, mtl_stream_t stream);
 
 /* ------------------------------------------------------------------------
+ * Batched single-token conv step fused with the x_proj split-K partials,
+ * fp32, 1 <= batch <= 32.  Replaces model.py:264-279 for the batch at once:
+ * the conv step of mtl_conv_step (history shifted in place, SiLU) into out
+ * [b, D] (batch stride out_sb), and
+ *   xpart[k, b, j] = sum_{c in block k} out[b, c] * W_xT[c, j]
+ * for blocks of 32 channels (nblk = ceil(D / 32)); mtl_sum_parts over the
+ * nblk blocks gives x_dbl [b, J] (J = xdbl_cols = R + 2N <= 288).
+ * x: [b, D] (batch stride x_sb, channel stride 1); W_xT: x_proj weight
+ * transposed, contiguous [D, J]; xpart: contiguous [nblk, b, J].
+ * ---------------------------------------------------------------------- */
+int mtl_conv_step_xproj(float* conv_state, const float* x, int64_t x_sb, const float* w, const float* bias,
+                        float* out, int64_t out_sb, const float* W_xT, float* xpart, int64_t batch, int64_t dim,
+                        int32_t width, int32_t xdbl_cols, mtl_stream_t stream);
+
+/* ------------------------------------------------------------------------
  * Single-token selective state update, in place.
  * Replaces model.py:280-292 after x_proj (dt = softplus(F.linear(dt_low,
  * W_dt, b_dt)), dA = exp(dt*A), dBx = dt*B*x, ssm_state.copy_(h*dA + dBx),
@@ -154,11 +169,14 @@ int mtl_add_rmsnorm(const float* x, const float* y, float* x_out, const float* w
                     int64_t rows, int64_t cols, float eps, mtl_stream_t stream);
 
 /* ------------------------------------------------------------------------
- * Sum of split-K partial products, in part order:
- *   out[i] = ((parts[0*n + i] + parts[1*n + i]) + ...) + parts[(nparts-1)*n + i]
+ * Sum of split-K partial products in a fixed order: for nparts <= 32
+ *   out[i] = ((parts[0*n + i] + parts[1*n + i]) + ...) + parts[(nparts-1)*n + i];
+ * above 32 the parts form 4 contiguous quarters of ceil(nparts/4), each
+ * summed in that order, and the non-empty quarter sums are added left to
+ * right.
  * The x_proj of the batched step (model.py:279, x_dbl = x_proj(x)) runs as
  * nparts GEMMs over channel chunks on hipBLASLt; this adds their outputs.
- * parts: contiguous fp32 [nparts, n]; out: fp32 [n].  1 <= nparts <= 64.
+ * parts: contiguous fp32 [nparts, n]; out: fp32 [n].  1 <= nparts <= 128.
  * ---------------------------------------------------------------------- */
 int mtl_sum_parts(const float* parts, int32_t nparts, int64_t n, float* out, mtl_stream_t stream);
 

@@ -210,6 +210,110 @@ int launch_conv_step(void* state, const void* x, int64_t x_sb, const float* w, c
     return check_launch("conv_step");
 }
 
+// Batched single-token conv step fused with the x_proj split-K partials
+// (model.py:264-279 for b rows at once): a workgroup owns kXpCB channels of
+// all b <= 32 rows.  Phase 1: conv step (history shifted in place) + SiLU for
+// its (channel, row) pairs, xc to global memory and to LDS.  Phase 2: the
+// block's partial x_dbl[b][j] = sum over its channels of xc[b][c] W_xT[c][j],
+// from LDS, a TB x (J/32) register tile per thread (rows b0.., columns jg +
+// 32 q).  Partials land in xpart[block][b][j]; the caller sums them in block
+// order.
+constexpr int kXpCB = 32;                 // channels per workgroup
+constexpr int kXpMaxJQ = 9;               // J <= 288 = 256 + 32
+
+template <int K, int TB, int JQ>
+__global__ void __launch_bounds__(256) conv_step_xproj_kernel(float* __restrict__ state, const float* __restrict__ x,
+                                                              int64_t x_sb, const float* __restrict__ w,
+                                                              const float* __restrict__ bias, float* __restrict__ out,
+                                                              int64_t o_sb, const float* __restrict__ WxT,
+                                                              float* __restrict__ xpart, int batch, int D, int J) {
+    constexpr int BMAX = 8 * TB;                     // rows covered: 8 row groups of TB
+    __shared__ float s_xc[BMAX][kXpCB + 1];
+    __shared__ float s_w[kXpCB][kXpMaxJQ * 32];       // rows c >= nch are never read (see phase 2)
+    const int tid = threadIdx.x;
+    const int c0 = blockIdx.x * kXpCB;
+    const int nch = min(kXpCB, D - c0);
+
+    // every load first, with clamped addresses: the block's x_proj columns
+    // (8 threads per channel row, element j = tid % 8 + 8 k), then the conv
+    // operands of pair e = tid + 256 q (channel fastest)
+    constexpr int kWLoads = kXpMaxJQ * 32 / 8;
+    const int wc = tid >> 3, wj = tid & 7;
+    const float* wrow = WxT + (int64_t)(c0 + min(wc, nch - 1)) * J;
+    float wl[kWLoads];
+#pragma unroll
+    for (int k = 0; k < kWLoads; ++k) wl[k] = wrow[min(wj + 8 * k, J - 1)];
+    constexpr int kPairs = kXpCB * BMAX;     // = 256 TB
+    float win[TB][K], wk[TB][K], bs[TB];
+#pragma unroll
+    for (int q = 0; q < TB; ++q) {
+        const int e = tid + 256 * q;
+        const int ch = c0 + min(tid % kXpCB, nch - 1), bi = min(tid / kXpCB + 8 * q, batch - 1);
+        const float* s = state + ((int64_t)bi * D + ch) * (K - 1);
+#pragma unroll
+        for (int k = 0; k < K - 1; ++k) win[q][k] = s[k];
+        win[q][K - 1] = x[bi * x_sb + ch];
+#pragma unroll
+        for (int k = 0; k < K; ++k) wk[q][k] = w[(int64_t)ch * K + k];
+        bs[q] = bias ? bias[ch] : 0.f;
+    }
+#pragma unroll
+    for (int k = 0; k < kWLoads; ++k)
+        if (wj + 8 * k < J) s_w[wc][wj + 8 * k] = wl[k];
+    // phase 1: conv step + SiLU
+    static_assert(kPairs == 256 * TB, "one pair per thread per row group");
+#pragma unroll
+    for (int q = 0; q < TB; ++q) {
+        const int c = tid % kXpCB, bi = tid / kXpCB + 8 * q;
+        float acc = 0.f;
+#pragma unroll
+        for (int k = 0; k < K; ++k) acc = fmaf(win[q][k], wk[q][k], acc);
+        acc += bs[q];
+        const bool ok = c < nch && bi < batch;
+        const float xcv = ok ? silu_f(acc) : 0.f;
+        if (ok) {
+            const int ch = c0 + c;
+            float* s = state + ((int64_t)bi * D + ch) * (K - 1);
+#pragma unroll
+            for (int k = 0; k < K - 1; ++k) s[k] = win[q][k + 1];
+            out[bi * o_sb + ch] = xcv;
+        }
+        s_xc[bi][c] = xcv;
+    }
+    __syncthreads();
+
+    // phase 2: thread = (row group rg of TB rows, column lane jg)
+    // JQ = column runs (J <= 32 JQ); columns past J read unwritten LDS and
+    // are never stored, so the loop has no branches
+    const int rg = tid / 32, jg = tid % 32;
+    float acc[TB][JQ];
+#pragma unroll
+    for (int i = 0; i < TB; ++i)
+#pragma unroll
+        for (int q = 0; q < JQ; ++q) acc[i][q] = 0.f;
+    for (int c = 0; c < nch; ++c) {
+        float xv[TB], wv[JQ];
+#pragma unroll
+        for (int i = 0; i < TB; ++i) xv[i] = s_xc[rg * TB + i][c];
+#pragma unroll
+        for (int q = 0; q < JQ; ++q) wv[q] = s_w[c][jg + 32 * q];
+#pragma unroll
+        for (int q = 0; q < JQ; ++q)
+#pragma unroll
+            for (int i = 0; i < TB; ++i) acc[i][q] = fmaf(xv[i], wv[q], acc[i][q]);
+    }
+#pragma unroll
+    for (int i = 0; i < TB; ++i) {
+        const int bi = rg * TB + i;
+        if (bi >= batch) continue;
+#pragma unroll
+        for (int q = 0; q < JQ; ++q) {
+            const int j = jg + 32 * q;
+            if (j < J) xpart[((int64_t)blockIdx.x * batch + bi) * J + j] = acc[i][q];
+        }
+    }
+}
+
 }  // namespace
 }  // namespace mtl
 
@@ -266,4 +370,40 @@ extern "C" int mtl_conv_step(void* conv_state, const void* x, int64_t x_sb, cons
                ? launch_conv_step<float>(conv_state, x, x_sb, w, bias, out, out_sb, batch, (int)dim, width, silu, st)
                : launch_conv_step<uint16_t>(conv_state, x, x_sb, w, bias, out, out_sb, batch, (int)dim, width, silu,
                                             st);
+}
+
+extern "C" int mtl_conv_step_xproj(float* conv_state, const float* x, int64_t x_sb, const float* w, const float* bias,
+                                   float* out, int64_t out_sb, const float* W_xT, float* xpart, int64_t batch,
+                                   int64_t dim, int32_t width, int32_t xdbl_cols, mtl_stream_t stream) {
+    using namespace mtl;
+    clear_error();
+    MTL_REQUIRE(batch >= 1 && batch <= 32, "batch must be in [1, 32]");
+    MTL_REQUIRE(dim >= 1 && dim < (int64_t(1) << 31), "dim out of range");
+    MTL_REQUIRE(width >= 2 && width <= kMaxK, "width (d_conv) must be in [2, 8]");
+    MTL_REQUIRE(xdbl_cols >= 1 && xdbl_cols <= kXpMaxJQ * 32, "xdbl_cols must be in [1, 288]");
+    MTL_REQUIRE(conv_state && x && w && out && W_xT && xpart, "null required pointer");
+    const dim3 grid((unsigned)((dim + kXpCB - 1) / kXpCB));
+    hipStream_t st = as_stream(stream);
+    const int D = (int)dim, J = xdbl_cols, B = (int)batch;
+#define MTL_XP_LAUNCH(KK, TBV, JQV) hipLaunchKernelGGL((conv_step_xproj_kernel<KK, TBV, JQV>), grid, dim3(256), 0, \
+        st, conv_state, x, x_sb, w, bias, out, out_sb, W_xT, xpart, B, D, J)
+#define MTL_XP_J(KK, TBV)                                                \
+    if (J <= 64) MTL_XP_LAUNCH(KK, TBV, 2);                              \
+    else if (J <= 96) MTL_XP_LAUNCH(KK, TBV, 3);                         \
+    else if (J <= 160) MTL_XP_LAUNCH(KK, TBV, 5);                        \
+    else MTL_XP_LAUNCH(KK, TBV, 9);
+#define MTL_XP_K(KK)                                                     \
+    case KK:                                                             \
+        if (B <= 8) { MTL_XP_J(KK, 1) }                                  \
+        else if (B <= 16) { MTL_XP_J(KK, 2) }                            \
+        else { MTL_XP_J(KK, 4) }                                         \
+        break;
+    switch (width) {
+        MTL_XP_K(2) MTL_XP_K(3) MTL_XP_K(4) MTL_XP_K(5) MTL_XP_K(6) MTL_XP_K(7) MTL_XP_K(8)
+        default: break;
+    }
+#undef MTL_XP_K
+#undef MTL_XP_J
+#undef MTL_XP_LAUNCH
+    return check_launch("conv_step_xproj");
 }

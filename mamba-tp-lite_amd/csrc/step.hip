@@ -107,6 +107,33 @@ ssm_step_kernel(float* __restrict__ state, const T* __restrict__ x, int64_t x_sb
     }
 }
 
+// More than 32 parts: the parts are split into 4 contiguous quarters of
+// ceil(P/4); wavefront q of a block sums quarter q of 64 outputs in part
+// order, and the (non-empty) quarter sums are added left to right.
+template <int PQ>
+__global__ void __launch_bounds__(256) sum_parts4_kernel(const float* __restrict__ parts, int nparts, int64_t n,
+                                                         float* __restrict__ out) {
+    __shared__ float s_q[4][64];
+    const int oq = threadIdx.x & 63, q = threadIdx.x >> 6;
+    const int64_t i = (int64_t)blockIdx.x * 64 + oq;
+    const int64_t ii = min(i, n - 1);
+    const int per = (nparts + 3) / 4, p0 = q * per, np = min(per, nparts - p0);
+    float v[PQ];
+#pragma unroll
+    for (int u = 0; u < PQ; ++u) v[u] = parts[(int64_t)max(min(p0 + u, nparts - 1), 0) * n + ii];
+    float acc = v[0];
+#pragma unroll
+    for (int u = 1; u < PQ; ++u) acc = u < np ? acc + v[u] : acc;
+    s_q[q][oq] = acc;
+    __syncthreads();
+    if (q == 0 && i < n) {
+        float r = s_q[0][oq];
+#pragma unroll
+        for (int k = 1; k < 4; ++k) r = k * per < nparts ? r + s_q[k][oq] : r;
+        out[i] = r;
+    }
+}
+
 // out[i] = parts[0][i] + parts[1][i] + ... in part order (split-K partials)
 template <int P>
 __global__ void __launch_bounds__(256) sum_parts_kernel(const float* __restrict__ parts, int nparts, int64_t n,
@@ -266,15 +293,16 @@ extern "C" int mtl_add_rmsnorm(const float* x, const float* y, float* x_out, con
 extern "C" int mtl_sum_parts(const float* parts, int32_t nparts, int64_t n, float* out, mtl_stream_t stream) {
     using namespace mtl;
     clear_error();
-    MTL_REQUIRE(nparts >= 1 && nparts <= 64 && n >= 0, "nparts must be in [1, 64]");
+    MTL_REQUIRE(nparts >= 1 && nparts <= 128 && n >= 0, "nparts must be in [1, 128]");
     if (n == 0) return MTL_OK;
     MTL_REQUIRE(parts && out, "null required pointer");
     MTL_REQUIRE(n < (int64_t(1) << 31), "n too large");
-    const dim3 grid((unsigned)((n + 255) / 256));
+    const dim3 grid((unsigned)((n + 255) / 256)), grid4((unsigned)((n + 63) / 64));
     hipStream_t st = as_stream(stream);
     if (nparts <= 8) hipLaunchKernelGGL((sum_parts_kernel<8>), grid, dim3(256), 0, st, parts, nparts, n, out);
     else if (nparts <= 16) hipLaunchKernelGGL((sum_parts_kernel<16>), grid, dim3(256), 0, st, parts, nparts, n, out);
     else if (nparts <= 32) hipLaunchKernelGGL((sum_parts_kernel<32>), grid, dim3(256), 0, st, parts, nparts, n, out);
-    else hipLaunchKernelGGL((sum_parts_kernel<64>), grid, dim3(256), 0, st, parts, nparts, n, out);
+    else if (nparts <= 64) hipLaunchKernelGGL((sum_parts4_kernel<16>), grid4, dim3(256), 0, st, parts, nparts, n, out);
+    else hipLaunchKernelGGL((sum_parts4_kernel<32>), grid4, dim3(256), 0, st, parts, nparts, n, out);
     return check_launch("sum_parts");
 }

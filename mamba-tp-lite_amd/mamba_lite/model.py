@@ -227,8 +227,16 @@ class MambaMixer(nn.Module):
         no allocation outside torch's caching allocator: graph-capturable."""
         Dm, R = self.cfg.d_inner, self.cfg.dt_rank
         xz = self.in_proj(x_t)                                   # [b, 2D]
-        xc = ops.conv_step(cache.conv_state, xz[:, :Dm], self._conv_w(), _f32(self.conv1d.bias), silu=True)
-        x_dbl = self._x_proj_step(xc)                            # [b, R+2N]
+        b = x_t.shape[0]
+        J = R + 2 * self.cfg.d_state
+        if xz.dtype == torch.float32 and b <= 32 and J <= 288 and cache.conv_state.dtype == torch.float32:
+            # conv step and the x_proj partials of 32-channel blocks in one kernel
+            xc, xpart = ops.conv_step_xproj(cache.conv_state, xz[:, :Dm], self._conv_w(), _f32(self.conv1d.bias),
+                                            self._xproj_t())
+            x_dbl = ops.sum_parts(xpart)                         # [b, R+2N]
+        else:
+            xc = ops.conv_step(cache.conv_state, xz[:, :Dm], self._conv_w(), _f32(self.conv1d.bias), silu=True)
+            x_dbl = self._x_proj_step(xc)                        # [b, R+2N]
         y = ops.selective_state_update(cache.ssm_state, xc, xz[:, Dm:], x_dbl, _f32(self.dt_proj.weight),
                                        _f32(self.dt_proj.bias), _f32(self.A_log), _f32(self.D), a_is_log=True)
         return self.out_proj(y)
@@ -239,17 +247,21 @@ class MambaMixer(nn.Module):
     # chunks (one batched call) whose outputs are added in chunk order
     _XPROJ_CHUNK = 128
 
-    def _xproj_chunks(self) -> torch.Tensor:
+    def _xproj_t(self) -> torch.Tensor:
+        """x_proj weight transposed, contiguous [D, R+2N] (rebuilt when the
+        weight changes: tracked by address and version)."""
         w = self.x_proj.weight
         key = (w.data_ptr(), w._version, w.dtype)
         cached = getattr(self, "_xproj_cache", None)
         if cached is None or cached[0] != key:
-            D, J = w.shape[1], w.shape[0]
             with torch.no_grad():
-                wt = w.detach().t().contiguous().view(D // self._XPROJ_CHUNK, self._XPROJ_CHUNK, J)
-            cached = (key, wt)
+                cached = (key, w.detach().t().contiguous())
             self._xproj_cache = cached
         return cached[1]
+
+    def _xproj_chunks(self) -> torch.Tensor:
+        wt = self._xproj_t()
+        return wt.view(wt.shape[0] // self._XPROJ_CHUNK, self._XPROJ_CHUNK, wt.shape[1])
 
     def _x_proj_step(self, xc: torch.Tensor) -> torch.Tensor:
         b, D = xc.shape

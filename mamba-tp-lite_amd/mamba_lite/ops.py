@@ -214,6 +214,41 @@ def conv_step(conv_state, x, weight, bias=None, silu=True, out=None):
     return out
 
 
+XPROJ_BLOCK = 32   # channels per x_proj partial block of conv_step_xproj
+
+
+def conv_step_xproj(conv_state, x, weight, bias, W_xT, out=None, xpart=None):
+    """mtl_conv_step_xproj: in-place conv step + SiLU of x [b, D] (fp32,
+    channel stride 1, b <= 32) into out [b, D], and the x_proj partials of
+    each 32-channel block into xpart [ceil(D/32), b, J] (W_xT: [D, J]).
+    Returns (out, xpart); ops.sum_parts(xpart) is x_dbl."""
+    b, Dm = x.shape
+    w = weight.reshape(weight.shape[0], weight.shape[-1]) if weight.dim() == 3 else weight
+    K = w.shape[1]
+    _f32_mat(w, (Dm, K), "weight")
+    _f32_vec(bias, Dm, "bias")
+    J = W_xT.shape[1]
+    _f32_mat(W_xT, (Dm, J), "W_xT")
+    _f32_mat(conv_state, (b, Dm, K - 1), "conv_state")
+    if x.dtype != torch.float32 or x.stride(1) != 1:
+        raise ValueError("x must be float32 with channel stride 1")
+    nblk = -(-Dm // XPROJ_BLOCK)
+    if out is None:
+        out = torch.empty(b, Dm, device=x.device, dtype=torch.float32)
+    elif tuple(out.shape) != (b, Dm) or out.dtype != torch.float32 or out.stride(1) != 1:
+        raise ValueError(f"out must be float32 {(b, Dm)} with channel stride 1")
+    if xpart is None:
+        xpart = torch.empty(nblk, b, J, device=x.device, dtype=torch.float32)
+    else:
+        _f32_mat(xpart, (nblk, b, J), "xpart")
+    _same_device(x, conv_state, w, bias, W_xT, out, xpart)
+    with _dev_guard(x):
+        _lib.check(_lib.load().mtl_conv_step_xproj(_ptr(conv_state), _ptr(x), x.stride(0), _ptr(w), _ptr(bias),
+                                                   _ptr(out), out.stride(0), _ptr(W_xT), _ptr(xpart), b, Dm, K, J,
+                                                   _stream(x)), "conv_step_xproj")
+    return out, xpart
+
+
 # --------------------------------------------------------------------------- step
 def selective_state_update(ssm_state, x, z, x_dbl, W_dt, b_dt, A, D=None, a_is_log=False, out=None):
     """In-place single-token SSM update (mtl_selective_state_update).

@@ -75,7 +75,10 @@ def test_invalid_arguments_are_rejected_without_a_gpu():
     ("mtl_decode_ssm", dict(dt_rank=300), b"dt_rank"),
     ("mtl_decode_ssm", dict(nblk=1000), b"partial blocks"),
     ("mtl_sum_parts", dict(nparts=0), b"nparts"),
-    ("mtl_sum_parts", dict(nparts=65), b"nparts"),
+    ("mtl_sum_parts", dict(nparts=129), b"nparts"),
+    ("mtl_conv_step_xproj", dict(batch=33), b"batch"),
+    ("mtl_conv_step_xproj", dict(xdbl_cols=289), b"xdbl_cols"),
+    ("mtl_conv_step_xproj", dict(width=1), b"width"),
     ("mtl_selective_state_update", dict(dstate=17), b"dstate"),
     ("mtl_selective_state_update", dict(dt_rank=257), b"dt_rank"),
     ("mtl_conv_step", dict(width=9), b"width"),
@@ -106,6 +109,10 @@ def test_entry_points_validate_sizes_on_the_host(case):
         a = dict(nparts=2)
         a.update(over)
         rc = lib.mtl_sum_parts(P, a["nparts"], 16, P, None)
+    elif name == "mtl_conv_step_xproj":
+        a = dict(batch=8, width=4, xdbl_cols=160)
+        a.update(over)
+        rc = lib.mtl_conv_step_xproj(P, P, 64, P, None, P, 64, P, P, a["batch"], 64, a["width"], a["xdbl_cols"], None)
     elif name == "mtl_selective_state_update":
         a = dict(dstate=16, dt_rank=4)
         a.update(over)

@@ -198,15 +198,50 @@ def test_add_rmsnorm(rows, cols):
     assert_rel(out2.cpu().numpy(), om.rmsnorm(x, w, 1e-5, np.float64), 1e-5, "norm only")
 
 
-@pytest.mark.parametrize("nparts,n", [(1, 5), (3, 1000), (16, 5120), (32, 257), (64, 300)])
+@pytest.mark.parametrize("nparts,n", [(1, 5), (3, 1000), (16, 5120), (32, 257), (33, 100), (64, 300), (97, 64),
+                                      (128, 5120)])
 def test_sum_parts_in_part_order(nparts, n):
-    """mtl_sum_parts adds the parts left to right in float32, bit for bit."""
+    """mtl_sum_parts adds the parts in its documented fixed order (left to
+    right up to 32 parts, four ordered quarters above), bit for bit."""
     rng = np.random.default_rng(nparts * 7 + n)
     scale = 10.0 ** rng.integers(-3, 4, (nparts, 1))
     parts = (rng.standard_normal((nparts, n)) * scale).astype(np.float32)
     assert parts.dtype == np.float32
     got = ops.sum_parts(_t(parts)).cpu().numpy()
-    ref = parts[0].copy()
-    for p in range(1, nparts):
-        ref = (ref + parts[p]).astype(np.float32)
+
+    def ordered(ps):
+        r = ps[0].copy()
+        for p in ps[1:]:
+            r = (r + p).astype(np.float32)
+        return r
+    if nparts <= 32:
+        ref = ordered(parts)
+    else:
+        per = -(-nparts // 4)
+        ref = ordered([ordered(parts[q * per:(q + 1) * per]) for q in range(4) if q * per < nparts])
     assert np.array_equal(got, ref)
+
+
+@pytest.mark.parametrize("b,D,J,K", [(1, 64, 36, 4), (5, 200, 80, 4), (8, 1536, 80, 4), (17, 333, 160, 3),
+                                     (32, 4096, 160, 4), (32, 96, 288, 8)])
+def test_conv_step_xproj_matches_conv_step_and_linear(b, D, J, K):
+    """The fused batched conv step + x_proj partials: conv output and state
+    equal mtl_conv_step's bit for bit; the block partials summed in order
+    match x_proj of the conv output (1e-5)."""
+    print(f"conv_step_xproj b={b} D={D} J={J} K={K}", flush=True)
+    rng = np.random.default_rng(b * 1000 + D + J + K)
+    st = rng.standard_normal((b, D, K - 1)).astype(np.float32)
+    xz = rng.standard_normal((b, 2 * D)).astype(np.float32)
+    w = rng.standard_normal((D, K)).astype(np.float32)
+    bias = rng.standard_normal(D).astype(np.float32)
+    Wx = (rng.standard_normal((J, D)) / np.sqrt(D)).astype(np.float32)
+    S1, S2 = _t(st), _t(st)
+    XZ = _t(xz)
+    ref = ops.conv_step(S1, XZ[:, :D], _t(w), _t(bias))
+    got, xpart = ops.conv_step_xproj(S2, XZ[:, :D], _t(w), _t(bias), _t(Wx.T))
+    x_dbl = ops.sum_parts(xpart)
+    torch.cuda.synchronize()
+    assert torch.equal(got, ref)
+    assert torch.equal(S1, S2)
+    xd_ref = ref.double().cpu().numpy() @ Wx.astype(np.float64).T
+    assert_rel(x_dbl.cpu().numpy(), xd_ref, 1e-5, "x_dbl")

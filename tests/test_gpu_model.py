@@ -219,10 +219,11 @@ def test_bf16_mixer_shard_shape():
     assert_rel(_np(outb), _np(out32), 5e-2, "bf16 out vs fp32 out")
 
 
-@pytest.mark.parametrize("b", [8, 32])
+@pytest.mark.parametrize("b", [8, 32, 40])
 def test_mixer_step_batched_x_proj_chunks(b):
-    """At b >= 8 and d_inner >= 1024 the step's x_proj runs as chunked GEMMs
-    plus mtl_sum_parts; the step still matches the oracle mixer step."""
+    """Batched per-op step: up to b = 32 the conv step and x_proj partials run
+    in mtl_conv_step_xproj + mtl_sum_parts; above it (d_inner >= 1024) x_proj
+    runs as chunked GEMMs + mtl_sum_parts.  Both match the oracle step."""
     print(f"batched mixer step b={b}", flush=True)
     torch.manual_seed(b)
     cfg = MambaConfig(d_model=512, n_layer=1, vocab_size=64, d_state=16)
