@@ -133,9 +133,10 @@ def test_selective_state_update(N, R, b):
     assert_rel(H.cpu().numpy(), h_ref, 1e-4, "state")
 
 
-def test_selective_state_update_bf16():
-    rng = np.random.default_rng(9)
-    b, D, N, R = 2, 256, 16, 48
+@pytest.mark.parametrize("b", [2, 16])
+def test_selective_state_update_bf16(b):
+    rng = np.random.default_rng(9 + b)
+    D, N, R = 256, 16, 48
     h = rng.standard_normal((b, D, N)).astype(np.float32)
     x = rng.standard_normal((b, D)).astype(np.float32)
     z = rng.standard_normal((b, D)).astype(np.float32)
