@@ -246,3 +246,28 @@ def test_conv_step_xproj_matches_conv_step_and_linear(b, D, J, K):
     assert torch.equal(S1, S2)
     xd_ref = ref.double().cpu().numpy() @ Wx.astype(np.float64).T
     assert_rel(x_dbl.cpu().numpy(), xd_ref, 1e-5, "x_dbl")
+
+
+def _conv_sweep(n=20, seed=77):
+    rng = np.random.default_rng(seed)
+    return [(int(rng.integers(1, 4)), int(rng.choice([1, 3, 4, 63, 64, 130, 257])),
+             int(rng.choice([1, 2, 15, 16, 17, 33, 80])), int(rng.integers(2, 9)), str(rng.choice(["cm", "tm"])),
+             bool(rng.integers(0, 2)), 500 + i) for i in range(n)]
+
+
+@pytest.mark.parametrize("b,D,L,K,layout,with_state,seed", _conv_sweep())
+def test_conv_seeded_shape_sweep(b, D, L, K, layout, with_state, seed):
+    """Seeded sweep over widths 2..8, channel counts with and without
+    4-vector alignment, lengths around the 16-step run edge, both layouts:
+    fp32 vs the float64 oracle, final state exact."""
+    print(f"conv sweep b={b} D={D} L={L} K={K} {layout} state={with_state} seed={seed}", flush=True)
+    rng = np.random.default_rng(seed)
+    x = rng.standard_normal((b, D, L)).astype(np.float32)
+    w = rng.standard_normal((D, K)).astype(np.float32)
+    bias = rng.standard_normal(D).astype(np.float32)
+    st = rng.standard_normal((b, D, K - 1)).astype(np.float32) if with_state else None
+    X = _t(x) if layout == "cm" else _t(x.transpose(0, 2, 1)).transpose(1, 2)
+    out, fs = ops.causal_conv1d(X, _t(w), _t(bias), conv_state=_t(st) if st is not None else None, silu=True)
+    ref, ref_fs = om.causal_conv1d(x, w, bias, st, dtype=np.float64)
+    assert_rel(out.cpu().numpy(), om.silu(ref), 1e-4, "conv out")
+    assert np.array_equal(fs.cpu().numpy(), ref_fs.astype(np.float32))

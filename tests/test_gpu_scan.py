@@ -174,3 +174,27 @@ def test_zero_batch_and_zero_channels_are_no_ops():
         out, fs = ops.causal_conv1d(u, torch.randn(D, 4, device=DEV))
         assert out.shape == (b, D, 8) and fs.shape == (b, D, 3)
     torch.cuda.synchronize()
+
+
+def _sweep_cases(n=24, seed=2024):
+    rng = np.random.default_rng(seed)
+    cases = []
+    for i in range(n):
+        cases.append((int(rng.integers(1, 4)), int(rng.choice([1, 7, 63, 64, 65, 128, 190, 257])),
+                      int(rng.choice([1, 2, 15, 16, 17, 31, 32, 33, 64, 100])), int(rng.choice([1, 2, 4, 8, 12, 16, 32])),
+                      str(rng.choice(["cm", "tm"])), bool(rng.integers(0, 2)), 1000 + i))
+    return cases
+
+
+@pytest.mark.parametrize("b,D,L,N,layout,with_h0,seed", _sweep_cases())
+def test_scan_seeded_shape_sweep(b, D, L, N, layout, with_h0, seed):
+    """Seeded sweep over ragged channel counts (tail channel blocks), lengths
+    around the 16/32-step tile edges, state sizes 1..32, both layouts, with
+    and without a carried state: fp32 vs the float64 oracle at 1e-4."""
+    print(f"scan sweep b={b} D={D} L={L} N={N} {layout} h0={with_h0} seed={seed}", flush=True)
+    c = scan_case(np.random.default_rng(seed), b, D, L, N)
+    h0 = np.random.default_rng(seed + 1).standard_normal((b, D, N)).astype(np.float32) if with_h0 else None
+    y, h = _run(c, layout, h0=h0)
+    y_ref, h_ref = _ref(c, h0=h0)
+    assert_rel(y, y_ref, 1e-4, "y")
+    assert_rel(h, h_ref, 1e-4, "h")
