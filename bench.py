@@ -330,8 +330,12 @@ def bench_shard(dev, iters=10):
     b, L, D, N, R = 32, 2048, 2048, 16, 128
     g = torch.Generator(device=dev).manual_seed(5)
     bf = torch.bfloat16
-    xz = torch.randn(b, L, 2 * D, device=dev, generator=g).to(bf)
-    xdbl = torch.randn(b, L, R + 2 * N, device=dev, generator=g).to(bf)
+    # the layouts MambaMixer.prefill produces: x and z as separate token-major
+    # [b, l, D] in_proj outputs, B and C as separate [b, l, N] x_proj outputs
+    xin = torch.randn(b, L, D, device=dev, generator=g).to(bf)
+    zin = torch.randn(b, L, D, device=dev, generator=g).to(bf)
+    Bin = torch.randn(b, L, N, device=dev, generator=g).to(bf)
+    Cin = torch.randn(b, L, N, device=dev, generator=g).to(bf)
     delta = (0.5 * torch.randn(b, L, D, device=dev, generator=g)).to(bf)
     bias = torch.from_numpy(dt_bias_init(D, 5)).to(dev)
     w = torch.randn(D, 4, device=dev, generator=g) * 0.5
@@ -342,8 +346,8 @@ def bench_shard(dev, iters=10):
     y = torch.empty(b, L, D, device=dev, dtype=bf)
     fs = torch.empty(b, D, 3, device=dev, dtype=bf)
     h = torch.empty(b, D, N, device=dev)
-    xs, z = xz[..., :D].transpose(1, 2), xz[..., D:].transpose(1, 2)
-    Bv, Cv = xdbl[..., R:R + N].transpose(1, 2), xdbl[..., R + N:].transpose(1, 2)
+    xs, z = xin.transpose(1, 2), zin.transpose(1, 2)
+    Bv, Cv = Bin.transpose(1, 2), Cin.transpose(1, 2)
     conv = lambda: ops.causal_conv1d(xs, w, cb, out=u.transpose(1, 2), final_state=fs)
     scan = lambda: ops.selective_scan(u.transpose(1, 2), delta.transpose(1, 2), A_log, Bv, Cv, D=Dv, z=z,
                                       delta_bias=bias, a_is_log=True, y=y.transpose(1, 2), h_out=h)
@@ -357,7 +361,7 @@ def bench_shard(dev, iters=10):
         cref = F.silu(F.conv1d(xr[None], w[sl][:, None, :], cb[sl], groups=64)[0])
         e_conv = float(((u[0, :, sl].float().T - cref).abs().max() / cref.abs().max()).item())
         yr = _torch_scan_ref(u[0, :, sl].float().T, delta[0, :, sl].float().T, -torch.exp(A_log[sl]),
-                             xdbl[0, :, R:R + N].float(), xdbl[0, :, R + N:].float(), Dv[sl], z[0, sl].float(),
+                             Bv[0].float().T.contiguous(), Cv[0].float().T.contiguous(), Dv[sl], z[0, sl].float(),
                              bias[sl])
         e_scan = float(((y[0, :, sl].float().T - yr).abs().max() / yr.abs().max()).item())
     conv_bytes = 2 * b * L * D * 2 + b * D * 3 * 2 + D * 4 * 4 + D * 4   # x, u; final state out; w, bias

@@ -334,8 +334,24 @@ __global__ void __launch_bounds__(NW * 64, CM ? 3 : 4) scan_fwd_kernel(const Sca
     // staged keeps the next tile in flight across two sub-tile scans within
     // the 3-waves-per-SIMD register budget.
     const int nfull = L / LT;
+    // Issue priority falls as the sequence progresses (levels change at 1/2,
+    // 3/4 and 7/8 of the load tiles).  The SIMDs issue oldest-wave-first, so
+    // without this the first workgroup resident on a CU runs far ahead and
+    // the last one finishes alone at low occupancy; with it, a workgroup
+    // that got ahead yields its issue slots to the ones behind it on the same
+    // CU at each level change, and the final level (where the spread builds
+    // up again) is only an eighth of the sequence.
+    auto set_prio = [&](int i) {
+        const int n8 = 8 * i, nf = max(nfull, 1);
+        const int lvl = n8 < 4 * nf ? 0 : n8 < 6 * nf ? 1 : n8 < 7 * nf ? 2 : 3;
+        if (lvl == 0) __builtin_amdgcn_s_setprio(3);
+        else if (lvl == 1) __builtin_amdgcn_s_setprio(2);
+        else if (lvl == 2) __builtin_amdgcn_s_setprio(1);
+        else __builtin_amdgcn_s_setprio(0);
+    };
     if constexpr (KC == 1) {
         auto run_full = [&](Raw& r, int i) {
+            set_prio(i);
             run_subtiles(r, i * LT, Full<true>{},
                          [&]() { load_tile(r, min(i + 2, nfull - 1) * LT, Full<true>{}); });
         };
@@ -349,9 +365,11 @@ __global__ void __launch_bounds__(NW * 64, CM ? 3 : 4) scan_fwd_kernel(const Sca
         if (i < nfull) run_full(r0, i);
     } else {
         if (nfull > 0) load_tile(r0, 0, Full<true>{});
-        for (int i = 0; i < nfull; ++i)
+        for (int i = 0; i < nfull; ++i) {
+            set_prio(i);
             run_subtiles(r0, i * LT, Full<true>{},
                          [&]() { load_tile(r0, min(i + 1, nfull - 1) * LT, Full<true>{}); });
+        }
     }
     if (nfull * LT < L) {  // the partial last load tile, outside the pipeline
         const int tb = nfull * LT;

@@ -118,6 +118,14 @@ class MambaCache:
         ])
 
 
+# Prefill runs in_proj and x_proj as separate GEMMs (x / z halves; dt_low / B /
+# C) once a call holds this many tokens: the scan then reads contiguous z rows
+# and contiguous [b, l, N] B and C instead of strided slices.  Below it the
+# extra GEMM launches cost more than the scan gains, so the fused projections
+# are kept and the scan reads the slices through their strides.
+SPLIT_PROJ_MIN_TOKENS = 16384
+
+
 def _f32(t: torch.Tensor | None) -> torch.Tensor | None:
     if t is None:
         return None
@@ -187,9 +195,17 @@ class MambaMixer(nn.Module):
             if tuple(out.ssm_state.shape) != (b, Dm, N) or out.ssm_state.dtype != torch.float32 or \
                     not out.ssm_state.is_contiguous():
                 raise ValueError(f"out.ssm_state must be contiguous float32 {(b, Dm, N)}")
-        xz = self.in_proj(x)                                     # [b, l, 2D]
-        xs = xz[..., :Dm].transpose(1, 2)                        # [b, D, l] view, D-stride 1
-        z = xz[..., Dm:].transpose(1, 2)
+        split = b * l >= SPLIT_PROJ_MIN_TOKENS
+        if split:
+            # in_proj as two GEMMs (x rows, z rows) so the conv and the scan read
+            # whole contiguous [b, l, D] rows rather than halves of [b, l, 2D] rows
+            w_in, b_in = self.in_proj.weight, self.in_proj.bias
+            xs = F.linear(x, w_in[:Dm], b_in[:Dm] if b_in is not None else None).transpose(1, 2)   # [b, D, l]
+            z = F.linear(x, w_in[Dm:], b_in[Dm:] if b_in is not None else None).transpose(1, 2)
+        else:
+            xz = self.in_proj(x)                                 # [b, l, 2D]
+            xs = xz[..., :Dm].transpose(1, 2)                    # [b, D, l] view, D-stride 1
+            z = xz[..., Dm:].transpose(1, 2)
         conv_in_state = cache.conv_state if cache is not None else None
         if conv_in_state is not None and conv_in_state.dtype != x.dtype:
             conv_in_state = conv_in_state.to(x.dtype)
@@ -201,10 +217,19 @@ class MambaMixer(nn.Module):
         u, conv_state = ops.causal_conv1d(xs, self._conv_w(), _f32(self.conv1d.bias), conv_state=conv_in_state,
                                           silu=True, out=u_store.transpose(1, 2),
                                           final_state=out.conv_state if out is not None else None)
-        x_dbl = F.linear(u_store, self.x_proj.weight)            # [b, l, R+2N]
-        dt = F.linear(x_dbl[..., :R], self.dt_proj.weight)        # [b, l, D]; bias fused in the scan
-        B = x_dbl[..., R:R + N].transpose(1, 2)                   # [b, N, l] view
-        C = x_dbl[..., R + N:].transpose(1, 2)
+        w_x = self.x_proj.weight
+        if split:
+            # x_proj as three GEMMs (dt_low, B, C), so B and C are each contiguous
+            # [b, l, N]: a scan tile's 16 steps of one of them are one 16N-element run
+            dt_low = F.linear(u_store, w_x[:R])                   # [b, l, R]
+            B = F.linear(u_store, w_x[R:R + N]).transpose(1, 2)   # [b, N, l] view, N-stride 1
+            C = F.linear(u_store, w_x[R + N:]).transpose(1, 2)
+        else:
+            x_dbl = F.linear(u_store, w_x)                        # [b, l, R+2N]
+            dt_low = x_dbl[..., :R]
+            B = x_dbl[..., R:R + N].transpose(1, 2)               # [b, N, l] view, row stride R+2N
+            C = x_dbl[..., R + N:].transpose(1, 2)
+        dt = F.linear(dt_low, self.dt_proj.weight)                # [b, l, D]; bias fused in the scan
         h0 = None
         if cache is not None:
             h0 = cache.ssm_state.float().contiguous()

@@ -56,8 +56,14 @@ def small_mixer():
     return m.to(DEV).eval()
 
 
+@pytest.mark.parametrize("split", [False, True])
 @pytest.mark.parametrize("bias", [False, True])
-def test_mixer_prefill_vs_oracle(bias):
+def test_mixer_prefill_vs_oracle(bias, split, monkeypatch):
+    """Both projection layouts: fused in_proj / x_proj with strided z, B, C
+    views, and (forced here at a small size) the split GEMMs that give
+    contiguous z, B, C."""
+    import mamba_lite.model as mm
+    monkeypatch.setattr(mm, "SPLIT_PROJ_MIN_TOKENS", 0 if split else 1 << 40)
     torch.manual_seed(1)
     cfg = MambaConfig(d_model=64, n_layer=1, vocab_size=100, d_state=16, bias=bias)
     m = MambaMixer(cfg, 0)
@@ -199,9 +205,12 @@ def test_graph_replay_bit_identical_to_eager(small_lm, batch):
         assert torch.equal(le.ssm_state, lg.ssm_state) and torch.equal(le.conv_state, lg.conv_state)
 
 
-def test_bf16_mixer_shard_shape():
+@pytest.mark.parametrize("split", [False, True])
+def test_bf16_mixer_shard_shape(split, monkeypatch):
     """bf16 activations, fp32 scan state, through conv + scan + gate at a
     reduced TP-rank shard shape; vs the oracle on bf16-rounded mixer inputs."""
+    import mamba_lite.model as mm
+    monkeypatch.setattr(mm, "SPLIT_PROJ_MIN_TOKENS", 0 if split else 1 << 40)
     torch.manual_seed(4)
     cfg = MambaConfig(d_model=128, n_layer=1, vocab_size=100, d_state=16)
     m = MambaMixer(cfg, 0)
