@@ -58,12 +58,16 @@ __device__ __forceinline__ float fast_exp(float x) { return __builtin_amdgcn_exp
 // For e = exp(x) < 1/32 log1p(e) is the alternating series to e^4 (relative
 // truncation error < e^4/5 < 2e-7); above it log2(1 + e) * ln2, where
 // 1 + e >= 1.03 keeps the hardware log's error relative to the result small.
+// The exponent is clamped at 20; above 20 the result is x, taken by the
+// final max since log1p(exp(20)) rounds to 20 in fp32 and log1p(exp(x)) >= x
+// below it.  Clamp and max are med3s: one instruction each, with no NaN
+// quieting step in front as fminf/fmaxf have.
 __device__ __forceinline__ float softplus_f(float x) {
-    const float e = fast_exp(fminf(x, 20.f));
+    const float e = fast_exp(__builtin_amdgcn_fmed3f(x, -1.0e30f, 20.f));
     const float series = e * (1.f - e * (0.5f - e * (0.33333334f - e * 0.25f)));
     const float viaLog = __builtin_amdgcn_logf(1.f + e) * kLn2;
     const float r = e < 0.03125f ? series : viaLog;
-    return x > 20.f ? x : r;
+    return __builtin_amdgcn_fmed3f(x, r, 3.0e38f);
 }
 
 // x * sigmoid(x)
