@@ -87,6 +87,42 @@ __device__ __forceinline__ void store_run(T* p, const float* v) {
 
 template <bool B> using Full = std::integral_constant<bool, B>;
 
+// p + off bytes, for a wavefront-uniform p and a 32-bit per-lane offset: the
+// load then takes the base from SGPRs and only the offset from a VGPR, with
+// no 64-bit address arithmetic on the VALU.
+template <typename T>
+__device__ __forceinline__ T* at_bytes(T* p, uint32_t off) {
+    using C = typename std::conditional<std::is_const<T>::value, const char, char>::type;
+    return reinterpret_cast<T*>(reinterpret_cast<C*>(p) + off);
+}
+
+// Token-major rows through buffer instructions: a resource (SGPRs) based at
+// the first row of a thread's run of steps, the lane's channel as the VGPR
+// byte offset and the step within the run as the SGPR offset -- no VALU
+// address arithmetic at all.  The resource's range covers exactly the run's
+// rows, so an access outside them reads 0 / is dropped instead of faulting.
+constexpr int kBufWord3 = 0x00020000;   // raw (untyped) 32-bit data format
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t row_rsrc(const void* p, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, kBufWord3);
+}
+template <typename T> struct BufAct;
+template <> struct BufAct<float> {
+    __device__ __forceinline__ static float load(__amdgpu_buffer_rsrc_t r, uint32_t vo, uint32_t so) {
+        return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, (int)vo, (int)so, 0));
+    }
+    __device__ __forceinline__ static void store(__amdgpu_buffer_rsrc_t r, uint32_t vo, uint32_t so, float v) {
+        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), r, (int)vo, (int)so, 0);
+    }
+};
+template <> struct BufAct<uint16_t> {
+    __device__ __forceinline__ static float load(__amdgpu_buffer_rsrc_t r, uint32_t vo, uint32_t so) {
+        return bf16_to_f32(__builtin_amdgcn_raw_buffer_load_b16(r, (int)vo, (int)so, 0));
+    }
+    __device__ __forceinline__ static void store(__amdgpu_buffer_rsrc_t r, uint32_t vo, uint32_t so, float v) {
+        __builtin_amdgcn_raw_buffer_store_b16(f32_to_bf16(v), r, (int)vo, (int)so, 0);
+    }
+};
+
 // NW wavefronts per workgroup = NW state groups of SPW states over the same
 // 64 channels.  CM: channel-major [b,D,l] rows (l-stride 1); otherwise
 // token-major (D-stride 1).  VEC: CM rows are aligned for vector access.
@@ -147,6 +183,24 @@ __global__ void __launch_bounds__(NW * 64, CM ? 3 : 4) scan_fwd_kernel(const Sca
     const T* __restrict__ Bp = static_cast<const T*>(a.B) + b * a.B_sb;
     const T* __restrict__ Cp = static_cast<const T*>(a.C) + b * a.C_sb;
     const bool bc_t_fast = a.B_sl == 1;
+    // token-major rows: the step's row start is uniform per wavefront (SGPRs),
+    // the lane's channel is a byte offset into it
+    const T* __restrict__ ub = static_cast<const T*>(a.u) + b * a.u_sb;
+    const T* __restrict__ db = static_cast<const T*>(a.delta) + b * a.d_sb;
+    const T* __restrict__ zb = has_z ? static_cast<const T*>(a.z) + b * a.z_sb : ub;
+    T* __restrict__ yb = static_cast<T*>(a.y) + b * a.y_sb;
+    const uint32_t ch_bytes = (uint32_t)cl * (uint32_t)sizeof(T);
+    const int ot_u = CM ? 0 : __builtin_amdgcn_readfirstlane(ot);   // token-major: ot = wave * E
+    // step strides and the byte span of E consecutive rows (host-checked < 2^31)
+    const uint32_t sl_bytes_u = (uint32_t)(a.u_sl * (int64_t)sizeof(T));
+    const uint32_t sl_bytes_d = (uint32_t)(a.d_sl * (int64_t)sizeof(T));
+    const uint32_t sl_bytes_z = (uint32_t)(z_sl * (int64_t)sizeof(T));
+    const uint32_t sl_bytes_y = (uint32_t)(a.y_sl * (int64_t)sizeof(T));
+    const uint32_t row_bytes = (uint32_t)D * (uint32_t)sizeof(T);
+    const uint32_t run_bytes_u = (E - 1) * sl_bytes_u + row_bytes;
+    const uint32_t run_bytes_d = (E - 1) * sl_bytes_d + row_bytes;
+    const uint32_t run_bytes_z = (E - 1) * sl_bytes_z + row_bytes;
+    const uint32_t run_bytes_y = (E - 1) * sl_bytes_y + row_bytes;
 
     const float bias_c = a.dbias ? a.dbias[cl] : 0.f;
     const float D_c = a.Dv ? a.Dv[cl] : 0.f;
@@ -179,6 +233,7 @@ __global__ void __launch_bounds__(NW * 64, CM ? 3 : 4) scan_fwd_kernel(const Sca
     // flight across the scan (a select right after a load would force a wait
     // for every outstanding load).
     int bc_off[BCE], bc_t[BCE], bc_slot[BCE];
+    uint32_t b_bytes[BCE], c_bytes[BCE];     // element (state, step) of a full tile, from the tile's row
     bool bc_ok[BCE];
 #pragma unroll
     for (int k = 0; k < BCE; ++k) {
@@ -189,6 +244,8 @@ __global__ void __launch_bounds__(NW * 64, CM ? 3 : 4) scan_fwd_kernel(const Sca
         bc_t[k] = min(t, LT - 1);
         bc_off[k] = min(n, N - 1);
         bc_slot[k] = (e < NP * LT) ? bc_t[k] * BS + n : -1;
+        b_bytes[k] = (uint32_t)((bc_off[k] * a.B_sn + bc_t[k] * a.B_sl) * (int64_t)sizeof(T));
+        c_bytes[k] = (uint32_t)((bc_off[k] * a.C_sn + bc_t[k] * a.C_sl) * (int64_t)sizeof(T));
     }
 
     auto load_tile = [&](Raw& r, int tb, auto full) {
@@ -200,22 +257,46 @@ __global__ void __launch_bounds__(NW * 64, CM ? 3 : 4) scan_fwd_kernel(const Sca
                 load_run<T, E, VEC>(up + t0, r.u[kc]);
                 load_run<T, E, VEC>(dp + t0, r.d[kc]);
                 load_run<T, E, VEC>(zp + t0, r.z[kc]);
-            } else {
-                const int64_t su = CM ? 1 : a.u_sl, sd = CM ? 1 : a.d_sl, sz = CM ? 1 : z_sl;
+            } else if constexpr (CM) {
 #pragma unroll
                 for (int j = 0; j < E; ++j) {
                     const int t = F ? t0 + j : min(t0 + j, L - 1);
-                    r.u[kc][j] = Act<T>::load(up + t * su);
-                    r.d[kc][j] = Act<T>::load(dp + t * sd);
-                    r.z[kc][j] = Act<T>::load(zp + t * sz);
+                    r.u[kc][j] = Act<T>::load(up + t);
+                    r.d[kc][j] = Act<T>::load(dp + t);
+                    r.z[kc][j] = Act<T>::load(zp + t);
+                }
+            } else {
+                // token-major: one buffer resource per tensor over the E rows of
+                // this thread's run; step j is an SGPR offset
+                const int tw = tb + kc * TT + ot_u;
+                const int t0c = F ? tw : min(tw, L - 1);
+                const auto ru = row_rsrc(ub + (int64_t)t0c * a.u_sl, run_bytes_u);
+                const auto rd = row_rsrc(db + (int64_t)t0c * a.d_sl, run_bytes_d);
+                const auto rz = row_rsrc(zb + (int64_t)t0c * z_sl, run_bytes_z);
+#pragma unroll
+                for (int j = 0; j < E; ++j) {
+                    const uint32_t dj = (uint32_t)((F ? tw + j : min(tw + j, L - 1)) - t0c);
+                    r.u[kc][j] = BufAct<T>::load(ru, ch_bytes, dj * sl_bytes_u);
+                    r.d[kc][j] = BufAct<T>::load(rd, ch_bytes, dj * sl_bytes_d);
+                    r.z[kc][j] = BufAct<T>::load(rz, ch_bytes, dj * sl_bytes_z);
                 }
             }
         }
+        if constexpr (F) {
+            const T* Bt = Bp + (int64_t)tb * a.B_sl;
+            const T* Ct = Cp + (int64_t)tb * a.C_sl;
 #pragma unroll
-        for (int k = 0; k < BCE; ++k) {
-            const int t = F ? tb + bc_t[k] : min(tb + bc_t[k], L - 1);
-            r.B[k] = Act<T>::load(Bp + bc_off[k] * a.B_sn + (int64_t)t * a.B_sl);
-            r.C[k] = Act<T>::load(Cp + bc_off[k] * a.C_sn + (int64_t)t * a.C_sl);
+            for (int k = 0; k < BCE; ++k) {
+                r.B[k] = Act<T>::load(at_bytes(Bt, b_bytes[k]));
+                r.C[k] = Act<T>::load(at_bytes(Ct, c_bytes[k]));
+            }
+        } else {
+#pragma unroll
+            for (int k = 0; k < BCE; ++k) {
+                const int t = min(tb + bc_t[k], L - 1);
+                r.B[k] = Act<T>::load(Bp + bc_off[k] * a.B_sn + (int64_t)t * a.B_sl);
+                r.C[k] = Act<T>::load(Cp + bc_off[k] * a.C_sn + (int64_t)t * a.C_sl);
+            }
         }
     };
 
@@ -304,11 +385,18 @@ __global__ void __launch_bounds__(NW * 64, CM ? 3 : 4) scan_fwd_kernel(const Sca
             const int t0 = tb + k2 * TT + ot;
             if constexpr (CM && F) {
                 store_run<T, E, VEC>(yp + t0, yout[k2]);
-            } else {
-                const int64_t sy = CM ? 1 : a.y_sl;
+            } else if constexpr (CM) {
 #pragma unroll
                 for (int j = 0; j < E; ++j)
-                    if (F || t0 + j < L) Act<T>::store(yp + (int64_t)(t0 + j) * sy, yout[k2][j]);
+                    if (F || t0 + j < L) Act<T>::store(yp + t0 + j, yout[k2][j]);
+            } else {
+                const int tw = tb + k2 * TT + ot_u;
+                if (F || tw < L) {
+                    const auto ry = row_rsrc(yb + (int64_t)tw * a.y_sl, run_bytes_y);
+#pragma unroll
+                    for (int j = 0; j < E; ++j)
+                        if (F || tw + j < L) BufAct<T>::store(ry, ch_bytes, (uint32_t)j * sl_bytes_y, yout[k2][j]);
+                }
             }
         }
     };
@@ -447,6 +535,24 @@ extern "C" int mtl_selective_scan_fwd(const mtl_scan_params* p, mtl_stream_t str
     a.y_sb = p->y_sb; a.y_sd = p->y_sd; a.y_sl = p->y_sl;
     a.L = (int)p->seqlen; a.D = (int)p->dim; a.N = (int)p->dstate;
     a.softplus = p->delta_softplus; a.a_is_log = p->a_is_log;
+    // B/C element offsets within a load tile and token-major channel offsets
+    // are 32-bit byte offsets (non-negative strides, spans under 4 GiB)
+    MTL_REQUIRE(p->B_sn >= 0 && p->B_sl >= 0 && p->C_sn >= 0 && p->C_sl >= 0, "negative B/C stride");
+    {
+        const int64_t es = p->dtype == MTL_F32 ? 4 : 2, lt = std::min<int64_t>(32, std::max<int64_t>(p->seqlen, 1));
+        const int64_t span_b = ((p->dstate - 1) * p->B_sn + (lt - 1) * p->B_sl + 1) * es;
+        const int64_t span_c = ((p->dstate - 1) * p->C_sn + (lt - 1) * p->C_sl + 1) * es;
+        MTL_REQUIRE(span_b < (int64_t(1) << 32) && span_c < (int64_t(1) << 32), "B/C strides too large");
+        MTL_REQUIRE(p->dim * es < (int64_t(1) << 32), "dim too large");
+        // token-major runs are addressed through buffer resources spanning
+        // (run - 1) row strides + one row (the run is at most 8 steps)
+        if (!(p->u_sl == 1 && p->delta_sl == 1 && p->y_sl == 1) && p->seqlen > 1) {
+            const int64_t sl_max = std::max({p->u_sl, p->delta_sl, p->y_sl, p->z ? p->z_sl : p->u_sl});
+            MTL_REQUIRE(p->u_sl >= 0 && p->delta_sl >= 0 && p->y_sl >= 0 && (!p->z || p->z_sl >= 0),
+                        "negative step stride");
+            MTL_REQUIRE((7 * sl_max + p->dim) * es < (int64_t(1) << 31), "token-major step stride too large");
+        }
+    }
 
     hipStream_t st = as_stream(stream);
     // seqlen <= 1 has no meaningful l-stride; the channel-major path handles it.
