@@ -33,12 +33,15 @@ constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
 
 // bf16 <-> fp32 (round to nearest even, NaN kept quiet)
+// fp32 -> bf16 is gfx950's v_cvt_pk_bf16_f32 (round to nearest even; a pair
+// per instruction where two values convert together).
 __device__ __forceinline__ float bf16_to_f32(uint16_t v) { return __uint_as_float(uint32_t(v) << 16); }
-__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
-    uint32_t u = __float_as_uint(f);
-    if ((u & 0x7fffffffu) > 0x7f800000u) return uint16_t((u >> 16) | 0x40u);
-    u += 0x7fffu + ((u >> 16) & 1u);
-    return uint16_t(u >> 16);
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) { return __builtin_bit_cast(uint16_t, (__bf16)f); }
+__device__ __forceinline__ uint32_t f32x2_to_bf16x2(float lo, float hi) {
+    typedef float F2 __attribute__((ext_vector_type(2)));
+    typedef __bf16 B2 __attribute__((ext_vector_type(2)));
+    const F2 v = {lo, hi};
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, B2));
 }
 
 template <typename T> struct Act;

@@ -59,8 +59,8 @@ template <> struct Vec<uint16_t, 4> {
     }
     __device__ __forceinline__ static void store(uint16_t* p, const float* v) {
         uint2 x;
-        x.x = (uint32_t)f32_to_bf16(v[0]) | ((uint32_t)f32_to_bf16(v[1]) << 16);
-        x.y = (uint32_t)f32_to_bf16(v[2]) | ((uint32_t)f32_to_bf16(v[3]) << 16);
+        x.x = f32x2_to_bf16x2(v[0], v[1]);
+        x.y = f32x2_to_bf16x2(v[2], v[3]);
         *reinterpret_cast<uint2*>(p) = x;
     }
 };

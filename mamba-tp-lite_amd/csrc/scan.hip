@@ -75,8 +75,8 @@ __device__ __forceinline__ void store_run(T* p, const float* v) {
 #pragma unroll
         for (int q = 0; q < E / 4; ++q) {
             uint2 x;
-            x.x = uint32_t(f32_to_bf16(v[4 * q])) | (uint32_t(f32_to_bf16(v[4 * q + 1])) << 16);
-            x.y = uint32_t(f32_to_bf16(v[4 * q + 2])) | (uint32_t(f32_to_bf16(v[4 * q + 3])) << 16);
+            x.x = f32x2_to_bf16x2(v[4 * q], v[4 * q + 1]);
+            x.y = f32x2_to_bf16x2(v[4 * q + 2], v[4 * q + 3]);
             reinterpret_cast<uint2*>(p)[q] = x;
         }
     } else {
