@@ -124,3 +124,31 @@ def test_entry_points_validate_sizes_on_the_host(case):
         rc = lib.mtl_conv_step(P, P, 64, P, None, P, 64, 1, 64, a["width"], 0, 1, None)
     assert rc == 1, (name, over)
     assert msg in lib.mtl_last_error(), lib.mtl_last_error()
+
+
+@pytest.mark.parametrize("over,msg", [
+    (dict(B_sn=-1), b"negative B/C stride"),
+    (dict(C_sl=1 << 30), b"B/C strides too large"),
+    (dict(u_sl=1 << 28, delta_sl=1 << 28, y_sl=1 << 28), b"token-major step stride too large"),
+])
+def test_scan_rejects_strides_outside_its_32_bit_offsets(over, msg):
+    """The scan addresses B/C tiles and token-major rows with 32-bit byte
+    offsets from a uniform base; strides that would overflow them, or point
+    backwards, are refused on the host (pointers are placeholders)."""
+    from mamba_lite import _lib
+
+    lib = _lib.load()
+    b, L, D, N = 2, 64, 64, 16
+    p = _lib.ScanParams()
+    P = 16
+    p.u = p.delta = p.z = p.B = p.C = p.y = P
+    p.A = P
+    for t in ("u", "delta", "z", "y"):        # token-major [b, l, D]
+        setattr(p, f"{t}_sb", L * D); setattr(p, f"{t}_sd", 1); setattr(p, f"{t}_sl", D)
+    for t in ("B", "C"):                       # [b, l, N] viewed as [b, N, l]
+        setattr(p, f"{t}_sb", L * N); setattr(p, f"{t}_sn", 1); setattr(p, f"{t}_sl", N)
+    p.batch, p.seqlen, p.dim, p.dstate, p.dtype = b, L, D, N, 0
+    for k, v in over.items():
+        setattr(p, k, v)
+    assert lib.mtl_selective_scan_fwd(ctypes.byref(p), None) == 1
+    assert msg in lib.mtl_last_error(), lib.mtl_last_error()
