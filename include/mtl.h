@@ -59,7 +59,10 @@ int mtl_abi_version(void);
  * stride pattern is rejected.  B, C: [b, N, l] with strides (sb, sn, sl).
  * h0 (nullable) and h_out (nullable): contiguous fp32 [b, D, N]; h_out may
  * be h0 (a state is read before it is overwritten, by the same thread).
- * Limits: 1 <= N <= 32, l >= 0.
+ * Limits: 1 <= N <= 32, l >= 0; B/C strides non-negative with
+ * ((N-1)*sn + 31*sl + 1) elements under 4 GiB; token-major step strides
+ * non-negative with (7*sl + D) elements under 2 GiB (the kernel addresses
+ * these spans with 32-bit offsets from a uniform base).
  * ---------------------------------------------------------------------- */
 typedef struct {
     const void* u;     int64_t u_sb, u_sd, u_sl;
