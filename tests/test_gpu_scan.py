@@ -198,3 +198,24 @@ def test_scan_seeded_shape_sweep(b, D, L, N, layout, with_h0, seed):
     y_ref, h_ref = _ref(c, h0=h0)
     assert_rel(y, y_ref, 1e-4, "y")
     assert_rel(h, h_ref, 1e-4, "h")
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_scan_generic_bc_strides(dtype):
+    """B and C with no unit stride at all (every other step of a wider
+    buffer, state stride 3): the scan's generic B/C staging path, against the
+    oracle on the same values."""
+    b, D, L, N = 2, 96, 45, 16
+    c = scan_case(np.random.default_rng(31), b, D, L, N)
+    bigB = torch.zeros(b, 3 * N, 2 * L, device=DEV, dtype=dtype)
+    bigC = torch.zeros(b, 3 * N, 2 * L, device=DEV, dtype=dtype)
+    Bv, Cv = bigB[:, ::3, ::2], bigC[:, ::3, ::2]
+    Bv.copy_(_t(c["B"], dtype)); Cv.copy_(_t(c["C"], dtype))
+    assert Bv.stride(1) != 1 and Bv.stride(2) != 1
+    y, h = ops.selective_scan(_t(c["u"], dtype), _t(c["delta"], dtype), _t(c["A"]), Bv, Cv, D=_t(c["D"]),
+                              z=_t(c["z"], dtype), delta_bias=_t(c["delta_bias"]))
+    torch.cuda.synchronize()
+    tol = 1e-4 if dtype == torch.float32 else 1e-2
+    y_ref, h_ref = _ref(c, round_bf16=dtype == torch.bfloat16)
+    assert_rel(y.float().cpu().numpy(), y_ref, tol, "y")
+    assert_rel(h.cpu().numpy(), h_ref, tol, "h")
