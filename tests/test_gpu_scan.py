@@ -219,3 +219,28 @@ def test_scan_generic_bc_strides(dtype):
     y_ref, h_ref = _ref(c, round_bf16=dtype == torch.bfloat16)
     assert_rel(y.float().cpu().numpy(), y_ref, tol, "y")
     assert_rel(h.cpu().numpy(), h_ref, tol, "h")
+
+
+def test_scan_nan_delta_skips_the_step():
+    """A NaN in delta + dt_bias gives dt = 0 in the fused softplus (its med3
+    selects return the non-NaN operand): that step leaves the state unchanged,
+    exactly as a very negative delta does, and other channels are untouched.
+    torch's softplus would propagate the NaN instead; this pins the
+    documented deviation."""
+    b, D, L, N = 1, 64, 8, 16
+    g = torch.Generator(device=DEV).manual_seed(0)
+    u = torch.randn(b, D, L, device=DEV, generator=g)
+    d = torch.randn(b, D, L, device=DEV, generator=g) * 0.5
+    Bm = torch.randn(b, N, L, device=DEV, generator=g)
+    Cm = torch.randn(b, N, L, device=DEV, generator=g)
+    A = -torch.arange(1, N + 1, device=DEV, dtype=torch.float32).repeat(D, 1).contiguous()
+    bias = torch.full((D,), -3.0, device=DEV)
+    y0, _ = ops.selective_scan(u, d, A, Bm, Cm, delta_bias=bias)
+    dn, dz = d.clone(), d.clone()
+    dn[0, 5, 3], dz[0, 5, 3] = float("nan"), -1e4
+    yn, hn = ops.selective_scan(u, dn, A, Bm, Cm, delta_bias=bias)
+    yz, hz = ops.selective_scan(u, dz, A, Bm, Cm, delta_bias=bias)
+    torch.cuda.synchronize()
+    assert not torch.isnan(yn).any() and not torch.isnan(hn).any()
+    assert torch.equal(yn, yz) and torch.equal(hn, hz)
+    assert torch.equal(yn[0, :5], y0[0, :5])
