@@ -68,24 +68,33 @@ struct InArgs {
 };
 
 constexpr int kCB = 8;                             // channels per decode_in workgroup
-constexpr int kRowsPerWave = 2 * kCB / kWaves;     // in_proj rows per wavefront (x rows, then z rows)
+constexpr int kRowsPerWave = kCB / kWaves;         // in_proj rows per wavefront
 constexpr int kMaxConv = 8;                        // d_conv <= 8
 
 // PL = float4 runs per lane (M <= 256 * PL; lanes past M/4 in the last run
-// are masked).  Every wavefront: 4 in_proj rows.  Every thread: PL elements
+// are masked).  Every wavefront: 2 in_proj rows.  Every thread: PL elements
 // of each activation row and of the norm weights.
+//
+// The grid is two sets of nblk workgroups over the same channel blocks: the
+// first takes the x rows of in_proj (then the conv step and the x_proj
+// partials), the second the z rows (then SiLU(z)).  Halving the rows per
+// workgroup puts the weight stream on twice as many CUs, so more of it is in
+// flight at once.
 template <int B, int PL>
 __global__ void __launch_bounds__(kThreads) decode_in_kernel(const InArgs a) {
     constexpr int G = kRowsPerWave;
     extern __shared__ __align__(16) float s_xw[];  // [B][M]: norm_w * x (the rms scale is applied to the dots)
-    __shared__ float s_pre[2 * kCB][B];
+    __shared__ float s_pre[kCB][B];
     __shared__ float s_xc[kCB][B];
     __shared__ float s_red[B][kWaves];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int M = a.M, D = a.D, J = a.J, K = a.K;
     const int K4 = M >> 2;
-    const int c0 = blockIdx.x * kCB;
+    const int nblk = (D + kCB - 1) / kCB;
+    const bool zblk = (int)blockIdx.x >= nblk;     // uniform: this workgroup takes the z rows
+    const int blk = zblk ? (int)blockIdx.x - nblk : (int)blockIdx.x;
+    const int c0 = blk * kCB;
     const int nch = min(kCB, D - c0);
 
     // ---- 0. every independent load, in one batch
@@ -94,13 +103,11 @@ __global__ void __launch_bounds__(kThreads) decode_in_kernel(const InArgs a) {
     float bin[G];
 #pragma unroll
     for (int g = 0; g < G; ++g) {
-        const int i = wave * G + g;                // local row: x rows 0..kCB-1, then z rows
-        const bool is_z = i >= kCB;
-        const int ch = is_z ? i - kCB : i;
+        const int ch = wave * G + g;               // local row = channel of the block
         const bool ok = ch < nch;
-        const int64_t row = ok ? (is_z ? (int64_t)D + c0 + ch : (int64_t)c0 + ch) : (int64_t)c0;
+        const int64_t row = (zblk ? (int64_t)D : 0) + c0 + (ok ? ch : 0);
         rows[g] = a.W_in + row * M;
-        rloc[g] = ok ? i : -1;
+        rloc[g] = ok ? ch : -1;
         bin[g] = a.b_in ? a.b_in[row] : 0.f;
     }
     float4 w[G][PL];
@@ -196,14 +203,18 @@ __global__ void __launch_bounds__(kThreads) decode_in_kernel(const InArgs a) {
     if (lane == 0) {
 #pragma unroll
         for (int g = 0; g < G; ++g) {
-            if (rloc[g] < 0) continue;
+            if (rloc[g] < 0) continue;   // rows past d_inner
 #pragma unroll
             for (int bi = 0; bi < B; ++bi) s_pre[rloc[g]][bi] = fmaf(acc[g][bi], r[bi], bin[g]);
         }
     }
     __syncthreads();
 
-    // ---- 3. conv step (history shifted in place) + SiLU; SiLU(z)
+    // ---- 3. z blocks: SiLU(z); x blocks: conv step (history shifted in place) + SiLU
+    if (zblk) {
+        if (tid < npair) a.gz[(int64_t)cv_b * D + cv_c] = silu_f(s_pre[cv_ch][cv_b]);
+        return;
+    }
     if (tid < npair) {
         const float xin = s_pre[cv_ch][cv_b];
         float cacc = 0.f;
@@ -221,7 +232,6 @@ __global__ void __launch_bounds__(kThreads) decode_in_kernel(const InArgs a) {
         const float xcv = silu_f(cacc);
         s_xc[cv_ch][cv_b] = xcv;
         a.xc[(int64_t)cv_b * D + cv_c] = xcv;
-        a.gz[(int64_t)cv_b * D + cv_c] = silu_f(s_pre[kCB + cv_ch][cv_b]);
     }
     if (!a.W_xT) return;
     __syncthreads();
@@ -231,13 +241,13 @@ __global__ void __launch_bounds__(kThreads) decode_in_kernel(const InArgs a) {
         float xacc = 0.f;
 #pragma unroll
         for (int ch = 0; ch < kCB; ++ch) xacc = ch < nch ? fmaf(wx[ch], s_xc[ch][xp_b], xacc) : xacc;
-        a.xpart[((int64_t)blockIdx.x * B + xp_b) * J + xp_j] = xacc;
+        a.xpart[((int64_t)blk * B + xp_b) * J + xp_j] = xacc;
     }
     for (int t = tid + kThreads; t < J * B; t += kThreads) {   // pairs beyond the first 256
         const int j = t % J, bi = t / J;
         float xacc = 0.f;
         for (int ch = 0; ch < nch; ++ch) xacc = fmaf(a.W_xT[(int64_t)(c0 + ch) * J + j], s_xc[ch][bi], xacc);
-        a.xpart[((int64_t)blockIdx.x * B + bi) * J + j] = xacc;
+        a.xpart[((int64_t)blk * B + bi) * J + j] = xacc;
     }
 }
 
@@ -489,7 +499,7 @@ extern "C" int mtl_decode_in(const float* x, const float* emb, const int64_t* id
     MTL_REQUIRE(smem <= 60 * 1024, "batch * d_model too large for the decode LDS tile");
     InArgs a{x, emb, ids, resid_out, norm_w, W_in, b_in, conv_state, conv_w, conv_b, W_xT, xc, gz, xpart,
              d_model, d_inner, d_conv, xdbl_cols, eps};
-    const dim3 grid((unsigned)((d_inner + kCB - 1) / kCB));
+    const dim3 grid((unsigned)(2 * ((d_inner + kCB - 1) / kCB)));   // x-row blocks, then z-row blocks
     hipStream_t st = as_stream(stream);
     const int plv = round_runs((d_model / 4 + 63) / 64);
     MTL_DISPATCH_B(batch, MTL_DISPATCH_RUNS(PL, plv, hipLaunchKernelGGL((decode_in_kernel<B, PL>), grid, dim3(kThreads),
