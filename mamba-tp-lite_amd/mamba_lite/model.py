@@ -118,11 +118,11 @@ class MambaCache:
         ])
 
 
-# Prefill runs in_proj and x_proj as separate GEMMs (x / z halves; dt_low / B /
-# C) once a call holds this many tokens: the scan then reads contiguous z rows
-# and contiguous [b, l, N] B and C instead of strided slices.  Below it the
-# extra GEMM launches cost more than the scan gains, so the fused projections
-# are kept and the scan reads the slices through their strides.
+# Prefill runs in_proj as two GEMMs (x / z halves) and copies B and C out of
+# x_dbl once a call holds this many tokens: the scan then reads contiguous z
+# rows and contiguous [b, l, N] B and C instead of strided slices.  Below it
+# the extra launches cost more than the scan gains, so the fused projection
+# is kept and the scan reads the slices through their strides.
 SPLIT_PROJ_MIN_TOKENS = 16384
 
 
@@ -218,15 +218,15 @@ class MambaMixer(nn.Module):
                                           silu=True, out=u_store.transpose(1, 2),
                                           final_state=out.conv_state if out is not None else None)
         w_x = self.x_proj.weight
+        x_dbl = F.linear(u_store, w_x)                            # [b, l, R+2N]
+        dt_low = x_dbl[..., :R]
         if split:
-            # x_proj as three GEMMs (dt_low, B, C), so B and C are each contiguous
-            # [b, l, N]: a scan tile's 16 steps of one of them are one 16N-element run
-            dt_low = F.linear(u_store, w_x[:R])                   # [b, l, R]
-            B = F.linear(u_store, w_x[R:R + N]).transpose(1, 2)   # [b, N, l] view, N-stride 1
-            C = F.linear(u_store, w_x[R + N:]).transpose(1, 2)
+            # B and C copied out of x_dbl into contiguous [b, l, N] (2 * b*l*N
+            # elements, against re-reading u for two more GEMMs): a scan
+            # tile's 16 steps of one of them are then one 16N-element run
+            B = x_dbl[..., R:R + N].contiguous().transpose(1, 2)  # [b, N, l] view, N-stride 1
+            C = x_dbl[..., R + N:].contiguous().transpose(1, 2)
         else:
-            x_dbl = F.linear(u_store, w_x)                        # [b, l, R+2N]
-            dt_low = x_dbl[..., :R]
             B = x_dbl[..., R:R + N].transpose(1, 2)               # [b, N, l] view, row stride R+2N
             C = x_dbl[..., R + N:].transpose(1, 2)
         dt = F.linear(dt_low, self.dt_proj.weight)                # [b, l, D]; bias fused in the scan
