@@ -244,3 +244,42 @@ def test_scan_nan_delta_skips_the_step():
     assert not torch.isnan(yn).any() and not torch.isnan(hn).any()
     assert torch.equal(yn, yz) and torch.equal(hn, hz)
     assert torch.equal(yn[0, :5], y0[0, :5])
+
+
+def test_scan_shard_size_bf16_properties():
+    """One TP rank's shard at its real shape: bf16 u, delta, z [32, 2048, 2048]
+    token-major (as the mixer lays them out), B, C contiguous [32, 2048, 16],
+    fp32 state.  (1) continuation from the carried state reproduces the
+    one-pass scan bit for bit, (2) sampled channel blocks match the float64
+    oracle on the same bf16 values at 1e-2, (3) every output is finite."""
+    b, D, L, N = 32, 2048, 2048, 16
+    print(f"scan shard size bf16 b={b} D={D} L={L}", flush=True)
+    g = torch.Generator(device=DEV).manual_seed(1)
+    bf = torch.bfloat16
+    mk = lambda *s: torch.randn(*s, device=DEV, generator=g).to(bf)
+    u, z, Bin, Cin = mk(b, L, D), mk(b, L, D), mk(b, L, N), mk(b, L, N)
+    delta = (0.5 * torch.randn(b, L, D, device=DEV, generator=g)).to(bf)
+    rng = np.random.default_rng(6)
+    bias = _t(om.inv_softplus(np.exp(rng.uniform(np.log(1e-3), np.log(0.1), D))).astype(np.float32))
+    A_log = torch.log(torch.arange(1, N + 1, device=DEV, dtype=torch.float32)).repeat(D, 1).contiguous()
+    Dv = torch.ones(D, device=DEV)
+    tv = lambda t: t.transpose(1, 2)
+    y, h = ops.selective_scan(tv(u), tv(delta), A_log, tv(Bin), tv(Cin), D=Dv, z=tv(z), delta_bias=bias,
+                              a_is_log=True)
+    k = 1024
+    y1, h1 = ops.selective_scan(tv(u[:, :k]), tv(delta[:, :k]), A_log, tv(Bin[:, :k]), tv(Cin[:, :k]), D=Dv,
+                                z=tv(z[:, :k]), delta_bias=bias, a_is_log=True)
+    y2, h2 = ops.selective_scan(tv(u[:, k:]), tv(delta[:, k:]), A_log, tv(Bin[:, k:]), tv(Cin[:, k:]), D=Dv,
+                                z=tv(z[:, k:]), delta_bias=bias, h0=h1, a_is_log=True)
+    torch.cuda.synchronize()
+    assert torch.isfinite(y.float()).all() and torch.isfinite(h).all()
+    assert torch.equal(torch.cat([y1, y2], -1), y) and torch.equal(h2, h)
+    A = -np.exp(A_log.cpu().numpy())
+    for bi, c0 in ((0, 0), (13, 1024), (31, 1984)):
+        sl = slice(c0, c0 + 64)
+        f = lambda t: t[bi:bi + 1].float().cpu().numpy()
+        yr, hr = om.selective_scan_bnl(f(tv(u))[:, sl], f(tv(delta))[:, sl], A[sl], f(tv(Bin)), f(tv(Cin)),
+                                       Dv[sl].cpu().numpy(), f(tv(z))[:, sl], bias[sl].cpu().numpy(), None,
+                                       dtype=np.float64)
+        assert_rel(y[bi:bi + 1, sl].float().cpu().numpy(), yr, 1e-2, f"y b={bi} c0={c0}")
+        assert_rel(h[bi:bi + 1, sl].cpu().numpy(), hr, 1e-2, f"h b={bi} c0={c0}")
