@@ -271,3 +271,30 @@ def test_conv_seeded_shape_sweep(b, D, L, K, layout, with_state, seed):
     ref, ref_fs = om.causal_conv1d(x, w, bias, st, dtype=np.float64)
     assert_rel(out.cpu().numpy(), om.silu(ref), 1e-4, "conv out")
     assert np.array_equal(fs.cpu().numpy(), ref_fs.astype(np.float32))
+
+
+def test_conv_shard_size_bf16_properties():
+    """The conv at one TP rank's real shape: bf16 x [32, 2048, 2048] as the
+    x half of a token-major [b, l, 2D] in_proj output.  (1) two halves with
+    the carried history reproduce the one-pass output and final state bit for
+    bit, (2) sampled channel blocks match the oracle (pre-activation conv,
+    then SiLU) on the same bf16 values at 1e-2."""
+    b, D, L, K = 32, 2048, 2048, 4
+    print(f"conv shard size bf16 b={b} D={D} L={L}", flush=True)
+    g = torch.Generator(device=DEV).manual_seed(2)
+    xz = torch.randn(b, L, 2 * D, device=DEV, generator=g).to(torch.bfloat16)
+    x = xz[..., :D].transpose(1, 2)                     # [b, D, l] view, channel stride 1
+    w = torch.randn(D, K, device=DEV, generator=g) * 0.5
+    cb = torch.randn(D, device=DEV, generator=g) * 0.1
+    out, fs = ops.causal_conv1d(x, w, cb)
+    k = 1000
+    o1, s1 = ops.causal_conv1d(x[..., :k], w, cb)
+    o2, s2 = ops.causal_conv1d(x[..., k:], w, cb, conv_state=s1)
+    torch.cuda.synchronize()
+    assert torch.equal(torch.cat([o1, o2], -1), out) and torch.equal(s2, fs)
+    for bi, c0 in ((0, 0), (19, 1024), (31, 1984)):
+        sl = slice(c0, c0 + 64)
+        xr = x[bi:bi + 1, sl].float().cpu().numpy()
+        pre, st = om.causal_conv1d(xr, w[sl].cpu().numpy(), cb[sl].cpu().numpy(), None, dtype=np.float64)
+        assert_rel(out[bi:bi + 1, sl].float().cpu().numpy(), om.silu(pre), 1e-2, f"out b={bi} c0={c0}")
+        assert np.array_equal(fs[bi:bi + 1, sl].float().cpu().numpy(), st.astype(np.float32))
