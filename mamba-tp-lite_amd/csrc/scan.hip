@@ -155,8 +155,16 @@ __global__ void __launch_bounds__(NW * 64, CM ? 3 : 4) scan_fwd_kernel(const Sca
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
-    const int b = blockIdx.y;
-    const int c0 = blockIdx.x * 64;
+    // XCD-aware tile order: workgroups are dealt to the 8 XCDs round robin,
+    // so workgroup w takes tile (w % 8) * (tiles / 8) + w / 8.  Each XCD then
+    // works through whole batch rows, and a row's B/C tiles are fetched from
+    // HBM into one L2 instead of all eight (reads 1.08 -> 1.005x the
+    // algorithmic bytes at [32,1536,1024])
+    int wlin = blockIdx.y * gridDim.x + blockIdx.x;
+    const int wtot = gridDim.x * gridDim.y;
+    if (wtot % 8 == 0) wlin = (wlin % 8) * (wtot / 8) + wlin / 8;
+    const int b = wlin / gridDim.x;
+    const int c0 = (wlin - b * gridDim.x) * 64;
     const int L = a.L, D = a.D, N = a.N;
 
     // staging ownership: channel oc and, in sub-tile kc, steps
@@ -510,6 +518,7 @@ extern "C" int mtl_selective_scan_fwd(const mtl_scan_params* p, mtl_stream_t str
     MTL_REQUIRE(p->batch >= 0 && p->seqlen >= 0 && p->dim >= 0, "negative size");
     MTL_REQUIRE(p->dstate >= 1 && p->dstate <= 32, "dstate must be in [1, 32]");
     MTL_REQUIRE(p->batch <= 65535, "batch must be <= 65535");
+    MTL_REQUIRE(p->batch * ((p->dim + 63) / 64) < (int64_t(1) << 31), "batch * ceil(dim / 64) overflows int32");
     MTL_REQUIRE(p->seqlen < (int64_t(1) << 31) && p->dim < (int64_t(1) << 31), "size overflows int32");
     MTL_REQUIRE(p->dtype == MTL_F32 || p->dtype == MTL_BF16, "dtype must be MTL_F32 or MTL_BF16");
     if (p->batch == 0 || p->dim == 0) return MTL_OK;
