@@ -72,9 +72,19 @@ template <> struct Vec<uint16_t, 4> {
 template <typename T, int K, int VC, int TC>
 __global__ void __launch_bounds__(kConvThreads) conv_fwd_kernel(const ConvArgs a) {
     constexpr int W = TC + K - 1;
-    const int c0 = (blockIdx.x * kConvThreads + threadIdx.x) * VC;
-    const int b = blockIdx.z;
-    const int t0 = blockIdx.y * TC;
+    // XCD-aware tile order: tiles are numbered (batch row, time tile, channel
+    // group), channel group fastest, and workgroups are dealt to the 8 XCDs
+    // round robin, so workgroup w takes tile (w % 8) * (tiles / 8) + w / 8.
+    // An XCD then walks consecutive time tiles of a row: the K-1 halo a tile
+    // re-reads was pulled into the same L2 by the tile before it.
+    const int ncg = gridDim.x, ntt = gridDim.y;
+    int wl = (blockIdx.z * ntt + blockIdx.y) * ncg + blockIdx.x;
+    const int wt = ncg * ntt * gridDim.z;
+    if (wt % 8 == 0) wl = (wl % 8) * (wt / 8) + wl / 8;
+    const int cg = wl % ncg, tt_i = (wl / ncg) % ntt;
+    const int c0 = (cg * kConvThreads + threadIdx.x) * VC;
+    const int b = wl / (ncg * ntt);
+    const int t0 = tt_i * TC;
     if (c0 >= a.D) return;
 
     const T* __restrict__ xp = static_cast<const T*>(a.x) + b * a.x_sb + (int64_t)c0 * a.x_sd;
@@ -164,6 +174,8 @@ __global__ void __launch_bounds__(256) conv_step_kernel(T* __restrict__ state, c
 
 template <typename T, int VC, int TC>
 int launch_conv_vc(const ConvArgs& a, int64_t batch, hipStream_t st) {
+    const int64_t tiles = (a.D / VC + kConvThreads - 1) / kConvThreads * ((a.L + TC - 1) / TC) * batch;
+    MTL_REQUIRE(tiles < (int64_t(1) << 31), "batch * channel groups * time tiles overflows int32");
     dim3 block(kConvThreads);
     dim3 grid((unsigned)((a.D / VC + kConvThreads - 1) / kConvThreads), (unsigned)((a.L + TC - 1) / TC),
               (unsigned)batch);
