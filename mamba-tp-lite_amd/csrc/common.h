@@ -73,6 +73,19 @@ __device__ __forceinline__ float softplus_f(float x) {
     return __builtin_amdgcn_fmed3f(x, r, 3.0e38f);
 }
 
+// softplus(x) * log2(e), from xl = x * log2(e) (same threshold, series and
+// NaN handling as softplus_f, with log2 e folded into the series
+// coefficients).  A scan that keeps dt in these units takes exp(dt * A) as
+// exp2(dt_l2 * A) with no log2 e factor, and saves softplus_f's final ln 2
+// multiply.
+__device__ __forceinline__ float softplus_l2_f(float xl) {
+    const float e = __builtin_amdgcn_exp2f(__builtin_amdgcn_fmed3f(xl, -1.0e30f, 20.f * kLog2e));
+    const float series = e * (kLog2e - e * (kLog2e / 2 - e * (kLog2e / 3 - e * (kLog2e / 4))));
+    const float viaLog = __builtin_amdgcn_logf(1.f + e);
+    const float r = e < 0.03125f ? series : viaLog;
+    return __builtin_amdgcn_fmed3f(xl, r, 3.0e38f);
+}
+
 // x * sigmoid(x)
 __device__ __forceinline__ float silu_f(float x) {
     return x * __builtin_amdgcn_rcpf(1.f + fast_exp(-x));

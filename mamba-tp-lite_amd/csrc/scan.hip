@@ -13,15 +13,16 @@
 //     cross-lane traffic happens inside the time loop.
 //   * The sequence is walked in tiles of TT timesteps.  All 256 threads load
 //     the tile of u / delta / z coalesced (layout-specialized), compute
-//     dt = softplus(delta + bias), dt*u, D*u and silu(z) ONCE per (channel,
-//     t) and stage dt, dt*u in LDS.  The next tile's raw loads are issued
+//     dt = softplus(delta + bias), dt*u and silu(z) ONCE per (channel, t)
+//     and stage dt, dt*u in LDS.  The next tile's raw loads are issued
 //     before the scan of the current one (register double buffering).
 //   * Each wavefront writes its partial y_t (sum over its states) to LDS;
 //     the loader threads add the 4 partials in a fixed order (deterministic),
 //     apply (y + D*u) * silu(z) and store y coalesced.
 // Per (channel, t, state) the inner loop costs one v_exp_f32 and four VALU
-// ops (mul, mul, fma, fma); exp(x) is exp2(x * log2 e) with log2 e folded
-// into A once per launch.
+// ops (mul, mul, fma, fma).  dt is staged in log2 units (dt * log2 e, which
+// softplus_l2_f returns directly), so exp(dt * A) is exp2(dt_l2 * A); the
+// injection dt * u * B then takes its ln 2 from B, scaled where B is staged.
 
 #include <type_traits>
 
@@ -123,9 +124,39 @@ template <> struct BufAct<uint16_t> {
     }
 };
 
+// 4 consecutive activations of a channel-major row through a buffer
+// resource: a wavefront-uniform SGPR offset (the tile's first step) plus the
+// lane's loop-invariant VGPR offset, so no VALU address arithmetic per tile.
+typedef unsigned int U4v __attribute__((ext_vector_type(4)));
+typedef unsigned int U2v __attribute__((ext_vector_type(2)));
+template <typename T> struct Buf4;
+template <> struct Buf4<float> {
+    __device__ __forceinline__ static void load(__amdgpu_buffer_rsrc_t r, uint32_t vo, uint32_t so, float* v) {
+        const U4v x = __builtin_amdgcn_raw_buffer_load_b128(r, (int)vo, (int)so, 0);
+        v[0] = __uint_as_float(x.x); v[1] = __uint_as_float(x.y);
+        v[2] = __uint_as_float(x.z); v[3] = __uint_as_float(x.w);
+    }
+    __device__ __forceinline__ static void store(__amdgpu_buffer_rsrc_t r, uint32_t vo, uint32_t so, const float* v) {
+        const U4v x = {__float_as_uint(v[0]), __float_as_uint(v[1]), __float_as_uint(v[2]), __float_as_uint(v[3])};
+        __builtin_amdgcn_raw_buffer_store_b128(x, r, (int)vo, (int)so, 0);
+    }
+};
+template <> struct Buf4<uint16_t> {
+    __device__ __forceinline__ static void load(__amdgpu_buffer_rsrc_t r, uint32_t vo, uint32_t so, float* v) {
+        const U2v x = __builtin_amdgcn_raw_buffer_load_b64(r, (int)vo, (int)so, 0);
+        v[0] = __uint_as_float(x.x << 16); v[1] = __uint_as_float(x.x & 0xffff0000u);
+        v[2] = __uint_as_float(x.y << 16); v[3] = __uint_as_float(x.y & 0xffff0000u);
+    }
+    __device__ __forceinline__ static void store(__amdgpu_buffer_rsrc_t r, uint32_t vo, uint32_t so, const float* v) {
+        const U2v x = {f32x2_to_bf16x2(v[0], v[1]), f32x2_to_bf16x2(v[2], v[3])};
+        __builtin_amdgcn_raw_buffer_store_b64(x, r, (int)vo, (int)so, 0);
+    }
+};
+
 // NW wavefronts per workgroup = NW state groups of SPW states over the same
 // 64 channels.  CM: channel-major [b,D,l] rows (l-stride 1); otherwise
-// token-major (D-stride 1).  VEC: CM rows are aligned for vector access.
+// token-major (D-stride 1).  VEC: CM rows are aligned for vector access and
+// each tensor's batch row spans under 2^31 bytes (buffer offsets).
 //
 // A load tile is KC sub-tiles of TT steps: channel-major rows are read KC*TT
 // steps at a time (a whole 128-byte line per row for fp32 when KC*TT = 32,
@@ -210,7 +241,21 @@ __global__ void __launch_bounds__(NW * 64, CM ? 3 : 4) scan_fwd_kernel(const Sca
     const uint32_t run_bytes_z = (E - 1) * sl_bytes_z + row_bytes;
     const uint32_t run_bytes_y = (E - 1) * sl_bytes_y + row_bytes;
 
-    const float bias_c = a.dbias ? a.dbias[cl] : 0.f;
+    // channel-major full tiles: resources over one batch row of each tensor,
+    // the lane's channel row and staging offset as a loop-invariant VGPR offset
+    auto cm_rsrc = [&](const void* p, int64_t sb, int64_t sd) {
+        return row_rsrc(static_cast<const T*>(p) + b * sb, (uint32_t)(((int64_t)(D - 1) * sd + L) * (int64_t)sizeof(T)));
+    };
+    const auto ru_cm = cm_rsrc(a.u, a.u_sb, a.u_sd);
+    const auto rd_cm = cm_rsrc(a.delta, a.d_sb, a.d_sd);
+    const auto rz_cm = has_z ? cm_rsrc(a.z, a.z_sb, a.z_sd) : ru_cm;
+    const auto ry_cm = cm_rsrc(a.y, a.y_sb, a.y_sd);
+    const uint32_t vo_u = (uint32_t)(((int64_t)cl * a.u_sd + ot) * (int64_t)sizeof(T));
+    const uint32_t vo_d = (uint32_t)(((int64_t)cl * a.d_sd + ot) * (int64_t)sizeof(T));
+    const uint32_t vo_z = has_z ? (uint32_t)(((int64_t)cl * a.z_sd + ot) * (int64_t)sizeof(T)) : vo_u;
+    const uint32_t vo_y = (uint32_t)(((int64_t)cl * a.y_sd + ot) * (int64_t)sizeof(T));
+
+    const float bias_c = (a.dbias ? a.dbias[cl] : 0.f) * kLog2e;   // log2 units, as dt
     const float D_c = a.Dv ? a.Dv[cl] : 0.f;
 
     // scan registers: states [wave*SPW, wave*SPW + SPW) of channel c0 + lane
@@ -222,7 +267,7 @@ __global__ void __launch_bounds__(NW * 64, CM ? 3 : 4) scan_fwd_kernel(const Sca
         const bool ok = lane_ok && n < N;
         float av = ok ? a.A[(int64_t)(c0 + lane) * N + n] : 0.f;
         if (ok && a.a_is_log) av = -expf(av);
-        a2[k] = av * kLog2e;
+        a2[k] = av;
         h[k] = (ok && a.h0) ? a.h0[((int64_t)b * D + c0 + lane) * N + n] : 0.f;
     }
 
@@ -261,7 +306,15 @@ __global__ void __launch_bounds__(NW * 64, CM ? 3 : 4) scan_fwd_kernel(const Sca
 #pragma unroll
         for (int kc = 0; kc < KC; ++kc) {
             const int t0 = tb + kc * TT + ot;
-            if constexpr (CM && F) {
+            if constexpr (CM && F && VEC) {
+                const uint32_t so = (uint32_t)(tb + kc * TT) * (uint32_t)sizeof(T);
+#pragma unroll
+                for (int q = 0; q < E / 4; ++q) {
+                    Buf4<T>::load(ru_cm, vo_u + q * 4 * sizeof(T), so, &r.u[kc][4 * q]);
+                    Buf4<T>::load(rd_cm, vo_d + q * 4 * sizeof(T), so, &r.d[kc][4 * q]);
+                    Buf4<T>::load(rz_cm, vo_z + q * 4 * sizeof(T), so, &r.z[kc][4 * q]);
+                }
+            } else if constexpr (CM && F) {
                 load_run<T, E, VEC>(up + t0, r.u[kc]);
                 load_run<T, E, VEC>(dp + t0, r.d[kc]);
                 load_run<T, E, VEC>(zp + t0, r.z[kc]);
@@ -316,8 +369,8 @@ __global__ void __launch_bounds__(NW * 64, CM ? 3 : 4) scan_fwd_kernel(const Sca
 #pragma unroll
         for (int j = 0; j < E; ++j) {
             const bool ok = F || tb + kc * TT + ot + j < L;
-            float dt = r.d[kc][j] + bias_c;
-            if (a.softplus) dt = softplus_f(dt);
+            float dt = fmaf(r.d[kc][j], kLog2e, bias_c);   // (delta + bias) * log2 e
+            if (a.softplus) dt = softplus_l2_f(dt);
             const float uv = ok ? r.u[kc][j] : 0.f;
             dt = ok ? dt : 0.f;                 // zero steps leave the state untouched past the end
             vdt[j] = dt;
@@ -337,7 +390,7 @@ __global__ void __launch_bounds__(NW * 64, CM ? 3 : 4) scan_fwd_kernel(const Sca
             for (int k = 0; k < BCE; ++k) {
                 if (bc_slot[k] >= 0) {
                     const bool ok = bc_ok[k] && (F || tb + bc_t[k] < L);
-                    (&s_B[0][0])[bc_slot[k]] = ok ? r.B[k] : 0.f;
+                    (&s_B[0][0])[bc_slot[k]] = ok ? r.B[k] * kLn2 : 0.f;
                     (&s_C[0][0])[bc_slot[k]] = ok ? r.C[k] : 0.f;
                 }
             }
@@ -391,7 +444,11 @@ __global__ void __launch_bounds__(NW * 64, CM ? 3 : 4) scan_fwd_kernel(const Sca
 #pragma unroll
         for (int k2 = 0; k2 < KC; ++k2) {
             const int t0 = tb + k2 * TT + ot;
-            if constexpr (CM && F) {
+            if constexpr (CM && F && VEC) {
+                const uint32_t so = (uint32_t)(tb + k2 * TT) * (uint32_t)sizeof(T);
+#pragma unroll
+                for (int q = 0; q < E / 4; ++q) Buf4<T>::store(ry_cm, vo_y + q * 4 * sizeof(T), so, &yout[k2][4 * q]);
+            } else if constexpr (CM && F) {
                 store_run<T, E, VEC>(yp + t0, yout[k2]);
             } else if constexpr (CM) {
 #pragma unroll
@@ -460,12 +517,20 @@ __global__ void __launch_bounds__(NW * 64, CM ? 3 : 4) scan_fwd_kernel(const Sca
         }
         if (i < nfull) run_full(r0, i);
     } else {
-        if (nfull > 0) load_tile(r0, 0, Full<true>{});
-        for (int i = 0; i < nfull; ++i) {
+        // two load tiles per iteration: the loop-carried registers then line
+        // up at the back edge without copies
+        auto run_cm = [&](int i) {
             set_prio(i);
             run_subtiles(r0, i * LT, Full<true>{},
                          [&]() { load_tile(r0, min(i + 1, nfull - 1) * LT, Full<true>{}); });
+        };
+        if (nfull > 0) load_tile(r0, 0, Full<true>{});
+        int i = 0;
+        for (; i + 1 < nfull; i += 2) {
+            run_cm(i);
+            run_cm(i + 1);
         }
+        if (i < nfull) run_cm(i);
     }
     if (nfull * LT < L) {  // the partial last load tile, outside the pipeline
         const int tb = nfull * LT;
@@ -504,8 +569,12 @@ bool rows_aligned(const ScanArgs& a, int64_t batch) {
         return p == nullptr || ((uintptr_t)p % al == 0 && (batch == 1 || (sb * (int64_t)sizeof(T)) % al == 0) &&
                                 (sd * (int64_t)sizeof(T)) % al == 0);
     };
+    auto span = [&](const void* p, int64_t sd) {
+        return p == nullptr || ((int64_t)(a.D - 1) * sd + a.L) * (int64_t)sizeof(T) < (int64_t(1) << 31);
+    };
     return ok(a.u, a.u_sb, a.u_sd) && ok(a.delta, a.d_sb, a.d_sd) && ok(a.z, a.z_sb, a.z_sd) &&
-           ok(a.y, a.y_sb, a.y_sd);
+           ok(a.y, a.y_sb, a.y_sd) && span(a.u, a.u_sd) && span(a.delta, a.d_sd) && span(a.z, a.z_sd) &&
+           span(a.y, a.y_sd);
 }
 
 }  // namespace

@@ -283,3 +283,58 @@ def test_scan_shard_size_bf16_properties():
                                        dtype=np.float64)
         assert_rel(y[bi:bi + 1, sl].float().cpu().numpy(), yr, 1e-2, f"y b={bi} c0={c0}")
         assert_rel(h[bi:bi + 1, sl].cpu().numpy(), hr, 1e-2, f"h b={bi} c0={c0}")
+
+
+@pytest.mark.parametrize("dtype,L,Lp,N,full_ops", [(torch.float32, 1000, 1000, 16, True),
+                                                   (torch.float32, 996, 1008, 13, False),
+                                                   (torch.bfloat16, 1000, 1000, 16, True)])
+def test_scan_large_ragged_grid(dtype, L, Lp, N, full_ops):
+    """A 552-block channel-major grid, [24, 1472, L]: 23 channel blocks of
+    64 per row (1472 = 23 * 64, so the grid is not a multiple of the CU
+    count), L leaves a partial last 16-step sub-tile, and rows of Lp >= L
+    steps make the inputs strided views.  Checked against (1) the float64
+    oracle on sampled channel blocks, including the last one, (2) the same
+    scan on a 3-block channel slice (a 72-block grid), bit for bit, and (3) bit-exact
+    continuation split off the 16-step tile grid."""
+    b, D = 24, 1472
+    print(f"scan large ragged grid b={b} D={D} L={L} N={N} {dtype} full_ops={full_ops}", flush=True)
+    g = torch.Generator(device=DEV).manual_seed(7)
+    mk = lambda *s, sc=1.0: (sc * torch.randn(*s[:-1], Lp, device=DEV, generator=g)).to(dtype)[..., :L]
+    u, z, delta = mk(b, D, L), mk(b, D, L), mk(b, D, L, sc=0.5)
+    Bm, Cm = mk(b, N, L), mk(b, N, L)
+    if not full_ops:                    # delta is dt itself: keep it a small positive step
+        delta.abs_().mul_(0.1)
+    rng = np.random.default_rng(8)
+    bias = _t(om.inv_softplus(np.exp(rng.uniform(np.log(1e-3), np.log(0.1), D))).astype(np.float32))
+    A = -torch.arange(1, N + 1, device=DEV, dtype=torch.float32).repeat(D, 1).contiguous()
+    Dv = torch.linspace(0.5, 1.5, D, device=DEV)
+    h0 = torch.randn(b, D, N, device=DEV, generator=g)
+    kw = dict(D=Dv, z=z, delta_bias=bias, h0=h0) if full_ops else {}
+    sp = full_ops                       # no bias / D / z / h0 and no softplus on the second case
+    y, h = ops.selective_scan(u, delta, A, Bm, Cm, delta_softplus=sp, **kw)
+    k = 504
+    kw1 = dict(kw); kw2 = dict(kw)
+    if full_ops:
+        kw1["z"], kw2["z"] = z[..., :k], z[..., k:]
+    y1, h1 = ops.selective_scan(u[..., :k], delta[..., :k], A, Bm[..., :k], Cm[..., :k], delta_softplus=sp, **kw1)
+    kw2["h0"] = h1
+    y2, h2 = ops.selective_scan(u[..., k:], delta[..., k:], A, Bm[..., k:], Cm[..., k:], delta_softplus=sp, **kw2)
+    kws = {kk: (v[:192] if kk in ("D", "delta_bias") else v[:, :192]) for kk, v in kw.items()}
+    if "h0" in kws:
+        kws["h0"] = kws["h0"].contiguous()
+    ys, hs = ops.selective_scan(u[:, :192], delta[:, :192], A[:192], Bm, Cm, delta_softplus=sp, **kws)
+    torch.cuda.synchronize()
+    assert torch.isfinite(y.float()).all() and torch.isfinite(h).all()
+    assert torch.equal(torch.cat([y1, y2], -1), y) and torch.equal(h2, h)
+    tol = 1e-4 if dtype == torch.float32 else 1e-2
+    assert torch.equal(y[:, :192], ys) and torch.equal(h[:, :192], hs)
+    f = lambda t, bi: t[bi:bi + 1].float().cpu().numpy()
+    for bi, c0 in ((0, 0), (11, 640), (23, 1408)):
+        sl = slice(c0, c0 + 64)
+        yr, hr = om.selective_scan_bnl(f(u, bi)[:, sl], f(delta, bi)[:, sl], A[sl].cpu().numpy(), f(Bm, bi),
+                                       f(Cm, bi), Dv[sl].cpu().numpy() if full_ops else None,
+                                       f(z, bi)[:, sl] if full_ops else None,
+                                       bias[sl].cpu().numpy() if full_ops else None,
+                                       f(h0, bi)[:, sl] if full_ops else None, delta_softplus=sp, dtype=np.float64)
+        assert_rel(y[bi:bi + 1, sl].float().cpu().numpy(), yr, tol, f"y b={bi} c0={c0}")
+        assert_rel(h[bi:bi + 1, sl].cpu().numpy(), hr, tol, f"h b={bi} c0={c0}")
