@@ -306,7 +306,9 @@ __global__ void __launch_bounds__(NW * 64, CM ? 3 : 4) scan_fwd_kernel(const Sca
 #pragma unroll
         for (int kc = 0; kc < KC; ++kc) {
             const int t0 = tb + kc * TT + ot;
-            if constexpr (CM && F && VEC) {
+            if constexpr (CM && VEC) {
+                // a partial tile reads past L into the next row (or past the
+                // resource, which returns 0); staging masks those steps
                 const uint32_t so = (uint32_t)(tb + kc * TT) * (uint32_t)sizeof(T);
 #pragma unroll
                 for (int q = 0; q < E / 4; ++q) {
@@ -444,10 +446,16 @@ __global__ void __launch_bounds__(NW * 64, CM ? 3 : 4) scan_fwd_kernel(const Sca
 #pragma unroll
         for (int k2 = 0; k2 < KC; ++k2) {
             const int t0 = tb + k2 * TT + ot;
-            if constexpr (CM && F && VEC) {
+            if constexpr (CM && VEC) {
                 const uint32_t so = (uint32_t)(tb + k2 * TT) * (uint32_t)sizeof(T);
+                if constexpr (F) {
 #pragma unroll
-                for (int q = 0; q < E / 4; ++q) Buf4<T>::store(ry_cm, vo_y + q * 4 * sizeof(T), so, &yout[k2][4 * q]);
+                    for (int q = 0; q < E / 4; ++q) Buf4<T>::store(ry_cm, vo_y + q * 4 * sizeof(T), so, &yout[k2][4 * q]);
+                } else {
+#pragma unroll
+                    for (int j = 0; j < E; ++j)
+                        if (t0 + j < L) BufAct<T>::store(ry_cm, vo_y + j * sizeof(T), so, yout[k2][j]);
+                }
             } else if constexpr (CM && F) {
                 store_run<T, E, VEC>(yp + t0, yout[k2]);
             } else if constexpr (CM) {
