@@ -230,6 +230,11 @@ int mtl_quant_dequant_sum_fp16(const float* const* parts, int32_t nparts, int64_
  * mtl_decode_gemv: out [b, rows] = W [rows, cols] . v [b, cols] (+ bias)
  *   (+ x_in, the residual add of model.py:311): the out_proj rows
  *   (model.py:293) and, in the 4-launch form, the x_proj rows (279).
+ * mtl_decode_norm_gemv: out [b, rows] = W [rows, cols] . RMSNorm(v) (+ bias)
+ *   with RMSNorm(v) = norm_w * v * rsqrt(mean(v^2) + eps): the final norm_f
+ *   and the tied lm_head of MambaLM.step (model.py:351-352, RMSNorm at
+ *   model.py:130-135, lm_head at 325-326) in one launch.  The rms scale is
+ *   applied to each row's dot product.
  * mtl_decode_ssm: x_dbl [b, J] = sum over nblk of xpart (block order) ->
  *   dt = softplus(W_dt [D, R] . dt_low + b_dt) (model.py:281-282) ->
  *   ssm_state [b, D, N] updated in place with A = -exp(A_log) (284-289) ->
@@ -243,6 +248,8 @@ int mtl_decode_in(const float* x, const float* emb, const int64_t* ids, float* r
                   mtl_stream_t stream);
 int mtl_decode_gemv(const float* v, const float* W, const float* bias, const float* x_in, float* out, int32_t batch,
                     int32_t rows, int32_t cols, mtl_stream_t stream);
+int mtl_decode_norm_gemv(const float* v, const float* norm_w, float eps, const float* W, const float* bias, float* out,
+                         int32_t batch, int32_t rows, int32_t cols, mtl_stream_t stream);
 int mtl_decode_ssm(const float* xpart, int32_t nblk, const float* xc, const float* gz, const float* W_dt,
                    const float* b_dt, const float* A_log, const float* Dv, float* ssm_state, float* y,
                    int32_t batch, int32_t d_inner, int32_t d_state, int32_t dt_rank, mtl_stream_t stream);

@@ -259,12 +259,18 @@ struct GemvArgs {
     const float* x_in;       // [b, Mrows] residual or null
     float* out;              // [b, Mrows]
     int Mrows, K;
+    const float* norm_w;     // [K]: v is RMS-normalized with these weights first (NORM kernels)
+    float eps;
 };
 
-// one wavefront per output row, 4 rows per workgroup; K <= 256 * PL
-template <int B, int PL>
+// one wavefront per output row, 4 rows per workgroup; K <= 256 * PL.
+// NORM: out = (W . (norm_w * v)) * rsqrt(mean(v^2) + eps) + bias -- the final
+// RMSNorm folded into the lm_head rows (every workgroup recomputes the rms of
+// the few-kB vector instead of waiting for a separate norm kernel)
+template <int B, int PL, bool NORM = false>
 __global__ void __launch_bounds__(kThreads) decode_gemv_kernel(const GemvArgs a) {
     extern __shared__ __align__(16) float s_v[];      // [B][K]
+    __shared__ float s_red[B][kWaves];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int K = a.K, K4 = K >> 2;
     const int m = min((int)blockIdx.x * kWaves + wave, a.Mrows - 1);
@@ -276,18 +282,37 @@ __global__ void __launch_bounds__(kThreads) decode_gemv_kernel(const GemvArgs a)
     float xin[B];
 #pragma unroll
     for (int bi = 0; bi < B; ++bi) xin[bi] = a.x_in ? a.x_in[(int64_t)bi * a.Mrows + m] : 0.f;
-    float vv[B][PL];
+    float vv[B][PL], nw[PL];
 #pragma unroll
-    for (int q = 0; q < PL; ++q)
+    for (int q = 0; q < PL; ++q) {
+        if constexpr (NORM) nw[q] = a.norm_w[min(tid + q * kThreads, K - 1)];
 #pragma unroll
         for (int bi = 0; bi < B; ++bi) vv[bi][q] = a.v[(int64_t)bi * K + min(tid + q * kThreads, K - 1)];
+    }
+    if constexpr (NORM) {
+        float ss[B];
+#pragma unroll
+        for (int bi = 0; bi < B; ++bi) {
+            ss[bi] = 0.f;
+#pragma unroll
+            for (int q = 0; q < PL; ++q) ss[bi] = tid + q * kThreads < K ? fmaf(vv[bi][q], vv[bi][q], ss[bi]) : ss[bi];
+        }
+        wave_sum<B>(ss);
+        if (lane == 0)
+#pragma unroll
+            for (int bi = 0; bi < B; ++bi) s_red[bi][wave] = ss[bi];
+    }
 #pragma unroll
     for (int q = 0; q < PL; ++q)
         if (tid + q * kThreads < K)
 #pragma unroll
-            for (int bi = 0; bi < B; ++bi) s_v[bi * K + tid + q * kThreads] = vv[bi][q];
+            for (int bi = 0; bi < B; ++bi) s_v[bi * K + tid + q * kThreads] = NORM ? nw[q] * vv[bi][q] : vv[bi][q];
     __syncthreads();
     if ((int)blockIdx.x * kWaves + wave >= a.Mrows) return;   // whole wavefront
+    float rs[B];
+#pragma unroll
+    for (int bi = 0; bi < B; ++bi)
+        rs[bi] = NORM ? rsqrtf(((s_red[bi][0] + s_red[bi][1]) + (s_red[bi][2] + s_red[bi][3])) / (float)K + a.eps) : 1.f;
 
     const bool tail_ok = (PL - 1) * 64 + lane < K4;
     float acc[B];
@@ -307,7 +332,7 @@ __global__ void __launch_bounds__(kThreads) decode_gemv_kernel(const GemvArgs a)
     if (lane == 0) {
 #pragma unroll
         for (int bi = 0; bi < B; ++bi) {
-            const float o = acc[bi] + bias;
+            const float o = NORM ? fmaf(acc[bi], rs[bi], bias) : acc[bi] + bias;
             a.out[(int64_t)bi * a.Mrows + m] = a.x_in ? xin[bi] + o : o;
         }
     }
@@ -519,7 +544,7 @@ extern "C" int mtl_decode_gemv(const float* v, const float* W, const float* bias
     MTL_REQUIRE(x_in == nullptr || x_in != out, "out must not alias x_in");
     const size_t smem = sizeof(float) * (size_t)batch * cols;
     MTL_REQUIRE(smem <= 64 * 1024, "batch * cols too large for the decode LDS tile");
-    GemvArgs a{v, W, bias, x_in, out, rows, cols};
+    GemvArgs a{v, W, bias, x_in, out, rows, cols, nullptr, 0.f};
     hipStream_t st = as_stream(stream);
     const int runs = (cols / 4 + 63) / 64;
     if (rows < 128 * kWaves && runs >= 2 * kWaves) {
@@ -535,6 +560,27 @@ extern "C" int mtl_decode_gemv(const float* v, const float* W, const float* bias
                                                                   grid, dim3(kThreads), smem, st, a)));
     }
     return check_launch("decode_gemv");
+}
+
+extern "C" int mtl_decode_norm_gemv(const float* v, const float* norm_w, float eps, const float* W, const float* bias,
+                                    float* out, int32_t batch, int32_t rows, int32_t cols, mtl_stream_t stream) {
+    using namespace mtl;
+    clear_error();
+    MTL_REQUIRE(batch == 1 || batch == 2 || batch == 4, "batch must be 1, 2 or 4");
+    MTL_REQUIRE(cols >= 4 && cols % 4 == 0 && cols <= 256 * kMaxPL && rows >= 1,
+                "cols must be a multiple of 4 in [4, 4096]");
+    MTL_REQUIRE(v && norm_w && W && out, "null required pointer");
+    MTL_REQUIRE(((uintptr_t)W % 16) == 0, "W must be 16-byte aligned");
+    MTL_REQUIRE(v != out, "out must not alias v");
+    const size_t smem = sizeof(float) * (size_t)batch * cols;
+    MTL_REQUIRE(smem <= 64 * 1024, "batch * cols too large for the decode LDS tile");
+    GemvArgs a{v, W, bias, nullptr, out, rows, cols, norm_w, eps};
+    hipStream_t st = as_stream(stream);
+    const int runs = (cols / 4 + 63) / 64;
+    const dim3 grid((unsigned)((rows + kWaves - 1) / kWaves));
+    MTL_DISPATCH_B(batch, MTL_DISPATCH_RUNS(PL, round_runs(runs), hipLaunchKernelGGL((decode_gemv_kernel<B, PL, true>),
+                                                              grid, dim3(kThreads), smem, st, a)));
+    return check_launch("decode_norm_gemv");
 }
 
 extern "C" int mtl_decode_ssm(const float* xpart, int32_t nblk, const float* xc, const float* gz, const float* W_dt,

@@ -71,6 +71,7 @@ SIGNATURES = {
     "mtl_decode_in": (ctypes.c_int, [_fp, _fp, _vp, _fp, _fp, ctypes.c_float, _fp, _fp, _fp, _fp, _fp, _fp, _fp, _fp,
                                      _fp, _i32, _i32, _i32, _i32, _i32, _i32, _vp]),
     "mtl_decode_gemv": (ctypes.c_int, [_fp, _fp, _fp, _fp, _fp, _i32, _i32, _i32, _vp]),
+    "mtl_decode_norm_gemv": (ctypes.c_int, [_fp, _fp, ctypes.c_float, _fp, _fp, _fp, _i32, _i32, _i32, _vp]),
     "mtl_decode_ssm": (ctypes.c_int, [_fp, _i32, _fp, _fp, _fp, _fp, _fp, _fp, _fp, _fp, _i32, _i32, _i32, _i32,
                                       _vp]),
 }

@@ -455,8 +455,10 @@ class MambaLM(nn.Module):
             x_next = xs[i % 2]
             ops.decode_gemv(y, mx.out_proj.weight, x_next, bias=mx.out_proj.bias, x_in=resid)
             x_cur = x_next
-        normed = ops.add_rmsnorm(x_cur, _f32(self.norm_f.weight), self.norm_f.eps)
-        return self.lm_head(normed).unsqueeze(1)
+        # final norm_f + tied lm_head in one launch (reference model.py:351-352)
+        logits = torch.empty(b, self.embedding.weight.shape[0], **f32)
+        ops.decode_norm_gemv(x_cur, _f32(self.norm_f.weight), self.norm_f.eps, self.embedding.weight, logits)
+        return logits.unsqueeze(1)
 
     @torch.no_grad()
     def generate(self, input_ids: torch.Tensor, max_new_tokens: int, greedy: bool = True):

@@ -444,6 +444,22 @@ def decode_gemv(v, W, out, bias=None, x_in=None):
     return out
 
 
+def decode_norm_gemv(v, norm_w, eps, W, out, bias=None):
+    """mtl_decode_norm_gemv: out [b, rows] = W [rows, cols] . RMSNorm(v) (+ bias),
+    RMSNorm(v) = norm_w * v * rsqrt(mean(v^2) + eps) -- the final norm and
+    lm_head of a decode step in one launch."""
+    for name, t in (("v", v), ("norm_w", norm_w), ("W", W), ("out", out), ("bias", bias)):
+        _f32c(t, name)
+    b, cols = v.shape
+    rows = W.shape[0]
+    if W.shape[1] != cols or tuple(out.shape) != (b, rows) or tuple(norm_w.shape) != (cols,):
+        raise ValueError("decode_norm_gemv: W [rows, cols], v [b, cols], norm_w [cols], out [b, rows] expected")
+    with _dev_guard(v):
+        _lib.check(_lib.load().mtl_decode_norm_gemv(_ptr(v), _ptr(norm_w), float(eps), _ptr(W), _ptr(bias), _ptr(out),
+                                                    b, rows, cols, _stream(v)), "decode_norm_gemv")
+    return out
+
+
 def decode_ssm(xpart, xc, gz, W_dt, b_dt, A_log, Dv, ssm_state, y):
     """mtl_decode_ssm: reduce x_proj partials [nblk, b, J] -> dt_proj +
     softplus -> ssm_state update in place -> y = (C.h + D x) * gz."""

@@ -71,6 +71,8 @@ def test_invalid_arguments_are_rejected_without_a_gpu():
     ("mtl_decode_in", dict(d_conv=9), b"bad sizes"),
     ("mtl_decode_gemv", dict(batch=8), b"batch must be 1, 2 or 4"),
     ("mtl_decode_gemv", dict(cols=8192), b"cols"),
+    ("mtl_decode_norm_gemv", dict(batch=3), b"batch must be 1, 2 or 4"),
+    ("mtl_decode_norm_gemv", dict(cols=6), b"cols"),
     ("mtl_decode_ssm", dict(d_state=17), b"d_state"),
     ("mtl_decode_ssm", dict(dt_rank=300), b"dt_rank"),
     ("mtl_decode_ssm", dict(nblk=1000), b"partial blocks"),
@@ -100,6 +102,10 @@ def test_entry_points_validate_sizes_on_the_host(case):
         a = dict(batch=1, rows=8, cols=64)
         a.update(over)
         rc = lib.mtl_decode_gemv(P, P, None, None, P, a["batch"], a["rows"], a["cols"], None)
+    elif name == "mtl_decode_norm_gemv":
+        a = dict(batch=1, rows=8, cols=64)
+        a.update(over)
+        rc = lib.mtl_decode_norm_gemv(P, P, 1e-5, P, None, ctypes.c_void_p(32), a["batch"], a["rows"], a["cols"], None)
     elif name == "mtl_decode_ssm":
         a = dict(nblk=4, batch=1, d_inner=64, d_state=16, dt_rank=4)
         a.update(over)

@@ -154,3 +154,26 @@ def test_fused_step_config_variants(kw, b):
         for l1, l2 in zip(c1.layers, c2.layers):
             assert_rel(_np(l1.ssm_state), _np(l2.ssm_state), 1e-4, "ssm_state")
             assert_rel(_np(l1.conv_state), _np(l2.conv_state), 1e-5, "conv_state")
+
+
+@pytest.mark.parametrize("b,cols,rows,with_bias", [(1, 768, 50280, False), (2, 2048, 1001, True), (4, 64, 7, True),
+                                                   (1, 4096, 300, False)])
+def test_decode_norm_gemv_matches_rmsnorm_then_linear(b, cols, rows, with_bias):
+    """mtl_decode_norm_gemv (the final norm_f and tied lm_head of a decode
+    step in one launch) against torch fp32 RMSNorm followed by F.linear, at
+    1e-4 relative: the lm_head shapes of the 130m and 1.4b widths, a ragged
+    row count, the smallest width and the widest."""
+    from mamba_lite import ops
+    print(f"decode_norm_gemv b={b} cols={cols} rows={rows} bias={with_bias}", flush=True)
+    g = torch.Generator(device=DEV).manual_seed(cols + rows)
+    v = 3.0 * torch.randn(b, cols, device=DEV, generator=g)
+    w = 1.0 + 0.1 * torch.randn(cols, device=DEV, generator=g)
+    W = torch.randn(rows, cols, device=DEV, generator=g) / cols ** 0.5
+    bias = torch.randn(rows, device=DEV, generator=g) if with_bias else None
+    out = torch.empty(b, rows, device=DEV)
+    ops.decode_norm_gemv(v, w, 1e-5, W, out, bias=bias)
+    vd, wd, Wd = v.double(), w.double(), W.double()
+    ref = torch.nn.functional.linear(wd * vd * torch.rsqrt(vd.pow(2).mean(-1, keepdim=True) + 1e-5), Wd,
+                                     bias.double() if with_bias else None)
+    torch.cuda.synchronize()
+    assert_rel(_np(out), ref.cpu().numpy(), 1e-4, "logits")
