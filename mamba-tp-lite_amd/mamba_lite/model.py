@@ -19,6 +19,7 @@ the reference casts it to the activation dtype (model.py:241).
 """
 from __future__ import annotations
 
+import contextlib
 import json
 import os
 from dataclasses import dataclass
@@ -124,6 +125,35 @@ class MambaCache:
 # the extra launches cost more than the scan gains, so the fused projection
 # is kept and the scan reads the slices through their strides.
 SPLIT_PROJ_MIN_TOKENS = 16384
+
+# Prefills of at most this many tokens run their per-layer projections on
+# torch's rocBLAS path instead of hipBLASLt: each hipBLASLt call costs about
+# 18.6 us of host time against 7.3 us for rocBLAS, and at these sizes the
+# host is the bottleneck (measured on MI355X at the 130m shape, 64 tokens: 4
+# projections per layer, device time 3-13 us each).  The tied lm_head stays on
+# hipBLASLt, whose kernel is faster there (54 us against 91 us for 64 x 50280).
+SMALL_PREFILL_TOKENS = 256
+
+
+@contextlib.contextmanager
+def _prefer_blas(lib: str | None):
+    """Selects torch's BLAS backend for the enclosed GEMMs and restores the
+    caller's choice afterwards.  It is a process-wide torch setting: GEMMs
+    another thread issues meanwhile run on the same backend, which can change
+    their speed and the rounding of their sums (each library is a correct
+    fp32 GEMM; they differ in summation order)."""
+    if lib is None or not torch.cuda.is_available():
+        yield
+        return
+    prev = torch.backends.cuda.preferred_blas_library()
+    if str(prev).lower().endswith(lib):
+        yield
+        return
+    torch.backends.cuda.preferred_blas_library(lib)
+    try:
+        yield
+    finally:
+        torch.backends.cuda.preferred_blas_library(prev)
 
 
 def _f32(t: torch.Tensor | None) -> torch.Tensor | None:
@@ -366,7 +396,8 @@ class MambaLM(nn.Module):
             new_layers.append(LayerCache(conv_state=cs, ssm_state=hs))
             return y
 
-        xf = self._run(x, layer)
+        with _prefer_blas("cublas" if input_ids.numel() <= SMALL_PREFILL_TOKENS else None):
+            xf = self._run(x, layer)
         return self.lm_head(xf), (out_cache if out_cache is not None else MambaCache(new_layers))
 
     def step(self, input_ids: torch.Tensor, cache: MambaCache):
