@@ -245,12 +245,14 @@ def cpu_baseline_decode(model, dev, prompt=64, steps=8):
             "gpu_step_max_rel_err_vs_oracle_f64": err}
 
 
-def bench_prefill(model, batch, seqlen, dev, iters=3):
+def bench_prefill(model, batch, seqlen, dev, iters=None):
     import torch
     g = torch.Generator(device=dev).manual_seed(7)
     ids = torch.randint(0, model.cfg.vocab_size, (batch, seqlen), device=dev, generator=g)
+    small = batch * seqlen <= 4096      # milliseconds per call: average more calls
+    iters = iters or (20 if small else 3)
     with torch.no_grad():
-        ms = _timed(lambda: model.prefill(ids), iters, 1)
+        ms = _timed(lambda: model.prefill(ids), iters, 3 if small else 1)
     return batch * seqlen / (ms / 1000.0)
 
 
