@@ -399,6 +399,10 @@ def main():
     torch.cuda.set_device(dev)
     result = {"metric": METRIC}
     extra = {}
+    # the tuned projection GEMMs of the prefill shapes (mamba_lite/gemm_table.py)
+    from mamba_lite import gemm_table
+    gemm_ok = gemm_table.enable() if args.only != "copy" else False
+    log(f"tuned GEMM table {'loaded' if gemm_ok else 'not used (default GEMM paths)'}")
 
     want = lambda s: args.only in ("all", s)
     if args.only == "copy":
@@ -504,6 +508,8 @@ def main():
                        "dtype": "f32", "data": "synthetic", "config": {"workload": f"partial run: {args.only}"}})
     result.update(extra)
     result["device"] = torch.cuda.get_device_name(dev)
+    result["gemm_table"] = {"loaded": gemm_ok, "file": "mamba-tp-lite_amd/mamba_lite/gemm_table_gfx950.csv",
+                            "covers": "prefill projection and lm_head shapes of the 130m model"}
     print(json.dumps(result), flush=True)
 
 

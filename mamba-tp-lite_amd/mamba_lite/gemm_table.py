@@ -1,0 +1,40 @@
+"""Tuned GEMM solutions for the projection shapes of the prefill workloads.
+
+The projections (in_proj, x_proj, dt_proj, out_proj, the tied lm_head) are
+torch fp32 GEMMs on hipBLASLt / rocBLAS.  `gemm_table_gfx950.csv` is a torch
+TunableOp results table: for each prefill projection shape of the mamba-130m
+model (64 tokens at batch 1 and 1024 tokens at batch 32) it names the
+hipBLASLt or rocBLAS solution that measured fastest on MI355X, among all
+solutions both libraries offer.  It was recorded by running the prefill
+benchmark once with TunableOp tuning on (10 iterations or 10 ms per
+candidate).
+
+`enable()` turns TunableOp on with tuning off and loads the table.  Shapes in
+the table then run their tuned solution; every other GEMM keeps torch's
+default path.  The table is tied to the builds it was measured with: torch
+rejects it (and `enable` returns False) when torch, HIP, hipBLASLt or rocBLAS
+versions or the GPU architecture differ, and every GEMM then keeps the
+default path.  TunableOp is a process-wide torch setting, so this is opt-in.
+
+Decode shapes are left out: at 32 rows the tuner preferred solutions that
+ran slower inside the captured decode graph than hipBLASLt's default.
+"""
+from __future__ import annotations
+
+import os
+
+import torch
+
+TABLE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "gemm_table_gfx950.csv")
+
+
+def enable(path: str = TABLE) -> bool:
+    """Use the tuned GEMM table (TunableOp on, tuning off).  Returns True if
+    torch accepted the table."""
+    import torch.cuda.tunable as tunable
+
+    if not torch.cuda.is_available() or not os.path.exists(path):
+        return False
+    tunable.enable(True)
+    tunable.tuning_enable(False)
+    return bool(tunable.read_file(path))

@@ -311,3 +311,28 @@ def test_graph_serves_a_second_prompt_after_prefill_into_its_cache(b):
             e = model.step(s, ce)
             torch.cuda.synchronize()
             assert torch.equal(g, e)
+
+
+def test_tuned_gemm_table_loads_and_keeps_prefill_results():
+    """mamba_lite.gemm_table: torch accepts the committed TunableOp table on
+    this build, and a 64-token prefill at the 130m width (whose in_proj,
+    x_proj, dt_proj, out_proj and lm_head shapes are in the table) gives the
+    same logits and states within 1e-4 relative as the default GEMM paths."""
+    import torch.cuda.tunable as tunable
+    from mamba_lite import gemm_table
+    torch.manual_seed(3)
+    cfg = MambaConfig(d_model=768, n_layer=2, vocab_size=50280, d_state=16)
+    with torch.device(DEV):
+        model = MambaLM(cfg).eval()
+    ids = torch.randint(0, cfg.vocab_size, (1, 64), device=DEV)
+    with torch.no_grad():
+        ref_logits, ref_cache = model.prefill(ids)
+        try:
+            assert gemm_table.enable()
+            logits, cache = model.prefill(ids)
+            torch.cuda.synchronize()
+        finally:
+            tunable.enable(False)
+    assert_rel(logits.cpu().numpy(), ref_logits.cpu().numpy(), 1e-4, "logits")
+    for a, r in zip(cache.layers, ref_cache.layers):
+        assert_rel(a.ssm_state.cpu().numpy(), r.ssm_state.cpu().numpy(), 1e-4, "ssm_state")

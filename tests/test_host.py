@@ -190,3 +190,20 @@ def test_from_pretrained_missing_checkpoint(tmp_path):
     from mamba_lite.model import load_hf_state_dict
     with pytest.raises(FileNotFoundError):
         load_hf_state_dict(str(tmp_path))
+
+
+def test_gemm_table_file_is_well_formed():
+    """The committed TunableOp table: validator lines for torch, HIP,
+    hipBLASLt, rocBLAS and gfx950, then one fp32 GEMM entry per tuned shape
+    with a solution name and a time."""
+    import csv
+    from mamba_lite import gemm_table
+    rows = list(csv.reader(open(gemm_table.TABLE)))
+    validators = {r[1]: r[2] for r in rows if r[0] == "Validator"}
+    assert {"PT_VERSION", "HIP_VERSION", "HIPBLASLT_VERSION", "ROCBLAS_VERSION", "GCN_ARCH_NAME"} <= set(validators)
+    assert validators["GCN_ARCH_NAME"].startswith("gfx950")
+    gemms = [r for r in rows if r[0].startswith("GemmTunableOp_float")]
+    assert len(gemms) >= 5 and all(len(r) == 4 and float(r[3]) > 0 for r in gemms)
+    # a CPU-only process keeps the default GEMM paths
+    if not __import__("torch").cuda.is_available():
+        assert gemm_table.enable() is False
