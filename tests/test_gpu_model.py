@@ -336,3 +336,44 @@ def test_tuned_gemm_table_loads_and_keeps_prefill_results():
     assert_rel(logits.cpu().numpy(), ref_logits.cpu().numpy(), 1e-4, "logits")
     for a, r in zip(cache.layers, ref_cache.layers):
         assert_rel(a.ssm_state.cpu().numpy(), r.ssm_state.cpu().numpy(), 1e-4, "ssm_state")
+
+
+def test_kernels_run_on_the_callers_current_stream():
+    """The wrappers launch on torch's current stream of the operands' device
+    (the raw-stream accessor): a prefill issued inside `torch.cuda.stream(s)`
+    on a side stream, synchronized through that stream only, equals the same
+    prefill on the default stream bit for bit."""
+    torch.manual_seed(5)
+    cfg = MambaConfig(d_model=64, n_layer=2, vocab_size=128, d_state=16)
+    with torch.device(DEV):
+        model = MambaLM(cfg).eval()
+    ids = torch.randint(0, cfg.vocab_size, (2, 40), device=DEV)
+    with torch.no_grad():
+        ref, ref_cache = model.prefill(ids)
+        torch.cuda.synchronize()
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            from mamba_lite import ops
+            assert ops._stream(ids).value == side.cuda_stream
+            out, cache = model.prefill(ids)
+        side.synchronize()
+    assert torch.equal(out, ref)
+    for a, r in zip(cache.layers, ref_cache.layers):
+        assert torch.equal(a.ssm_state, r.ssm_state) and torch.equal(a.conv_state, r.conv_state)
+
+
+def test_small_prefill_restores_the_blas_backend():
+    """A prefill of at most SMALL_PREFILL_TOKENS tokens runs its projections on
+    rocBLAS and leaves torch's backend choice as it found it."""
+    from mamba_lite import model as mm
+    torch.manual_seed(6)
+    cfg = MambaConfig(d_model=64, n_layer=1, vocab_size=128, d_state=16)
+    with torch.device(DEV):
+        model = MambaLM(cfg).eval()
+    before = torch.backends.cuda.preferred_blas_library()
+    ids = torch.randint(0, cfg.vocab_size, (1, 16), device=DEV)
+    with torch.no_grad():
+        model.prefill(ids)
+    assert torch.backends.cuda.preferred_blas_library() == before
+    assert ids.numel() <= mm.SMALL_PREFILL_TOKENS
