@@ -112,6 +112,37 @@ def test_shard_params_partition_the_dense_mixer():
     assert torch.equal(s0["out_proj.bias"], dense.out_proj.bias.detach())
 
 
+def test_naive_shard_cuts_the_packed_in_proj():
+    """Reference NaiveTPMambaMixer (tp_model.py:217-244): at world_size 2
+    rank 0 gets only x rows and rank 1 only z rows."""
+    torch.manual_seed(0)
+    cfg = MambaConfig(d_model=32, n_layer=1, vocab_size=100, d_state=8)
+    dense = MambaMixer(cfg, 0)
+    Di = cfg.d_inner
+    w = dense.in_proj.weight.detach()
+    assert torch.equal(tp_utils.naive_shard_mixer_params(dense, 0, 2)["in_proj.weight"], w[:Di])
+    n1 = tp_utils.naive_shard_mixer_params(dense, 1, 2)
+    assert torch.equal(n1["in_proj.weight"], w[Di:])
+    assert torch.equal(n1["x_proj.weight"], tp_utils.shard_mixer_params(dense, 1, 2)["x_proj.weight"])
+
+
+def test_site_dtype_lookup():
+    """Reference tests/test_per_site_allreduce.py:69-74, plus the variants not built here."""
+    assert tp_utils.site_dtype("fp16", 5, "x_proj") == "fp16"
+    m = {(2, "out_proj"): "int8_gather_tok"}
+    assert tp_utils.site_dtype(m, 2, "out_proj") == "int8_gather_tok"
+    assert tp_utils.site_dtype(m, 2, "x_proj") == "fp32"
+    assert tp_utils.site_dtype(m, 3, "out_proj") == "fp32"
+    assert tp_utils.site_dtype("int8", 0, "x_proj") == "int8"
+    with pytest.raises(AssertionError):
+        tp_utils.site_dtype("fp32", 0, "in_proj")
+    with pytest.raises(AssertionError):
+        tp_utils.site_dtype("bf8", 0, "x_proj")
+    for unbuilt in ("int8_legacy", "int8_sum", "int8_gather"):
+        with pytest.raises(NotImplementedError):
+            tp_utils.site_dtype({(0, "x_proj"): unbuilt}, 0, "x_proj")
+
+
 def test_layer_cache_is_a_dataclass_pair():
     lc = LayerCache(conv_state=torch.zeros(1, 2, 3), ssm_state=torch.zeros(1, 2, 4))
     assert lc.conv_state.shape == (1, 2, 3) and lc.ssm_state.shape == (1, 2, 4)
