@@ -47,3 +47,34 @@ def scan_case(rng, b, D, L, N, dtype=np.float32):
     A = -np.tile(np.arange(1, N + 1, dtype=np.float32), (D, 1))
     Dv = np.ones(D, np.float32)
     return dict(u=u, delta=delta, A=A, B=B, C=C, D=Dv, z=z, delta_bias=bias)
+
+
+def write_hf_snapshot(path, cfg, sd, shards=1):
+    """A local `mamba-*-hf` style directory: config.json + safetensors with
+    the `backbone.` names (embeddings, layers.{i}.mixer.*, norm_f)."""
+    import json
+    from safetensors.torch import save_file
+    (path / "config.json").write_text(json.dumps({
+        "hidden_size": cfg.d_model, "num_hidden_layers": cfg.n_layer, "vocab_size": cfg.vocab_size,
+        "state_size": cfg.d_state, "conv_kernel": cfg.d_conv, "expand": cfg.expand, "time_step_rank": cfg.dt_rank,
+        "use_conv_bias": cfg.conv_bias, "use_bias": cfg.bias}))
+    hf = {}
+    for k, v in sd.items():
+        if k == "embedding.weight":
+            hf["backbone.embeddings.weight"] = v
+        elif k == "norm_f.weight":
+            hf["backbone.norm_f.weight"] = v
+        else:
+            hf["backbone." + k] = v
+    hf["lm_head.weight"] = sd["embedding.weight"].clone()   # tied; ignored by the loader
+    keys = sorted(hf)
+    if shards == 1:
+        save_file({k: hf[k].contiguous() for k in keys}, str(path / "model.safetensors"))
+        return
+    weight_map = {}
+    for s in range(shards):
+        part = keys[s::shards]
+        name = f"model-{s + 1:05d}-of-{shards:05d}.safetensors"
+        save_file({k: hf[k].contiguous() for k in part}, str(path / name))
+        weight_map.update({k: name for k in part})
+    (path / "model.safetensors.index.json").write_text(json.dumps({"weight_map": weight_map}))

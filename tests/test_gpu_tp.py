@@ -1,4 +1,4 @@
-"""Tensor-parallel mixer with every rank on one GPU (mamba_lite.tp_utils.LocalTPMixer),
+"""Tensor-parallel mixer and model with every rank on one GPU (mamba_lite.tp_model),
 checked the way the reference checks its 2-process TPMambaMixer
 (tests/test_tp_correctness.py:76-88, tests/test_quantized_allreduce.py:73-87,
 tests/test_per_site_allreduce.py:77-112): the correct channel split equals the
@@ -7,13 +7,15 @@ packed-tensor split does not, an all-fp32 site map is bit-identical to the
 global fp32 setting, an int8 site changes only its own site, fp16 is close but
 not exact, and the per-token int8 all-reduce is close but lossy with under a
 third of the fp32 wire bytes.  Beyond the reference's tests: prefill
-continuation from per-rank caches, and a teacher-forced step loop against the
-dense step and the dense prefill."""
+continuation from per-rank caches, a teacher-forced step loop against the
+dense step and the dense prefill, and the full TP model (LocalTPLM) against
+the dense LM, loaded shard by shard from a local safetensors snapshot."""
 import pytest
 import torch
 
-from mamba_lite import tp_utils
-from mamba_lite.model import LayerCache, MambaConfig, MambaMixer
+from _util import write_hf_snapshot
+from mamba_lite.model import LayerCache, MambaConfig, MambaLM, MambaMixer
+from mamba_lite.tp_model import LocalTPLM, LocalTPMixer
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
@@ -40,7 +42,7 @@ def test_correct_split_matches_dense_with_two_allreduces(d_model, d_state, b, l,
     print(f"tp local prefill d_model={d_model} b={b} l={l} ws={ws}", flush=True)
     dense = _dense(d_model, d_state)
     x = _x(b, l, d_model)
-    tp = tp_utils.LocalTPMixer(dense, ws)
+    tp = LocalTPMixer.from_dense(dense, ws)
     with torch.no_grad():
         ref, ref_conv, ref_ssm = dense.prefill(x)
         out, conv, ssm = tp.prefill(x)
@@ -59,7 +61,7 @@ def test_prefill_continues_from_rank_caches(d_model, d_state, b, l, ws):
     print(f"tp local continuation d_model={d_model} ws={ws}", flush=True)
     dense = _dense(d_model, d_state)
     x = _x(b, l, d_model)
-    tp = tp_utils.LocalTPMixer(dense, ws)
+    tp = LocalTPMixer.from_dense(dense, ws)
     k = l // 3
     with torch.no_grad():
         ref, _, ref_ssm = dense.prefill(x)
@@ -77,7 +79,7 @@ def test_step_matches_dense_step_and_prefill(d_model, d_state, b, l, ws):
     dense = _dense(d_model, d_state)
     cfg = dense.cfg
     x = _x(b, l, d_model)
-    tp = tp_utils.LocalTPMixer(dense, ws)
+    tp = LocalTPMixer.from_dense(dense, ws)
     caches = tp.allocate_caches(b, device=DEV)
     dcache = LayerCache(torch.zeros(b, cfg.d_inner, cfg.d_conv - 1, device=DEV),
                         torch.zeros(b, cfg.d_inner, cfg.d_state, device=DEV))
@@ -100,7 +102,7 @@ def test_naive_split_gives_wrong_result():
     x = _x(2, 5, 32)
     with torch.no_grad():
         ref = dense(x)
-        out = tp_utils.LocalTPMixer(dense, 2, naive=True)(x)
+        out = LocalTPMixer.from_dense(dense, 2, naive=True)(x)
     assert not torch.allclose(out, ref, atol=1e-2)
 
 
@@ -110,7 +112,7 @@ def test_fp16_allreduce_close_but_not_exact(d_model, d_state, b, l, ws):
     x = _x(b, l, d_model)
     with torch.no_grad():
         ref = dense(x)
-        out = tp_utils.LocalTPMixer(dense, ws, allreduce_dtype="fp16")(x)
+        out = LocalTPMixer.from_dense(dense, ws, allreduce_dtype="fp16")(x)
     torch.testing.assert_close(out, ref, atol=1e-2, rtol=1e-2)
     assert not torch.allclose(out, ref, atol=1e-6)
 
@@ -121,8 +123,8 @@ def test_int8_allreduce_close_but_lossy(d_model, d_state, b, l, ws):
     x = _x(b, l, d_model)
     with torch.no_grad():
         ref = dense(x)
-        tp8 = tp_utils.LocalTPMixer(dense, ws, allreduce_dtype="int8_gather_tok")
-        tp32 = tp_utils.LocalTPMixer(dense, ws)
+        tp8 = LocalTPMixer.from_dense(dense, ws, allreduce_dtype="int8_gather_tok")
+        tp32 = LocalTPMixer.from_dense(dense, ws)
         out = tp8(x)
         tp32(x)
     torch.testing.assert_close(out, ref, atol=0.1, rtol=0.2)
@@ -150,7 +152,7 @@ def test_per_site_dtype_map():
     with torch.no_grad():
         ref = dense(x)
         for name, (spec, layer) in specs.items():
-            tp = tp_utils.LocalTPMixer(dense, 2, allreduce_dtype=spec, layer_idx=layer)
+            tp = LocalTPMixer.from_dense(dense, 2, allreduce_dtype=spec, layer_idx=layer)
             res[name] = (tp(x), tp.comm.count, tp.comm.bytes)
     base = res["fp32_str"][0]
     assert torch.equal(res["fp32_map"][0], base) and torch.equal(res["empty_map"][0], base)
@@ -167,9 +169,56 @@ def test_per_site_dtype_map():
 
 def test_rank_caches_are_this_ranks_channels_only():
     dense = _dense(768, 16)
-    tp = tp_utils.LocalTPMixer(dense, 4)
+    tp = LocalTPMixer.from_dense(dense, 4)
     caches = tp.allocate_caches(3, device=DEV)
     assert len(caches) == 4
     for c in caches:
         assert tuple(c.conv_state.shape) == (3, 384, 3) and tuple(c.ssm_state.shape) == (3, 384, 16)
         assert c.ssm_state.dtype == torch.float32 and not c.conv_state.any() and not c.ssm_state.any()
+
+
+@pytest.mark.parametrize("ws,shards", [(2, 1), (4, 3)])
+def test_tp_lm_matches_dense_lm(tmp_path, ws, shards):
+    """tests/test_tp_lm_correctness.py:43-81 on a synthetic local snapshot
+    (no checkpoint is reachable offline): the TP LM loaded shard by shard
+    from safetensors gives the dense LM's prefill logits and greedy tokens,
+    with 2 AllReduces per prefill or step on layer 0 (prefill + generate of 8
+    tokens = 2 * (1 + 1 + 7) = 18)."""
+    print(f"tp local lm ws={ws} shards={shards}", flush=True)
+    torch.manual_seed(0)
+    cfg = MambaConfig(d_model=64, n_layer=3, vocab_size=256, d_state=16)
+    src = MambaLM(cfg)
+    write_hf_snapshot(tmp_path, cfg, {k: v.detach().clone() for k, v in src.state_dict().items()}, shards)
+    dense = MambaLM.from_pretrained(str(tmp_path)).to(DEV).eval()
+    tp = LocalTPLM.from_pretrained_shard(str(tmp_path), ws, device=DEV)
+    torch.manual_seed(42)
+    ids = torch.randint(0, cfg.vocab_size, (1, 12), device=DEV)
+    with torch.no_grad():
+        dense_logits, _ = dense.prefill(ids)
+        dense_tokens = dense.generate(ids, max_new_tokens=8)
+        tp_logits, _ = tp.prefill(ids)
+        tp_tokens = tp.generate(ids, max_new_tokens=8)
+    torch.testing.assert_close(tp_logits, dense_logits, atol=1e-4, rtol=1e-4)
+    assert torch.equal(tp_tokens, dense_tokens), (tp_tokens.tolist(), dense_tokens.tolist())
+    assert tp.layers[0].mixer.comm.count == 18
+
+
+def test_tp_lm_teacher_forced_steps_match_prefill():
+    """A prefill of the first token, then steps over the rest, reproduce the
+    full prefill's logits (reference tests/test_correctness.py:49-72 on the
+    TP model), from a dense LM sharded in memory at batch 2."""
+    torch.manual_seed(1)
+    cfg = MambaConfig(d_model=128, n_layer=2, vocab_size=300, d_state=16)
+    with torch.device(DEV):
+        dense = MambaLM(cfg).eval()
+    tp = LocalTPLM.from_dense(dense, 2)
+    ids = torch.randint(0, cfg.vocab_size, (2, 10), device=DEV)
+    with torch.no_grad():
+        full, _ = tp.prefill(ids)
+        dense_full, _ = dense.prefill(ids)
+        first, cache = tp.prefill(ids[:, :1])
+        steps = [first] + [tp.step(ids[:, t:t + 1], cache) for t in range(1, ids.shape[1])]
+    torch.testing.assert_close(full, dense_full, atol=1e-4, rtol=1e-4)
+    torch.testing.assert_close(torch.cat(steps, 1), full, atol=1e-4, rtol=1e-4)
+    assert len(cache.layers) == 2 and len(cache.layers[0]) == 2
+    assert tuple(cache.layers[1][1].ssm_state.shape) == (2, cfg.d_inner // 2, 16)

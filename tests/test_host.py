@@ -3,6 +3,7 @@ import numpy as np
 import pytest
 import torch
 
+from _util import write_hf_snapshot
 from mamba_lite import ops, tp_utils
 from mamba_lite.cuda_graph import CUDAGraphUnsupported, GraphedStepper
 from mamba_lite.model import LayerCache, MambaCache, MambaConfig, MambaLM, MambaMixer
@@ -166,37 +167,6 @@ def test_product_package_never_imports_the_oracle():
     assert hits == []
 
 
-def _write_hf_snapshot(path, cfg, sd, shards=1):
-    """A local `mamba-*-hf` style directory: config.json + safetensors with
-    the `backbone.` names (embeddings, layers.{i}.mixer.*, norm_f)."""
-    import json
-    from safetensors.torch import save_file
-    (path / "config.json").write_text(json.dumps({
-        "hidden_size": cfg.d_model, "num_hidden_layers": cfg.n_layer, "vocab_size": cfg.vocab_size,
-        "state_size": cfg.d_state, "conv_kernel": cfg.d_conv, "expand": cfg.expand, "time_step_rank": cfg.dt_rank,
-        "use_conv_bias": cfg.conv_bias, "use_bias": cfg.bias}))
-    hf = {}
-    for k, v in sd.items():
-        if k == "embedding.weight":
-            hf["backbone.embeddings.weight"] = v
-        elif k == "norm_f.weight":
-            hf["backbone.norm_f.weight"] = v
-        else:
-            hf["backbone." + k] = v
-    hf["lm_head.weight"] = sd["embedding.weight"].clone()   # tied; ignored by the loader
-    keys = sorted(hf)
-    if shards == 1:
-        save_file({k: hf[k].contiguous() for k in keys}, str(path / "model.safetensors"))
-        return
-    weight_map = {}
-    for s in range(shards):
-        part = keys[s::shards]
-        name = f"model-{s + 1:05d}-of-{shards:05d}.safetensors"
-        save_file({k: hf[k].contiguous() for k in part}, str(path / name))
-        weight_map.update({k: name for k in part})
-    (path / "model.safetensors.index.json").write_text(json.dumps({"weight_map": weight_map}))
-
-
 @pytest.mark.parametrize("shards", [1, 3])
 def test_from_pretrained_local_snapshot(tmp_path, shards):
     """reference model.py:28-47 (single file or index-named shards) and
@@ -208,7 +178,7 @@ def test_from_pretrained_local_snapshot(tmp_path, shards):
         for p in src.parameters():
             p.normal_()
     sd = {k: v.detach().clone() for k, v in src.state_dict().items()}
-    _write_hf_snapshot(tmp_path, cfg, sd, shards)
+    write_hf_snapshot(tmp_path, cfg, sd, shards)
     m = MambaLM.from_pretrained(str(tmp_path))
     got = m.state_dict()
     assert set(got) == set(sd)
