@@ -271,6 +271,9 @@ __global__ void __launch_bounds__(NW * 64, CM ? 3 : 4) scan_fwd_kernel(const Sca
         h[k] = (ok && a.h0) ? a.h0[((int64_t)b * D + c0 + lane) * N + n] : 0.f;
     }
 
+    // The lambdas below are forced inline: an outlined one takes the state
+    // arrays it captures through scratch memory (seen at 2 wavefronts x 8
+    // states: 6x slower).
     // raw load-tile registers: two sets, so the next load tile is in flight
     // while the current one is scanned
     struct Raw { float u[KC][E], d[KC][E], z[KC][E], B[BCE], C[BCE]; };
@@ -301,7 +304,7 @@ __global__ void __launch_bounds__(NW * 64, CM ? 3 : 4) scan_fwd_kernel(const Sca
         c_bytes[k] = (uint32_t)((bc_off[k] * a.C_sn + bc_t[k] * a.C_sl) * (int64_t)sizeof(T));
     }
 
-    auto load_tile = [&](Raw& r, int tb, auto full) {
+    auto load_tile = [&](Raw& r, int tb, auto full) __attribute__((always_inline)) {
         constexpr bool F = decltype(full)::value;
 #pragma unroll
         for (int kc = 0; kc < KC; ++kc) {
@@ -365,7 +368,7 @@ __global__ void __launch_bounds__(NW * 64, CM ? 3 : 4) scan_fwd_kernel(const Sca
 
     // stage sub-tile kc of the load tile at tb (B/C of the whole load tile
     // are staged with sub-tile 0)
-    auto stage_tile = [&](const Raw& r, int tb, int kc, auto full) {
+    auto stage_tile = [&](const Raw& r, int tb, int kc, auto full) __attribute__((always_inline)) {
         constexpr bool F = decltype(full)::value;
         float vdt[E], vdx[E];
 #pragma unroll
@@ -401,7 +404,7 @@ __global__ void __launch_bounds__(NW * 64, CM ? 3 : 4) scan_fwd_kernel(const Sca
 
     // TT recurrence steps of sub-tile kc; padded steps past the end have
     // dt = dt*u = 0 and leave h unchanged, so the loop never needs a bound check
-    auto scan_tile = [&](int kc) {
+    auto scan_tile = [&](int kc) __attribute__((always_inline)) {
 #pragma unroll
         for (int tt = 0; tt < TT; tt += 4) {
             const float4 dt4 = *reinterpret_cast<const float4*>(&s_dt[lane][tt]);
@@ -427,7 +430,7 @@ __global__ void __launch_bounds__(NW * 64, CM ? 3 : 4) scan_fwd_kernel(const Sca
 
     // y of sub-tile kc into registers; the whole load tile is stored after
     // its last sub-tile
-    auto finish_tile = [&](int tb, int kc, auto full) {
+    auto finish_tile = [&](int tb, int kc, auto full) __attribute__((always_inline)) {
         constexpr bool F = decltype(full)::value;
 #pragma unroll
         for (int q = 0; q < E / 4; ++q) {
@@ -474,7 +477,7 @@ __global__ void __launch_bounds__(NW * 64, CM ? 3 : 4) scan_fwd_kernel(const Sca
         }
     };
 
-    auto run_subtiles = [&](Raw& r, int tb, auto full, auto refill) {
+    auto run_subtiles = [&](Raw& r, int tb, auto full, auto refill) __attribute__((always_inline)) {
 #pragma unroll
         for (int kc = 0; kc < KC; ++kc) {
             stage_tile(r, tb, kc, full);
@@ -502,7 +505,7 @@ __global__ void __launch_bounds__(NW * 64, CM ? 3 : 4) scan_fwd_kernel(const Sca
     // that got ahead yields its issue slots to the ones behind it on the same
     // CU at each level change, and the final level (where the spread builds
     // up again) is only an eighth of the sequence.
-    auto set_prio = [&](int i) {
+    auto set_prio = [&](int i) __attribute__((always_inline)) {
         const int n8 = 8 * i, nf = max(nfull, 1);
         const int lvl = n8 < 4 * nf ? 0 : n8 < 6 * nf ? 1 : n8 < 7 * nf ? 2 : 3;
         if (lvl == 0) __builtin_amdgcn_s_setprio(3);
@@ -511,7 +514,7 @@ __global__ void __launch_bounds__(NW * 64, CM ? 3 : 4) scan_fwd_kernel(const Sca
         else __builtin_amdgcn_s_setprio(0);
     };
     if constexpr (KC == 1) {
-        auto run_full = [&](Raw& r, int i) {
+        auto run_full = [&](Raw& r, int i) __attribute__((always_inline)) {
             set_prio(i);
             run_subtiles(r, i * LT, Full<true>{},
                          [&]() { load_tile(r, min(i + 2, nfull - 1) * LT, Full<true>{}); });
@@ -527,7 +530,7 @@ __global__ void __launch_bounds__(NW * 64, CM ? 3 : 4) scan_fwd_kernel(const Sca
     } else {
         // two load tiles per iteration: the loop-carried registers then line
         // up at the back edge without copies
-        auto run_cm = [&](int i) {
+        auto run_cm = [&](int i) __attribute__((always_inline)) {
             set_prio(i);
             run_subtiles(r0, i * LT, Full<true>{},
                          [&]() { load_tile(r0, min(i + 1, nfull - 1) * LT, Full<true>{}); });
