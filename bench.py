@@ -13,6 +13,8 @@ Reported beside it in the same JSON line, each with its own parity check:
   decode_us_per_token  hipGraph-replayed MambaLM.step, 130m shape b=1 and
                        1.4b shape b=1 / b=32 (random-init fp32 weights)
   prefill_tok_s        MambaLM.prefill, 130m shape (b=1 x 64, b=32 x 1024)
+  prefill_graph_tok_s  the b=1 x 64 prefill captured once (GraphedPrefill)
+                       and replayed per prompt
   quant                per-token int8 and fp16 quantize->dequantize-sum of
                        two [32768, 768] fp32 partials (GB/s)
   shard_bf16           one TP rank's 1.4b channel shard (D=2048), bf16
@@ -256,6 +258,32 @@ def bench_prefill(model, batch, seqlen, dev, iters=None):
     return batch * seqlen / (ms / 1000.0)
 
 
+def bench_prefill_graph(model, batch, seqlen, dev, iters=20):
+    """The same prefill captured once with cuda_graph.GraphedPrefill and
+    replayed per prompt (final states into a preallocated cache).  Checks
+    the replay against an eager prefill on the backend a capture uses, bit
+    for bit, before timing."""
+    import torch
+    from mamba_lite import model as mm
+    from mamba_lite.cuda_graph import GraphedPrefill
+    g = torch.Generator(device=dev).manual_seed(7)
+    ids = torch.randint(0, model.cfg.vocab_size, (batch, seqlen), device=dev, generator=g)
+    cache = mm.MambaCache.allocate(model.cfg, batch, dev, torch.float32)
+    gp = GraphedPrefill(model, cache, batch, seqlen, "cuda")
+    gp.capture()
+    orig = mm.SMALL_PREFILL_BLAS
+    try:
+        with torch.no_grad():
+            got = gp.replay(ids).clone()
+            mm.SMALL_PREFILL_BLAS = None
+            ref, _ = model.prefill(ids)
+    finally:
+        mm.SMALL_PREFILL_BLAS = orig
+    ms = _timed(lambda: gp.replay(ids), iters, 3)
+    return {"tok_s": batch * seqlen / (ms / 1000.0), "ms_per_prompt": ms,
+            "replay_equals_eager": bool(torch.equal(got, ref))}
+
+
 # --------------------------------------------------------------------------- quant / shard
 def cpu_baseline_quant(parts, pays, out, rows=4096):
     """cpu_baseline leg of the int8 payload op: the oracle's per-token int8
@@ -483,6 +511,8 @@ def main():
             extra["prefill_tok_s"] = {"130m_b1_l64": bench_prefill(model, 1, 64, dev),
                                       "130m_b32_l1024": bench_prefill(model, 32, 1024, dev)}
             log(f"prefill: {extra['prefill_tok_s']}")
+            extra["prefill_graph_tok_s"] = {"130m_b1_l64": bench_prefill_graph(model, 1, 64, dev)}
+            log(f"prefill graph: {extra['prefill_graph_tok_s']}")
             del model
             torch.cuda.empty_cache()
         except Exception as e:

@@ -77,3 +77,59 @@ class GraphedStepper:
         self.static_ids.copy_(next_id)
         self.graph.replay()
         return self.static_logits
+
+
+class GraphedPrefill:
+    """Captures `model.prefill(static_ids, out_cache=cache)` for one fixed
+    [batch_size, seqlen] prompt shape, then replays it per prompt.
+
+        prefill = GraphedPrefill(model, cache, batch_size=1, seqlen=64, device="cuda")
+        prefill.capture()
+        logits = prefill.replay(prompt_ids)    # [batch, seqlen] int64
+
+    A replay writes the prompt's final conv and SSM states into `cache` in
+    place and its logits into `static_logits`; the next replay overwrites
+    both.  Passing the cache a GraphedStepper captured lets decoding continue
+    from the prompt with no copy.  Every replay starts from zero state, as
+    MambaLM.prefill without an incoming cache does.  A short prompt's eager
+    prefill is bound by host time (about a hundred launches through torch and
+    the kernel wrappers); a replay is one graph launch.  The reference graphs
+    only the decode step; this is the same capture for the prompt."""
+
+    def __init__(self, model, cache, batch_size: int, seqlen: int, device: str, n_warmup: int = 3):
+        if device != "cuda" or not torch.cuda.is_available():
+            raise CUDAGraphUnsupported("graph capture needs a GPU device ('cuda'); there is no CPU fallback.")
+        if len(cache.layers) != len(model.layers):
+            raise ValueError("cache has the wrong number of layers")
+        self.model = model
+        self.cache = cache
+        self.static_ids = torch.zeros((batch_size, seqlen), dtype=torch.long, device=device)
+        self.static_logits = None
+        self.graph = None
+        self.n_warmup = n_warmup
+
+    def capture(self):
+        warm = _clone_cache(self.cache)
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side), torch.no_grad():
+            for _ in range(self.n_warmup):
+                self.model.prefill(self.static_ids, out_cache=warm)
+        torch.cuda.current_stream().wait_stream(side)
+        torch.cuda.synchronize()
+        del warm
+
+        self.graph = torch.cuda.CUDAGraph()
+        try:
+            with torch.cuda.graph(self.graph), torch.no_grad():
+                self.static_logits, _ = self.model.prefill(self.static_ids, out_cache=self.cache)
+        except RuntimeError as e:
+            self.graph = None
+            raise CUDAGraphUnsupported(f"graph capture failed: {e}") from e
+
+    def replay(self, ids: torch.Tensor) -> torch.Tensor:
+        if tuple(ids.shape) != tuple(self.static_ids.shape):
+            raise ValueError(f"ids must be {tuple(self.static_ids.shape)}, got {tuple(ids.shape)}")
+        self.static_ids.copy_(ids)
+        self.graph.replay()
+        return self.static_logits

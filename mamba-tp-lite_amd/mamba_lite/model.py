@@ -132,7 +132,10 @@ SPLIT_PROJ_MIN_TOKENS = 16384
 # host is the bottleneck (measured on MI355X at the 130m shape, 64 tokens: 4
 # projections per layer, device time 3-13 us each).  The tied lm_head stays on
 # hipBLASLt, whose kernel is faster there (54 us against 91 us for 64 x 50280).
-# Set SMALL_PREFILL_BLAS to None to leave torch's backend choice alone.
+# Set SMALL_PREFILL_BLAS to None to leave torch's backend choice alone.  A
+# prefill being captured into a HIP graph (cuda_graph.GraphedPrefill) has no
+# host cost per launch, so it keeps hipBLASLt (a 64-token 130m prefill replays
+# in 1.42 ms that way against 1.64 ms on rocBLAS).
 SMALL_PREFILL_TOKENS = 256
 SMALL_PREFILL_BLAS: str | None = "cublas"
 
@@ -398,7 +401,8 @@ class MambaLM(nn.Module):
             new_layers.append(LayerCache(conv_state=cs, ssm_state=hs))
             return y
 
-        with _prefer_blas(SMALL_PREFILL_BLAS if input_ids.numel() <= SMALL_PREFILL_TOKENS else None):
+        small = input_ids.numel() <= SMALL_PREFILL_TOKENS and not torch.cuda.is_current_stream_capturing()
+        with _prefer_blas(SMALL_PREFILL_BLAS if small else None):
             xf = self._run(x, layer)
         return self.lm_head(xf), (out_cache if out_cache is not None else MambaCache(new_layers))
 

@@ -315,27 +315,27 @@ def test_graph_serves_a_second_prompt_after_prefill_into_its_cache(b):
 
 def test_tuned_gemm_table_loads_and_keeps_prefill_results():
     """mamba_lite.gemm_table: torch accepts the committed TunableOp table on
-    this build, and a 64-token prefill at the 130m width (whose in_proj,
-    x_proj, dt_proj, out_proj and lm_head shapes are in the table) gives the
-    same logits and states within 1e-4 relative as the default GEMM paths."""
+    this build, and a 130m-width mixer prefill of 32 x 1024 tokens (whose
+    in_proj halves, x_proj, dt_proj and out_proj shapes are in the table)
+    gives the same output and states within 1e-4 relative as the default
+    GEMM paths."""
     import torch.cuda.tunable as tunable
     from mamba_lite import gemm_table
     torch.manual_seed(3)
-    cfg = MambaConfig(d_model=768, n_layer=2, vocab_size=50280, d_state=16)
+    cfg = MambaConfig(d_model=768, n_layer=1, vocab_size=50280, d_state=16)
     with torch.device(DEV):
-        model = MambaLM(cfg).eval()
-    ids = torch.randint(0, cfg.vocab_size, (1, 64), device=DEV)
+        mixer = MambaMixer(cfg, 0).eval()
+    x = torch.randn(32, 1024, 768, device=DEV)
     with torch.no_grad():
-        ref_logits, ref_cache = model.prefill(ids)
+        ref, _, ref_h = mixer.prefill(x)
         try:
             assert gemm_table.enable()
-            logits, cache = model.prefill(ids)
+            out, _, h = mixer.prefill(x)
             torch.cuda.synchronize()
         finally:
             tunable.enable(False)
-    assert_rel(logits.cpu().numpy(), ref_logits.cpu().numpy(), 1e-4, "logits")
-    for a, r in zip(cache.layers, ref_cache.layers):
-        assert_rel(a.ssm_state.cpu().numpy(), r.ssm_state.cpu().numpy(), 1e-4, "ssm_state")
+    assert_rel(out[:4].cpu().numpy(), ref[:4].cpu().numpy(), 1e-4, "out")
+    assert_rel(h.cpu().numpy(), ref_h.cpu().numpy(), 1e-4, "ssm_state")
 
 
 def test_kernels_run_on_the_callers_current_stream():
@@ -377,3 +377,50 @@ def test_small_prefill_restores_the_blas_backend():
         model.prefill(ids)
     assert torch.backends.cuda.preferred_blas_library() == before
     assert ids.numel() <= mm.SMALL_PREFILL_TOKENS
+
+
+def test_graphed_prefill_replays_match_eager_and_feed_the_stepper():
+    """GraphedPrefill: every replay equals an eager prefill on the graph's BLAS
+    backend bit for bit (logits, and every layer's final states written into
+    the shared cache), and the default eager prefill within fp32 tolerance;
+    between replays the program runs its own eager work.  A GraphedStepper
+    captured on the same cache then decodes from the graphed prompt exactly
+    as eager steps decode from the eager prompt."""
+    from mamba_lite import model as mm
+    from mamba_lite.cuda_graph import GraphedPrefill
+    torch.manual_seed(8)
+    cfg = MambaConfig(d_model=128, n_layer=3, vocab_size=300, d_state=16)
+    with torch.device(DEV):
+        model = MambaLM(cfg).eval()
+    b, l = 2, 24
+    cache = MambaCache.allocate(cfg, b, DEV, torch.float32)
+    gp = GraphedPrefill(model, cache, b, l, DEV)
+    gp.capture()
+    st = GraphedStepper(model, cache, b, DEV)
+    st.capture()
+    g = torch.Generator(device=DEV).manual_seed(3)
+    orig = mm.SMALL_PREFILL_BLAS
+    try:
+        with torch.no_grad():
+            for k in range(3):
+                print(f"graphed prefill replay {k}", flush=True)
+                ids = torch.randint(0, cfg.vocab_size, (b, l), device=DEV, generator=g)
+                logits = gp.replay(ids).clone()
+                mm.SMALL_PREFILL_BLAS = None                 # the backend a capture uses
+                ref, rc = model.prefill(ids)
+                mm.SMALL_PREFILL_BLAS = orig
+                assert torch.equal(logits, ref), k
+                for a, r in zip(cache.layers, rc.layers):
+                    assert torch.equal(a.conv_state, r.conv_state) and torch.equal(a.ssm_state, r.ssm_state)
+                dflt, _ = model.prefill(ids)
+                torch.testing.assert_close(logits, dflt, atol=1e-4, rtol=1e-4)
+                nxt = ref[:, -1:].argmax(-1)
+                for _ in range(4):
+                    got = st.replay(nxt).clone()
+                    exp = model.step(nxt, rc)
+                    assert torch.equal(got, exp)
+                    nxt = exp[:, -1].argmax(-1, keepdim=True)
+    finally:
+        mm.SMALL_PREFILL_BLAS = orig
+    with pytest.raises(ValueError):
+        gp.replay(torch.zeros(b, l + 1, dtype=torch.long, device=DEV))

@@ -81,6 +81,13 @@ def test_graphed_stepper_rejects_cpu():
         GraphedStepper(MambaLM(cfg), MambaCache.allocate(cfg, 1, "cpu", torch.float32), 1, "cpu")
 
 
+def test_graphed_prefill_rejects_cpu():
+    from mamba_lite.cuda_graph import GraphedPrefill
+    cfg = MambaConfig(d_model=32, n_layer=1, vocab_size=100, d_state=8)
+    with pytest.raises(CUDAGraphUnsupported):
+        GraphedPrefill(MambaLM(cfg), MambaCache.allocate(cfg, 1, "cpu", torch.float32), 1, 8, "cpu")
+
+
 def test_graphed_stepper_rejects_int8_legacy():
     class M:
         allreduce_dtype = {(0, "x_proj"): "int8_legacy"}
