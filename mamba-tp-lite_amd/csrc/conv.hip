@@ -104,13 +104,18 @@ __global__ void __launch_bounds__(kConvThreads) conv_fwd_kernel(const ConvArgs a
         for (int k = 0; k < K; ++k) w[k][ci] = a.w[(int64_t)(c0 + ci) * K + k];
         bias[ci] = a.bias ? a.bias[c0 + ci] : 0.f;
     }
-    if (t0 == 0) {  // the first K-1 padded positions: carried history or zeros (uniform per block)
+    // padded positions below K-1 are the carried history or zeros; with runs
+    // shorter than K-1 they reach past the first run (uniform per block)
+    if (t0 < K - 1) {
         const T* __restrict__ sin = a.st_in ? static_cast<const T*>(a.st_in) : nullptr;
 #pragma unroll
-        for (int j = 0; j < K - 1; ++j)
+        for (int j = 0; j < K - 1; ++j) {
+            const int p = t0 + j;
+            if (p < K - 1)
 #pragma unroll
-            for (int ci = 0; ci < VC; ++ci)
-                v[j][ci] = sin ? Act<T>::load(sin + ((int64_t)b * a.D + c0 + ci) * (K - 1) + j) : 0.f;
+                for (int ci = 0; ci < VC; ++ci)
+                    v[j][ci] = sin ? Act<T>::load(sin + ((int64_t)b * a.D + c0 + ci) * (K - 1) + p) : 0.f;
+        }
     }
 
 #pragma unroll
@@ -200,6 +205,12 @@ int launch_conv(const ConvArgs& a, int64_t batch, hipStream_t st) {
                      (uintptr_t)a.out % al == 0 && (a.x_sl * (int64_t)sizeof(T)) % al == 0 &&
                      (a.o_sl * (int64_t)sizeof(T)) % al == 0 &&
                      (batch == 1 || ((a.x_sb * (int64_t)sizeof(T)) % al == 0 && (a.o_sb * (int64_t)sizeof(T)) % al == 0));
+    // Short sequences: with 16-step runs a 64-token prompt at D = 1536 is 8
+    // workgroups, each thread forming 16 outputs in turn; 4-step runs give
+    // 4x the workgroups and a quarter of the serial work per thread.
+    const int64_t groups = (a.D / (vec ? kVC : 1) + kConvThreads - 1) / kConvThreads;
+    if (groups * ((a.L + kTC - 1) / kTC) * batch < 256)
+        return vec ? launch_conv_vc<T, kVC, 4>(a, batch, st) : launch_conv_vc<T, 1, 4>(a, batch, st);
     return vec ? launch_conv_vc<T, kVC, kTC>(a, batch, st) : launch_conv_vc<T, 1, kTC>(a, batch, st);
 }
 

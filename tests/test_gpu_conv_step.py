@@ -73,6 +73,24 @@ def test_conv_no_activation_and_widths():
         assert np.array_equal(fs.cpu().numpy(), ref_fs.astype(np.float32))
 
 
+@pytest.mark.parametrize("K", [6, 8])
+@pytest.mark.parametrize("L", [1, 5, 6, 9, 13])
+def test_conv_short_runs_read_history_past_the_first_run(K, L):
+    """Small grids use 4-step runs: with K - 1 > 4 the second run's window
+    also starts inside the carried history, which must come from conv_state
+    (not clamped inputs), in both layouts."""
+    rng = np.random.default_rng(K * 100 + L)
+    x = rng.standard_normal((2, 96, L)).astype(np.float32)
+    w = rng.standard_normal((96, K)).astype(np.float32)
+    bias = rng.standard_normal(96).astype(np.float32)
+    st = rng.standard_normal((2, 96, K - 1)).astype(np.float32)
+    ref, ref_fs = om.causal_conv1d(x, w, bias, st, dtype=np.float64)
+    for X in (_t(x), _t(np.ascontiguousarray(x.transpose(0, 2, 1))).transpose(1, 2)):
+        out, fs = ops.causal_conv1d(X, _t(w), _t(bias), conv_state=_t(st), silu=True)
+        assert_rel(out.cpu().numpy(), om.silu(ref), 1e-4, f"K={K} L={L}")
+        assert np.array_equal(fs.cpu().numpy(), ref_fs.astype(np.float32))
+
+
 def test_conv_zero_length_passes_state_through():
     st = torch.randn(2, 64, 3, device=DEV)
     x = torch.empty(2, 64, 0, device=DEV)
