@@ -222,3 +222,18 @@ def test_tp_lm_teacher_forced_steps_match_prefill():
     torch.testing.assert_close(torch.cat(steps, 1), full, atol=1e-4, rtol=1e-4)
     assert len(cache.layers) == 2 and len(cache.layers[0]) == 2
     assert tuple(cache.layers[1][1].ssm_state.shape) == (2, cfg.d_inner // 2, 16)
+
+
+def test_bf16_split_tracks_the_dense_bf16_mixer():
+    """bf16 activations with fp32 SSM state, as the TP-rank shard workload
+    runs: the split over 2 ranks tracks the dense bf16 mixer within the bf16
+    tolerance (each rank's partial sums round to bf16 before the fp32
+    all-reduce, the dense GEMM rounds once), and keeps fp32 rank states."""
+    dense = _dense(256, 16).to(torch.bfloat16)
+    x = _x(2, 37, 256).bfloat16()
+    with torch.no_grad():
+        ref, _, ref_h = dense.prefill(x)
+        out, _, h = LocalTPMixer.from_dense(dense, 2).prefill(x)
+    assert out.dtype == torch.bfloat16 and all(t.dtype == torch.float32 for t in h)
+    torch.testing.assert_close(out.float(), ref.float(), atol=2e-2, rtol=2e-2)
+    torch.testing.assert_close(torch.cat(h, 1), ref_h, atol=2e-2, rtol=2e-2)

@@ -215,3 +215,13 @@ def test_gemm_table_file_is_well_formed():
     # a CPU-only process keeps the default GEMM paths
     if not __import__("torch").cuda.is_available():
         assert gemm_table.enable() is False
+
+
+def test_local_tp_mixer_needs_a_divisible_world_size():
+    """Reference tp_model.py:65 (d_inner % world_size == 0)."""
+    from mamba_lite.tp_model import LocalTPMixer
+    cfg = MambaConfig(d_model=32, n_layer=1, vocab_size=100, d_state=8)
+    with pytest.raises(AssertionError):
+        LocalTPMixer(cfg, world_size=3)
+    with pytest.raises(RuntimeError, match="no shards"):
+        LocalTPMixer(cfg, world_size=2).prefill(torch.randn(1, 2, 32))
