@@ -22,13 +22,21 @@ from . import _lib
 _ACT_DTYPES = {torch.float32: _lib.MTL_F32, torch.bfloat16: _lib.MTL_BF16}
 
 
+# These helpers run on every launch; at small sizes host time decides the
+# speed of a call, so they compare device indices rather than building
+# torch.device objects, and hand ctypes plain ints.
+_NO_GUARD = contextlib.nullcontext()
+_current_device = getattr(torch._C, "_cuda_getDevice", None) or torch.cuda.current_device
+
+
 def _dev_guard(t: torch.Tensor):
-    if t.device.type != "cuda":
+    if not t.is_cuda:
         raise RuntimeError(f"mamba_lite kernels need GPU tensors, got a tensor on {t.device} "
                            "(there is no CPU fallback)")
-    if t.device.index is not None and t.device.index != torch.cuda.current_device():
-        return torch.cuda.device(t.device)
-    return contextlib.nullcontext()
+    idx = t.get_device()
+    if idx != _current_device():
+        return torch.cuda.device(idx)
+    return _NO_GUARD
 
 
 # torch's current stream of a device as a raw handle: the private accessor
@@ -38,30 +46,39 @@ def _dev_guard(t: torch.Tensor):
 _raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
 
 
-def _stream(t: torch.Tensor) -> ctypes.c_void_p:
+def _stream(t: torch.Tensor) -> int:
     if _raw_stream is not None:
-        idx = t.device.index
-        return ctypes.c_void_p(_raw_stream(torch.cuda.current_device() if idx is None else idx))
-    return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
+        return _raw_stream(t.get_device())
+    return torch.cuda.current_stream(t.device).cuda_stream
 
 
 def _ptr(t):
-    return None if t is None else ctypes.c_void_p(t.data_ptr())
+    return None if t is None else t.data_ptr()
 
 
 def _act_code(*ts) -> int:
-    dts = {t.dtype for t in ts if t is not None}
-    if len(dts) != 1:
+    dt = None
+    for t in ts:
+        if t is None:
+            continue
+        if dt is None:
+            dt = t.dtype
+        elif t.dtype != dt:
+            dt = False
+            break
+    if dt is None or dt is False:
+        dts = {t.dtype for t in ts if t is not None}
         raise TypeError(f"activations must share one dtype, got {sorted(map(str, dts))}")
-    dt = dts.pop()
-    if dt not in _ACT_DTYPES:
+    code = _ACT_DTYPES.get(dt)
+    if code is None:
         raise TypeError(f"activation dtype must be float32 or bfloat16, got {dt}")
-    return _ACT_DTYPES[dt]
+    return code
 
 
 def _same_device(ref: torch.Tensor, *ts):
+    dev = ref.get_device()
     for t in ts:
-        if t is not None and t.device != ref.device:
+        if t is not None and t.get_device() != dev:
             raise RuntimeError(f"all operands must be on {ref.device}, got {t.device}")
 
 
@@ -75,7 +92,7 @@ def _f32_vec(t, n, name):
 
 
 def _f32_mat(t, shape, name):
-    if t.dtype != torch.float32 or tuple(t.shape) != tuple(shape) or not t.is_contiguous():
+    if t.dtype != torch.float32 or t.shape != shape or not t.is_contiguous():
         raise ValueError(f"{name} must be contiguous float32 {tuple(shape)}, got {tuple(t.shape)} {t.dtype}"
                          f"{'' if t.is_contiguous() else ' (non-contiguous)'}")
     return t
@@ -84,8 +101,13 @@ def _f32_mat(t, shape, name):
 def _bdl_layout_ok(*ts):
     """True if every [b,D,l] operand is channel-major (l-stride 1) or every one
     is token-major (D-stride 1)."""
-    ts = [t for t in ts if t is not None]
-    return all(t.stride(2) == 1 for t in ts) or all(t.stride(1) == 1 for t in ts)
+    cm = tm = True
+    for t in ts:
+        if t is not None:
+            st = t.stride()
+            cm = cm and st[2] == 1
+            tm = tm and st[1] == 1
+    return cm or tm
 
 
 # --------------------------------------------------------------------------- selective scan

@@ -355,7 +355,7 @@ def test_kernels_run_on_the_callers_current_stream():
         side.wait_stream(torch.cuda.current_stream())
         with torch.cuda.stream(side):
             from mamba_lite import ops
-            assert ops._stream(ids).value == side.cuda_stream
+            assert ops._stream(ids) == side.cuda_stream
             out, cache = model.prefill(ids)
         side.synchronize()
     assert torch.equal(out, ref)
