@@ -77,6 +77,66 @@ quant_int8_tok_kernel(PartPtrs pp, int nparts, int64_t rows, int cols, float* __
     }
 }
 
+// The same arithmetic with four adjacent columns per lane (cols % 4 == 0,
+// 16-byte aligned rows): float4 loads, the four codes of a lane packed into
+// one 4-byte store (a wavefront writes whole 256-byte runs of the payload,
+// where one byte per lane wrote partial lines), float4 output stores.
+template <int PER4>
+__global__ void __launch_bounds__(kQThreads)
+quant_int8_tok_vec_kernel(PartPtrs pp, int nparts, int64_t rows, int cols, float* __restrict__ out) {
+#pragma clang fp contract(off)
+    typedef float F4 __attribute__((ext_vector_type(4)));
+    const int lane = threadIdx.x & 63;
+    const int64_t row = (int64_t)blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
+    if (row >= rows) return;  // uniform over the wavefront
+    const int64_t base = row * cols;
+    const int cols4 = cols >> 2;
+
+    float acc[PER4][4];
+#pragma unroll
+    for (int j = 0; j < PER4; ++j)
+#pragma unroll
+        for (int k = 0; k < 4; ++k) acc[j][k] = 0.f;
+
+    for (int r = 0; r < nparts; ++r) {
+        const F4* src = reinterpret_cast<const F4*>(pp.p[r] + base);
+        F4 v[PER4];
+        float amax = 0.f;
+#pragma unroll
+        for (int j = 0; j < PER4; ++j) {
+            const int c4 = lane + 64 * j;
+            v[j] = c4 < cols4 ? src[c4] : F4{0.f, 0.f, 0.f, 0.f};
+            amax = fmaxf(amax, fmaxf(fmaxf(fabsf(v[j].x), fabsf(v[j].y)), fmaxf(fabsf(v[j].z), fabsf(v[j].w))));
+        }
+        amax = group_max<64>(amax);
+        const float scale = fmaxf(amax, 1e-8f) / 127.0f;
+        uint8_t* pay = pp.pay[r];
+        if (pay && lane == 0) reinterpret_cast<float*>(pay)[row] = scale;  // 4*rows scale bytes first
+#pragma unroll
+        for (int j = 0; j < PER4; ++j) {
+            const int c4 = lane + 64 * j;
+            if (c4 < cols4) {
+                float q[4];
+                uint32_t packed = 0;
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    q[k] = fminf(fmaxf(rintf(v[j][k] / scale), -127.f), 127.f);
+                    packed |= (uint32_t)(uint8_t)(int8_t)q[k] << (8 * k);
+                    acc[j][k] = acc[j][k] + q[k] * scale;
+                }
+                if (pay) __builtin_nontemporal_store(packed, reinterpret_cast<uint32_t*>(pay + 4 * rows + base) + c4);
+            }
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < PER4; ++j) {
+        const int c4 = lane + 64 * j;
+        if (c4 < cols4)
+            __builtin_nontemporal_store(F4{acc[j][0], acc[j][1], acc[j][2], acc[j][3]},
+                                        reinterpret_cast<F4*>(out + base) + c4);
+    }
+}
+
 // Rows wider than the register tile: the row is re-read from HBM (L2) for
 // every pass instead of held in registers.
 __global__ void __launch_bounds__(kQThreads)
@@ -166,7 +226,19 @@ extern "C" int mtl_quant_dequant_sum_int8_tok(const float* const* parts, int32_t
     dim3 grid((unsigned)((rows + kRowsPerBlock - 1) / kRowsPerBlock));
     const int c = (int)cols;
     const int per_lane = (c + 63) / 64;
-    if (per_lane <= 4) hipLaunchKernelGGL((quant_int8_tok_kernel<4>), grid, dim3(kQThreads), 0, st, pp, nparts, rows, c, out);
+    bool vec = c % 4 == 0 && (uintptr_t)out % 16 == 0;
+    for (int r = 0; r < nparts; ++r)
+        vec = vec && (uintptr_t)pp.p[r] % 16 == 0 && (uintptr_t)pp.pay[r] % 4 == 0;
+    const int per4 = (c / 4 + 63) / 64;
+    if (vec && per4 <= 8) {
+        switch (per4) {
+#define MTL_Q8V_CASE(P4) \
+    case P4: hipLaunchKernelGGL((quant_int8_tok_vec_kernel<P4>), grid, dim3(kQThreads), 0, st, pp, nparts, rows, c, out); break;
+            MTL_Q8V_CASE(1) MTL_Q8V_CASE(2) MTL_Q8V_CASE(3) MTL_Q8V_CASE(4)
+            MTL_Q8V_CASE(5) MTL_Q8V_CASE(6) MTL_Q8V_CASE(7) MTL_Q8V_CASE(8)
+#undef MTL_Q8V_CASE
+        }
+    } else if (per_lane <= 4) hipLaunchKernelGGL((quant_int8_tok_kernel<4>), grid, dim3(kQThreads), 0, st, pp, nparts, rows, c, out);
     else if (per_lane <= 8) hipLaunchKernelGGL((quant_int8_tok_kernel<8>), grid, dim3(kQThreads), 0, st, pp, nparts, rows, c, out);
     else if (per_lane <= 16) hipLaunchKernelGGL((quant_int8_tok_kernel<16>), grid, dim3(kQThreads), 0, st, pp, nparts, rows, c, out);
     else if (per_lane <= kMaxColsPerLane) hipLaunchKernelGGL((quant_int8_tok_kernel<kMaxColsPerLane>), grid, dim3(kQThreads), 0, st, pp, nparts, rows, c, out);

@@ -16,7 +16,8 @@ def _student(rng, shape):
     return (rng.standard_t(3, shape) * 0.5).astype(np.float32)
 
 
-@pytest.mark.parametrize("rows,cols", [(1024, 768), (1000, 80), (33, 160), (5, 2048), (3, 4097), (17, 1)])
+@pytest.mark.parametrize("rows,cols", [(1024, 768), (1000, 80), (33, 160), (5, 2048), (3, 4097), (17, 1),
+                                       (7, 1028), (9, 12), (4, 770)])
 @pytest.mark.parametrize("nparts", [2, 1, 3])
 def test_int8_tok_bit_exact(rows, cols, nparts):
     rng = np.random.default_rng(rows * 7 + cols + nparts)
