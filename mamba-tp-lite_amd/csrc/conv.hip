@@ -267,7 +267,7 @@ __global__ void __launch_bounds__(256) conv_step_xproj_kernel(float* __restrict_
 
     // every load first, with clamped addresses: the block's x_proj columns
     // (8 threads per channel row, element j = tid % 8 + 8 k), then the conv
-    // operands of pair e = tid + 256 q (channel fastest)
+    // operands of pair tid + 256 q (channel fastest)
     constexpr int kWLoads = kXpMaxJQ * 32 / 8;
     const int wc = tid >> 3, wj = tid & 7;
     const float* wrow = WxT + (int64_t)(c0 + min(wc, nch - 1)) * J;
@@ -278,7 +278,6 @@ __global__ void __launch_bounds__(256) conv_step_xproj_kernel(float* __restrict_
     float win[TB][K], wk[TB][K], bs[TB];
 #pragma unroll
     for (int q = 0; q < TB; ++q) {
-        const int e = tid + 256 * q;
         const int ch = c0 + min(tid % kXpCB, nch - 1), bi = min(tid / kXpCB + 8 * q, batch - 1);
         const float* s = state + ((int64_t)bi * D + ch) * (K - 1);
 #pragma unroll
