@@ -461,7 +461,9 @@ def main():
                          "frac": gbps / HBM_PEAK_GBPS,
                          "traffic": traffic_from_profiles("scan_fp32_b32_d1536_l1024"),
                          "kernel": "scan_fwd_kernel<float, NW=4, SPW=4, TT=16, channel-major>",
-                         "algorithmic_bytes": SCAN_BYTES},
+                         "algorithmic_bytes": SCAN_BYTES,
+                         "limiter": "VALU issue, not HBM: 106 VALU instructions per 64 (channel, step) pairs, "
+                                    "80 of them the 16-state recurrence; 81% VALU busy (rocprofv3 counters)"},
         })
         extra["scan_trials_ms"] = trials
         log(f"scan: {ms*1000:.1f} us/call, {gbps:.0f} GB/s ({gbps/HBM_PEAK_GBPS:.1%} of peak), {wall:.1f}s")
