@@ -43,6 +43,15 @@ __device__ __forceinline__ void wave_sum(float* v) {
     for (int i = 0; i < B; ++i) v[i] = group_sum<64>(v[i]);
 }
 
+// Weight rows are read once per token and are larger than the caches (516 MB
+// at the 130m shape), so they are loaded nontemporally: 130m batch 1 went
+// from 338.5 to 320.3 us per token and 1.4b batch 1 from 1517 to 1468 us.
+__device__ __forceinline__ float4 ntload4(const float4* p) {
+    typedef float F4 __attribute__((ext_vector_type(4)));
+    const F4 v = __builtin_nontemporal_load(reinterpret_cast<const F4*>(p));
+    return make_float4(v.x, v.y, v.z, v.w);
+}
+
 __device__ __forceinline__ float dot4(const float4 w, const float4 x, float acc) {
     return fmaf(w.x, x.x, fmaf(w.y, x.y, fmaf(w.z, x.z, fmaf(w.w, x.w, acc))));
 }
@@ -115,7 +124,7 @@ __global__ void __launch_bounds__(kThreads) decode_in_kernel(const InArgs a) {
     for (int g = 0; g < G; ++g)
 #pragma unroll
         for (int p = 0; p < PL; ++p)
-            w[g][p] = reinterpret_cast<const float4*>(rows[g])[min(p * 64 + lane, K4 - 1)];
+            w[g][p] = ntload4(reinterpret_cast<const float4*>(rows[g]) + min(p * 64 + lane, K4 - 1));
 
     // conv operands of (channel, batch) pair tid (clamped to a valid pair)
     const int npair = nch * B;
@@ -277,7 +286,7 @@ __global__ void __launch_bounds__(kThreads) decode_gemv_kernel(const GemvArgs a)
     const float4* row = reinterpret_cast<const float4*>(a.W + (int64_t)m * K);
     float4 w[PL];
 #pragma unroll
-    for (int p = 0; p < PL; ++p) w[p] = row[min(p * 64 + lane, K4 - 1)];
+    for (int p = 0; p < PL; ++p) w[p] = ntload4(row + min(p * 64 + lane, K4 - 1));
     const float bias = a.bias ? a.bias[m] : 0.f;
     float xin[B];
 #pragma unroll
@@ -350,7 +359,7 @@ __global__ void __launch_bounds__(kThreads) decode_gemv_split_kernel(const GemvA
     const float4* row = reinterpret_cast<const float4*>(a.W + (int64_t)m * K);
     float4 w[PLW];
 #pragma unroll
-    for (int p = 0; p < PLW; ++p) w[p] = row[min((wave * PLW + p) * 64 + lane, K4 - 1)];
+    for (int p = 0; p < PLW; ++p) w[p] = ntload4(row + min((wave * PLW + p) * 64 + lane, K4 - 1));
     const float bias = a.bias ? a.bias[m] : 0.f;
     float xin[B];
 #pragma unroll
