@@ -97,7 +97,8 @@ int mtl_selective_scan_fwd(const mtl_scan_params* p, mtl_stream_t stream);
  *
  * x, out: [b, D, l] strided (sb, sd, sl); w: [D, K] fp32 contiguous;
  * bias: [D] fp32 nullable; conv_state_in/out: contiguous [b, D, K-1] in the
- * activation dtype, nullable, must not alias each other.  2 <= K <= 8.
+ * activation dtype, nullable, must not alias each other.  1 <= K <= 8
+ * (K = 1 carries no history: the states are empty and may be NULL).
  * ---------------------------------------------------------------------- */
 typedef struct {
     const void* x;   int64_t x_sb, x_sd, x_sl;
@@ -123,6 +124,9 @@ int mtl_causal_conv1d_fwd(const mtl_conv_params* p, mtl_stream_t stream);
  * conv_state: [b, D, K-1] contiguous (activation dtype), updated in place.
  * x: [b, D] with batch stride x_sb (channel stride 1); out: [b, D] with
  * batch stride out_sb.  w: [D, K] fp32; bias: [D] fp32 nullable.
+ * 1 <= K <= 8; with K = 1 conv_state is empty and may be NULL.  (The
+ * reference's step takes x unchanged when d_conv == 1, model.py:275-276:
+ * its caller passes a unit weight and no bias for that.)
  * ---------------------------------------------------------------------- */
 int mtl_conv_step(void* conv_state, const void* x, int64_t x_sb, const float* w, const float* bias,
                   void* out, int64_t out_sb, int64_t batch, int64_t dim, int32_t width,
@@ -179,7 +183,8 @@ int mtl_add_rmsnorm(const float* x, const float* y, float* x_out, const float* w
  * right.
  * The x_proj of the batched step (model.py:279, x_dbl = x_proj(x)) runs as
  * nparts GEMMs over channel chunks on hipBLASLt; this adds their outputs.
- * parts: contiguous fp32 [nparts, n]; out: fp32 [n].  1 <= nparts <= 128.
+ * parts: contiguous fp32 [nparts, n]; out: fp32 [n].  nparts >= 1 (with
+ * nparts * n elements addressable by int64).
  * ---------------------------------------------------------------------- */
 int mtl_sum_parts(const float* parts, int32_t nparts, int64_t n, float* out, mtl_stream_t stream);
 
@@ -217,8 +222,10 @@ int mtl_quant_dequant_sum_fp16(const float* const* parts, int32_t nparts, int64_
  * runs as its own row GEMV) instead of one per ATen op, every weight byte
  * read once.  Deterministic: no atomics, fixed summation orders.
  *
- * mtl_decode_in: x [b, M] (or, for the first layer, emb [V, M] + ids [b],
- *   with resid_out [b, M] receiving the gathered rows, model.py:348) ->
+ * mtl_decode_in: x [b, M] (or, for the first layer, emb [vocab, M] + ids
+ *   [b], with resid_out [b, M] receiving the gathered rows, model.py:348; an
+ *   id outside [0, vocab) makes that batch row NaN instead of reading
+ *   outside the table, where the reference's nn.Embedding raises) ->
  *   RMSNorm (norm_w, eps; model.py:130-135) -> in_proj rows W_in [2D, M]
  *   (+ b_in) of channel blocks of `channels_per_block` (must be 8: one
  *   workgroup per 8 channels, 4 in_proj rows per wavefront; model.py:261) ->
@@ -241,7 +248,7 @@ int mtl_quant_dequant_sum_fp16(const float* const* parts, int32_t nparts, int64_
  *   y [b, D] = (C . h + D x) * gz (model.py:290-292).  N <= 16.
  * All pointers are device memory; W_in, W and v must be 16-byte aligned.
  * ---------------------------------------------------------------------- */
-int mtl_decode_in(const float* x, const float* emb, const int64_t* ids, float* resid_out, const float* norm_w,
+int mtl_decode_in(const float* x, const float* emb, const int64_t* ids, int32_t vocab, float* resid_out, const float* norm_w,
                   float eps, const float* W_in, const float* b_in, float* conv_state, const float* conv_w,
                   const float* conv_b, const float* W_xT, float* xc, float* gz, float* xpart, int32_t batch,
                   int32_t d_model, int32_t d_inner, int32_t d_conv, int32_t xdbl_cols, int32_t channels_per_block,

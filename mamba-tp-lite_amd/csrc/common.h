@@ -129,6 +129,29 @@ __device__ __forceinline__ float group_max(float v) {
     return v;
 }
 
+// Max over a 16- or 64-lane group of unsigned words (same lane moves as
+// group_max).  On the bit patterns of |x| (sign cleared) this is a float max
+// that returns NaN when any input is NaN -- fmaxf would drop it.
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_mov_u(uint32_t v) {
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xF, 0xF, false);
+}
+__device__ __forceinline__ uint32_t lane_read_u(uint32_t v, int lane) {
+    return (uint32_t)__builtin_amdgcn_readlane((int)v, lane);
+}
+template <int WIDTH>
+__device__ __forceinline__ uint32_t group_umax(uint32_t v) {
+    static_assert(WIDTH == 16 || WIDTH == 64, "16 or 64 lanes");
+    v = max(v, dpp_mov_u<kDppXor1>(v));
+    v = max(v, dpp_mov_u<kDppXor2>(v));
+    v = max(v, dpp_mov_u<kDppHalfMirror>(v));
+    v = max(v, dpp_mov_u<kDppRowMirror>(v));
+    if constexpr (WIDTH == 64)
+        v = max(max(lane_read_u(v, 0), lane_read_u(v, 16)), max(lane_read_u(v, 32), lane_read_u(v, 48)));
+    return v;
+}
+__device__ __forceinline__ uint32_t abs_bits(float x) { return __float_as_uint(x) & 0x7fffffffu; }
+
 // Fixed-count register blocking: kernels that hold RUNS values per lane are
 // instantiated for these counts; a size needing `need` runs uses the
 // smallest instantiated count >= need (the extra runs are masked).

@@ -195,7 +195,7 @@ int launch_conv_vc(const ConvArgs& a, int64_t batch, hipStream_t st) {
     switch (a.K) {
 #define MTL_CONV_CASE(KK) \
     case KK: hipLaunchKernelGGL((conv_fwd_kernel<T, KK, VC, TC>), grid, block, 0, st, a); break;
-        MTL_CONV_CASE(2) MTL_CONV_CASE(3) MTL_CONV_CASE(4) MTL_CONV_CASE(5)
+        MTL_CONV_CASE(1) MTL_CONV_CASE(2) MTL_CONV_CASE(3) MTL_CONV_CASE(4) MTL_CONV_CASE(5)
         MTL_CONV_CASE(6) MTL_CONV_CASE(7) MTL_CONV_CASE(8)
 #undef MTL_CONV_CASE
         default: set_error("conv width unsupported"); return MTL_EINVAL;
@@ -233,7 +233,7 @@ int launch_conv_step(void* state, const void* x, int64_t x_sb, const float* w, c
     switch (K) {
 #define MTL_STEP_CASE(KK) \
     case KK: hipLaunchKernelGGL((conv_step_kernel<T, KK>), grid, block, 0, st, s, xx, x_sb, w, bias, o, o_sb, D, silu); break;
-        MTL_STEP_CASE(2) MTL_STEP_CASE(3) MTL_STEP_CASE(4) MTL_STEP_CASE(5)
+        MTL_STEP_CASE(1) MTL_STEP_CASE(2) MTL_STEP_CASE(3) MTL_STEP_CASE(4) MTL_STEP_CASE(5)
         MTL_STEP_CASE(6) MTL_STEP_CASE(7) MTL_STEP_CASE(8)
 #undef MTL_STEP_CASE
         default: set_error("conv width unsupported"); return MTL_EINVAL;
@@ -352,7 +352,7 @@ extern "C" int mtl_causal_conv1d_fwd(const mtl_conv_params* p, mtl_stream_t stre
     clear_error();
     MTL_REQUIRE(p != nullptr, "null params");
     MTL_REQUIRE(p->batch >= 0 && p->seqlen >= 0 && p->dim >= 0, "negative size");
-    MTL_REQUIRE(p->width >= 2 && p->width <= kMaxK, "width (d_conv) must be in [2, 8]");
+    MTL_REQUIRE(p->width >= 1 && p->width <= kMaxK, "width (d_conv) must be in [1, 8]");
     MTL_REQUIRE(p->batch <= 65535, "batch must be <= 65535");
     MTL_REQUIRE(p->seqlen < (int64_t(1) << 31) && p->dim < (int64_t(1) << 31), "size overflows int32");
     MTL_REQUIRE((p->seqlen + kTC - 1) / kTC <= 65535, "seqlen too long for one launch");
@@ -362,8 +362,8 @@ extern "C" int mtl_causal_conv1d_fwd(const mtl_conv_params* p, mtl_stream_t stre
     if (p->batch == 0 || p->dim == 0) return MTL_OK;
     hipStream_t st = as_stream(stream);
     if (p->seqlen == 0) {
-        if (!p->conv_state_out) return MTL_OK;
         const int64_t n = p->batch * p->dim * (p->width - 1);
+        if (!p->conv_state_out || n == 0) return MTL_OK;
         const unsigned blocks = (unsigned)((n + 255) / 256);
         if (p->dtype == MTL_F32)
             hipLaunchKernelGGL((conv_state_copy_kernel<float>), dim3(blocks), dim3(256), 0, st,
@@ -390,11 +390,11 @@ extern "C" int mtl_conv_step(void* conv_state, const void* x, int64_t x_sb, cons
     using namespace mtl;
     clear_error();
     MTL_REQUIRE(batch >= 0 && dim >= 0, "negative size");
-    MTL_REQUIRE(width >= 2 && width <= kMaxK, "width (d_conv) must be in [2, 8]");
+    MTL_REQUIRE(width >= 1 && width <= kMaxK, "width (d_conv) must be in [1, 8]");
     MTL_REQUIRE(batch <= 65535 && dim < (int64_t(1) << 31), "size out of range");
     MTL_REQUIRE(dtype == MTL_F32 || dtype == MTL_BF16, "dtype must be MTL_F32 or MTL_BF16");
     if (batch == 0 || dim == 0) return MTL_OK;
-    MTL_REQUIRE(conv_state && x && w && out, "null required pointer");
+    MTL_REQUIRE((conv_state || width == 1) && x && w && out, "null required pointer");
     hipStream_t st = as_stream(stream);
     return dtype == MTL_F32
                ? launch_conv_step<float>(conv_state, x, x_sb, w, bias, out, out_sb, batch, (int)dim, width, silu, st)
@@ -409,9 +409,9 @@ extern "C" int mtl_conv_step_xproj(float* conv_state, const float* x, int64_t x_
     clear_error();
     MTL_REQUIRE(batch >= 1 && batch <= 32, "batch must be in [1, 32]");
     MTL_REQUIRE(dim >= 1 && dim < (int64_t(1) << 31), "dim out of range");
-    MTL_REQUIRE(width >= 2 && width <= kMaxK, "width (d_conv) must be in [2, 8]");
+    MTL_REQUIRE(width >= 1 && width <= kMaxK, "width (d_conv) must be in [1, 8]");
     MTL_REQUIRE(xdbl_cols >= 1 && xdbl_cols <= kXpMaxJQ * 32, "xdbl_cols must be in [1, 288]");
-    MTL_REQUIRE(conv_state && x && w && out && W_xT && xpart, "null required pointer");
+    MTL_REQUIRE((conv_state || width == 1) && x && w && out && W_xT && xpart, "null required pointer");
     const dim3 grid((unsigned)((dim + kXpCB - 1) / kXpCB));
     hipStream_t st = as_stream(stream);
     const int D = (int)dim, J = xdbl_cols, B = (int)batch;
@@ -429,7 +429,7 @@ extern "C" int mtl_conv_step_xproj(float* conv_state, const float* x, int64_t x_
         else { MTL_XP_J(KK, 4) }                                         \
         break;
     switch (width) {
-        MTL_XP_K(2) MTL_XP_K(3) MTL_XP_K(4) MTL_XP_K(5) MTL_XP_K(6) MTL_XP_K(7) MTL_XP_K(8)
+        MTL_XP_K(1) MTL_XP_K(2) MTL_XP_K(3) MTL_XP_K(4) MTL_XP_K(5) MTL_XP_K(6) MTL_XP_K(7) MTL_XP_K(8)
         default: break;
     }
 #undef MTL_XP_K

@@ -61,6 +61,7 @@ struct InArgs {
     const float* x;          // [b, M] residual stream (null for the first layer)
     const float* emb;        // [V, M] embedding table (first layer)
     const int64_t* ids;      // [b] token ids (first layer)
+    int V;                   // rows of emb
     float* resid_out;        // [b, M] residual copy written by block 0 (first layer), else null
     const float* norm_w;     // [M]
     const float* W_in;       // [2D, M]
@@ -148,10 +149,22 @@ __global__ void __launch_bounds__(kThreads) decode_in_kernel(const InArgs a) {
     }
 
     // activation rows and norm weights: element e = tid + 256 q
+    // A token id outside [0, V) reads row 0 instead and turns that batch
+    // row's residual into NaN, so its logits come out NaN (no device trap,
+    // no read outside the table).
     const float* rows_in[B];
+    bool id_ok[B];
 #pragma unroll
-    for (int bi = 0; bi < B; ++bi)
-        rows_in[bi] = a.x ? a.x + (int64_t)bi * M : a.emb + a.ids[bi] * (int64_t)M;
+    for (int bi = 0; bi < B; ++bi) {
+        if (a.x) {
+            rows_in[bi] = a.x + (int64_t)bi * M;
+            id_ok[bi] = true;
+        } else {
+            const int64_t id = a.ids[bi];
+            id_ok[bi] = id >= 0 && id < a.V;
+            rows_in[bi] = a.emb + (id_ok[bi] ? id : 0) * (int64_t)M;
+        }
+    }
     float xv[B][PL], nw[PL];
 #pragma unroll
     for (int q = 0; q < PL; ++q) {
@@ -160,6 +173,10 @@ __global__ void __launch_bounds__(kThreads) decode_in_kernel(const InArgs a) {
 #pragma unroll
         for (int bi = 0; bi < B; ++bi) xv[bi][q] = rows_in[bi][e];
     }
+#pragma unroll
+    for (int bi = 0; bi < B; ++bi)
+#pragma unroll
+        for (int q = 0; q < PL; ++q) xv[bi][q] = id_ok[bi] ? xv[bi][q] : __builtin_nanf("");
 
     // ---- 1. sum of squares; norm_w * x into LDS
     float ss[B];
@@ -513,7 +530,7 @@ __global__ void __launch_bounds__(kThreads) decode_ssm_kernel(const SsmArgs a) {
 }  // namespace
 }  // namespace mtl
 
-extern "C" int mtl_decode_in(const float* x, const float* emb, const int64_t* ids, float* resid_out,
+extern "C" int mtl_decode_in(const float* x, const float* emb, const int64_t* ids, int32_t vocab, float* resid_out,
                              const float* norm_w, float eps, const float* W_in, const float* b_in, float* conv_state,
                              const float* conv_w, const float* conv_b, const float* W_xT, float* xc, float* gz,
                              float* xpart, int32_t batch, int32_t d_model, int32_t d_inner, int32_t d_conv,
@@ -526,12 +543,13 @@ extern "C" int mtl_decode_in(const float* x, const float* emb, const int64_t* id
     MTL_REQUIRE(d_inner >= 1 && d_conv >= 2 && d_conv <= kMaxConv && xdbl_cols >= 1, "bad sizes");
     MTL_REQUIRE(channels_per_block == kCB, "channels_per_block must be 8");
     MTL_REQUIRE((x != nullptr) != (emb != nullptr && ids != nullptr), "give either x or (emb, ids)");
+    MTL_REQUIRE(x != nullptr || vocab >= 1, "vocab must be >= 1 with (emb, ids)");
     MTL_REQUIRE(norm_w && W_in && conv_state && conv_w && xc && gz, "null required pointer");
     MTL_REQUIRE((W_xT == nullptr) == (xpart == nullptr), "W_xT and xpart go together");
     MTL_REQUIRE(((uintptr_t)W_in % 16) == 0, "W_in must be 16-byte aligned");
     const size_t smem = sizeof(float) * (size_t)batch * d_model;
     MTL_REQUIRE(smem <= 60 * 1024, "batch * d_model too large for the decode LDS tile");
-    InArgs a{x, emb, ids, resid_out, norm_w, W_in, b_in, conv_state, conv_w, conv_b, W_xT, xc, gz, xpart,
+    InArgs a{x, emb, ids, vocab, resid_out, norm_w, W_in, b_in, conv_state, conv_w, conv_b, W_xT, xc, gz, xpart,
              d_model, d_inner, d_conv, xdbl_cols, eps};
     const dim3 grid((unsigned)(2 * ((d_inner + kCB - 1) / kCB)));   // x-row blocks, then z-row blocks
     hipStream_t st = as_stream(stream);

@@ -11,7 +11,12 @@
 // rounded fp32 divide; this file must never be built with fast-math), rint
 // is round-half-to-even, and the dequantize-sum runs with FP contraction off
 // so every q*s and every + rounds once, as torch's separate CPU ops do.
-// amax is a max of absolute values: order-independent, hence exact.
+// amax is a max of absolute values: order-independent, hence exact.  It is
+// taken on the bit patterns of |x| as unsigned words, so a NaN in the row
+// makes amax NaN, as torch's amax does (tp_utils.py:111); the clamp at 1e-8
+// keeps the NaN (torch.clamp does), the row's scale is NaN and its outputs
+// are NaN.  The codes of such a row are -127 here; the reference's
+// float -> int8 conversion of NaN has no defined value.
 
 #include "common.h"
 
@@ -49,15 +54,15 @@ quant_int8_tok_kernel(PartPtrs pp, int nparts, int64_t rows, int cols, float* __
     for (int r = 0; r < nparts; ++r) {
         const float* src = pp.p[r] + base;
         float v[PER_LANE];
-        float amax = 0.f;
+        uint32_t abits = 0;
 #pragma unroll
         for (int j = 0; j < PER_LANE; ++j) {
             const int col = lane + 64 * j;
             v[j] = col < cols ? src[col] : 0.f;
-            amax = fmaxf(amax, fabsf(v[j]));
+            abits = max(abits, abs_bits(v[j]));
         }
-        amax = group_max<64>(amax);
-        const float scale = fmaxf(amax, 1e-8f) / 127.0f;
+        const float amax = __uint_as_float(group_umax<64>(abits));
+        const float scale = (amax < 1e-8f ? 1e-8f : amax) / 127.0f;
         uint8_t* pay = pp.pay[r];
         if (pay && lane == 0) reinterpret_cast<float*>(pay)[row] = scale;  // 4*rows scale bytes first
 #pragma unroll
@@ -101,15 +106,15 @@ quant_int8_tok_vec_kernel(PartPtrs pp, int nparts, int64_t rows, int cols, float
     for (int r = 0; r < nparts; ++r) {
         const F4* src = reinterpret_cast<const F4*>(pp.p[r] + base);
         F4 v[PER4];
-        float amax = 0.f;
+        uint32_t abits = 0;
 #pragma unroll
         for (int j = 0; j < PER4; ++j) {
             const int c4 = lane + 64 * j;
             v[j] = c4 < cols4 ? src[c4] : F4{0.f, 0.f, 0.f, 0.f};
-            amax = fmaxf(amax, fmaxf(fmaxf(fabsf(v[j].x), fabsf(v[j].y)), fmaxf(fabsf(v[j].z), fabsf(v[j].w))));
+            abits = max(abits, max(max(abs_bits(v[j].x), abs_bits(v[j].y)), max(abs_bits(v[j].z), abs_bits(v[j].w))));
         }
-        amax = group_max<64>(amax);
-        const float scale = fmaxf(amax, 1e-8f) / 127.0f;
+        const float amax = __uint_as_float(group_umax<64>(abits));
+        const float scale = (amax < 1e-8f ? 1e-8f : amax) / 127.0f;
         uint8_t* pay = pp.pay[r];
         if (pay && lane == 0) reinterpret_cast<float*>(pay)[row] = scale;  // 4*rows scale bytes first
 #pragma unroll
@@ -148,10 +153,10 @@ quant_int8_tok_wide_kernel(PartPtrs pp, int nparts, int64_t rows, int cols, floa
     const int64_t base = row * cols;
     for (int r = 0; r < nparts; ++r) {
         const float* src = pp.p[r] + base;
-        float amax = 0.f;
-        for (int col = lane; col < cols; col += 64) amax = fmaxf(amax, fabsf(src[col]));
-        amax = group_max<64>(amax);
-        const float scale = fmaxf(amax, 1e-8f) / 127.0f;
+        uint32_t abits = 0;
+        for (int col = lane; col < cols; col += 64) abits = max(abits, abs_bits(src[col]));
+        const float amax = __uint_as_float(group_umax<64>(abits));
+        const float scale = (amax < 1e-8f ? 1e-8f : amax) / 127.0f;
         uint8_t* pay = pp.pay[r];
         if (pay && lane == 0) reinterpret_cast<float*>(pay)[row] = scale;
         for (int col = lane; col < cols; col += 64) {

@@ -310,14 +310,18 @@ __global__ void __launch_bounds__(NW * 64, CM ? 3 : 4) scan_fwd_kernel(const Sca
         for (int kc = 0; kc < KC; ++kc) {
             const int t0 = tb + kc * TT + ot;
             if constexpr (CM && VEC) {
-                // a partial tile reads past L into the next row (or past the
-                // resource, which returns 0); staging masks those steps
-                const uint32_t so = (uint32_t)(tb + kc * TT) * (uint32_t)sizeof(T);
+                // Full tiles put the tile's first step in the SGPR offset.  A
+                // partial tile reads past L into the next row, or past the end
+                // of the resource on the last row: its step goes into the VGPR
+                // offset, which the buffer range check covers (reads past the
+                // resource return 0); staging masks those steps either way.
+                const uint32_t st = (uint32_t)(tb + kc * TT) * (uint32_t)sizeof(T);
+                const uint32_t so = F ? st : 0u, vs = F ? 0u : st;
 #pragma unroll
                 for (int q = 0; q < E / 4; ++q) {
-                    Buf4<T>::load(ru_cm, vo_u + q * 4 * sizeof(T), so, &r.u[kc][4 * q]);
-                    Buf4<T>::load(rd_cm, vo_d + q * 4 * sizeof(T), so, &r.d[kc][4 * q]);
-                    Buf4<T>::load(rz_cm, vo_z + q * 4 * sizeof(T), so, &r.z[kc][4 * q]);
+                    Buf4<T>::load(ru_cm, vo_u + vs + q * 4 * sizeof(T), so, &r.u[kc][4 * q]);
+                    Buf4<T>::load(rd_cm, vo_d + vs + q * 4 * sizeof(T), so, &r.d[kc][4 * q]);
+                    Buf4<T>::load(rz_cm, vo_z + vs + q * 4 * sizeof(T), so, &r.z[kc][4 * q]);
                 }
             } else if constexpr (CM && F) {
                 load_run<T, E, VEC>(up + t0, r.u[kc]);

@@ -134,6 +134,31 @@ __global__ void __launch_bounds__(256) sum_parts4_kernel(const float* __restrict
     }
 }
 
+// The same four-quarter order for any part count: each quarter's parts are
+// summed by a runtime-count loop (a load round trip per part, for the part
+// counts above 128 that only models wider than d_inner 4096 reach).
+__global__ void __launch_bounds__(256) sum_parts4_any_kernel(const float* __restrict__ parts, int nparts, int64_t n,
+                                                             float* __restrict__ out) {
+    __shared__ float s_q[4][64];
+    const int oq = threadIdx.x & 63, q = threadIdx.x >> 6;
+    const int64_t i = (int64_t)blockIdx.x * 64 + oq;
+    const int64_t ii = min(i, n - 1);
+    const int per = (nparts + 3) / 4, p0 = q * per, np = min(per, nparts - p0);
+    float acc = 0.f;
+    if (np > 0) {
+        acc = parts[(int64_t)p0 * n + ii];
+        for (int u = 1; u < np; ++u) acc += parts[(int64_t)(p0 + u) * n + ii];
+    }
+    s_q[q][oq] = acc;
+    __syncthreads();
+    if (q == 0 && i < n) {
+        float r = s_q[0][oq];
+#pragma unroll
+        for (int k = 1; k < 4; ++k) r = k * per < nparts ? r + s_q[k][oq] : r;
+        out[i] = r;
+    }
+}
+
 // out[i] = parts[0][i] + parts[1][i] + ... in part order (split-K partials)
 template <int P>
 __global__ void __launch_bounds__(256) sum_parts_kernel(const float* __restrict__ parts, int nparts, int64_t n,
@@ -293,7 +318,7 @@ extern "C" int mtl_add_rmsnorm(const float* x, const float* y, float* x_out, con
 extern "C" int mtl_sum_parts(const float* parts, int32_t nparts, int64_t n, float* out, mtl_stream_t stream) {
     using namespace mtl;
     clear_error();
-    MTL_REQUIRE(nparts >= 1 && nparts <= 128 && n >= 0, "nparts must be in [1, 128]");
+    MTL_REQUIRE(nparts >= 1 && n >= 0, "nparts must be >= 1");
     if (n == 0) return MTL_OK;
     MTL_REQUIRE(parts && out, "null required pointer");
     MTL_REQUIRE(n < (int64_t(1) << 31), "n too large");
@@ -303,6 +328,7 @@ extern "C" int mtl_sum_parts(const float* parts, int32_t nparts, int64_t n, floa
     else if (nparts <= 16) hipLaunchKernelGGL((sum_parts_kernel<16>), grid, dim3(256), 0, st, parts, nparts, n, out);
     else if (nparts <= 32) hipLaunchKernelGGL((sum_parts_kernel<32>), grid, dim3(256), 0, st, parts, nparts, n, out);
     else if (nparts <= 64) hipLaunchKernelGGL((sum_parts4_kernel<16>), grid4, dim3(256), 0, st, parts, nparts, n, out);
-    else hipLaunchKernelGGL((sum_parts4_kernel<32>), grid4, dim3(256), 0, st, parts, nparts, n, out);
+    else if (nparts <= 128) hipLaunchKernelGGL((sum_parts4_kernel<32>), grid4, dim3(256), 0, st, parts, nparts, n, out);
+    else hipLaunchKernelGGL(sum_parts4_any_kernel, grid4, dim3(256), 0, st, parts, nparts, n, out);
     return check_launch("sum_parts");
 }

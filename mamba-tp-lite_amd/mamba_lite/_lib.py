@@ -15,7 +15,7 @@ import os
 import torch  # noqa: F401  (must be loaded first, see module docstring)
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libmtl.so")
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 MTL_F32 = 0
 MTL_BF16 = 1
@@ -68,7 +68,7 @@ SIGNATURES = {
     "mtl_quant_dequant_sum_int8_tok": (ctypes.c_int, [ctypes.POINTER(_vp), _i32, _i64, _i64,
                                                       ctypes.POINTER(_vp), _fp, _vp]),
     "mtl_quant_dequant_sum_fp16": (ctypes.c_int, [ctypes.POINTER(_vp), _i32, _i64, ctypes.POINTER(_vp), _fp, _vp]),
-    "mtl_decode_in": (ctypes.c_int, [_fp, _fp, _vp, _fp, _fp, ctypes.c_float, _fp, _fp, _fp, _fp, _fp, _fp, _fp, _fp,
+    "mtl_decode_in": (ctypes.c_int, [_fp, _fp, _vp, _i32, _fp, _fp, ctypes.c_float, _fp, _fp, _fp, _fp, _fp, _fp, _fp, _fp,
                                      _fp, _i32, _i32, _i32, _i32, _i32, _i32, _vp]),
     "mtl_decode_gemv": (ctypes.c_int, [_fp, _fp, _fp, _fp, _fp, _i32, _i32, _i32, _vp]),
     "mtl_decode_norm_gemv": (ctypes.c_int, [_fp, _fp, ctypes.c_float, _fp, _fp, _fp, _i32, _i32, _i32, _vp]),

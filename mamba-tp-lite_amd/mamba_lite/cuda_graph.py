@@ -72,8 +72,21 @@ class GraphedStepper:
         except RuntimeError as e:
             self.graph = None
             raise CUDAGraphUnsupported(f"graph capture failed: {e}") from e
+        # the step reads derived weight copies (transposed x_proj, the fused
+        # decode plan) at addresses now baked into the graph: keep them alive,
+        # and remember which parameter versions they were built from
+        key_fn = getattr(self.model, "_derived_key", None)
+        self._derived_key = key_fn() if key_fn is not None else None
+        held_fn = getattr(self.model, "_derived_tensors", None)
+        self._held = held_fn() if held_fn is not None else None
 
     def replay(self, next_id: torch.Tensor) -> torch.Tensor:
+        if self.graph is None:
+            raise RuntimeError("call capture() before replay()")
+        if self._derived_key is not None and self.model._derived_key() != self._derived_key:
+            # the reference's graph reads the parameters themselves; this one
+            # reads copies made at capture, so a weight update needs a new capture
+            raise RuntimeError("model weights changed after capture(); capture again before replaying")
         self.static_ids.copy_(next_id)
         self.graph.replay()
         return self.static_logits

@@ -215,6 +215,21 @@ class MambaMixer(nn.Module):
         w = self.conv1d.weight
         return _f32(w.reshape(w.shape[0], w.shape[-1]))
 
+    def _step_conv(self):
+        """(weight [D, K], bias) of the single-token conv.  With d_conv == 1 the
+        reference's step uses x as is, with neither the 1-tap weight nor the
+        conv bias (model.py:265-276), while its prefill applies both
+        (206-208): the step then runs the kernel with a unit weight and no
+        bias, which returns x exactly."""
+        if self.cfg.d_conv > 1:
+            return self._conv_w(), _f32(self.conv1d.bias)
+        w = self.conv1d.weight
+        ones = getattr(self, "_unit_conv_w", None)
+        if ones is None or ones.device != w.device or ones.shape[0] != w.shape[0]:
+            ones = torch.ones(w.shape[0], 1, device=w.device, dtype=torch.float32)
+            self._unit_conv_w = ones
+        return ones, None
+
     def prefill(self, x: torch.Tensor, cache: LayerCache | None = None, out: LayerCache | None = None):
         """x: [b, l, d_model] -> (out [b, l, d_model], conv_state [b, D, K-1],
         ssm_state [b, D, N]) -- reference model.py:184-241.  The cache is read
@@ -289,13 +304,13 @@ class MambaMixer(nn.Module):
         xz = self.in_proj(x_t)                                   # [b, 2D]
         b = x_t.shape[0]
         J = R + 2 * self.cfg.d_state
+        conv_w, conv_b = self._step_conv()
         if xz.dtype == torch.float32 and b <= 32 and J <= 288 and cache.conv_state.dtype == torch.float32:
             # conv step and the x_proj partials of 32-channel blocks in one kernel
-            xc, xpart = ops.conv_step_xproj(cache.conv_state, xz[:, :Dm], self._conv_w(), _f32(self.conv1d.bias),
-                                            self._xproj_t())
+            xc, xpart = ops.conv_step_xproj(cache.conv_state, xz[:, :Dm], conv_w, conv_b, self._xproj_t())
             x_dbl = ops.sum_parts(xpart)                         # [b, R+2N]
         else:
-            xc = ops.conv_step(cache.conv_state, xz[:, :Dm], self._conv_w(), _f32(self.conv1d.bias), silu=True)
+            xc = ops.conv_step(cache.conv_state, xz[:, :Dm], conv_w, conv_b, silu=True)
             x_dbl = self._x_proj_step(xc)                        # [b, R+2N]
         y = ops.selective_state_update(cache.ssm_state, xc, xz[:, Dm:], x_dbl, _f32(self.dt_proj.weight),
                                        _f32(self.dt_proj.bias), _f32(self.A_log), _f32(self.D), a_is_log=True)
@@ -422,7 +437,7 @@ class MambaLM(nn.Module):
         cfg = self.cfg
         b = input_ids.shape[0]
         if b not in (1, 2, 4) or cfg.d_state > 16 or cfg.d_model % 4 or cfg.d_inner % 4 or \
-                b * cfg.d_model > 15 * 1024 or cfg.d_inner > 4096 or cfg.dt_rank > 256 or cfg.d_conv > 8:
+                b * cfg.d_model > 15 * 1024 or cfg.d_inner > 4096 or cfg.dt_rank > 256 or not 2 <= cfg.d_conv <= 8:
             return False
         if self.embedding.weight.dtype != torch.float32 or not input_ids.is_cuda:
             return False
@@ -430,12 +445,27 @@ class MambaLM(nn.Module):
         return lc.conv_state.dtype == torch.float32 and lc.ssm_state.dtype == torch.float32 and \
             lc.conv_state.is_contiguous() and lc.ssm_state.is_contiguous()
 
+    def _derived_key(self):
+        """(address, version) of the parameters that derived weight copies are
+        built from: the fused decode plan and the per-op step's transposed
+        x_proj.  A captured graph reads those copies, so it is stale once
+        this key changes."""
+        return tuple((m.mixer.x_proj.weight.data_ptr(), m.mixer.x_proj.weight._version,
+                      m.mixer.conv1d.weight.data_ptr(), m.mixer.conv1d.weight._version) for m in self.layers)
+
+    def _derived_tensors(self):
+        """The derived copies a step reads now (held by a captured graph so a
+        rebuild cannot free memory the graph still addresses)."""
+        held = [getattr(self, "_plan", None)]
+        for m in self.layers:
+            held += [getattr(m.mixer, "_xproj_cache", None), getattr(m.mixer, "_unit_conv_w", None)]
+        return held
+
     def _decode_plan(self):
         """Per-layer tensors of the fused step: x_proj transposed [D, J] for the
         split-K partials, conv weights as [D, K].  Rebuilt whenever a source
         parameter changes (tracked by tensor version and address)."""
-        key = tuple((m.mixer.x_proj.weight.data_ptr(), m.mixer.x_proj.weight._version,
-                     m.mixer.conv1d.weight.data_ptr(), m.mixer.conv1d.weight._version) for m in self.layers)
+        key = self._derived_key()
         plan = getattr(self, "_plan", None)
         if plan is not None and plan["key"] == key:
             return plan
@@ -470,7 +500,7 @@ class MambaLM(nn.Module):
         b, M, D, J = input_ids.shape[0], cfg.d_model, cfg.d_inner, plan["J"]
         split_k = b <= plan["split_k_max_b"]
         dev = input_ids.device
-        ids = input_ids.reshape(-1)
+        ids = input_ids.reshape(-1).contiguous()   # a column slice of a longer id tensor is strided
         f32 = dict(device=dev, dtype=torch.float32)
         xc = torch.empty(b, D, **f32)
         gz = torch.empty(b, D, **f32)

@@ -204,7 +204,8 @@ def causal_conv1d(x, weight, bias=None, conv_state=None, silu=True, out=None, fi
         final_state = torch.empty(b, Dm, K - 1, device=x.device, dtype=x.dtype)
     elif final_state is not None and (tuple(final_state.shape) != (b, Dm, K - 1) or not final_state.is_contiguous()):
         raise ValueError(f"final_state must be contiguous {(b, Dm, K - 1)}")
-    if final_state is not None and conv_state is not None and final_state.data_ptr() == conv_state.data_ptr():
+    if final_state is not None and conv_state is not None and final_state.numel() > 0 and \
+            final_state.data_ptr() == conv_state.data_ptr():
         raise ValueError("final_state must not alias conv_state")
 
     p = _lib.ConvParams()
@@ -212,8 +213,9 @@ def causal_conv1d(x, weight, bias=None, conv_state=None, silu=True, out=None, fi
     p.out, (p.out_sb, p.out_sd, p.out_sl) = out.data_ptr(), out.stride()
     p.w = w.data_ptr()
     p.bias = bias.data_ptr() if bias is not None else None
-    p.conv_state_in = conv_state.data_ptr() if conv_state is not None else None
-    p.conv_state_out = final_state.data_ptr() if final_state is not None else None
+    # K = 1 carries no history: its empty states go over as NULL
+    p.conv_state_in = conv_state.data_ptr() if conv_state is not None and conv_state.numel() else None
+    p.conv_state_out = final_state.data_ptr() if final_state is not None and final_state.numel() else None
     p.batch, p.seqlen, p.dim, p.width = b, L, Dm, K
     p.dtype, p.silu = code, int(bool(silu))
     with _dev_guard(x):
@@ -455,7 +457,8 @@ def decode_in(norm_w, eps, W_in, conv_state, conv_w, xc, gz, *, x=None, emb=None
         if tuple(W_xT.shape) != (D, J) or xpart is None or tuple(xpart.shape) != (nblk, b, J):
             raise ValueError("decode_in: W_xT [D, J] and xpart [nblk, b, J] expected")
     with _dev_guard(xc):
-        _lib.check(_lib.load().mtl_decode_in(_ptr(x), _ptr(emb), _ptr(ids), _ptr(resid_out), _ptr(norm_w), float(eps),
+        _lib.check(_lib.load().mtl_decode_in(_ptr(x), _ptr(emb), _ptr(ids), emb.shape[0] if emb is not None else 0,
+                                             _ptr(resid_out), _ptr(norm_w), float(eps),
                                              _ptr(W_in), _ptr(b_in), _ptr(conv_state), _ptr(conv_w), _ptr(conv_b),
                                              _ptr(W_xT), _ptr(xc), _ptr(gz), _ptr(xpart), b, M, D, K, J,
                                              channels_per_block, _stream(xc)), "decode_in")

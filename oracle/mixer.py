@@ -202,8 +202,13 @@ def mixer_step(p, x_t, conv_state, ssm_state, dtype=np.float32):
     R = P["dt_proj_w"].shape[1]
     xz = _linear(np.asarray(x_t, dtype), P["in_proj_w"], P.get("in_proj_b"))  # model.py:261
     xs, z = xz[..., :Dm], xz[..., Dm:]
-    conv, new_cs = conv_step(conv_state, xs, P["conv_w"], P.get("conv_b"), dtype)
-    conv_state[...] = new_cs                                            # model.py:274
+    if P["conv_w"].shape[1] > 1:
+        conv, new_cs = conv_step(conv_state, xs, P["conv_w"], P.get("conv_b"), dtype)
+        conv_state[...] = new_cs                                        # model.py:274
+    else:
+        # d_conv == 1: the step takes x as is, with neither the 1-tap weight
+        # nor the conv bias (model.py:275-276), unlike prefill (206-208)
+        conv = xs
     xs = silu(conv)                                                     # model.py:277
     x_dbl = _linear(xs, P["x_proj_w"])                                  # model.py:279
     dt_low, B, C = x_dbl[..., :R], x_dbl[..., R:R + N], x_dbl[..., R + N:]

@@ -69,6 +69,8 @@ def test_invalid_arguments_are_rejected_without_a_gpu():
     ("mtl_decode_in", dict(d_model=6), b"d_model"),
     ("mtl_decode_in", dict(channels_per_block=16), b"channels_per_block"),
     ("mtl_decode_in", dict(d_conv=9), b"bad sizes"),
+    ("mtl_decode_in", dict(d_conv=1), b"bad sizes"),
+    ("mtl_decode_in", dict(first_layer=True, vocab=0), b"vocab"),
     ("mtl_decode_gemv", dict(batch=8), b"batch must be 1, 2 or 4"),
     ("mtl_decode_gemv", dict(cols=8192), b"cols"),
     ("mtl_decode_norm_gemv", dict(batch=3), b"batch must be 1, 2 or 4"),
@@ -77,10 +79,11 @@ def test_invalid_arguments_are_rejected_without_a_gpu():
     ("mtl_decode_ssm", dict(dt_rank=300), b"dt_rank"),
     ("mtl_decode_ssm", dict(nblk=1000), b"partial blocks"),
     ("mtl_sum_parts", dict(nparts=0), b"nparts"),
-    ("mtl_sum_parts", dict(nparts=129), b"nparts"),
+    ("mtl_sum_parts", dict(nparts=-3), b"nparts"),
     ("mtl_conv_step_xproj", dict(batch=33), b"batch"),
     ("mtl_conv_step_xproj", dict(xdbl_cols=289), b"xdbl_cols"),
-    ("mtl_conv_step_xproj", dict(width=1), b"width"),
+    ("mtl_conv_step_xproj", dict(width=9), b"width"),
+    ("mtl_conv_step_xproj", dict(width=0), b"width"),
     ("mtl_selective_state_update", dict(dstate=17), b"dstate"),
     ("mtl_selective_state_update", dict(dt_rank=257), b"dt_rank"),
     ("mtl_conv_step", dict(width=9), b"width"),
@@ -94,10 +97,13 @@ def test_entry_points_validate_sizes_on_the_host(case):
     name, over, msg = case
     P = ctypes.c_void_p(16)     # a non-null, 16-byte aligned placeholder that is never used
     if name == "mtl_decode_in":
-        a = dict(batch=1, d_model=64, d_inner=128, d_conv=4, xdbl_cols=36, channels_per_block=8)
+        a = dict(batch=1, d_model=64, d_inner=128, d_conv=4, xdbl_cols=36, channels_per_block=8, first_layer=False,
+                 vocab=0)
         a.update(over)
-        rc = lib.mtl_decode_in(P, None, None, None, P, 1e-5, P, None, P, P, None, None, P, P, None, a["batch"],
-                               a["d_model"], a["d_inner"], a["d_conv"], a["xdbl_cols"], a["channels_per_block"], None)
+        x, emb, ids = (None, P, P) if a["first_layer"] else (P, None, None)
+        rc = lib.mtl_decode_in(x, emb, ids, a["vocab"], None, P, 1e-5, P, None, P, P, None, None, P, P, None,
+                               a["batch"], a["d_model"], a["d_inner"], a["d_conv"], a["xdbl_cols"],
+                               a["channels_per_block"], None)
     elif name == "mtl_decode_gemv":
         a = dict(batch=1, rows=8, cols=64)
         a.update(over)

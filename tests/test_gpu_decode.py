@@ -118,6 +118,51 @@ def test_plan_refreshes_after_weight_change():
         assert torch.equal(p2["layers"][0]["W_xT"], model.layers[0].mixer.x_proj.weight.t().contiguous())
 
 
+def test_graph_replay_refuses_stale_weights():
+    """The captured step reads copies derived from the weights (the fused
+    plan); after an in-place weight update a replay raises instead of using
+    them, and a new capture serves the updated weights."""
+    model = _model(64, 1, 128, seed=4)
+    ids = torch.randint(0, 128, (1, 4), device=DEV)
+    tok = torch.randint(0, 128, (1, 1), device=DEV)
+    with torch.no_grad():
+        _, cg = model.prefill(ids)
+        st = GraphedStepper(model, cg, 1, "cuda")
+        st.capture()
+        st.replay(tok)
+        model.layers[0].mixer.x_proj.weight.mul_(0.5)
+        with pytest.raises(RuntimeError, match="capture again"):
+            st.replay(tok)
+        _, ce = model.prefill(ids)
+        _, cg = model.prefill(ids)
+        st = GraphedStepper(model, cg, 1, "cuda")
+        st.capture()
+        g = st.replay(tok).clone()
+        e = model.step(tok, ce)
+        torch.cuda.synchronize()
+        assert torch.equal(g, e)
+
+
+@pytest.mark.parametrize("b", [1, 2, 4])
+def test_fused_step_out_of_range_id_gives_nan_row(b):
+    """An id outside [0, vocab) reads no memory outside the embedding: that
+    batch row's logits are NaN, the other rows are unaffected."""
+    model = _model(64, 2, 128, seed=6)
+    ids = torch.randint(0, 128, (b, 4), device=DEV)
+    tok = torch.randint(0, 128, (b, 1), device=DEV)
+    bad = tok.clone()
+    bad[b - 1, 0] = 128 if b != 2 else -1
+    with torch.no_grad():
+        _, c1 = model.prefill(ids)
+        _, c2 = model.prefill(ids)
+        assert model._fused_step_ok(tok, c1)
+        good = model.step(tok, c1)
+        got = model.step(bad, c2)
+    assert torch.isnan(got[b - 1]).all()
+    if b > 1:
+        assert torch.equal(got[:b - 1], good[:b - 1])
+
+
 @pytest.mark.parametrize("kw", [dict(d_state=8, d_conv=3, bias=True, conv_bias=False),
                                 dict(d_state=4, d_conv=2, dt_rank=5),
                                 dict(d_state=16, d_conv=8, bias=True)])
