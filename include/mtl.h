@@ -148,6 +148,24 @@ int mtl_conv_step_xproj(float* conv_state, const float* x, int64_t x_sb, const f
                         int32_t width, int32_t xdbl_cols, mtl_stream_t stream);
 
 /* ------------------------------------------------------------------------
+ * Allocation-free form of mtl_conv_step_xproj + mtl_sum_parts.  No
+ * counterpart in the reference: it is for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  Same conv step into out [b, D] and
+ * conv_state as mtl_conv_step_xproj, and x_dbl [b, J] (contiguous) =
+ * the ordered sum of the block partials, exactly as mtl_sum_parts gives
+ * it -- but the partials live in a fixed device array inside the library
+ * (2^20 floats = 4 MiB per GPU, held until the process ends) instead of a
+ * caller buffer.  Rejects ceil(D / 32) * b * J > 2^20 with MTL_EINVAL.
+ * Allocates and frees nothing.  Every call on one GPU shares that GPU's
+ * array: calls that overlap on one GPU (different streams, threads or
+ * processes sharing a context) race and must be serialized by the caller.
+ * ---------------------------------------------------------------------- */
+int mtl_conv_step_xproj_noalloc(float* conv_state, const float* x, int64_t x_sb, const float* w, const float* bias,
+                                float* out, int64_t out_sb, const float* W_xT, float* x_dbl, int64_t batch,
+                                int64_t dim, int32_t width, int32_t xdbl_cols, mtl_stream_t stream);
+
+/* ------------------------------------------------------------------------
  * Single-token selective state update, in place.
  * Replaces model.py:280-292 after x_proj (dt = softplus(F.linear(dt_low,
  * W_dt, b_dt)), dA = exp(dt*A), dBx = dt*B*x, ssm_state.copy_(h*dA + dBx),

@@ -15,6 +15,8 @@
 // consecutive lanes read consecutive vectors: fully coalesced.  Layouts
 // without unit channel stride use one channel per thread.
 
+#include <mutex>
+
 #include "common.h"
 
 namespace mtl {
@@ -402,18 +404,14 @@ extern "C" int mtl_conv_step(void* conv_state, const void* x, int64_t x_sb, cons
                                             st);
 }
 
-extern "C" int mtl_conv_step_xproj(float* conv_state, const float* x, int64_t x_sb, const float* w, const float* bias,
-                                   float* out, int64_t out_sb, const float* W_xT, float* xpart, int64_t batch,
-                                   int64_t dim, int32_t width, int32_t xdbl_cols, mtl_stream_t stream) {
-    using namespace mtl;
-    clear_error();
-    MTL_REQUIRE(batch >= 1 && batch <= 32, "batch must be in [1, 32]");
-    MTL_REQUIRE(dim >= 1 && dim < (int64_t(1) << 31), "dim out of range");
-    MTL_REQUIRE(width >= 1 && width <= kMaxK, "width (d_conv) must be in [1, 8]");
-    MTL_REQUIRE(xdbl_cols >= 1 && xdbl_cols <= kXpMaxJQ * 32, "xdbl_cols must be in [1, 288]");
-    MTL_REQUIRE((conv_state || width == 1) && x && w && out && W_xT && xpart, "null required pointer");
+namespace mtl {
+namespace {
+
+// Launches conv_step_xproj_kernel (sizes already checked).
+int launch_conv_step_xproj(float* conv_state, const float* x, int64_t x_sb, const float* w, const float* bias,
+                           float* out, int64_t out_sb, const float* W_xT, float* xpart, int64_t batch, int64_t dim,
+                           int32_t width, int32_t xdbl_cols, hipStream_t st) {
     const dim3 grid((unsigned)((dim + kXpCB - 1) / kXpCB));
-    hipStream_t st = as_stream(stream);
     const int D = (int)dim, J = xdbl_cols, B = (int)batch;
 #define MTL_XP_LAUNCH(KK, TBV, JQV) hipLaunchKernelGGL((conv_step_xproj_kernel<KK, TBV, JQV>), grid, dim3(256), 0, \
         st, conv_state, x, x_sb, w, bias, out, out_sb, W_xT, xpart, B, D, J)
@@ -436,4 +434,91 @@ extern "C" int mtl_conv_step_xproj(float* conv_state, const float* x, int64_t x_
 #undef MTL_XP_J
 #undef MTL_XP_LAUNCH
     return check_launch("conv_step_xproj");
+}
+
+}  // namespace
+
+// ---- scratch of the allocation-free batched step (mtl_conv_step_xproj_noalloc)
+// The x_proj partials live in this array instead of a caller buffer.  In host
+// code its name is only a stand-in: the device address comes from
+// hipGetSymbolAddress, once per device (each GPU holds its own copy of the
+// array for the life of the process), and only that address is ever handed
+// to a kernel.
+constexpr int64_t kXpScratchFloats = int64_t(1) << 20;     // 4 MiB: nblk * batch * xdbl_cols <= 2^20
+static __device__ __align__(256) float scratch[kXpScratchFloats];
+
+namespace {
+constexpr int kMaxScratchDevices = 64;
+std::mutex g_scratch_mu;
+float* g_scratch_ptr[kMaxScratchDevices] = {};
+
+// Device address of `scratch` on the current device (looked up on the first
+// call on each device).
+int scratch_on_current_device(float** out) {
+    int dev = -1;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) {
+        set_error(std::string("hipGetDevice: ") + hipGetErrorString(e));
+        return MTL_EHIP;
+    }
+    if (dev < 0 || dev >= kMaxScratchDevices) {
+        set_error("device index beyond the scratch table");
+        return MTL_EUNSUPPORTED;
+    }
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (g_scratch_ptr[dev] == nullptr) {
+        void* p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || p == nullptr) {
+            set_error(std::string("hipGetSymbolAddress(scratch): ") + hipGetErrorString(e));
+            return MTL_EHIP;
+        }
+        g_scratch_ptr[dev] = static_cast<float*>(p);
+    }
+    *out = g_scratch_ptr[dev];
+    return MTL_OK;
+}
+
+}  // namespace
+}  // namespace mtl
+
+extern "C" int mtl_conv_step_xproj(float* conv_state, const float* x, int64_t x_sb, const float* w, const float* bias,
+                                   float* out, int64_t out_sb, const float* W_xT, float* xpart, int64_t batch,
+                                   int64_t dim, int32_t width, int32_t xdbl_cols, mtl_stream_t stream) {
+    using namespace mtl;
+    clear_error();
+    MTL_REQUIRE(batch >= 1 && batch <= 32, "batch must be in [1, 32]");
+    MTL_REQUIRE(dim >= 1 && dim < (int64_t(1) << 31), "dim out of range");
+    MTL_REQUIRE(width >= 1 && width <= kMaxK, "width (d_conv) must be in [1, 8]");
+    MTL_REQUIRE(xdbl_cols >= 1 && xdbl_cols <= kXpMaxJQ * 32, "xdbl_cols must be in [1, 288]");
+    MTL_REQUIRE((conv_state || width == 1) && x && w && out && W_xT && xpart, "null required pointer");
+    return launch_conv_step_xproj(conv_state, x, x_sb, w, bias, out, out_sb, W_xT, xpart, batch, dim, width,
+                                  xdbl_cols, as_stream(stream));
+}
+
+extern "C" int mtl_conv_step_xproj_noalloc(float* conv_state, const float* x, int64_t x_sb, const float* w,
+                                           const float* bias, float* out, int64_t out_sb, const float* W_xT,
+                                           float* x_dbl, int64_t batch, int64_t dim, int32_t width,
+                                           int32_t xdbl_cols, mtl_stream_t stream) {
+    using namespace mtl;
+    clear_error();
+    MTL_REQUIRE(batch >= 1 && batch <= 32, "batch must be in [1, 32]");
+    MTL_REQUIRE(dim >= 1 && dim < (int64_t(1) << 31), "dim out of range");
+    MTL_REQUIRE(width >= 1 && width <= kMaxK, "width (d_conv) must be in [1, 8]");
+    MTL_REQUIRE(xdbl_cols >= 1 && xdbl_cols <= kXpMaxJQ * 32, "xdbl_cols must be in [1, 288]");
+    const int64_t nblk = (dim + kXpCB - 1) / kXpCB;
+    MTL_REQUIRE(nblk * batch * xdbl_cols <= kXpScratchFloats,
+                "ceil(dim / 32) * batch * xdbl_cols exceeds the 2^20-float scratch; use mtl_conv_step_xproj with "
+                "a caller buffer");
+    MTL_REQUIRE((conv_state || width == 1) && x && w && out && W_xT && x_dbl, "null required pointer");
+    float* part = nullptr;
+    const int rc = scratch_on_current_device(&part);
+    if (rc != MTL_OK) return rc;
+    hipStream_t st = as_stream(stream);
+    // every [block, row, column] of the partials is written before it is read:
+    // nothing in the scratch needs clearing between calls
+    const int r1 = launch_conv_step_xproj(conv_state, x, x_sb, w, bias, out, out_sb, W_xT, part, batch, dim, width,
+                                          xdbl_cols, st);
+    if (r1 != MTL_OK) return r1;
+    return mtl_sum_parts(part, (int32_t)nblk, batch * xdbl_cols, x_dbl, stream);
 }

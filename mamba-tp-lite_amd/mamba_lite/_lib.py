@@ -65,6 +65,8 @@ SIGNATURES = {
     "mtl_sum_parts": (ctypes.c_int, [_fp, _i32, _i64, _fp, _vp]),
     "mtl_conv_step_xproj": (ctypes.c_int, [_fp, _fp, _i64, _fp, _fp, _fp, _i64, _fp, _fp, _i64, _i64, _i32, _i32,
                                            _vp]),
+    "mtl_conv_step_xproj_noalloc": (ctypes.c_int, [_fp, _fp, _i64, _fp, _fp, _fp, _i64, _fp, _fp, _i64, _i64, _i32,
+                                                   _i32, _vp]),
     "mtl_quant_dequant_sum_int8_tok": (ctypes.c_int, [ctypes.POINTER(_vp), _i32, _i64, _i64,
                                                       ctypes.POINTER(_vp), _fp, _vp]),
     "mtl_quant_dequant_sum_fp16": (ctypes.c_int, [ctypes.POINTER(_vp), _i32, _i64, ctypes.POINTER(_vp), _fp, _vp]),
