@@ -46,6 +46,22 @@ def log(msg):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
+def host_info():
+    """The host the cpu_baseline legs ran on: logical CPUs, torch's intra-op
+    thread count and the CPU model string."""
+    import torch
+    model = None
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"cpu_count": os.cpu_count(), "torch_num_threads": torch.get_num_threads(), "cpu_model": model}
+
+
 def dt_bias_init(D, seed):
     """dt_proj.bias = inv_softplus(dt), dt log-uniform in [1e-3, 0.1] (the HF
     Mamba init): inv_softplus(y) = y + log(-expm1(-y))."""
@@ -96,6 +112,13 @@ def make_scan_inputs(dev, seed=0):
     )
 
 
+# Wall time of scan launches run before the timed trials: the GPU's clocks
+# and power state settle over the first second or two of sustained load (a
+# short warmup left the first trials ~10% slow), so every run is timed in the
+# same steady state.
+SCAN_PREWARM_S = 2.0
+
+
 def bench_scan(dev, steps, warmup):
     import torch
     from mamba_lite import ops
@@ -107,9 +130,17 @@ def bench_scan(dev, steps, warmup):
         ops.selective_scan(x["u"], x["delta"], x["A"], x["B"], x["C"], D=x["D"], z=x["z"],
                            delta_bias=x["delta_bias"], y=y, h_out=h)
 
+    t0 = time.perf_counter()
+    n_pre = 0
+    while time.perf_counter() - t0 < SCAN_PREWARM_S:
+        for _ in range(20):
+            step()
+        n_pre += 20
+        torch.cuda.synchronize()
+    prewarm_ms = (time.perf_counter() - t0) * 1e3
     ms, trials = _median_trials(step, steps, warmup)
     torch.cuda.synchronize()
-    return ms, trials, (x, y, h)
+    return ms, trials, (x, y, h), {"prewarm_ms": prewarm_ms, "prewarm_launches": n_pre}
 
 
 def cpu_baseline_scan(workers, gpu_run):
@@ -209,7 +240,7 @@ def _oracle_lm_weights(model):
     return {"embedding": f(model.embedding.weight), "norm_f": f(model.norm_f.weight), "layers": layers}
 
 
-def cpu_baseline_decode(model, dev, prompt=64, steps=8):
+def cpu_baseline_decode(model, dev, prompt=64, steps=32):
     """cpu_baseline leg of the decode metric at the 130m shape, batch 1: the
     oracle's LM (numpy float32, the reference's materialize-then-loop prefill
     and its step) on the host, `prompt` ids then `steps` timed greedy steps
@@ -244,7 +275,7 @@ def cpu_baseline_decode(model, dev, prompt=64, steps=8):
     return {"value": secs / steps * 1e6, "unit": "us/token", "cores": cores, "kind": "port",
             "sample": f"130m shape b=1: {prompt}-token prefill, then {steps} greedy steps timed (numpy float32 oracle; "
                       f"BLAS threads up to {cores})",
-            "gpu_step_max_rel_err_vs_oracle_f64": err}
+            "gpu_step_max_rel_err_vs_oracle_f64": err, **host_info()}
 
 
 def bench_prefill(model, batch, seqlen, dev, iters=None):
@@ -307,7 +338,7 @@ def cpu_baseline_quant(parts, pays, out, rows=4096):
         exact = exact and bool(np.array_equal(s[:rows], rs) and np.array_equal(q[:rows], rq))
     nbytes = 2 * rows * cols * 4 + 2 * rows * (cols + 4) + rows * cols * 4
     return {"value": nbytes / secs / 1e9, "unit": "GB/s", "cores": 1, "kind": "port",
-            "sample": f"first {rows} of {R} rows, numpy oracle", "bit_exact_codes_scales_out": exact}
+            "sample": f"first {rows} of {R} rows, numpy oracle", "bit_exact_codes_scales_out": exact, **host_info()}
 
 
 def bench_quant(dev, iters=20):
@@ -329,9 +360,27 @@ def bench_quant(dev, iters=20):
     ref16 = (parts[0].half() + parts[1].half()).float()
     exact16 = bool(torch.equal(out, ref16))
     bytes16 = 2 * rows * cols * 4 + 2 * rows * cols * 2 + rows * cols * 4
+    # cold-HBM rates: calls cycle over 4 distinct sets of partials (805 MB of
+    # inputs against the 256 MB MALL), so each call reads its partials from
+    # HBM; the back-to-back figures above re-read one 201 MB set, which the
+    # MALL partly serves
+    sets = [parts] + [[p.roll(k + 1, 0) for p in parts] for k in range(3)]
+    ring = {"i": 0}
+
+    def cold(fn):
+        def call():
+            ring["i"] = (ring["i"] + 1) % len(sets)
+            fn(sets[ring["i"]])
+        return call
+    ms8c = _timed(cold(lambda ps: ops.quant_dequant_sum_int8_tok(ps, payloads=pays, out=out)), iters, 4)
+    ms16c = _timed(cold(lambda ps: ops.quant_dequant_sum_fp16(ps, payloads=p16, out=out)), iters, 4)
+    del sets
     return {"int8_us": ms8 * 1e3, "int8_gbps": bytes8 / ms8 / 1e6, "int8_frac_hbm_peak": bytes8 / ms8 / 1e6 / HBM_PEAK_GBPS,
             "int8_cpu_baseline": cpu,
             "fp16_us": ms16 * 1e3, "fp16_gbps": bytes16 / ms16 / 1e6, "fp16_bit_exact_vs_torch": exact16,
+            "cold_hbm": {"int8_us": ms8c * 1e3, "int8_gbps": bytes8 / ms8c / 1e6,
+                         "fp16_us": ms16c * 1e3, "fp16_gbps": bytes16 / ms16c / 1e6,
+                         "how": "4 distinct partial sets (805 MB) cycled, so inputs are not MALL-resident"},
             "algorithmic_bytes": {"int8": bytes8, "fp16": bytes16}}
 
 
@@ -381,6 +430,11 @@ def bench_shard(dev, iters=10):
     conv = lambda: ops.causal_conv1d(xs, w, cb, out=u.transpose(1, 2), final_state=fs)
     scan = lambda: ops.selective_scan(u.transpose(1, 2), delta.transpose(1, 2), A_log, Bv, Cv, D=Dv, z=z,
                                       delta_bias=bias, a_is_log=True, y=y.transpose(1, 2), h_out=h)
+    t0 = time.perf_counter()      # settle clocks under sustained load first, as for the headline scan
+    while time.perf_counter() - t0 < 1.5:
+        scan()
+        conv()
+        torch.cuda.synchronize()
     ms_conv = _timed(conv, iters, 2)
     ms_scan = _timed(scan, iters, 2)
     torch.cuda.synchronize()
@@ -447,7 +501,7 @@ def main():
     if want("scan"):
         log("scan: isolated selective scan fp32 [32,1536,1024]")
         t0 = time.perf_counter()
-        ms, trials, gpu_run = bench_scan(dev, args.steps, args.warmup)
+        ms, trials, gpu_run, prewarm = bench_scan(dev, args.steps, args.warmup)
         wall = time.perf_counter() - t0
         gbps = SCAN_BYTES / ms / 1e6
         result.update({
@@ -466,6 +520,7 @@ def main():
                                     "80 of them the 16-state recurrence; 81% VALU busy (rocprofv3 counters)"},
         })
         extra["scan_trials_ms"] = trials
+        extra["scan_prewarm"] = prewarm
         log(f"scan: {ms*1000:.1f} us/call, {gbps:.0f} GB/s ({gbps/HBM_PEAK_GBPS:.1%} of peak), {wall:.1f}s")
         if not args.no_cpu_baseline:
             workers = max(1, min(16, os.cpu_count() or 1))
@@ -477,7 +532,7 @@ def main():
                 "sample": f"the full isolated-scan workload (32 rows x 1536 ch x 1024 steps x 16 states), numpy "
                           f"float32 materialize-then-loop, one batch row per process over {workers} processes; "
                           f"{secs:.1f} s wall",
-                "cpu_count": os.cpu_count()}
+                **host_info()}
             log(f"cpu baseline: {secs:.1f}s; GPU scan max rel err vs oracle {err:.2e}")
 
     if want("decode"):

@@ -57,33 +57,27 @@ template <> struct Act<uint16_t> {  // bf16 storage
 // exp(x) through the hardware base-2 exponential.
 __device__ __forceinline__ float fast_exp(float x) { return __builtin_amdgcn_exp2f(x * kLog2e); }
 
-// torch softplus (beta 1, threshold 20): x above 20, else log1p(exp(x)).
-// For e = exp(x) < 1/32 log1p(e) is the alternating series to e^4 (relative
-// truncation error < e^4/5 < 2e-7); above it log2(1 + e) * ln2, where
-// 1 + e >= 1.03 keeps the hardware log's error relative to the result small.
-// The exponent is clamped at 20; above 20 the result is x, taken by the
-// final max since log1p(exp(20)) rounds to 20 in fp32 and log1p(exp(x)) >= x
-// below it.  Clamp and max are med3s: one instruction each, with no NaN
-// quieting step in front as fminf/fmaxf have.
-__device__ __forceinline__ float softplus_f(float x) {
-    const float e = fast_exp(__builtin_amdgcn_fmed3f(x, -1.0e30f, 20.f));
-    const float series = e * (1.f - e * (0.5f - e * (0.33333334f - e * 0.25f)));
-    const float viaLog = __builtin_amdgcn_logf(1.f + e) * kLn2;
-    const float r = e < 0.03125f ? series : viaLog;
-    return __builtin_amdgcn_fmed3f(x, r, 3.0e38f);
+// softplus in log2 units: softplus(x) * log2(e) from xl = x * log2(e), as
+//   max(xl, 0) + log2(1 + e),  e = 2^-|xl|  (= log2(1 + 2^xl) for either sign).
+// 1 + e rounds; its rounding error d = e - ((1 + e) - 1) is exact and is put
+// back as d * log2(e) (the first-order term of log2(1 + d / (1 + e)); the
+// neglected factor 1 / (1 + e) changes the result by < 2^-24 relative).
+// Measured on gfx950 against float64 over x in [-30, 30]: relative error
+// under 7e-7 for x in [-8, -2], where the dt of a Mamba layer lives, and
+// under 2e-6 everywhere the result is a normal float.  Above x = 20 torch's
+// softplus returns x; here x + log1p(e^-x) has rounded to x from x = 16 on.
+// A NaN input gives NaN, as torch's does.
+// A scan that keeps dt in these units takes exp(dt * A) as exp2(dt_l2 * A).
+__device__ __forceinline__ float softplus_l2_f(float xl) {
+    const float e = __builtin_amdgcn_exp2f(-fabsf(xl));
+    const float u = 1.f + e;
+    const float d = e - (u - 1.f);
+    return fmaxf(xl, 0.f) + fmaf(d, kLog2e, __builtin_amdgcn_logf(u));
 }
 
-// softplus(x) * log2(e), from xl = x * log2(e) (same threshold, series and
-// NaN handling as softplus_f, with log2 e folded into the series
-// coefficients).  A scan that keeps dt in these units takes exp(dt * A) as
-// exp2(dt_l2 * A) with no log2 e factor, and saves softplus_f's final ln 2
-// multiply.
-__device__ __forceinline__ float softplus_l2_f(float xl) {
-    const float e = __builtin_amdgcn_exp2f(__builtin_amdgcn_fmed3f(xl, -1.0e30f, 20.f * kLog2e));
-    const float series = e * (kLog2e - e * (kLog2e / 2 - e * (kLog2e / 3 - e * (kLog2e / 4))));
-    const float viaLog = __builtin_amdgcn_logf(1.f + e);
-    const float r = e < 0.03125f ? series : viaLog;
-    return __builtin_amdgcn_fmed3f(xl, r, 3.0e38f);
+// torch softplus (beta 1, threshold 20), through softplus_l2_f.
+__device__ __forceinline__ float softplus_f(float x) {
+    return softplus_l2_f(x * kLog2e) * kLn2;
 }
 
 // x * sigmoid(x)

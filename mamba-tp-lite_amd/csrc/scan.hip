@@ -165,7 +165,9 @@ template <> struct Buf4<uint16_t> {
 // reads are full lines at any tile length, so there KC = 1.
 // Channel-major tiles hold twice the raw registers (3 waves per SIMD);
 // token-major ones fit 128 VGPRs, so 4 workgroups share a CU.
-template <typename T, int NW, int SPW, int TT, bool CM, bool VEC>
+// GEN: softplus and the z gate follow the runtime flags; without it both are
+// on (the mixer's case), and the staging has no per-element selects for them.
+template <typename T, int NW, int SPW, int TT, bool CM, bool VEC, bool GEN>
 __global__ void __launch_bounds__(NW * 64, CM ? 3 : 4) scan_fwd_kernel(const ScanArgs a) {
     constexpr int NT = NW * 64;
     constexpr int E = TT * 64 / NT;            // consecutive steps one thread stages per sub-tile
@@ -212,7 +214,8 @@ __global__ void __launch_bounds__(NW * 64, CM ? 3 : 4) scan_fwd_kernel(const Sca
 
     const T* __restrict__ up = static_cast<const T*>(a.u) + b * a.u_sb + (int64_t)cl * (CM ? a.u_sd : 1);
     const T* __restrict__ dp = static_cast<const T*>(a.delta) + b * a.d_sb + (int64_t)cl * (CM ? a.d_sd : 1);
-    const bool has_z = a.z != nullptr;
+    const bool has_z = !GEN || a.z != nullptr;
+    const bool do_softplus = !GEN || a.softplus;
     // without a gate z aliases u: its loads stay unconditional (a branch
     // around them would merge registers through copies that wait for loads)
     const T* __restrict__ zp = has_z ? static_cast<const T*>(a.z) + b * a.z_sb + (int64_t)cl * (CM ? a.z_sd : 1)
@@ -379,12 +382,12 @@ __global__ void __launch_bounds__(NW * 64, CM ? 3 : 4) scan_fwd_kernel(const Sca
         for (int j = 0; j < E; ++j) {
             const bool ok = F || tb + kc * TT + ot + j < L;
             float dt = fmaf(r.d[kc][j], kLog2e, bias_c);   // (delta + bias) * log2 e
-            if (a.softplus) dt = softplus_l2_f(dt);
+            if (do_softplus) dt = softplus_l2_f(dt);
             const float uv = ok ? r.u[kc][j] : 0.f;
             dt = ok ? dt : 0.f;                 // zero steps leave the state untouched past the end
             vdt[j] = dt;
             vdx[j] = dt * uv;
-            du[j] = D_c * uv;
+            du[j] = uv;                         // D * u is folded into the output fma
             gz[j] = has_z ? silu_f(r.z[kc][j]) : 1.f;
         }
 #pragma unroll
@@ -444,10 +447,10 @@ __global__ void __launch_bounds__(NW * 64, CM ? 3 : 4) scan_fwd_kernel(const Sca
                 const float4 p = *reinterpret_cast<const float4*>(&s_y[w][oc][ot + 4 * q]);
                 acc.x += p.x; acc.y += p.y; acc.z += p.z; acc.w += p.w;
             }
-            yout[kc][4 * q] = (acc.x + du[4 * q]) * gz[4 * q];
-            yout[kc][4 * q + 1] = (acc.y + du[4 * q + 1]) * gz[4 * q + 1];
-            yout[kc][4 * q + 2] = (acc.z + du[4 * q + 2]) * gz[4 * q + 2];
-            yout[kc][4 * q + 3] = (acc.w + du[4 * q + 3]) * gz[4 * q + 3];
+            yout[kc][4 * q] = fmaf(D_c, du[4 * q], acc.x) * gz[4 * q];
+            yout[kc][4 * q + 1] = fmaf(D_c, du[4 * q + 1], acc.y) * gz[4 * q + 1];
+            yout[kc][4 * q + 2] = fmaf(D_c, du[4 * q + 2], acc.z) * gz[4 * q + 2];
+            yout[kc][4 * q + 3] = fmaf(D_c, du[4 * q + 3], acc.w) * gz[4 * q + 3];
         }
         if (kc != KC - 1 || !c_ok) return;
 #pragma unroll
@@ -565,7 +568,10 @@ __global__ void __launch_bounds__(NW * 64, CM ? 3 : 4) scan_fwd_kernel(const Sca
 template <typename T, int NW, int SPW, int TT, bool CM, bool VEC>
 void launch_scan(const ScanArgs& a, int64_t batch, hipStream_t st) {
     dim3 grid((unsigned)((a.D + 63) / 64), (unsigned)batch);
-    hipLaunchKernelGGL((scan_fwd_kernel<T, NW, SPW, TT, CM, VEC>), grid, dim3(NW * 64), 0, st, a);
+    if (a.softplus && a.z != nullptr)
+        hipLaunchKernelGGL((scan_fwd_kernel<T, NW, SPW, TT, CM, VEC, false>), grid, dim3(NW * 64), 0, st, a);
+    else
+        hipLaunchKernelGGL((scan_fwd_kernel<T, NW, SPW, TT, CM, VEC, true>), grid, dim3(NW * 64), 0, st, a);
 }
 
 // 4 state groups of ceil(N/4) states: 4 wavefronts of 64 channels
