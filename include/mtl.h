@@ -59,6 +59,15 @@ int mtl_abi_version(void);
  * stride pattern is rejected.  B, C: [b, N, l] with strides (sb, sn, sl).
  * h0 (nullable) and h_out (nullable): contiguous fp32 [b, D, N]; h_out may
  * be h0 (a state is read before it is overwritten, by the same thread).
+ * Two kernels compute this.  The tiled one (algo 1) walks the steps of a
+ * sequence in turn with the state in registers: its time is the sequence
+ * length times one step's latency, which is the right trade when the grid
+ * (batch * ceil(D / 64) workgroups) fills the GPU.  The chunked one (algo 2)
+ * gives each (batch row, channel) a wavefront whose 64 lanes hold 64 steps
+ * and scans them in parallel, carrying (prod dA, h) from chunk to chunk:
+ * more arithmetic per step, but a latency of l / 64 chunks.  algo 0 takes
+ * the chunked kernel when batch * ceil(D / 64) < 160 and l > 32.  Both are
+ * deterministic and agree within fp32 rounding.
  * Limits: 1 <= N <= 32, l >= 0; B/C strides non-negative with
  * ((N-1)*sn + 31*sl + 1) elements under 4 GiB; token-major step strides
  * non-negative with (7*sl + D) elements under 2 GiB (the kernel addresses
@@ -80,7 +89,7 @@ typedef struct {
     int32_t dtype;             /* mtl_dtype of u, delta, z, B, C, y */
     int32_t delta_softplus;
     int32_t a_is_log;
-    int32_t reserved;
+    int32_t algo;              /* 0: choose by grid size; 1: tiled (steps in turn); 2: chunked over lanes */
 } mtl_scan_params;
 
 int mtl_selective_scan_fwd(const mtl_scan_params* p, mtl_stream_t stream);

@@ -574,6 +574,216 @@ void launch_scan(const ScanArgs& a, int64_t batch, hipStream_t st) {
         hipLaunchKernelGGL((scan_fwd_kernel<T, NW, SPW, TT, CM, VEC, true>), grid, dim3(NW * 64), 0, st, a);
 }
 
+// ---------------------------------------------------------------------------
+// Chunked scan across the lanes of a wavefront, for grids that leave the GPU
+// mostly idle (few batch rows x 64-channel blocks): the tiled kernel above
+// walks every step of a sequence in turn, so its time is the sequence length
+// times the latency of one step whatever the size of the grid.  Here one
+// wavefront owns one (batch row, channel), and its 64 lanes hold 64
+// consecutive steps -- a chunk.  For each state n the recurrence
+//   h_t = dA_t h_{t-1} + dBx_t
+// is the composition of the affine maps (dA_t, dBx_t), and
+//   (a1, b1) then (a2, b2) = (a2 a1, a2 b1 + b2)
+// is associative, so an inclusive scan over the lanes gives every step's
+// (prod of dA, h from a zero start) at once: six DPP levels (row_shr 1, 2, 4,
+// 8 within each 16-lane row, then row_bcast 15 and 31 across rows), each
+// lane combining with the identity (1, 0) where it has no source.  The state
+// entering the chunk is then folded in as h_t = P_t h_in + h_t, and lane 63's
+// h (identical to the last valid step's: steps past the end are identity
+// maps with dt = 0) is carried into the next chunk -- the (prod dA, h) carry
+// of a chunked scan.  The order of every operation is fixed, so results are
+// deterministic; the tree order of the scan rounds differently from the
+// step-by-step loop (within fp32 rounding of it).
+// The eight wavefronts of a workgroup take eight consecutive channels of one
+// batch row, share each chunk's B and C tiles through LDS, and move their u,
+// delta, z and y tiles through LDS as well (coalesced in either layout).
+constexpr int kLaneChannels = 8;   // wavefronts (channels) per workgroup
+
+// One level of the inclusive scan, for the four states of a group at once:
+// (a, b) <- (source lane's map) then (a, b), i.e. b += b_src * a, a *= a_src.
+// Each is one VOP2 instruction with a DPP source (v_fmac_f32_dpp,
+// v_mul_f32_dpp) written in place: a lane with no source in this level (the
+// first lanes of a row for row_shr; the rows row_mask leaves out for
+// row_bcast) is not written, which is the identity map (1, 0) without a
+// register to hold it.  b is updated before a, as it needs a's old value.
+// The compiler's hazard checks do not see into asm, so the DPP read-after-
+// VALU-write distance (2 wait states on gfx9) is kept by the interleave: the
+// four chains put 7 instructions between a write and the next level's DPP
+// read of the same register, and an s_nop guards the first level.
+#define MTL_SCAN_LEVEL4(DPP)                                                                               \
+    asm volatile("v_fmac_f32_dpp %0, %0, %4 " DPP "\n\t"                                                  \
+                 "v_mul_f32_dpp %4, %4, %4 " DPP "\n\t"                                                   \
+                 "v_fmac_f32_dpp %1, %1, %5 " DPP "\n\t"                                                  \
+                 "v_mul_f32_dpp %5, %5, %5 " DPP "\n\t"                                                   \
+                 "v_fmac_f32_dpp %2, %2, %6 " DPP "\n\t"                                                  \
+                 "v_mul_f32_dpp %6, %6, %6 " DPP "\n\t"                                                   \
+                 "v_fmac_f32_dpp %3, %3, %7 " DPP "\n\t"                                                  \
+                 "v_mul_f32_dpp %7, %7, %7 " DPP                                                            \
+                 : "+v"(bv[0]), "+v"(bv[1]), "+v"(bv[2]), "+v"(bv[3]), "+v"(av[0]), "+v"(av[1]), "+v"(av[2]), \
+                   "+v"(av[3]))
+
+template <typename T, int NS>
+__global__ void __launch_bounds__(kLaneChannels * 64) scan_lanes_kernel(const ScanArgs a) {
+    constexpr int CW = kLaneChannels, NT = CW * 64;
+    __shared__ float s_B[NS][65];                      // padded rows: the state-fastest fill hits distinct banks
+    __shared__ float s_C[NS][65];
+    __shared__ float s_x[3][CW][65];                   // u, delta, z of the workgroup's channels, then y
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int b = blockIdx.y;
+    const int L = a.L, D = a.D, N = a.N;
+    const int c0 = blockIdx.x * CW;
+    const int c_raw = c0 + wave;
+    const bool c_ok = c_raw < D;                       // waves past D still take part in the barriers
+    const int c = c_ok ? c_raw : D - 1;
+    const bool has_z = a.z != nullptr;
+
+    // The workgroup's u, delta, z (and y) tiles of CW channels x 64 steps move
+    // between HBM and LDS cooperatively: with unit step stride thread e takes
+    // channel e / 64, step e % 64; otherwise (token-major rows) step e / CW,
+    // channel e % CW, so a wavefront reads whole CW-channel runs of 64 / CW rows
+    // instead of one word of 64 rows.  Wavefront w then works on channel w
+    // with lane = step.
+    const bool x_t_fast = a.u_sl == 1;
+    const int xe_c = x_t_fast ? tid >> 6 : tid % CW, xe_t = x_t_fast ? tid & 63 : tid / CW;
+    const int xc = min(c0 + xe_c, D - 1);
+    const T* up = static_cast<const T*>(a.u) + b * a.u_sb + (int64_t)xc * a.u_sd;
+    const T* dp = static_cast<const T*>(a.delta) + b * a.d_sb + (int64_t)xc * a.d_sd;
+    const T* zp = has_z ? static_cast<const T*>(a.z) + b * a.z_sb + (int64_t)xc * a.z_sd : up;
+    const int64_t z_sl = has_z ? a.z_sl : a.u_sl;
+    T* yp = static_cast<T*>(a.y) + b * a.y_sb + (int64_t)xc * a.y_sd;
+    const bool xc_ok = c0 + xe_c < D;
+    const T* Bp = static_cast<const T*>(a.B) + b * a.B_sb;
+    const T* Cp = static_cast<const T*>(a.C) + b * a.C_sb;
+
+    constexpr int kFill = (NS * 64 + NT - 1) / NT;     // B and C values each thread stages per chunk
+    // B/C tile element e of a chunk: state n, step tl.  With unit step stride
+    // consecutive threads take consecutive steps; otherwise (B and C as
+    // columns of the token-major x_dbl) consecutive states.
+    const bool bc_t_fast = a.B_sl == 1;
+    struct Chunk { float fb[kFill], fc[kFill], u, d, z; };
+    auto load_chunk = [&](Chunk& k, int t0) __attribute__((always_inline)) {
+#pragma unroll
+        for (int q = 0; q < kFill; ++q) {
+            const int e = min(tid + q * NT, NS * 64 - 1);
+            const int n = bc_t_fast ? e >> 6 : e % NS, tl = bc_t_fast ? e & 63 : e / NS;
+            const int tcq = min(t0 + tl, L - 1), nn = min(n, N - 1);
+            k.fb[q] = Act<T>::load(Bp + (int64_t)nn * a.B_sn + (int64_t)tcq * a.B_sl);
+            k.fc[q] = Act<T>::load(Cp + (int64_t)nn * a.C_sn + (int64_t)tcq * a.C_sl);
+        }
+        const int tc = min(t0 + xe_t, L - 1);
+        k.u = Act<T>::load(up + (int64_t)tc * a.u_sl);
+        k.d = Act<T>::load(dp + (int64_t)tc * a.d_sl);
+        k.z = Act<T>::load(zp + (int64_t)tc * z_sl);
+    };
+    // software pipeline: the next chunk's loads are in flight while this one is scanned
+    Chunk cur, nxt;
+    load_chunk(cur, 0);
+
+    // (after the first chunk's loads are issued, so the two round trips overlap)
+    // lane n < N fetches state n's A (and h0) once; every lane then reads
+    // them out uniformly.  States n >= N have A = 0 and B = C = 0: identity
+    // maps that add nothing, so the state loop needs no branch and its
+    // chains interleave.
+    const float bias_l2 = (a.dbias ? a.dbias[c] : 0.f) * kLog2e;
+    const float D_c = a.Dv ? a.Dv[c] : 0.f;
+    const int nl = min(lane, N - 1);
+    float a_lane = a.A[(int64_t)c * N + nl];
+    if (a.a_is_log) a_lane = -expf(a_lane);
+    a_lane = lane < N ? a_lane : 0.f;
+    float h_lane = a.h0 ? a.h0[((int64_t)b * D + c) * N + nl] : 0.f;
+    h_lane = lane < N ? h_lane : 0.f;
+    float A_c[NS], h_in[NS];
+#pragma unroll
+    for (int n = 0; n < NS; ++n) {
+        A_c[n] = lane_read(a_lane, n);
+        h_in[n] = lane_read(h_lane, n);
+    }
+
+    const int last0 = (L - 1) / 64 * 64;
+    for (int t0 = 0; t0 < L; t0 += 64) {
+#pragma unroll
+        for (int q = 0; q < kFill; ++q) {
+            const int e = tid + q * NT;
+            if (NS * 64 % NT == 0 || e < NS * 64) {
+                const int n = bc_t_fast ? e >> 6 : e % NS, tl = bc_t_fast ? e & 63 : e / NS;
+                s_B[n][tl] = n < N ? cur.fb[q] : 0.f;  // padded states: identity, no output
+                s_C[n][tl] = n < N ? cur.fc[q] : 0.f;
+            }
+        }
+        s_x[0][xe_c][xe_t] = cur.u;
+        s_x[1][xe_c][xe_t] = cur.d;
+        s_x[2][xe_c][xe_t] = cur.z;
+        load_chunk(nxt, min(t0 + 64, last0));          // the last chunk re-reads itself rather than branch
+        __syncthreads();
+        const int t = t0 + lane;
+        const bool valid = t < L;
+        const float uv = s_x[0][wave][lane], zv = s_x[2][wave][lane];
+        float dt = fmaf(s_x[1][wave][lane], kLog2e, bias_l2);   // log2 units
+        if (a.softplus) dt = softplus_l2_f(dt);
+        dt = valid ? dt : 0.f;                         // identity map past the end
+        const float dx = dt * kLn2 * uv;               // dt (natural units) * u
+        float yacc = 0.f;
+        // states in groups of four: each level of the four scans is issued
+        // together, so one chain's DPP latency is covered by the others
+#pragma unroll
+        for (int n0 = 0; n0 < NS; n0 += 4) {
+            float av[4], bv[4];
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                av[k] = __builtin_amdgcn_exp2f(dt * A_c[n0 + k]);
+                bv[k] = dx * s_B[n0 + k][lane];
+            }
+            asm volatile("s_nop 2" ::: "memory");
+            MTL_SCAN_LEVEL4("row_shr:1 row_mask:0xf bank_mask:0xf");
+            MTL_SCAN_LEVEL4("row_shr:2 row_mask:0xf bank_mask:0xf");
+            MTL_SCAN_LEVEL4("row_shr:4 row_mask:0xf bank_mask:0xf");
+            MTL_SCAN_LEVEL4("row_shr:8 row_mask:0xf bank_mask:0xf");
+            MTL_SCAN_LEVEL4("row_bcast:15 row_mask:0xa bank_mask:0xf");
+            MTL_SCAN_LEVEL4("row_bcast:31 row_mask:0xc bank_mask:0xf");
+            asm volatile("s_nop 1" ::: "memory");
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const float hv = fmaf(av[k], h_in[n0 + k], bv[k]);
+                yacc = fmaf(s_C[n0 + k][lane], hv, yacc);
+                h_in[n0 + k] = lane_read(hv, 63);
+            }
+        }
+        const float yv = fmaf(D_c, uv, yacc) * (has_z ? silu_f(zv) : 1.f);
+        __syncthreads();                               // every wavefront has read its u, delta, z
+        s_x[0][wave][lane] = yv;
+        __syncthreads();
+        const int ty = t0 + xe_t;
+        if (xc_ok && ty < L) Act<T>::store(yp + (int64_t)ty * a.y_sl, s_x[0][xe_c][xe_t]);
+        cur = nxt;
+    }
+    if (a.h_out && c_ok) {
+        float hv = 0.f;
+#pragma unroll
+        for (int n = 0; n < NS; ++n) hv = lane == n ? h_in[n] : hv;
+        if (lane < N) a.h_out[((int64_t)b * D + c) * N + lane] = hv;
+    }
+}
+
+template <typename T>
+void launch_scan_lanes(const ScanArgs& a, int64_t batch, hipStream_t st) {
+    dim3 grid((unsigned)((a.D + kLaneChannels - 1) / kLaneChannels), (unsigned)batch);
+    dim3 block(kLaneChannels * 64);
+    if (a.N <= 4) hipLaunchKernelGGL((scan_lanes_kernel<T, 4>), grid, block, 0, st, a);
+    else if (a.N <= 8) hipLaunchKernelGGL((scan_lanes_kernel<T, 8>), grid, block, 0, st, a);
+    else if (a.N <= 16) hipLaunchKernelGGL((scan_lanes_kernel<T, 16>), grid, block, 0, st, a);
+    else hipLaunchKernelGGL((scan_lanes_kernel<T, 32>), grid, block, 0, st, a);
+}
+
+// algo 0 takes the chunked kernel when the tiled kernel's grid (batch *
+// ceil(D / 64) workgroups of 4 wavefronts) is below this and the sequence is
+// longer than kChunkedMinSteps.  Measured on MI355X as HIP-graph replays,
+// mixer layout, fp32: the chunked kernel wins from 12 to 128 workgroups at
+// 64 steps and more (D 1536, 64 steps, batch 1: 5.4 against 11.2 us; 1024
+// steps: 37 against 126 us; D 4096, batch 2, 64 steps: a tie) and loses from
+// 192 workgroups on, and at 16 steps, where both are at launch latency.
+constexpr int64_t kChunkedBelowWorkgroups = 160;
+constexpr int64_t kChunkedMinSteps = 32;
+
 // 4 state groups of ceil(N/4) states: 4 wavefronts of 64 channels
 template <typename T, bool CM, bool VEC>
 void dispatch_spw(const ScanArgs& a, int64_t batch, hipStream_t st) {
@@ -653,7 +863,17 @@ extern "C" int mtl_selective_scan_fwd(const mtl_scan_params* p, mtl_stream_t str
         }
     }
 
+    MTL_REQUIRE(p->algo >= 0 && p->algo <= 2, "algo must be 0 (auto), 1 (tiled) or 2 (chunked)");
     hipStream_t st = as_stream(stream);
+    if (p->seqlen == 0) {
+        // no steps: h_out = h0 (or zeros); the tiled kernel's path carries it
+    } else if (p->algo == 2 || (p->algo == 0 && p->batch * ((p->dim + 63) / 64) < kChunkedBelowWorkgroups &&
+                                p->seqlen > kChunkedMinSteps)) {
+        MTL_REQUIRE(p->batch * ((p->dim + kLaneChannels - 1) / kLaneChannels) < (int64_t(1) << 31), "grid too large");
+        if (p->dtype == MTL_F32) launch_scan_lanes<float>(a, p->batch, st);
+        else launch_scan_lanes<uint16_t>(a, p->batch, st);
+        return check_launch("selective_scan_fwd(chunked)");
+    }
     // seqlen <= 1 has no meaningful l-stride; the channel-major path handles it.
     const bool use_cm = cm || (!tm);
     if (p->dtype == MTL_F32) {

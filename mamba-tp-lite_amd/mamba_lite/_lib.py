@@ -37,7 +37,7 @@ class ScanParams(ctypes.Structure):
         ("y", _vp), ("y_sb", _i64), ("y_sd", _i64), ("y_sl", _i64),
         ("A", _fp), ("D", _fp), ("delta_bias", _fp), ("h0", _fp), ("h_out", _fp),
         ("batch", _i64), ("seqlen", _i64), ("dim", _i64), ("dstate", _i64),
-        ("dtype", _i32), ("delta_softplus", _i32), ("a_is_log", _i32), ("reserved", _i32),
+        ("dtype", _i32), ("delta_softplus", _i32), ("a_is_log", _i32), ("algo", _i32),
     ]
 
 

@@ -111,8 +111,11 @@ def _bdl_layout_ok(*ts):
 
 
 # --------------------------------------------------------------------------- selective scan
+SCAN_ALGOS = {"auto": 0, "tiled": 1, "chunked": 2}
+
+
 def selective_scan(u, delta, A, B, C, D=None, z=None, delta_bias=None, h0=None, delta_softplus=True,
-                   a_is_log=False, y=None, h_out=None, return_last_state=True):
+                   a_is_log=False, y=None, h_out=None, return_last_state=True, algo="auto"):
     """Fused selective scan (mtl_selective_scan_fwd); see include/mtl.h.
 
     Returns (y [b,D,l] in the activation dtype, h_last [b,D,N] fp32) -- the
@@ -169,6 +172,7 @@ def selective_scan(u, delta, A, B, C, D=None, z=None, delta_bias=None, h0=None, 
     p.h_out = h_out.data_ptr() if h_out is not None else None
     p.batch, p.seqlen, p.dim, p.dstate = b, L, Dm, N
     p.dtype, p.delta_softplus, p.a_is_log = code, int(bool(delta_softplus)), int(bool(a_is_log))
+    p.algo = SCAN_ALGOS[algo]
     with _dev_guard(u):
         _lib.check(_lib.load().mtl_selective_scan_fwd(ctypes.byref(p), _stream(u)), "selective_scan_fwd")
     return y, h_out

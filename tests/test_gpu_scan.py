@@ -20,7 +20,8 @@ def _t(a, dtype=torch.float32):
     return torch.from_numpy(np.ascontiguousarray(a)).to(DEV, dtype)
 
 
-def _run(c, layout="cm", h0=None, dtype=torch.float32, with_z=True, with_D=True, with_bias=True, a_is_log=False):
+def _run(c, layout="cm", h0=None, dtype=torch.float32, with_z=True, with_D=True, with_bias=True, a_is_log=False,
+         algo="auto"):
     u, delta, z = c["u"], c["delta"], c["z"]
     if layout == "tm":   # token-major storage [b, l, D] viewed as [b, D, l]
         U = _t(u.transpose(0, 2, 1), dtype).transpose(1, 2)
@@ -41,7 +42,7 @@ def _run(c, layout="cm", h0=None, dtype=torch.float32, with_z=True, with_D=True,
     A = np.log(-c["A"]) if a_is_log else c["A"]
     y, h = ops.selective_scan(U, Dl, _t(A), Bt, Ct, D=_t(c["D"]) if with_D else None, z=Z if with_z else None,
                               delta_bias=_t(c["delta_bias"]) if with_bias else None,
-                              h0=_t(h0) if h0 is not None else None, a_is_log=a_is_log, y=Y)
+                              h0=_t(h0) if h0 is not None else None, a_is_log=a_is_log, y=Y, algo=algo)
     torch.cuda.synchronize()
     return y.float().cpu().numpy(), h.cpu().numpy()
 
@@ -53,65 +54,77 @@ def _ref(c, h0=None, with_z=True, with_D=True, with_bias=True, round_bf16=False)
                                  c["delta_bias"] if with_bias else None, h0, dtype=np.float64)
 
 
+ALGOS = ["tiled", "chunked"]
+
+
+@pytest.mark.parametrize("algo", ALGOS)
 @pytest.mark.parametrize("layout", ["cm", "tm"])
 @pytest.mark.parametrize("b,D,L,N", [(2, 64, 16, 16), (2, 200, 70, 16), (1, 96, 33, 8), (3, 70, 5, 4),
-                                     (1, 64, 40, 32), (1, 130, 129, 1)])
-def test_scan_fp32_vs_oracle(layout, b, D, L, N):
-    print(f"scan fp32 {layout} b={b} D={D} L={L} N={N}", flush=True)
+                                     (1, 64, 40, 32), (1, 130, 129, 1), (2, 32, 64, 16), (1, 48, 65, 16),
+                                     (1, 20, 1000, 16), (2, 8, 191, 5)])
+def test_scan_fp32_vs_oracle(algo, layout, b, D, L, N):
+    """Chunk boundaries of the chunked kernel sit every 64 steps: lengths
+    below, at and past one chunk, and many chunks (1000 steps)."""
+    print(f"scan fp32 {algo} {layout} b={b} D={D} L={L} N={N}", flush=True)
     c = scan_case(np.random.default_rng(b * 1000 + D + L + N), b, D, L, N)
     h0 = np.random.default_rng(7).standard_normal((b, D, N)).astype(np.float32)
-    y, h = _run(c, layout, h0=h0)
+    y, h = _run(c, layout, h0=h0, algo=algo)
     y_ref, h_ref = _ref(c, h0=h0)
     assert_rel(y, y_ref, 1e-4, "y")
     assert_rel(h, h_ref, 1e-4, "h")
 
 
+@pytest.mark.parametrize("algo", ALGOS)
 @pytest.mark.parametrize("opts", [dict(with_z=False), dict(with_D=False), dict(with_bias=False),
                                   dict(with_z=False, with_D=False, with_bias=False)])
-def test_scan_optional_operands(opts):
+def test_scan_optional_operands(opts, algo):
     c = scan_case(np.random.default_rng(11), 2, 96, 48, 16)
-    y, h = _run(c, **opts)
+    y, h = _run(c, algo=algo, **opts)
     y_ref, h_ref = _ref(c, **opts)
     assert_rel(y, y_ref, 1e-4, f"y {opts}")
     assert_rel(h, h_ref, 1e-4, f"h {opts}")
 
 
-def test_scan_a_log_input():
+@pytest.mark.parametrize("algo", ALGOS)
+def test_scan_a_log_input(algo):
     c = scan_case(np.random.default_rng(12), 2, 64, 32, 16)
-    y1, h1 = _run(c, a_is_log=True)
+    y1, h1 = _run(c, a_is_log=True, algo=algo)
     y_ref, h_ref = _ref(c)
     assert_rel(y1, y_ref, 1e-4, "y")
     assert_rel(h1, h_ref, 1e-4, "h")
 
 
-def test_scan_zero_and_one_length():
+@pytest.mark.parametrize("algo", ALGOS)
+def test_scan_zero_and_one_length(algo):
     c = scan_case(np.random.default_rng(13), 2, 64, 1, 16)
     h0 = np.random.default_rng(3).standard_normal((2, 64, 16)).astype(np.float32)
-    y, h = _run(c, h0=h0)
+    y, h = _run(c, h0=h0, algo=algo)
     y_ref, h_ref = _ref(c, h0=h0)
     assert_rel(y, y_ref, 1e-4, "y L=1")
     assert_rel(h, h_ref, 1e-4, "h L=1")
     # L = 0: no output, state passes through unchanged
     u = torch.empty(2, 64, 0, device=DEV)
     B = torch.empty(2, 16, 0, device=DEV)
-    y0, hz = ops.selective_scan(u, u, _t(c["A"]), B, B, h0=_t(h0))
+    y0, hz = ops.selective_scan(u, u, _t(c["A"]), B, B, h0=_t(h0), algo=algo)
     assert y0.shape == (2, 64, 0)
     assert torch.equal(hz.cpu(), torch.from_numpy(h0))
 
 
+@pytest.mark.parametrize("algo", ALGOS)
 @pytest.mark.parametrize("layout", ["cm", "tm"])
-def test_scan_bf16_vs_oracle(layout):
+def test_scan_bf16_vs_oracle(layout, algo):
     c = scan_case(np.random.default_rng(21), 2, 128, 80, 16)
-    y, h = _run(c, layout, dtype=torch.bfloat16)
+    y, h = _run(c, layout, dtype=torch.bfloat16, algo=algo)
     y_ref, h_ref = _ref(c, round_bf16=True)
     assert_rel(y, y_ref, 1e-2, "y bf16")
     assert_rel(h, h_ref, 1e-2, "h bf16")
 
 
-def test_scan_is_deterministic():
+@pytest.mark.parametrize("algo", ALGOS)
+def test_scan_is_deterministic(algo):
     c = scan_case(np.random.default_rng(22), 2, 128, 100, 16)
-    y1, h1 = _run(c)
-    y2, h2 = _run(c)
+    y1, h1 = _run(c, algo=algo)
+    y2, h2 = _run(c, algo=algo)
     assert np.array_equal(y1, y2) and np.array_equal(h1, h2)
 
 
@@ -152,15 +165,16 @@ def test_scan_full_size_properties():
         assert_rel(h[bi:bi + 1, sl].cpu().numpy(), hr, 1e-4, f"h b={bi} c0={c0}")
 
 
-def test_scan_channel_shard_equals_dense_slice():
+@pytest.mark.parametrize("algo", ALGOS)
+def test_scan_channel_shard_equals_dense_slice(algo):
     """Per-channel independence the TP shard relies on (reference
     test_tp_correctness.py:76-79): scanning channels [1024, 2048) alone gives
     exactly the dense result's slice."""
     c = scan_case(np.random.default_rng(23), 2, 2048, 64, 16)
-    y, h = _run(c)
+    y, h = _run(c, algo=algo)
     sub = {k: (v[:, 1024:] if k in ("u", "delta", "z") else v[1024:] if k in ("A", "D", "delta_bias") else v)
            for k, v in c.items()}
-    ys, hs = _run(sub)
+    ys, hs = _run(sub, algo=algo)
     assert np.array_equal(ys, y[:, 1024:]) and np.array_equal(hs, h[:, 1024:])
 
 
@@ -321,7 +335,10 @@ def test_scan_large_ragged_grid(dtype, L, Lp, N, full_ops):
     kws = {kk: (v[:192] if kk in ("D", "delta_bias") else v[:, :192]) for kk, v in kw.items()}
     if "h0" in kws:
         kws["h0"] = kws["h0"].contiguous()
-    ys, hs = ops.selective_scan(u[:, :192], delta[:, :192], A[:192], Bm, Cm, delta_softplus=sp, **kws)
+    # a 72-block grid is one the automatic choice gives to the chunked kernel: force the tiled one,
+    # whose results do not depend on the grid
+    ys, hs = ops.selective_scan(u[:, :192], delta[:, :192], A[:192], Bm, Cm, delta_softplus=sp, algo="tiled",
+                                **kws)
     torch.cuda.synchronize()
     assert torch.isfinite(y.float()).all() and torch.isfinite(h).all()
     assert torch.equal(torch.cat([y1, y2], -1), y) and torch.equal(h2, h)
@@ -337,3 +354,26 @@ def test_scan_large_ragged_grid(dtype, L, Lp, N, full_ops):
                                        f(h0, bi)[:, sl] if full_ops else None, delta_softplus=sp, dtype=np.float64)
         assert_rel(y[bi:bi + 1, sl].float().cpu().numpy(), yr, tol, f"y b={bi} c0={c0}")
         assert_rel(h[bi:bi + 1, sl].cpu().numpy(), hr, tol, f"h b={bi} c0={c0}")
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_chunked_matches_tiled_and_continues(dtype):
+    """The two kernels on one mid-size mixer-layout input agree (fp32 1e-4,
+    bf16 outputs within 1e-2), and the chunked kernel continued from its own
+    state at a step that is not a chunk boundary reproduces its one-pass
+    result."""
+    b, D, L, N = 2, 1536, 300, 16
+    print(f"scan chunked vs tiled {dtype} b={b} D={D} L={L}", flush=True)
+    c = scan_case(np.random.default_rng(31), b, D, L, N)
+    y1, h1 = _run(c, "tm", dtype=dtype, algo="tiled")
+    y2, h2 = _run(c, "tm", dtype=dtype, algo="chunked")
+    tol = 1e-4 if dtype == torch.float32 else 1e-2
+    assert_rel(y2, y1, tol, "y chunked vs tiled")
+    assert_rel(h2, h1, 1e-4, "h chunked vs tiled")
+    k = 77
+    cut = lambda a, sl: {**c, "u": a["u"][..., sl], "delta": a["delta"][..., sl], "z": a["z"][..., sl],
+                         "B": a["B"][..., sl], "C": a["C"][..., sl]}
+    ya, ha = _run(cut(c, slice(0, k)), "tm", dtype=dtype, algo="chunked")
+    yb, hb = _run(cut(c, slice(k, L)), "tm", h0=ha, dtype=dtype, algo="chunked")
+    assert_rel(np.concatenate([ya, yb], -1), y2, tol, "continued y")
+    assert_rel(hb, h2, 1e-4, "continued h")
