@@ -307,10 +307,10 @@ __global__ void __launch_bounds__(NW * 64, CM ? 3 : 4) scan_fwd_kernel(const Sca
         c_bytes[k] = (uint32_t)((bc_off[k] * a.C_sn + bc_t[k] * a.C_sl) * (int64_t)sizeof(T));
     }
 
-    auto load_tile = [&](Raw& r, int tb, auto full) __attribute__((always_inline)) {
+    // the raw u / delta / z of sub-tile kc of the load tile at tb
+    auto load_sub = [&](Raw& r, int tb, int kc, auto full) __attribute__((always_inline)) {
         constexpr bool F = decltype(full)::value;
-#pragma unroll
-        for (int kc = 0; kc < KC; ++kc) {
+        {
             const int t0 = tb + kc * TT + ot;
             if constexpr (CM && VEC) {
                 // Full tiles put the tile's first step in the SGPR offset.  A
@@ -355,6 +355,10 @@ __global__ void __launch_bounds__(NW * 64, CM ? 3 : 4) scan_fwd_kernel(const Sca
                 }
             }
         }
+    };
+    // the raw B / C of the load tile at tb
+    auto load_bc = [&](Raw& r, int tb, auto full) __attribute__((always_inline)) {
+        constexpr bool F = decltype(full)::value;
         if constexpr (F) {
             const T* Bt = Bp + (int64_t)tb * a.B_sl;
             const T* Ct = Cp + (int64_t)tb * a.C_sl;
@@ -371,6 +375,11 @@ __global__ void __launch_bounds__(NW * 64, CM ? 3 : 4) scan_fwd_kernel(const Sca
                 r.C[k] = Act<T>::load(Cp + bc_off[k] * a.C_sn + (int64_t)t * a.C_sl);
             }
         }
+    };
+    auto load_tile = [&](Raw& r, int tb, auto full) __attribute__((always_inline)) {
+#pragma unroll
+        for (int kc = 0; kc < KC; ++kc) load_sub(r, tb, kc, full);
+        load_bc(r, tb, full);
     };
 
     // stage sub-tile kc of the load tile at tb (B/C of the whole load tile
@@ -412,6 +421,19 @@ __global__ void __launch_bounds__(NW * 64, CM ? 3 : 4) scan_fwd_kernel(const Sca
     // TT recurrence steps of sub-tile kc; padded steps past the end have
     // dt = dt*u = 0 and leave h unchanged, so the loop never needs a bound check
     auto scan_tile = [&](int kc) __attribute__((always_inline)) {
+        // the B / C broadcasts of step st are read two steps before their use
+        // (at 8 states per wavefront the registers for that would spill)
+        constexpr int PRE = SPW <= 4 ? 2 : 0;
+        float bq[TT][SPW], cq[TT][SPW];
+        auto read_bc = [&](int st) __attribute__((always_inline)) {
+#pragma unroll
+            for (int k = 0; k < SPW; ++k) {
+                bq[st][k] = s_B[kc * TT + st][wave * SPW + k];
+                cq[st][k] = s_C[kc * TT + st][wave * SPW + k];
+            }
+        };
+#pragma unroll
+        for (int st = 0; st < PRE; ++st) read_bc(st);
 #pragma unroll
         for (int tt = 0; tt < TT; tt += 4) {
             const float4 dt4 = *reinterpret_cast<const float4*>(&s_dt[lane][tt]);
@@ -421,11 +443,13 @@ __global__ void __launch_bounds__(NW * 64, CM ? 3 : 4) scan_fwd_kernel(const Sca
             float yq[4];
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
+                const int st = tt + q;
+                if (PRE > 0 && st + PRE < TT) read_bc(st + PRE);
                 float acc = 0.f;
 #pragma unroll
                 for (int k = 0; k < SPW; ++k) {
-                    const float bk = s_B[kc * TT + tt + q][wave * SPW + k];
-                    const float ck = s_C[kc * TT + tt + q][wave * SPW + k];
+                    const float bk = PRE > 0 ? bq[st][k] : s_B[kc * TT + st][wave * SPW + k];
+                    const float ck = PRE > 0 ? cq[st][k] : s_C[kc * TT + st][wave * SPW + k];
                     h[k] = fmaf(__builtin_amdgcn_exp2f(dts[q] * a2[k]), h[k], dxs[q] * bk);
                     acc = fmaf(h[k], ck, acc);
                 }
@@ -484,12 +508,13 @@ __global__ void __launch_bounds__(NW * 64, CM ? 3 : 4) scan_fwd_kernel(const Sca
         }
     };
 
+    // refill(kc) runs once sub-tile kc is staged, when its raw registers are free
     auto run_subtiles = [&](Raw& r, int tb, auto full, auto refill) __attribute__((always_inline)) {
 #pragma unroll
         for (int kc = 0; kc < KC; ++kc) {
             stage_tile(r, tb, kc, full);
             __syncthreads();
-            if (kc == KC - 1) refill();
+            refill(kc);
             scan_tile(kc);
             __syncthreads();
             finish_tile(tb, kc, full);
@@ -500,10 +525,12 @@ __global__ void __launch_bounds__(NW * 64, CM ? 3 : 4) scan_fwd_kernel(const Sca
     // single code path (two paths would merge through register copies that
     // wait for the loads).  The refill is unconditional: the last tiles
     // re-read tile nfull-1 rather than branch.  Token-major keeps two raw
-    // sets (the tile two ahead in flight); channel-major load tiles are
-    // twice as long, so one set refilled right after its last sub-tile is
-    // staged keeps the next tile in flight across two sub-tile scans within
-    // the 3-waves-per-SIMD register budget.
+    // sets (the tile two ahead in flight).  Channel-major load tiles are
+    // twice as long and hold one set within the 3-waves-per-SIMD register
+    // budget: each sub-tile's registers are refilled with the same sub-tile
+    // of the next load tile as soon as it is staged (B/C with sub-tile 0), so
+    // every load is in flight across two sub-tile scans (refilling the whole
+    // tile after its last sub-tile gave the first half one scan: 3% slower).
     const int nfull = L / LT;
     // Issue priority falls as the sequence progresses (levels change at 1/2,
     // 3/4 and 7/8 of the load tiles).  The SIMDs issue oldest-wave-first, so
@@ -524,7 +551,7 @@ __global__ void __launch_bounds__(NW * 64, CM ? 3 : 4) scan_fwd_kernel(const Sca
         auto run_full = [&](Raw& r, int i) __attribute__((always_inline)) {
             set_prio(i);
             run_subtiles(r, i * LT, Full<true>{},
-                         [&]() { load_tile(r, min(i + 2, nfull - 1) * LT, Full<true>{}); });
+                         [&](int) { load_tile(r, min(i + 2, nfull - 1) * LT, Full<true>{}); });
         };
         if (nfull > 0) load_tile(r0, 0, Full<true>{});
         if (nfull > 1) load_tile(r1, LT, Full<true>{});
@@ -539,8 +566,11 @@ __global__ void __launch_bounds__(NW * 64, CM ? 3 : 4) scan_fwd_kernel(const Sca
         // up at the back edge without copies
         auto run_cm = [&](int i) __attribute__((always_inline)) {
             set_prio(i);
-            run_subtiles(r0, i * LT, Full<true>{},
-                         [&]() { load_tile(r0, min(i + 1, nfull - 1) * LT, Full<true>{}); });
+            const int nb = min(i + 1, nfull - 1) * LT;
+            run_subtiles(r0, i * LT, Full<true>{}, [&](int kc) {
+                load_sub(r0, nb, kc, Full<true>{});
+                if (kc == 0) load_bc(r0, nb, Full<true>{});
+            });
         };
         if (nfull > 0) load_tile(r0, 0, Full<true>{});
         int i = 0;
@@ -553,7 +583,7 @@ __global__ void __launch_bounds__(NW * 64, CM ? 3 : 4) scan_fwd_kernel(const Sca
     if (nfull * LT < L) {  // the partial last load tile, outside the pipeline
         const int tb = nfull * LT;
         load_tile(r0, tb, Full<false>{});
-        run_subtiles(r0, tb, Full<false>{}, []() {});
+        run_subtiles(r0, tb, Full<false>{}, [](int) {});
     }
 
     if (a.h_out) {

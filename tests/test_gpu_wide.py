@@ -8,7 +8,9 @@ element plus the tensor's rms):
     update; model.py:249-294, 343-353);
   * MambaLM.step on the fused decode path at batch 1, 2 and 4;
   * d_model 2560 (d_inner 5120: 160 x_proj partial blocks, past the fused
-    path's 4096-channel limit) at batch 1 and 8.
+    path's 4096-channel limit) at batch 1 and 8;
+  * the full-size mamba-130m model (24 layers, vocab 50280) on the fused
+    decode path at batch 1.
 
 Weights come from the seeded recipe of tests/_golden.py (A_log and D off
 their constant init, so a channel-blind read shows)."""
@@ -112,3 +114,13 @@ def test_lm_step_d_inner_5120(b):
     print(f"\n[wide: lm step d_model=2560 b={b}]", flush=True)
     lm, W = _lm(47, 2560, 1, 512)
     _lm_steps_vs_oracle(lm, W, b, 5, 2, 512, 48 + b, expect_fused=False)
+
+
+def test_lm_130m_full_depth_fused_step():
+    """The mamba-130m model at full size (d_model 768, 24 layers, vocab
+    50280, tied head) on the fused decode path at batch 1: prefill logits,
+    three teacher-forced steps and every layer's states against the float64
+    oracle (model.py:328-353)."""
+    print("\n[wide: lm 130m 24 layers vocab 50280 b=1 fused]", flush=True)
+    lm, W = _lm(49, 768, 24, 50280)
+    _lm_steps_vs_oracle(lm, W, 1, 8, 3, 50280, 50, expect_fused=True)
