@@ -203,6 +203,16 @@ int mtl_add_rmsnorm(const float* x, const float* y, float* x_out, const float* w
                     int64_t rows, int64_t cols, float eps, mtl_stream_t stream);
 
 /* ------------------------------------------------------------------------
+ * mtl_add_rmsnorm with y given as nparts split-K partial products
+ * y_parts [nparts, rows, cols] (contiguous): y = ((p0 + p1) + ...) in part
+ * order, then x_out = x + y and normed as above -- the residual add of
+ * model.py:311 after an out_proj computed by mtl_linear_skinny with
+ * ksplit = nparts, without a separate reduction launch.  1 <= nparts <= 64.
+ * ---------------------------------------------------------------------- */
+int mtl_add_rmsnorm_parts(const float* x, const float* y_parts, int32_t nparts, float* x_out, const float* w,
+                          float* normed, int64_t rows, int64_t cols, float eps, mtl_stream_t stream);
+
+/* ------------------------------------------------------------------------
  * Sum of split-K partial products in a fixed order: for nparts <= 32
  *   out[i] = ((parts[0*n + i] + parts[1*n + i]) + ...) + parts[(nparts-1)*n + i];
  * above 32 the parts form 4 contiguous quarters of ceil(nparts/4), each
@@ -241,6 +251,25 @@ int mtl_quant_dequant_sum_int8_tok(const float* const* parts, int32_t nparts, in
  * ---------------------------------------------------------------------- */
 int mtl_quant_dequant_sum_fp16(const float* const* parts, int32_t nparts, int64_t n,
                                uint16_t* const* payloads, float* out, mtl_stream_t stream);
+
+/* ------------------------------------------------------------------------
+ * Skinny fp32 GEMM on the matrix cores for the projections of a batched
+ * decode step: y = x W^T (+ bias), nn.Linear on [b, K] with b <= 32 tokens --
+ * in_proj (model.py:261), out_proj (model.py:293) and the tied lm_head
+ * (model.py:326, 353) in MambaMixer.step / MambaLM.step.
+ *   x: [M, K], row stride x_rs (>= K, multiple of 4), 1 <= M <= 32;
+ *   W: [N, K] contiguous, N a multiple of 4; bias: [N] or NULL;
+ *   y: [M, N] with row stride y_rs (>= N, multiple of 4).
+ * K must be a multiple of 128 * ksplit.  With ksplit > 1 the K range is cut
+ * into ksplit equal parts and part s writes its partial product to
+ * y + s * y_ks (bias in part 0 only); the caller adds the parts in order
+ * (mtl_sum_parts, or mtl_add_rmsnorm_parts for out_proj).  rows_per_block
+ * (16 or 32) is the weight rows per workgroup.  Every pointer 16-byte
+ * aligned.  Deterministic (fixed summation order).
+ * ---------------------------------------------------------------------- */
+int mtl_linear_skinny(const float* x, int64_t x_rs, const float* W, const float* bias, float* y, int64_t y_rs,
+                      int64_t y_ks, int64_t M, int64_t N, int64_t K, int32_t ksplit, int32_t rows_per_block,
+                      mtl_stream_t stream);
 
 /* ------------------------------------------------------------------------
  * Fused single-token decode step, fp32, batch 1, 2 or 4.

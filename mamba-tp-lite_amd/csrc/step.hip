@@ -178,15 +178,17 @@ constexpr int kNormThreads = 256;
 
 // One workgroup per row.  RUNS elements per thread (cols <= 256 RUNS),
 // loaded up front with clamped addresses.
-template <int RUNS>
+// y: NP parts (NP = 0: none) at stride yps, added to each other in part order
+// and then to x -- the split-K partial products of the out_proj before the
+// residual add
+template <int RUNS, int NP>
 __global__ void __launch_bounds__(kNormThreads)
-add_rmsnorm_kernel(const float* __restrict__ x, const float* __restrict__ y, float* x_out,
+add_rmsnorm_kernel(const float* __restrict__ x, const float* __restrict__ y, int64_t yps, float* x_out,
                    const float* __restrict__ w, float* __restrict__ normed, int cols, float eps) {
     __shared__ float s_part[kNormThreads / 64];
     const int64_t row = blockIdx.x;
     const int tid = threadIdx.x;
     const float* xr = x + row * cols;
-    const float* yr = y ? y + row * cols : nullptr;
     float v[RUNS], wv[RUNS];
 #pragma unroll
     for (int q = 0; q < RUNS; ++q) {
@@ -194,12 +196,19 @@ add_rmsnorm_kernel(const float* __restrict__ x, const float* __restrict__ y, flo
         v[q] = xr[i];
         wv[q] = w[i];
     }
-    if (yr) {
-        float yv[RUNS];
+    if constexpr (NP > 0) {
+        float yv[NP][RUNS];
 #pragma unroll
-        for (int q = 0; q < RUNS; ++q) yv[q] = yr[min(tid + q * kNormThreads, cols - 1)];
+        for (int p = 0; p < NP; ++p)
 #pragma unroll
-        for (int q = 0; q < RUNS; ++q) v[q] += yv[q];
+            for (int q = 0; q < RUNS; ++q) yv[p][q] = y[p * yps + row * cols + min(tid + q * kNormThreads, cols - 1)];
+#pragma unroll
+        for (int q = 0; q < RUNS; ++q) {
+            float t = yv[0][q];
+#pragma unroll
+            for (int p = 1; p < NP; ++p) t += yv[p][q];
+            v[q] += t;
+        }
     }
     float ss = 0.f;
 #pragma unroll
@@ -222,16 +231,21 @@ add_rmsnorm_kernel(const float* __restrict__ x, const float* __restrict__ y, flo
 
 // rows longer than 256 * kMaxRuns
 __global__ void __launch_bounds__(kNormThreads)
-add_rmsnorm_long_kernel(const float* __restrict__ x, const float* __restrict__ y, float* x_out,
+add_rmsnorm_long_kernel(const float* __restrict__ x, const float* __restrict__ y, int np, int64_t yps, float* x_out,
                         const float* __restrict__ w, float* __restrict__ normed, int cols, float eps) {
     __shared__ float s_part[kNormThreads / 64];
     const int64_t row = blockIdx.x;
     const float* xr = x + row * cols;
-    const float* yr = y ? y + row * cols : nullptr;
+    const float* yr = np > 0 ? y + row * cols : nullptr;
+    auto ysum = [&](int i) {
+        float t = yr[i];
+        for (int p = 1; p < np; ++p) t += yr[p * yps + i];
+        return t;
+    };
     float ss = 0.f;
     for (int i = threadIdx.x; i < cols; i += kNormThreads) {
         float v = xr[i];
-        if (yr) v += yr[i];
+        if (yr) v += ysum(i);
         ss = fmaf(v, v, ss);
     }
     ss = group_sum<64>(ss);
@@ -241,7 +255,7 @@ add_rmsnorm_long_kernel(const float* __restrict__ x, const float* __restrict__ y
     const float r = rsqrtf(tot / (float)cols + eps);
     for (int i = threadIdx.x; i < cols; i += kNormThreads) {
         float v = xr[i];
-        if (yr) v += yr[i];
+        if (yr) v += ysum(i);
         if (x_out) x_out[row * cols + i] = v;
         normed[row * cols + i] = w[i] * (v * r);
     }
@@ -295,6 +309,31 @@ extern "C" int mtl_selective_state_update(float* ssm_state, const void* x, int64
     return check_launch("selective_state_update");
 }
 
+namespace mtl {
+namespace {
+int add_rmsnorm_launch(const float* x, const float* y, int32_t nparts, int64_t yps, float* x_out, const float* w,
+                       float* normed, int64_t rows, int64_t cols, float eps, hipStream_t st) {
+    const int runs = (int)((cols + kNormThreads - 1) / kNormThreads);
+    const int np = y ? nparts : 0;
+    if (runs > kMaxRuns || (np != 0 && np != 1 && np != 2 && np != 4)) {
+        hipLaunchKernelGGL(add_rmsnorm_long_kernel, dim3((unsigned)rows), dim3(kNormThreads), 0, st, x, y, np, yps,
+                           x_out, w, normed, (int)cols, eps);
+    } else {
+#define MTL_NORM_NP(NPV)                                                                                             \
+    MTL_DISPATCH_RUNS(RUNS, round_runs(runs), hipLaunchKernelGGL((add_rmsnorm_kernel<RUNS, NPV>), dim3((unsigned)rows), \
+                                                                 dim3(kNormThreads), 0, st, x, y, yps, x_out, w,       \
+                                                                 normed, (int)cols, eps))
+        if (np == 0) { MTL_NORM_NP(0); }
+        else if (np == 1) { MTL_NORM_NP(1); }
+        else if (np == 2) { MTL_NORM_NP(2); }
+        else { MTL_NORM_NP(4); }
+#undef MTL_NORM_NP
+    }
+    return check_launch("add_rmsnorm");
+}
+}  // namespace
+}  // namespace mtl
+
 extern "C" int mtl_add_rmsnorm(const float* x, const float* y, float* x_out, const float* w, float* normed,
                                int64_t rows, int64_t cols, float eps, mtl_stream_t stream) {
     using namespace mtl;
@@ -303,16 +342,20 @@ extern "C" int mtl_add_rmsnorm(const float* x, const float* y, float* x_out, con
     MTL_REQUIRE(rows < (int64_t(1) << 31), "too many rows");
     if (rows == 0) return MTL_OK;
     MTL_REQUIRE(x && w && normed, "null required pointer");
-    hipStream_t st = as_stream(stream);
-    const int runs = (int)((cols + kNormThreads - 1) / kNormThreads);
-    if (runs > kMaxRuns)
-        hipLaunchKernelGGL(add_rmsnorm_long_kernel, dim3((unsigned)rows), dim3(kNormThreads), 0, st, x, y, x_out, w,
-                           normed, (int)cols, eps);
-    else
-        MTL_DISPATCH_RUNS(RUNS, round_runs(runs), hipLaunchKernelGGL((add_rmsnorm_kernel<RUNS>), dim3((unsigned)rows),
-                                                                     dim3(kNormThreads), 0, st, x, y, x_out, w,
-                                                                     normed, (int)cols, eps));
-    return check_launch("add_rmsnorm");
+    return add_rmsnorm_launch(x, y, 1, 0, x_out, w, normed, rows, cols, eps, as_stream(stream));
+}
+
+extern "C" int mtl_add_rmsnorm_parts(const float* x, const float* y_parts, int32_t nparts, float* x_out,
+                                     const float* w, float* normed, int64_t rows, int64_t cols, float eps,
+                                     mtl_stream_t stream) {
+    using namespace mtl;
+    clear_error();
+    MTL_REQUIRE(rows >= 0 && cols >= 1 && cols < (int64_t(1) << 31), "size out of range");
+    MTL_REQUIRE(rows < (int64_t(1) << 31), "too many rows");
+    MTL_REQUIRE(nparts >= 1 && nparts <= 64, "nparts must be in [1, 64]");
+    if (rows == 0) return MTL_OK;
+    MTL_REQUIRE(x && y_parts && w && normed, "null required pointer");
+    return add_rmsnorm_launch(x, y_parts, nparts, rows * cols, x_out, w, normed, rows, cols, eps, as_stream(stream));
 }
 
 extern "C" int mtl_sum_parts(const float* parts, int32_t nparts, int64_t n, float* out, mtl_stream_t stream) {

@@ -62,6 +62,7 @@ SIGNATURES = {
     "mtl_selective_state_update": (ctypes.c_int, [_fp, _vp, _i64, _vp, _i64, _vp, _i64, _fp, _fp, _fp, _fp,
                                                   _vp, _i64, _i64, _i64, _i64, _i64, _i32, _i32, _vp]),
     "mtl_add_rmsnorm": (ctypes.c_int, [_fp, _fp, _fp, _fp, _fp, _i64, _i64, ctypes.c_float, _vp]),
+    "mtl_add_rmsnorm_parts": (ctypes.c_int, [_fp, _fp, _i32, _fp, _fp, _fp, _i64, _i64, ctypes.c_float, _vp]),
     "mtl_sum_parts": (ctypes.c_int, [_fp, _i32, _i64, _fp, _vp]),
     "mtl_conv_step_xproj": (ctypes.c_int, [_fp, _fp, _i64, _fp, _fp, _fp, _i64, _fp, _fp, _i64, _i64, _i32, _i32,
                                            _vp]),
@@ -73,6 +74,7 @@ SIGNATURES = {
     "mtl_decode_in": (ctypes.c_int, [_fp, _fp, _vp, _i32, _fp, _fp, ctypes.c_float, _fp, _fp, _fp, _fp, _fp, _fp, _fp, _fp,
                                      _fp, _i32, _i32, _i32, _i32, _i32, _i32, _vp]),
     "mtl_decode_gemv": (ctypes.c_int, [_fp, _fp, _fp, _fp, _fp, _i32, _i32, _i32, _vp]),
+    "mtl_linear_skinny": (ctypes.c_int, [_fp, _i64, _fp, _fp, _fp, _i64, _i64, _i64, _i64, _i64, _i32, _i32, _vp]),
     "mtl_decode_norm_gemv": (ctypes.c_int, [_fp, _fp, ctypes.c_float, _fp, _fp, _fp, _i32, _i32, _i32, _vp]),
     "mtl_decode_ssm": (ctypes.c_int, [_fp, _i32, _fp, _fp, _fp, _fp, _fp, _fp, _fp, _fp, _i32, _i32, _i32, _i32,
                                       _vp]),

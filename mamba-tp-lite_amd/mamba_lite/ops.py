@@ -322,9 +322,16 @@ def selective_state_update(ssm_state, x, z, x_dbl, W_dt, b_dt, A, D=None, a_is_l
 
 
 # --------------------------------------------------------------------------- norm
-def add_rmsnorm(x, weight, eps, y=None, x_out=None, out=None):
+def add_rmsnorm(x, weight, eps, y=None, x_out=None, out=None, y_parts=None):
     """normed = weight * rmsnorm(x + y) (fp32, rows = all leading dims);
-    x_out (may alias x) receives x + y."""
+    x_out (may alias x) receives x + y.  y_parts [P, *x.shape] instead of y:
+    y = the sum of the P parts in order (split-K partial products)."""
+    if y_parts is not None:
+        if y is not None:
+            raise ValueError("give y or y_parts, not both")
+        if (y_parts.dtype != torch.float32 or not y_parts.is_contiguous() or y_parts.dim() != x.dim() + 1
+                or tuple(y_parts.shape[1:]) != tuple(x.shape)):
+            raise ValueError(f"y_parts must be contiguous float32 [P, {', '.join(map(str, x.shape))}]")
     if x.dtype != torch.float32 or not x.is_contiguous():
         raise ValueError("x must be contiguous float32")
     cols = x.shape[-1]
@@ -337,10 +344,15 @@ def add_rmsnorm(x, weight, eps, y=None, x_out=None, out=None):
         out = torch.empty_like(x)
     elif out.shape != x.shape or out.dtype != torch.float32 or not out.is_contiguous():
         raise ValueError("out must be contiguous float32 like x")
-    _same_device(x, weight, y, x_out, out)
+    _same_device(x, weight, y, x_out, out, y_parts)
     with _dev_guard(x):
-        _lib.check(_lib.load().mtl_add_rmsnorm(_ptr(x), _ptr(y), _ptr(x_out), _ptr(weight), _ptr(out), rows, cols,
-                                               float(eps), _stream(x)), "add_rmsnorm")
+        if y_parts is not None:
+            _lib.check(_lib.load().mtl_add_rmsnorm_parts(_ptr(x), _ptr(y_parts), y_parts.shape[0], _ptr(x_out),
+                                                         _ptr(weight), _ptr(out), rows, cols, float(eps), _stream(x)),
+                       "add_rmsnorm")
+        else:
+            _lib.check(_lib.load().mtl_add_rmsnorm(_ptr(x), _ptr(y), _ptr(x_out), _ptr(weight), _ptr(out), rows, cols,
+                                                   float(eps), _stream(x)), "add_rmsnorm")
     return out
 
 
@@ -480,6 +492,51 @@ def decode_gemv(v, W, out, bias=None, x_in=None):
     with _dev_guard(v):
         _lib.check(_lib.load().mtl_decode_gemv(_ptr(v), _ptr(W), _ptr(bias), _ptr(x_in), _ptr(out), b, rows, cols,
                                                _stream(v)), "decode_gemv")
+    return out
+
+
+SKINNY_MAX_ROWS = 32
+
+
+def linear_skinny_ok(x, W) -> bool:
+    """Whether mtl_linear_skinny takes y = x W^T for these operands: fp32 on
+    the GPU, 1..32 rows of x, K a multiple of 128, W rows a multiple of 4,
+    16-byte aligned rows."""
+    if x.dim() != 2 or W.dim() != 2 or x.dtype != torch.float32 or W.dtype != torch.float32:
+        return False
+    M, K = x.shape
+    N = W.shape[0]
+    return (x.is_cuda and W.is_cuda and 1 <= M <= SKINNY_MAX_ROWS and W.shape[1] == K and K % 128 == 0
+            and N % 4 == 0 and x.stride(1) == 1 and x.stride(0) % 4 == 0 and W.is_contiguous()
+            and x.data_ptr() % 16 == 0 and W.data_ptr() % 16 == 0)
+
+
+def linear_skinny(x, W, bias=None, out=None, ksplit=1, rows_per_block=None):
+    """mtl_linear_skinny: out [M, N] = x [M, K] . W [N, K]^T (+ bias) on the
+    matrix cores, for M <= 32 (the projections of a batched decode step).
+    With ksplit > 1, out is [ksplit, M, N]: the partial products over K
+    split into ksplit equal ranges (bias in part 0), to be added in order."""
+    if not linear_skinny_ok(x, W):
+        raise ValueError("linear_skinny: fp32 x [M<=32, K%128==0] (unit column stride, 16B rows) and contiguous "
+                         "W [N%4==0, K] expected")
+    M, K = x.shape
+    N = W.shape[0]
+    if bias is not None:
+        _f32_vec(bias, N, "bias")
+    if K % (128 * ksplit):
+        raise ValueError("linear_skinny: K must be a multiple of 128 * ksplit")
+    shape = (M, N) if ksplit == 1 else (ksplit, M, N)
+    if out is None:
+        out = torch.empty(shape, device=x.device, dtype=torch.float32)
+    elif tuple(out.shape) != shape or out.dtype != torch.float32 or not out.is_contiguous():
+        raise ValueError(f"linear_skinny: out must be contiguous float32 {shape}")
+    if rows_per_block is None:
+        # enough workgroups to keep every CU streaming the weight
+        rows_per_block = 32 if (N + 31) // 32 * ksplit >= 256 else 16
+    _same_device(x, W, bias, out)
+    with _dev_guard(x):
+        _lib.check(_lib.load().mtl_linear_skinny(_ptr(x), x.stride(0), _ptr(W), _ptr(bias), _ptr(out), N, M * N,
+                                                 M, N, K, ksplit, rows_per_block, _stream(x)), "linear_skinny")
     return out
 
 

@@ -87,6 +87,13 @@ def test_invalid_arguments_are_rejected_without_a_gpu():
     ("mtl_selective_state_update", dict(dstate=17), b"dstate"),
     ("mtl_selective_state_update", dict(dt_rank=257), b"dt_rank"),
     ("mtl_conv_step", dict(width=9), b"width"),
+    ("mtl_linear_skinny", dict(M=33), b"M (rows of x)"),
+    ("mtl_linear_skinny", dict(M=0), b"M (rows of x)"),
+    ("mtl_linear_skinny", dict(K=96), b"multiple of 128"),
+    ("mtl_linear_skinny", dict(K=256, ksplit=4), b"multiple of 128 * ksplit"),
+    ("mtl_linear_skinny", dict(N=6), b"multiple of 4"),
+    ("mtl_linear_skinny", dict(rows_per_block=8), b"rows_per_block"),
+    ("mtl_linear_skinny", dict(K=256, ksplit=2, y_ks=64), b"overlap"),
 ])
 def test_entry_points_validate_sizes_on_the_host(case):
     """Each entry point rejects sizes its kernels do not cover, with a message,
@@ -130,6 +137,11 @@ def test_entry_points_validate_sizes_on_the_host(case):
         a.update(over)
         rc = lib.mtl_selective_state_update(P, P, 64, None, 0, P, 36, P, P, P, None, P, 64, 1, 64, a["dstate"],
                                             a["dt_rank"], 0, 0, None)
+    elif name == "mtl_linear_skinny":
+        a = dict(M=8, N=64, K=128, ksplit=1, rows_per_block=16, y_ks=0)
+        a.update(over)
+        rc = lib.mtl_linear_skinny(P, a["K"], P, None, P, a["N"], a["y_ks"], a["M"], a["N"], a["K"], a["ksplit"],
+                                   a["rows_per_block"], None)
     else:
         a = dict(width=4)
         a.update(over)

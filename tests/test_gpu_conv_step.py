@@ -217,6 +217,27 @@ def test_add_rmsnorm(rows, cols):
     assert_rel(out2.cpu().numpy(), om.rmsnorm(x, w, 1e-5, np.float64), 1e-5, "norm only")
 
 
+@pytest.mark.parametrize("rows,cols,nparts", [(32, 2048, 4), (32, 768, 4), (5, 768, 2), (3, 100, 1), (2, 4500, 3),
+                                               (7, 300, 4)])
+def test_add_rmsnorm_parts(rows, cols, nparts):
+    """y given as split-K parts: x_out = x + ((p0 + p1) + ...), bit for bit
+    what the parts summed in order and then mtl_add_rmsnorm give."""
+    rng = np.random.default_rng(rows * 3 + cols + nparts)
+    x = rng.standard_normal((rows, cols)).astype(np.float32)
+    parts = rng.standard_normal((nparts, rows, cols)).astype(np.float32)
+    w = (1 + 0.1 * rng.standard_normal(cols)).astype(np.float32)
+    X = _t(x)
+    out = ops.add_rmsnorm(X, _t(w), 1e-5, y_parts=_t(parts), x_out=X)
+    ysum = parts[0].copy()
+    for p in range(1, nparts):
+        ysum = ysum + parts[p]                   # float32, part order
+    X2 = _t(x)
+    out2 = ops.add_rmsnorm(X2, _t(w), 1e-5, y=_t(ysum), x_out=X2)
+    assert torch.equal(X, X2) and torch.equal(out, out2)
+    assert_rel(out.cpu().numpy(), om.rmsnorm(x.astype(np.float64) + parts.astype(np.float64).sum(0), w, 1e-5,
+                                             np.float64), 1e-5, "normed")
+
+
 @pytest.mark.parametrize("nparts,n", [(1, 5), (3, 1000), (16, 5120), (32, 257), (33, 100), (64, 300), (97, 64),
                                       (128, 5120)])
 def test_sum_parts_in_part_order(nparts, n):
