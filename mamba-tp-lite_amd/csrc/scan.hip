@@ -729,7 +729,6 @@ __global__ void __launch_bounds__(kLaneChannels * 64) scan_lanes_kernel(const Sc
         h_in[n] = lane_read(h_lane, n);
     }
 
-    const int last0 = (L - 1) / 64 * 64;
     for (int t0 = 0; t0 < L; t0 += 64) {
 #pragma unroll
         for (int q = 0; q < kFill; ++q) {
@@ -743,7 +742,10 @@ __global__ void __launch_bounds__(kLaneChannels * 64) scan_lanes_kernel(const Sc
         s_x[0][xe_c][xe_t] = cur.u;
         s_x[1][xe_c][xe_t] = cur.d;
         s_x[2][xe_c][xe_t] = cur.z;
-        load_chunk(nxt, min(t0 + 64, last0));          // the last chunk re-reads itself rather than branch
+        // the next chunk's loads only when there is one: a last chunk that
+        // re-read itself made every wavefront wait for those loads before
+        // exiting (64-token prompt: 4.94 -> 4.76 us per launch)
+        if (t0 + 64 < L) load_chunk(nxt, t0 + 64);
         __syncthreads();
         const int t = t0 + lane;
         const bool valid = t < L;
