@@ -293,6 +293,11 @@ int mtl_linear_skinny(const float* x, int64_t x_rs, const float* W, const float*
  * mtl_decode_gemv: out [b, rows] = W [rows, cols] . v [b, cols] (+ bias)
  *   (+ x_in, the residual add of model.py:311): the out_proj rows
  *   (model.py:293) and, in the 4-launch form, the x_proj rows (279).
+ * mtl_decode_gemv_parts: out_parts [nparts, b, rows], part p = the product
+ *   of columns [p cols/nparts, (p+1) cols/nparts) of W [rows, cols] and v
+ *   [b, cols] (cols/nparts a multiple of 4, at most 4096): the x_proj rows
+ *   (model.py:279) of a width whose block partials do not fit decode_in, as
+ *   split-K parts that mtl_decode_ssm adds in part order (nblk = nparts).
  * mtl_decode_norm_gemv: out [b, rows] = W [rows, cols] . RMSNorm(v) (+ bias)
  *   with RMSNorm(v) = norm_w * v * rsqrt(mean(v^2) + eps): the final norm_f
  *   and the tied lm_head of MambaLM.step (model.py:351-352, RMSNorm at
@@ -311,6 +316,8 @@ int mtl_decode_in(const float* x, const float* emb, const int64_t* ids, int32_t 
                   mtl_stream_t stream);
 int mtl_decode_gemv(const float* v, const float* W, const float* bias, const float* x_in, float* out, int32_t batch,
                     int32_t rows, int32_t cols, mtl_stream_t stream);
+int mtl_decode_gemv_parts(const float* v, const float* W, float* out_parts, int32_t batch, int32_t rows, int32_t cols,
+                          int32_t nparts, mtl_stream_t stream);
 int mtl_decode_norm_gemv(const float* v, const float* norm_w, float eps, const float* W, const float* bias, float* out,
                          int32_t batch, int32_t rows, int32_t cols, mtl_stream_t stream);
 int mtl_decode_ssm(const float* xpart, int32_t nblk, const float* xc, const float* gz, const float* W_dt,

@@ -287,6 +287,8 @@ struct GemvArgs {
     int Mrows, K;
     const float* norm_w;     // [K]: v is RMS-normalized with these weights first (NORM kernels)
     float eps;
+    int ld;                  // row stride of W and v (the split kernel's parts: K = ld / parts)
+    int64_t out_ps;          // split kernel: part p writes out + p * out_ps
 };
 
 // one wavefront per output row, 4 rows per workgroup; K <= 256 * PL.
@@ -364,29 +366,33 @@ __global__ void __launch_bounds__(kThreads) decode_gemv_kernel(const GemvArgs a)
     }
 }
 
-// Few long rows (x_proj at d_inner 4096: 160 rows): one workgroup per row,
-// the 4 wavefronts take quarters of it (PLW float4 runs per lane each,
-// K <= 1024 PLW) and their sums are added in wavefront order.
+// Few long rows (x_proj at d_inner 4096: 160 rows): one workgroup per row
+// and column part (blockIdx.y: columns [p K, (p + 1) K) of rows of length
+// ld), the 4 wavefronts take quarters of it (PLW float4 runs per lane each,
+// K <= 1024 PLW) and their sums are added in wavefront order; part p writes
+// its partial product to out + p * out_ps (bias and x_in in part 0).
 template <int B, int PLW>
 __global__ void __launch_bounds__(kThreads) decode_gemv_split_kernel(const GemvArgs a) {
     extern __shared__ __align__(16) float s_v[];      // [B][K], then the [kWaves][B] wavefront sums
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int K = a.K, K4 = K >> 2;
-    const int m = blockIdx.x;
-    const float4* row = reinterpret_cast<const float4*>(a.W + (int64_t)m * K);
+    const int m = blockIdx.x, part = blockIdx.y;
+    const int64_t k0 = (int64_t)part * K;
+    const float4* row = reinterpret_cast<const float4*>(a.W + (int64_t)m * a.ld + k0);
     float4 w[PLW];
 #pragma unroll
     for (int p = 0; p < PLW; ++p) w[p] = ntload4(row + min((wave * PLW + p) * 64 + lane, K4 - 1));
-    const float bias = a.bias ? a.bias[m] : 0.f;
+    const float bias = a.bias && part == 0 ? a.bias[m] : 0.f;
+    const bool add_x = a.x_in && part == 0;
     float xin[B];
 #pragma unroll
-    for (int bi = 0; bi < B; ++bi) xin[bi] = a.x_in ? a.x_in[(int64_t)bi * a.Mrows + m] : 0.f;
+    for (int bi = 0; bi < B; ++bi) xin[bi] = add_x ? a.x_in[(int64_t)bi * a.Mrows + m] : 0.f;
     constexpr int PL = kWaves * PLW;
     float vv[B][PL];
 #pragma unroll
     for (int q = 0; q < PL; ++q)
 #pragma unroll
-        for (int bi = 0; bi < B; ++bi) vv[bi][q] = a.v[(int64_t)bi * K + min(tid + q * kThreads, K - 1)];
+        for (int bi = 0; bi < B; ++bi) vv[bi][q] = a.v[(int64_t)bi * a.ld + k0 + min(tid + q * kThreads, K - 1)];
 #pragma unroll
     for (int q = 0; q < PL; ++q)
         if (tid + q * kThreads < K)
@@ -416,7 +422,7 @@ __global__ void __launch_bounds__(kThreads) decode_gemv_split_kernel(const GemvA
     __syncthreads();
     if (tid < B) {
         const float o = ((s_v[tid] + s_v[B + tid]) + (s_v[2 * B + tid] + s_v[3 * B + tid])) + bias;
-        a.out[(int64_t)tid * a.Mrows + m] = a.x_in ? xin[tid] + o : o;
+        a.out[part * a.out_ps + (int64_t)tid * a.Mrows + m] = add_x ? xin[tid] + o : o;
     }
 }
 
@@ -571,7 +577,7 @@ extern "C" int mtl_decode_gemv(const float* v, const float* W, const float* bias
     MTL_REQUIRE(x_in == nullptr || x_in != out, "out must not alias x_in");
     const size_t smem = sizeof(float) * (size_t)batch * cols;
     MTL_REQUIRE(smem <= 64 * 1024, "batch * cols too large for the decode LDS tile");
-    GemvArgs a{v, W, bias, x_in, out, rows, cols, nullptr, 0.f};
+    GemvArgs a{v, W, bias, x_in, out, rows, cols, nullptr, 0.f, cols, 0};
     hipStream_t st = as_stream(stream);
     const int runs = (cols / 4 + 63) / 64;
     if (rows < 128 * kWaves && runs >= 2 * kWaves) {
@@ -589,6 +595,29 @@ extern "C" int mtl_decode_gemv(const float* v, const float* W, const float* bias
     return check_launch("decode_gemv");
 }
 
+extern "C" int mtl_decode_gemv_parts(const float* v, const float* W, float* out_parts, int32_t batch, int32_t rows,
+                                     int32_t cols, int32_t nparts, mtl_stream_t stream) {
+    using namespace mtl;
+    clear_error();
+    MTL_REQUIRE(batch == 1 || batch == 2 || batch == 4, "batch must be 1, 2 or 4");
+    MTL_REQUIRE(nparts >= 1 && nparts <= 64 && rows >= 1, "nparts must be in [1, 64]");
+    MTL_REQUIRE(cols >= 4 && cols % (4 * nparts) == 0, "cols must be a multiple of 4 * nparts");
+    const int K = cols / nparts;
+    const int runs = (K / 4 + 63) / 64;
+    const int plw = round_runs((runs + kWaves - 1) / kWaves);
+    MTL_REQUIRE(plw * kWaves <= kMaxPL, "cols / nparts must be at most 4096");
+    MTL_REQUIRE(v && W && out_parts, "null required pointer");
+    MTL_REQUIRE(((uintptr_t)W % 16) == 0 && ((uintptr_t)v % 16) == 0, "W and v must be 16-byte aligned");
+    const size_t smem = sizeof(float) * (size_t)batch * K;
+    MTL_REQUIRE(smem <= 64 * 1024, "batch * cols / nparts too large for the decode LDS tile");
+    GemvArgs a{v, W, nullptr, nullptr, out_parts, rows, K, nullptr, 0.f, cols, (int64_t)batch * rows};
+    hipStream_t st = as_stream(stream);
+    MTL_DISPATCH_B(batch, MTL_DISPATCH_RUNS(PLW, plw,
+        if constexpr (PLW * kWaves <= kMaxPL) hipLaunchKernelGGL((decode_gemv_split_kernel<B, PLW>),
+            dim3((unsigned)rows, (unsigned)nparts), dim3(kThreads), smem, st, a)));
+    return check_launch("decode_gemv_parts");
+}
+
 extern "C" int mtl_decode_norm_gemv(const float* v, const float* norm_w, float eps, const float* W, const float* bias,
                                     float* out, int32_t batch, int32_t rows, int32_t cols, mtl_stream_t stream) {
     using namespace mtl;
@@ -601,7 +630,7 @@ extern "C" int mtl_decode_norm_gemv(const float* v, const float* norm_w, float e
     MTL_REQUIRE(v != out, "out must not alias v");
     const size_t smem = sizeof(float) * (size_t)batch * cols;
     MTL_REQUIRE(smem <= 64 * 1024, "batch * cols too large for the decode LDS tile");
-    GemvArgs a{v, W, bias, nullptr, out, rows, cols, norm_w, eps};
+    GemvArgs a{v, W, bias, nullptr, out, rows, cols, norm_w, eps, cols, 0};
     hipStream_t st = as_stream(stream);
     const int runs = (cols / 4 + 63) / 64;
     const dim3 grid((unsigned)((rows + kWaves - 1) / kWaves));

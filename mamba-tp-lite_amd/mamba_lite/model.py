@@ -141,6 +141,9 @@ SMALL_PREFILL_TOKENS = 256
 # Batched step projections on mtl_linear_skinny (fp32, <= 32 tokens): in_proj
 # up to this many weight elements, out_proj as this many split-K parts.
 SKINNY_IN_PROJ_MAX = 4 * 1024 * 1024
+
+# column parts of the fused step's stand-alone x_proj GEMV
+_XPROJ_PARTS = 4
 SKINNY_OUT_SPLIT = 4
 SMALL_PREFILL_BLAS: str | None = "cublas"
 
@@ -552,7 +555,10 @@ class MambaLM(nn.Module):
         gz = torch.empty(b, D, **f32)
         y = torch.empty(b, D, **f32)
         xs = [torch.empty(b, M, **f32) for _ in range(3)]
-        xpart = torch.empty(plan["nblk"] if split_k else 1, b, J, **f32)
+        # without block partials, x_proj runs as its own row GEMV in column parts
+        # (more workgroups on its 160 rows at the 1.4b width) that decode_ssm adds
+        xp_parts = 1 if split_k else _XPROJ_PARTS if D % (4 * _XPROJ_PARTS) == 0 else 1
+        xpart = torch.empty(plan["nblk"] if split_k else xp_parts, b, J, **f32)
         x_cur = None
         for i, blk in enumerate(self.layers):
             mx, lp, lc = blk.mixer, plan["layers"][i], cache.layers[i]
@@ -563,7 +569,7 @@ class MambaLM(nn.Module):
                           W_xT=lp["W_xT"] if split_k else None, xpart=xpart if split_k else None,
                           channels_per_block=plan["cpb"])
             if not split_k:
-                ops.decode_gemv(xc, mx.x_proj.weight, xpart[0])
+                ops.decode_gemv_parts(xc, mx.x_proj.weight, xpart)
             ops.decode_ssm(xpart, xc, gz, mx.dt_proj.weight, mx.dt_proj.bias, mx.A_log, mx.D, lc.ssm_state, y)
             x_next = xs[i % 2]
             ops.decode_gemv(y, mx.out_proj.weight, x_next, bias=mx.out_proj.bias, x_in=resid)

@@ -540,6 +540,22 @@ def linear_skinny(x, W, bias=None, out=None, ksplit=1, rows_per_block=None):
     return out
 
 
+def decode_gemv_parts(v, W, out_parts):
+    """mtl_decode_gemv_parts: out_parts [P, b, rows], part p = W[:, p-th of P
+    column ranges] . v[:, same range] (summed in order by decode_ssm)."""
+    for name, t in (("v", v), ("W", W), ("out_parts", out_parts)):
+        _f32c(t, name)
+    b, cols = v.shape
+    rows = W.shape[0]
+    P = out_parts.shape[0]
+    if W.shape[1] != cols or tuple(out_parts.shape) != (P, b, rows):
+        raise ValueError("decode_gemv_parts: W [rows, cols], v [b, cols], out_parts [P, b, rows] expected")
+    with _dev_guard(v):
+        _lib.check(_lib.load().mtl_decode_gemv_parts(_ptr(v), _ptr(W), _ptr(out_parts), b, rows, cols, P, _stream(v)),
+                   "decode_gemv_parts")
+    return out_parts
+
+
 def decode_norm_gemv(v, norm_w, eps, W, out, bias=None):
     """mtl_decode_norm_gemv: out [b, rows] = W [rows, cols] . RMSNorm(v) (+ bias),
     RMSNorm(v) = norm_w * v * rsqrt(mean(v^2) + eps) -- the final norm and

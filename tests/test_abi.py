@@ -87,6 +87,10 @@ def test_invalid_arguments_are_rejected_without_a_gpu():
     ("mtl_selective_state_update", dict(dstate=17), b"dstate"),
     ("mtl_selective_state_update", dict(dt_rank=257), b"dt_rank"),
     ("mtl_conv_step", dict(width=9), b"width"),
+    ("mtl_decode_gemv_parts", dict(nparts=0), b"nparts"),
+    ("mtl_decode_gemv_parts", dict(cols=4100, nparts=4), b"multiple of 4 * nparts"),
+    ("mtl_decode_gemv_parts", dict(cols=8192 * 4, nparts=4), b"at most 4096"),
+    ("mtl_decode_gemv_parts", dict(batch=3), b"batch must be 1, 2 or 4"),
     ("mtl_linear_skinny", dict(M=33), b"M (rows of x)"),
     ("mtl_linear_skinny", dict(M=0), b"M (rows of x)"),
     ("mtl_linear_skinny", dict(K=96), b"multiple of 128"),
@@ -137,6 +141,10 @@ def test_entry_points_validate_sizes_on_the_host(case):
         a.update(over)
         rc = lib.mtl_selective_state_update(P, P, 64, None, 0, P, 36, P, P, P, None, P, 64, 1, 64, a["dstate"],
                                             a["dt_rank"], 0, 0, None)
+    elif name == "mtl_decode_gemv_parts":
+        a = dict(batch=1, rows=8, cols=4096, nparts=4)
+        a.update(over)
+        rc = lib.mtl_decode_gemv_parts(P, P, P, a["batch"], a["rows"], a["cols"], a["nparts"], None)
     elif name == "mtl_linear_skinny":
         a = dict(M=8, N=64, K=128, ksplit=1, rows_per_block=16, y_ks=0)
         a.update(over)
