@@ -516,8 +516,10 @@ def main():
                          "traffic": traffic_from_profiles("scan_fp32_b32_d1536_l1024"),
                          "kernel": "scan_fwd_kernel<float, NW=4, SPW=4, TT=16, channel-major>",
                          "algorithmic_bytes": SCAN_BYTES,
-                         "limiter": "VALU issue, not HBM: 106 VALU instructions per 64 (channel, step) pairs, "
-                                    "80 of them the 16-state recurrence; 81% VALU busy (rocprofv3 counters)"},
+                         "limiter": "VALU issue and the access pattern together: 102 VALU instructions per 64 "
+                                    "(channel, step) pairs, 80 of them the 16-state recurrence, 76% VALU busy "
+                                    "(rocprofv3 counters; 170 us of VALU work at 100%); the same channel-major "
+                                    "u/delta/z/y stream with no arithmetic takes 173 us (4.65 TB/s)"},
         })
         extra["scan_trials_ms"] = trials
         extra["scan_prewarm"] = prewarm
