@@ -205,6 +205,43 @@ def test_graph_replay_bit_identical_to_eager(small_lm, batch):
         assert torch.equal(le.ssm_state, lg.ssm_state) and torch.equal(le.conv_state, lg.conv_state)
 
 
+@pytest.mark.parametrize("batch", [8, 32])
+def test_graph_replay_on_the_skinny_gemm_step(batch, monkeypatch):
+    """The batched per-op step with in_proj and out_proj on mtl_linear_skinny
+    (out_proj as 4 split-K parts summed by the residual add): graph replays
+    equal eager bit for bit, with eager work between replays, and the eager
+    step matches the float64 oracle."""
+    from mamba_lite import ops as mops
+    calls = []
+    real = mops.linear_skinny
+    monkeypatch.setattr(mops, "linear_skinny", lambda *a, **k: calls.append(k.get("ksplit", 1)) or real(*a, **k))
+    torch.manual_seed(6)
+    cfg = MambaConfig(d_model=256, n_layer=2, vocab_size=512, d_state=16)
+    model = MambaLM(cfg)
+    _init_dt_bias(model, 6)
+    model = model.to(DEV).eval()
+    ids = torch.randint(0, 512, (batch, 6), device=DEV)
+    steps = [torch.randint(0, 512, (batch, 1), device=DEV) for _ in range(4)]
+    with torch.no_grad():
+        _, cache_e = model.prefill(ids)
+        eager = [model.step(s, cache_e).clone() for s in steps]
+        assert 1 in calls and 4 in calls, calls      # in_proj whole, out_proj in 4 parts
+        ref_logits, rcache = om.lm_prefill(_lm_weights(model), ids.cpu().numpy(), dtype=np.float64)
+        for k, s in enumerate(steps):
+            ref = om.lm_step(_lm_weights(model), s.cpu().numpy(), rcache, dtype=np.float64)
+            assert_rel(eager[k].cpu().numpy(), ref, 1e-4, f"step {k}")
+        _, cache_g = model.prefill(ids)
+        st = GraphedStepper(model, cache_g, batch, "cuda")
+        st.capture()
+        for i, s in enumerate(steps):
+            g = st.replay(s).clone()
+            torch.cuda.synchronize()
+            _ = model.prefill(ids[:, :3])
+            assert torch.equal(g, eager[i]), f"replay {i} differs"
+    for le, lg in zip(cache_e.layers, cache_g.layers):
+        assert torch.equal(le.ssm_state, lg.ssm_state) and torch.equal(le.conv_state, lg.conv_state)
+
+
 @pytest.mark.parametrize("split", [False, True])
 def test_bf16_mixer_shard_shape(split, monkeypatch):
     """bf16 activations, fp32 scan state, through conv + scan + gate at a
