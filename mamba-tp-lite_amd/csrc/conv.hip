@@ -245,7 +245,7 @@ int launch_conv_step(void* state, const void* x, int64_t x_sb, const float* w, c
 
 // Batched single-token conv step fused with the x_proj split-K partials
 // (model.py:264-279 for b rows at once): a workgroup owns kXpCB channels of
-// all b <= 32 rows.  Phase 1: conv step (history shifted in place) + SiLU for
+// 8 TB rows (blockIdx.y: rows [8 TB y, 8 TB (y + 1)) of b <= 32).  Phase 1: conv step (history shifted in place) + SiLU for
 // its (channel, row) pairs, xc to global memory and to LDS.  Phase 2: the
 // block's partial x_dbl[b][j] = sum over its channels of xc[b][c] W_xT[c][j],
 // from LDS, a TB x (J/32) register tile per thread (rows b0.., columns jg +
@@ -253,6 +253,10 @@ int launch_conv_step(void* state, const void* x, int64_t x_sb, const float* w, c
 // order.
 constexpr int kXpCB = 32;                 // channels per workgroup
 constexpr int kXpMaxJQ = 9;               // J <= 288 = 256 + 32
+#ifndef MTL_XP_ROW_TB
+#define MTL_XP_ROW_TB 2
+#endif
+constexpr int kXpRowTB = MTL_XP_ROW_TB;   // above 8 rows: 8 kXpRowTB rows per workgroup
 
 template <int K, int TB, int JQ>
 __global__ void __launch_bounds__(256) conv_step_xproj_kernel(float* __restrict__ state, const float* __restrict__ x,
@@ -261,7 +265,8 @@ __global__ void __launch_bounds__(256) conv_step_xproj_kernel(float* __restrict_
                                                               int64_t o_sb, const float* __restrict__ WxT,
                                                               float* __restrict__ xpart, int batch, int D, int J) {
     constexpr int BMAX = 8 * TB;                     // rows covered: 8 row groups of TB
-    __shared__ float s_xc[BMAX][kXpCB + 1];
+    __shared__ float s_xc[BMAX][kXpCB + 1];          // local rows
+    const int b0 = blockIdx.y * BMAX;
     __shared__ float s_w[kXpCB][kXpMaxJQ * 32];       // rows c >= nch are never read (see phase 2)
     const int tid = threadIdx.x;
     const int c0 = blockIdx.x * kXpCB;
@@ -280,7 +285,7 @@ __global__ void __launch_bounds__(256) conv_step_xproj_kernel(float* __restrict_
     float win[TB][K], wk[TB][K], bs[TB];
 #pragma unroll
     for (int q = 0; q < TB; ++q) {
-        const int ch = c0 + min(tid % kXpCB, nch - 1), bi = min(tid / kXpCB + 8 * q, batch - 1);
+        const int ch = c0 + min(tid % kXpCB, nch - 1), bi = min(b0 + tid / kXpCB + 8 * q, batch - 1);
         const float* s = state + ((int64_t)bi * D + ch) * (K - 1);
 #pragma unroll
         for (int k = 0; k < K - 1; ++k) win[q][k] = s[k];
@@ -296,7 +301,7 @@ __global__ void __launch_bounds__(256) conv_step_xproj_kernel(float* __restrict_
     static_assert(kPairs == 256 * TB, "one pair per thread per row group");
 #pragma unroll
     for (int q = 0; q < TB; ++q) {
-        const int c = tid % kXpCB, bi = tid / kXpCB + 8 * q;
+        const int c = tid % kXpCB, bl = tid / kXpCB + 8 * q, bi = b0 + bl;
         float acc = 0.f;
 #pragma unroll
         for (int k = 0; k < K; ++k) acc = fmaf(win[q][k], wk[q][k], acc);
@@ -310,7 +315,7 @@ __global__ void __launch_bounds__(256) conv_step_xproj_kernel(float* __restrict_
             for (int k = 0; k < K - 1; ++k) s[k] = win[q][k + 1];
             out[bi * o_sb + ch] = xcv;
         }
-        s_xc[bi][c] = xcv;
+        s_xc[bl][c] = xcv;
     }
     __syncthreads();
 
@@ -336,7 +341,7 @@ __global__ void __launch_bounds__(256) conv_step_xproj_kernel(float* __restrict_
     }
 #pragma unroll
     for (int i = 0; i < TB; ++i) {
-        const int bi = rg * TB + i;
+        const int bi = b0 + rg * TB + i;
         if (bi >= batch) continue;
 #pragma unroll
         for (int q = 0; q < JQ; ++q) {
@@ -411,8 +416,11 @@ namespace {
 int launch_conv_step_xproj(float* conv_state, const float* x, int64_t x_sb, const float* w, const float* bias,
                            float* out, int64_t out_sb, const float* W_xT, float* xpart, int64_t batch, int64_t dim,
                            int32_t width, int32_t xdbl_cols, hipStream_t st) {
-    const dim3 grid((unsigned)((dim + kXpCB - 1) / kXpCB));
     const int D = (int)dim, J = xdbl_cols, B = (int)batch;
+    // rows per workgroup: 8 TB; above 8 rows the rows are split over
+    // workgroups of 16 (kXpRowSplit) so that the grid covers every CU
+    const int tb = B <= 8 ? 1 : kXpRowTB;
+    const dim3 grid((unsigned)((dim + kXpCB - 1) / kXpCB), (unsigned)((B + 8 * tb - 1) / (8 * tb)));
 #define MTL_XP_LAUNCH(KK, TBV, JQV) hipLaunchKernelGGL((conv_step_xproj_kernel<KK, TBV, JQV>), grid, dim3(256), 0, \
         st, conv_state, x, x_sb, w, bias, out, out_sb, W_xT, xpart, B, D, J)
 #define MTL_XP_J(KK, TBV)                                                \
@@ -422,9 +430,8 @@ int launch_conv_step_xproj(float* conv_state, const float* x, int64_t x_sb, cons
     else MTL_XP_LAUNCH(KK, TBV, 9);
 #define MTL_XP_K(KK)                                                     \
     case KK:                                                             \
-        if (B <= 8) { MTL_XP_J(KK, 1) }                                  \
-        else if (B <= 16) { MTL_XP_J(KK, 2) }                            \
-        else { MTL_XP_J(KK, 4) }                                         \
+        if (tb == 1) { MTL_XP_J(KK, 1) }                                 \
+        else { MTL_XP_J(KK, kXpRowTB) }                                  \
         break;
     switch (width) {
         MTL_XP_K(1) MTL_XP_K(2) MTL_XP_K(3) MTL_XP_K(4) MTL_XP_K(5) MTL_XP_K(6) MTL_XP_K(7) MTL_XP_K(8)
