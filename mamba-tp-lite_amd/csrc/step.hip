@@ -12,6 +12,8 @@
 // mtl_add_rmsnorm replaces the residual add of MambaBlock (model.py:306,
 // 311) fused with the following RMSNorm (model.py:130-135).
 
+#include <type_traits>
+
 #include "common.h"
 
 namespace mtl {
@@ -269,10 +271,161 @@ add_rmsnorm_long_kernel(const float* __restrict__ x, const float* __restrict__ y
         default: { constexpr int BB = 8; __VA_ARGS__; } break;     \
     }
 
+// Batched form for many rows (fp32, 16 states, dt_rank a multiple of 16):
+// one workgroup per 16 channels x 16 MB batch rows (MB = 1; 32-row tiles
+// measured the same at batch 32 and slower at 16).
+//  * dt_low . W_dt for the tile on the matrix cores: A = W_dt rows (16
+//    channels), B = the rows' dt_low (MB 16-row blocks), K = dt_rank in
+//    16-column blocks dealt to the four wavefronts; lane r + 16 kk loads a
+//    float4 of columns k + 4 kk and feeds four v_mfma_f32_16x16x4_f32, the
+//    q-th taking component q on both sides.  The wavefronts' tiles are added
+//    in wavefront order through LDS (deterministic).
+//  * Then thread t owns the (row, channel) pairs (16 u + t / 16, t % 16),
+//    u < MB, with all 16 states in registers: the state moves
+//    as four float4 per pair (a row's 16 channels are 1 KB contiguous), y is
+//    a sum over registers, and B, C of the row and A of the channel come from
+//    LDS broadcasts -- no cross-lane reduction per row as in the 16-lanes-per-
+//    channel form above, whose dt dot, state stores and y butterflies measured
+//    1.6, 1.1 and 0.2 us of its 9.2 us at batch 32, d_inner 4096 (this form:
+//    6.7 us; batch 16: 6.4 -> 4.3 us).
+constexpr int kRowsCh = 16;
+#ifndef MTL_ROWS_MIN_BATCH
+#define MTL_ROWS_MIN_BATCH 16
+#endif
+constexpr int64_t kRowsMinBatch = MTL_ROWS_MIN_BATCH;   // the rows form from this batch on
+#ifndef MTL_ROWS_TILE
+#define MTL_ROWS_TILE 16
+#endif
+constexpr int kRowsTile = MTL_ROWS_TILE;                  // batch rows per workgroup (16 or 32)
+typedef float F4s __attribute__((ext_vector_type(4)));
+
+template <int KBW, int MB>   // KBW: 16-column blocks of dt_rank per wavefront (dt_rank <= 64 KBW); MB: 16-row blocks
+__global__ void __launch_bounds__(kStepThreads)
+ssm_step_rows_kernel(float* __restrict__ state, const float* __restrict__ x, int64_t x_sb,
+                     const float* __restrict__ z, int64_t z_sb, const float* __restrict__ xdbl, int64_t xdbl_sb,
+                     const float* __restrict__ Wdt, const float* __restrict__ bdt, const float* __restrict__ A,
+                     const float* __restrict__ Dv, float* __restrict__ y, int64_t y_sb, int D, int R, int batch,
+                     int a_is_log) {
+    constexpr int N = 16, TR = 16 * MB;               // rows per workgroup
+    __shared__ __align__(16) F4s s_dt[kStepThreads / 64][MB][64];
+    __shared__ __align__(16) float s_bc[TR][2 * N];
+    __shared__ __align__(16) float s_a[kRowsCh][N];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int c0 = blockIdx.x * kRowsCh, b0 = blockIdx.y * TR;
+
+    // ---- every independent load first
+    const int r16 = lane & 15, kk = lane >> 4;
+    const int nkb = R / 16;
+    const float* wrow = Wdt + (int64_t)min(c0 + r16, D - 1) * R + 4 * kk;
+    const float* xr[MB];
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) xr[mb] = xdbl + (int64_t)min(b0 + 16 * mb + r16, batch - 1) * xdbl_sb + 4 * kk;
+    F4s wv[KBW], xo[KBW][MB];
+#pragma unroll
+    for (int j = 0; j < KBW; ++j) {
+        const int kc = min(wave + 4 * j, nkb - 1) * 16;
+        wv[j] = *reinterpret_cast<const F4s*>(wrow + kc);
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb) xo[j][mb] = *reinterpret_cast<const F4s*>(xr[mb] + kc);
+    }
+    // pairs (row, channel): u-th = (16 u + tid / 16, tid % 16)
+    const int pc = tid & 15, pr = tid >> 4;
+    const int cg = min(c0 + pc, D - 1);
+    int64_t brow[MB];
+    float hs[MB][N], xv[MB], zv[MB];
+#pragma unroll
+    for (int u = 0; u < MB; ++u) {
+        brow[u] = min(b0 + pr + 16 * u, batch - 1);
+        const F4s* sp = reinterpret_cast<const F4s*>(state + (brow[u] * D + cg) * N);
+#pragma unroll
+        for (int q = 0; q < N / 4; ++q) {
+            const F4s v = sp[q];
+            hs[u][4 * q] = v.x; hs[u][4 * q + 1] = v.y; hs[u][4 * q + 2] = v.z; hs[u][4 * q + 3] = v.w;
+        }
+        xv[u] = x[brow[u] * x_sb + cg];
+        zv[u] = z ? z[brow[u] * z_sb + cg] : 0.f;
+    }
+    const float bd = bdt[cg];
+    const float Dc = Dv ? Dv[cg] : 0.f;
+    // A of (channel tid / 16, state tid % 16), in log2 units
+    float av = A[(int64_t)min(c0 + (tid >> 4), D - 1) * N + (tid & 15)];
+    // B | C of row tid / 8, columns 4 (tid % 8) .. + 3
+    const int bcr = tid >> 3, bcj = 4 * (tid & 7);
+    const F4s bc = *reinterpret_cast<const F4s*>(xdbl + (int64_t)min(b0 + min(bcr, TR - 1), batch - 1) * xdbl_sb + R +
+                                                 bcj);
+
+    // ---- dt_raw tile on the matrix cores
+    F4s acc[MB];
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) acc[mb] = F4s{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < KBW; ++j) {
+        if (wave + 4 * j < nkb) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+#pragma unroll
+                for (int mb = 0; mb < MB; ++mb)
+                    acc[mb] = __builtin_amdgcn_mfma_f32_16x16x4f32(wv[j][q], xo[j][mb][q], acc[mb], 0, 0, 0);
+        }
+    }
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) s_dt[wave][mb][lane] = acc[mb];
+    if (a_is_log) av = -expf(av);
+    s_a[tid >> 4][tid & 15] = av * kLog2e;
+    if (bcr < TR) *reinterpret_cast<F4s*>(&s_bc[bcr][bcj]) = bc;
+    __syncthreads();
+
+    // ---- per pair: dt, the 16 state updates, y
+#pragma unroll
+    for (int u = 0; u < MB; ++u) {
+        const int r = pr + 16 * u;
+        // D[i][j] of block u sits in lane j + 16 (i / 4), register i % 4 (i = channel, j = row)
+        const int dl = (r & 15) + 16 * (pc >> 2), dr = pc & 3;
+        float raw = s_dt[0][u][dl][dr];
+#pragma unroll
+        for (int w = 1; w < kStepThreads / 64; ++w) raw += s_dt[w][u][dl][dr];
+        const float dt = softplus_f(raw + bd);
+        const float dtx = dt * xv[u];
+        float yv = 0.f;
+#pragma unroll
+        for (int n = 0; n < N; ++n) {
+            const float dA = __builtin_amdgcn_exp2f(dt * s_a[pc][n]);
+            hs[u][n] = fmaf(hs[u][n], dA, dtx * s_bc[r][n]);
+            yv = fmaf(hs[u][n], s_bc[r][N + n], yv);
+        }
+        if (b0 + r < batch && c0 + pc < D) {
+            F4s* sp = reinterpret_cast<F4s*>(state + ((int64_t)(b0 + r) * D + c0 + pc) * N);
+#pragma unroll
+            for (int q = 0; q < N / 4; ++q)
+                sp[q] = F4s{hs[u][4 * q], hs[u][4 * q + 1], hs[u][4 * q + 2], hs[u][4 * q + 3]};
+            yv = fmaf(xv[u], Dc, yv);
+            if (z) yv *= silu_f(zv[u]);
+            y[(int64_t)(b0 + r) * y_sb + c0 + pc] = yv;
+        }
+    }
+}
+
 template <typename T>
 void launch_ssm_step(float* state, const void* x, int64_t x_sb, const void* z, int64_t z_sb, const void* xdbl,
                      int64_t xdbl_sb, const float* Wdt, const float* bdt, const float* A, const float* Dv, void* y,
                      int64_t y_sb, int64_t batch, int D, int N, int R, int a_is_log, hipStream_t st) {
+    if constexpr (std::is_same<T, float>::value) {
+        const bool aligned = ((uintptr_t)state | (uintptr_t)xdbl | (uintptr_t)Wdt) % 16 == 0 && xdbl_sb % 4 == 0;
+        if (batch >= kRowsMinBatch && N == 16 && R % 16 == 0 && R <= 256 && aligned) {
+            const int tr = kRowsTile;
+            dim3 grid((unsigned)((D + kRowsCh - 1) / kRowsCh), (unsigned)((batch + tr - 1) / tr));
+            const int kbw = (R / 16 + 3) / 4;
+#define MTL_ROWS(KB) hipLaunchKernelGGL((ssm_step_rows_kernel<KB, kRowsTile / 16>), grid, dim3(kStepThreads), 0, st, state, \
+        static_cast<const float*>(x), x_sb, static_cast<const float*>(z), z_sb, static_cast<const float*>(xdbl),      \
+        xdbl_sb, Wdt, bdt, A, Dv, static_cast<float*>(y), y_sb, D, R, (int)batch, a_is_log)
+            if (kbw <= 1) MTL_ROWS(1);
+            else if (kbw == 2) MTL_ROWS(2);
+            else if (kbw == 3) MTL_ROWS(3);
+            else MTL_ROWS(4);
+#undef MTL_ROWS
+            return;
+        }
+    }
     const int bb = batch >= 8 ? 8 : batch >= 4 ? 4 : batch >= 2 ? 2 : 1;
     const int rq = round_runs((R + 15) / 16);
     dim3 grid((unsigned)((D + kChPerBlock - 1) / kChPerBlock), (unsigned)((batch + bb - 1) / bb));

@@ -128,10 +128,13 @@ def test_conv_step_in_place():
     assert np.array_equal(S.cpu().numpy(), ref_st.astype(np.float32))
 
 
-@pytest.mark.parametrize("N,R", [(16, 48), (16, 128), (8, 2), (4, 5), (16, 256)])
-@pytest.mark.parametrize("b", [1, 4, 11, 32])
+@pytest.mark.parametrize("N,R", [(16, 48), (16, 128), (8, 2), (4, 5), (16, 256), (16, 32)])
+@pytest.mark.parametrize("b", [1, 4, 11, 16, 17, 32, 40])
 def test_selective_state_update(N, R, b):
-    """b = 11 and 32 cover the 8-row batch blocks (with a ragged last block)."""
+    """b = 11 covers the 8-row batch blocks with a ragged last block; from 16
+    rows (16 states, dt_rank a multiple of 16) the 32-row form with the dt
+    dot on the matrix cores runs, b = 17 and 40 with a ragged last 32-row
+    block, D = 200 with a ragged last 16-channel block."""
     print(f"state update N={N} R={R} b={b}", flush=True)
     rng = np.random.default_rng(N * 100 + R + b)
     D = 200
