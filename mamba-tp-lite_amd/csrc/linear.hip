@@ -8,29 +8,38 @@
 // (model.py:326, 353) of MambaMixer.step / MambaLM.step.  At these shapes the
 // product streams the weight once and does 2*M flops per weight element, so
 // it is bound by HBM; a GEMM library tiles it for large M and leaves much of
-// the weight stream idle (fp32 M=32 at the mamba-1.4b width: in_proj 3.8,
-// out_proj 2.0 TB/s).
+// the weight stream idle (fp32 M=32, weights cold in HBM, mamba-1.4b width:
+// in_proj 3.6-3.8, out_proj 2.0 TB/s).
 //
 // Mapping: one workgroup per n-tile of 16*RB weight rows; optionally KS
 // workgroups per n-tile split K and write KS partial outputs that the
-// consumer adds in split order.  K is walked in stages of kKC columns:
-//   * all 256 threads load the stage's W tile [16 RB x kKC] and X tile
-//     [16 MB x kKC] with float4 loads in row order (every 32 lanes read one
-//     512-byte run of a row) into registers, two stages ahead, and write them
-//     to a double-buffered LDS tile (rows padded by 4 floats);
-//   * wavefront w multiplies the stage's k-blocks 2w and 2w+1 (16 columns
-//     each) on the matrix cores: per block a lane l = r + 16 kk (r < 16,
-//     kk < 4) reads W[16 rb + r][k + 4 kk .. + 3] and X[16 mb + r][same k]
-//     from LDS and feeds four v_mfma_f32_16x16x4_f32, the q-th taking
-//     component q of both as its A and B operand, so the 16 columns enter in
-//     the order (kk, q) on both sides and each MFMA adds
+// consumer adds in split order.  Each of the four wavefronts owns a
+// contiguous quarter of the workgroup's K range and walks it in stages of
+// 32 columns:
+//   * a stage is the wavefront's W rows [16 RB x 32] and X rows [16 MB x 32],
+//     copied from global memory straight into a ring of D stage slots of
+//     its own in LDS by global_load_lds_dwordx4 (no register staging, so the
+//     ring depth costs LDS, not VGPRs).  One such instruction moves 8 rows x
+//     128 bytes (8 lanes per row); lane p of a row fetches 16-byte chunk
+//     p ^ (row & 7), so chunk c of a row sits at position c ^ (row & 7);
+//   * it multiplies a stage as two 16-column blocks: lane l = r + 16 kk
+//     (r < 16, kk < 4) reads chunk 4 kb + kk of W row 16 rb + r and of X row
+//     16 mb + r (the swizzle puts 8 consecutive rows of one chunk in
+//     distinct banks) and feeds four v_mfma_f32_16x16x4_f32, the q-th taking
+//     component q of both as its A and B operand, so the 16 columns enter
+//     in the order (kk, q) on both sides and each MFMA adds
 //     sum_kk W[n][k + 4 kk + q] X[m][k + 4 kk + q] into D[n][m];
-//   * one barrier per stage.
+//   * the copies count on the vector-memory counter, and the compiler does
+//     not track their LDS writes: the loop waits with explicit
+//     s_waitcnt vmcnt(n), n = the copies still allowed in flight, before it
+//     reads a stage, and lgkmcnt(0) (its reads of the slot done) before it
+//     refills a slot.  Only the wavefront reads what it copied, so the K
+//     loop has no barrier.
 // The four wavefronts' accumulators are added in wavefront order through LDS
-// at the end, so the result is deterministic.  Reading the weight rows in
-// 512-byte runs instead of the MFMA operand layout's 64-byte pieces per row
-// took the mamba-1.4b in_proj (M=32) from 19.5 to 13.3 us (time measured on
-// the bytes alone).
+// at the end, so the result is deterministic.  Measured on the mamba-1.4b
+// in_proj at M = 32 with the weights cold in HBM: hipBLASLt 17.8-18.7 us;
+// register-staged per-wavefront LDS stages 19.2-21.7 us; this form 15.6-15.8
+// us (out_proj 16.7 / 12.6 / 10.0 us).
 
 #include "common.h"
 
@@ -50,59 +59,49 @@ struct LinArgs {
 
 constexpr int kLinThreads = 256;
 constexpr int kLinWaves = kLinThreads / 64;
-constexpr int kKC = 128;                          // K columns per stage
-constexpr int kKP = kKC + 4;                      // padded LDS row: b128 reads of 16 rows hit distinct banks
-constexpr int kC4 = kKC / 4;                      // float4 per stage row
+constexpr int kKW = 32;                           // K columns per wavefront per stage
+constexpr int kKC = kLinWaves * kKW;              // K granule of a workgroup (128)
 
 __device__ __forceinline__ F4v ld4(const float* p) { return *reinterpret_cast<const F4v*>(p); }
 
-template <int RB, int MB>
+#define MTL_WAIT_VMCNT(n) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(n) : "memory")
+
+template <int RB, int MB, int D>
 __global__ void __launch_bounds__(kLinThreads) linear_skinny_kernel(const LinArgs a) {
-    constexpr int WR = 16 * RB, XR = 16 * MB;          // tile rows
-    constexpr int WL = WR * kC4 / kLinThreads;          // float4 loads per thread per stage
-    constexpr int XL = XR * kC4 / kLinThreads;
-    static_assert(WL >= 1 && XL >= 1, "tile shape");
-    __shared__ __align__(16) float s_w[2][WR][kKP];
-    __shared__ __align__(16) float s_x[2][XR][kKP];
+    constexpr int WR = 16 * RB, XR = 16 * MB, SROWS = WR + XR;   // rows of a stage: W then X
+    constexpr int NI = SROWS / 8;                                 // copies per stage (8 rows each)
+    static_assert(D >= 2 && D <= 3, "ring depth");
+    static_assert((D - 1) * NI <= 63, "vmcnt range");
+    __shared__ __align__(16) float ring[kLinWaves][D][SROWS * kKW];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int r = lane & 15, kk = lane >> 4;
     const int n0 = blockIdx.x * WR;
     const int ks = blockIdx.y;
-    const int kper = a.K / a.KS;                        // a multiple of kKC (host-checked)
-    const int kbeg = ks * kper;
-    const int ns = kper / kKC;
+    const int kper = a.K / a.KS;                       // a multiple of kKC (host-checked)
+    const int ns = kper / kKC;                         // stages per wavefront, >= D - 1 (host-checked)
+    const int kbeg = ks * kper + wave * (kper / kLinWaves);
 
-    // loader slots: float4 e = tid + 256 i of a stage tile is (row e / kC4, column 4 (e % kC4))
-    const float* wsrc[WL];
-    int wdst[WL];
+    // copy lane: row 8 i + lane / 8 of the stage, fetching chunk (lane % 8) ^ (row & 7)
+    const int crow = lane >> 3, cch = (lane & 7) ^ crow;
+    const float* src[NI];
 #pragma unroll
-    for (int i = 0; i < WL; ++i) {
-        const int e = tid + kLinThreads * i, row = e / kC4, c = 4 * (e % kC4);
-        wsrc[i] = a.W + (int64_t)min(n0 + row, a.N - 1) * a.K + kbeg + c;
-        wdst[i] = row * kKP + c;
+    for (int i = 0; i < NI; ++i) {
+        const int row = 8 * i + crow;
+        src[i] = row < WR ? a.W + (int64_t)min(n0 + row, a.N - 1) * a.K + kbeg + 4 * cch
+                          : a.x + (int64_t)min(row - WR, a.M - 1) * a.x_rs + kbeg + 4 * cch;
     }
-    const float* xsrc[XL];
-    int xdst[XL];
+    auto issue = [&](int s) __attribute__((always_inline)) {
+        float* dst = &ring[wave][s % D][0];
+        // the builtin exists for the device pass only; the host pass still
+        // has to see the kernel to emit its launch stub
+#if defined(__HIP_DEVICE_COMPILE__)
 #pragma unroll
-    for (int i = 0; i < XL; ++i) {
-        const int e = tid + kLinThreads * i, row = e / kC4, c = 4 * (e % kC4);
-        xsrc[i] = a.x + (int64_t)min(row, a.M - 1) * a.x_rs + kbeg + c;
-        xdst[i] = row * kKP + c;
-    }
-    struct Set { F4v w[WL], x[XL]; };
-    auto load = [&](Set& st, int s) __attribute__((always_inline)) {
-        const int off = min(s, ns - 1) * kKC;           // past the end: the last stage again, never used
-#pragma unroll
-        for (int i = 0; i < WL; ++i) st.w[i] = ld4(wsrc[i] + off);
-#pragma unroll
-        for (int i = 0; i < XL; ++i) st.x[i] = ld4(xsrc[i] + off);
-    };
-    auto store = [&](const Set& st, int buf) __attribute__((always_inline)) {
-#pragma unroll
-        for (int i = 0; i < WL; ++i) *reinterpret_cast<F4v*>(&s_w[buf][0][0] + wdst[i]) = st.w[i];
-#pragma unroll
-        for (int i = 0; i < XL; ++i) *reinterpret_cast<F4v*>(&s_x[buf][0][0] + xdst[i]) = st.x[i];
+        for (int i = 0; i < NI; ++i)
+            __builtin_amdgcn_global_load_lds(src[i] + s * kKW, dst + i * 256, 16, 0, 0);
+#else
+        (void)dst;
+#endif
     };
 
     F4v acc[RB][MB];
@@ -110,15 +109,22 @@ __global__ void __launch_bounds__(kLinThreads) linear_skinny_kernel(const LinArg
     for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
         for (int mb = 0; mb < MB; ++mb) acc[rb][mb] = F4v{0.f, 0.f, 0.f, 0.f};
-    auto mma = [&](int buf) __attribute__((always_inline)) {
+    auto mma = [&](int s) __attribute__((always_inline)) {
+        const float* st = &ring[wave][s % D][0];
 #pragma unroll
-        for (int kb = 0; kb < 2; ++kb) {
-            const int k = 32 * wave + 16 * kb + 4 * kk;
+        for (int kb = 0; kb < kKW / 16; ++kb) {
+            const int c = 4 * kb + kk;
             F4v wv[RB], xv[MB];
 #pragma unroll
-            for (int rb = 0; rb < RB; ++rb) wv[rb] = ld4(&s_w[buf][16 * rb + r][k]);
+            for (int rb = 0; rb < RB; ++rb) {
+                const int row = 16 * rb + r;
+                wv[rb] = ld4(st + (row * 8 + (c ^ (row & 7))) * 4);
+            }
 #pragma unroll
-            for (int mb = 0; mb < MB; ++mb) xv[mb] = ld4(&s_x[buf][16 * mb + r][k]);
+            for (int mb = 0; mb < MB; ++mb) {
+                const int row = WR + 16 * mb + r;
+                xv[mb] = ld4(st + (row * 8 + (c ^ (row & 7))) * 4);
+            }
 #pragma unroll
             for (int q = 0; q < 4; ++q)
 #pragma unroll
@@ -129,35 +135,30 @@ __global__ void __launch_bounds__(kLinThreads) linear_skinny_kernel(const LinArg
         }
     };
 
-    // stage s is in LDS buffer s % 2; register sets A and B hold the stages
-    // one and two ahead of the one being multiplied
-    Set A, B;
-    load(A, 0);
-    load(B, 1);
-    store(A, 0);
-    load(A, 2);
-    __syncthreads();
-    // one stage: multiply s from LDS, move stage s + 1 from its registers
-    // into the other buffer, refill those registers with stage s + 3
-    auto stage = [&](int s, Set& nxt) __attribute__((always_inline)) {
-        mma(s & 1);
-        store(nxt, (s + 1) & 1);
-        load(nxt, s + 3);
-        __syncthreads();
-    };
+    // D - 1 stages in flight ahead of the one being multiplied
+#pragma unroll
+    for (int s = 0; s < D - 1; ++s) issue(s);
     int s = 0;
-    for (; s + 2 <= ns; s += 2) {
-        stage(s, B);       // B holds s + 1, then s + 3
-        stage(s + 1, A);   // A holds s + 2, then s + 4
+    for (; s < ns - (D - 1); ++s) {
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");   // reads of slot (s - 1) % D are done
+        issue(s + D - 1);
+        MTL_WAIT_VMCNT((D - 1) * NI);                          // stage s has landed
+        mma(s);
     }
-    if (s < ns) mma(s & 1);
+    // the last D - 1 stages are already in flight
+    MTL_WAIT_VMCNT((D - 2) * NI);
+    mma(s);
+    if constexpr (D == 3) {
+        MTL_WAIT_VMCNT(0);
+        mma(s + 1);
+    }
 
     // D[i][j] of an MFMA tile sits in lane j + 16 (i / 4), register i % 4:
     // n = n0 + 16 rb + 4 (lane / 16) + reg, m = 16 mb + lane % 16.  The
-    // reduction reuses the W buffers (every wavefront is past its last read).
+    // reduction reuses the ring once every wavefront is past its reads.
     __syncthreads();
-    F4v* s_acc = reinterpret_cast<F4v*>(&s_w[0][0][0]);
-    static_assert(sizeof(s_w) >= sizeof(F4v) * kLinWaves * RB * MB * 64, "reduction space");
+    F4v* s_acc = reinterpret_cast<F4v*>(&ring[0][0][0]);
+    static_assert(sizeof(ring) >= sizeof(F4v) * kLinWaves * RB * MB * 64, "reduction space");
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
@@ -181,7 +182,10 @@ __global__ void __launch_bounds__(kLinThreads) linear_skinny_kernel(const LinArg
 template <int RB, int MB>
 void launch_linear(const LinArgs& a, hipStream_t st) {
     dim3 grid((unsigned)((a.N + 16 * RB - 1) / (16 * RB)), (unsigned)a.KS);
-    hipLaunchKernelGGL((linear_skinny_kernel<RB, MB>), grid, dim3(kLinThreads), 0, st, a);
+    if (a.K / a.KS >= 2 * kKC)
+        hipLaunchKernelGGL((linear_skinny_kernel<RB, MB, 3>), grid, dim3(kLinThreads), 0, st, a);
+    else
+        hipLaunchKernelGGL((linear_skinny_kernel<RB, MB, 2>), grid, dim3(kLinThreads), 0, st, a);
 }
 
 }  // namespace

@@ -137,15 +137,14 @@ SPLIT_PROJ_MIN_TOKENS = 16384
 # host cost per launch, so it keeps hipBLASLt (a 64-token 130m prefill replays
 # in 1.42 ms that way against 1.64 ms on rocBLAS).
 SMALL_PREFILL_TOKENS = 256
+SMALL_PREFILL_BLAS: str | None = "cublas"
 
-# Batched step projections on mtl_linear_skinny (fp32, <= 32 tokens): in_proj
-# up to this many weight elements, out_proj as this many split-K parts.
-SKINNY_IN_PROJ_MAX = 4 * 1024 * 1024
+# Batched step projections run on mtl_linear_skinny (fp32, <= 32 tokens);
+# out_proj as this many split-K parts.
+SKINNY_OUT_SPLIT = 4
 
 # column parts of the fused step's stand-alone x_proj GEMV
 _XPROJ_PARTS = 4
-SKINNY_OUT_SPLIT = 4
-SMALL_PREFILL_BLAS: str | None = "cublas"
 
 
 @contextlib.contextmanager
@@ -311,25 +310,26 @@ class MambaMixer(nn.Module):
         return self.out_proj(self._step_y(x_t, cache))
 
     def _in_proj_step(self, x_t: torch.Tensor) -> torch.Tensor:
-        """in_proj of a batched step: the matrix-core skinny GEMM where it
-        outruns the library at this shape (measured: the mamba-130m width at
-        32 tokens, 6.0 -> 5.3 us; at the 1.4b width the library's 15.3 us
-        beats its 17.7), else nn.Linear."""
+        """in_proj of a batched step: the matrix-core skinny GEMM where its
+        operand rules hold, else nn.Linear.  Measured at 32 tokens with the
+        weight cold in HBM, against the library's GEMM: the mamba-130m width
+        9.8 -> 6.0 us, 1.4b 17.8-18.7 -> 15.6-15.8 us."""
         w = self.in_proj.weight
-        if w.numel() <= SKINNY_IN_PROJ_MAX and ops.linear_skinny_ok(x_t, w):
+        if ops.linear_skinny_ok(x_t, w):
             return ops.linear_skinny(x_t, w, self.in_proj.bias)
         return self.in_proj(x_t)
 
     def _out_proj_parts(self, y: torch.Tensor):
         """out_proj of a batched step as split-K partial products [P, b,
         d_model] (summed in order by the residual add that follows), or None
-        where the skinny GEMM does not apply.  Measured at 32 tokens: the
-        mamba-1.4b out_proj 13.5 -> 10.2 us, 130m 7.0 -> 4.0 us."""
+        where the skinny GEMM does not apply.  Measured at 32 tokens with the
+        weight cold in HBM, against the library's GEMM: the mamba-1.4b
+        out_proj 16.7 -> 10.0 us, 130m 7.9 -> 3.7 us."""
         w = self.out_proj.weight
         K = w.shape[1]
         if K % (128 * SKINNY_OUT_SPLIT) or not ops.linear_skinny_ok(y, w):
             return None
-        return ops.linear_skinny(y, w, self.out_proj.bias, ksplit=SKINNY_OUT_SPLIT, rows_per_block=16)
+        return ops.linear_skinny(y, w, self.out_proj.bias, ksplit=SKINNY_OUT_SPLIT)
 
     def _step_y(self, x_t: torch.Tensor, cache: LayerCache) -> torch.Tensor:
         """The step up to the gated SSM output y [b, d_inner] (before out_proj)."""

@@ -531,8 +531,9 @@ def linear_skinny(x, W, bias=None, out=None, ksplit=1, rows_per_block=None):
     elif tuple(out.shape) != shape or out.dtype != torch.float32 or not out.is_contiguous():
         raise ValueError(f"linear_skinny: out must be contiguous float32 {shape}")
     if rows_per_block is None:
-        # enough workgroups to keep every CU streaming the weight
-        rows_per_block = 32 if (N + 31) // 32 * ksplit >= 256 else 16
+        # 32-row tiles halve the re-reads of x where they still give every CU
+        # a workgroup; at 16 rows or fewer of x the 16-row tiles stream faster
+        rows_per_block = 32 if M > 16 and (N + 31) // 32 * ksplit >= 256 else 16
     _same_device(x, W, bias, out)
     with _dev_guard(x):
         _lib.check(_lib.load().mtl_linear_skinny(_ptr(x), x.stride(0), _ptr(W), _ptr(bias), _ptr(out), N, M * N,
