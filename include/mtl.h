@@ -272,6 +272,33 @@ int mtl_linear_skinny(const float* x, int64_t x_rs, const float* W, const float*
                       mtl_stream_t stream);
 
 /* ------------------------------------------------------------------------
+ * A batched step's in_proj, conv step and x_proj partials in one launch:
+ * model.py:261 (xz = in_proj(x)), 264-277 (conv step + SiLU of the x half,
+ * the history shifted in place) and 279 (x_dbl = x_proj(xc)) for b <= 32
+ * tokens, fp32.  The in_proj product runs on the matrix cores like
+ * mtl_linear_skinny (same operand rules, K = d_model); a workgroup that owns
+ * channels [c0, c0 + channels_per_part) of the x half then does their conv
+ * step and writes
+ *   xpart[c0 / channels_per_part][m][j] = sum over its channels c, in order,
+ *                                          of xc[m][c] W_xT[c][j],
+ * which the caller adds in block order (mtl_sum_parts) to get x_dbl.
+ *   x: [b, d_model] (row stride x_rs); W_in: [2 d_inner, d_model]
+ *   contiguous; b_in: [2 d_inner] or NULL; conv_state: [b, d_inner,
+ *   d_conv - 1] contiguous, in place; conv_w: [d_inner, d_conv]; conv_b:
+ *   [d_inner] or NULL; W_xT: [d_inner, J] (x_proj weight transposed);
+ *   xc: [b, d_inner] contiguous; z: [b, d_inner], row stride z_rs; xpart:
+ *   [d_inner / channels_per_part, b, J].
+ * 1 <= b <= 32; d_model a multiple of 128, at least 256; channels_per_part
+ * 16 or 32, dividing d_inner; d_conv 2, 3 or 4; J <= 288.  x, W_in, b_in,
+ * conv_state, conv_w, conv_b, xc and z 16-byte aligned.  Deterministic.
+ * Replaces mtl_linear_skinny (in_proj) + mtl_conv_step_xproj in the step.
+ * ---------------------------------------------------------------------- */
+int mtl_in_proj_conv_xproj(const float* x, int64_t x_rs, const float* W_in, const float* b_in, float* conv_state,
+                           const float* conv_w, const float* conv_b, int32_t d_conv, const float* W_xT, int32_t J,
+                           float* xc, float* z, int64_t z_rs, float* xpart, int64_t batch, int64_t d_model,
+                           int64_t d_inner, int32_t channels_per_part, mtl_stream_t stream);
+
+/* ------------------------------------------------------------------------
  * Fused single-token decode step, fp32, batch 1, 2 or 4.
  * Together these replace one MambaBlock.step (model.py:308-311) around
  * MambaMixer.step (model.py:249-294): 3 launches per layer (4 when x_proj

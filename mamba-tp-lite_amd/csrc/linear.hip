@@ -66,21 +66,25 @@ __device__ __forceinline__ F4v ld4(const float* p) { return *reinterpret_cast<co
 
 #define MTL_WAIT_VMCNT(n) asm volatile("s_waitcnt vmcnt(%0)" ::"n"(n) : "memory")
 
+// The tile product of one workgroup: W rows [n0, n0 + 16 RB) against the M
+// rows of x over the K range of split ks.  On return every wavefront's
+// accumulators sit in s_acc = the ring's first RB MB 4 KB (after a barrier),
+// and tile_sum() adds them in wavefront order.  A kernel that calls it keeps
+// all of its LDS in the ring array (see in_conv_xproj_kernel).
 template <int RB, int MB, int D>
-__global__ void __launch_bounds__(kLinThreads) linear_skinny_kernel(const LinArgs a) {
+__device__ __forceinline__ void skinny_tile(const LinArgs& a, float* ring, int n0, int ks) {
     constexpr int WR = 16 * RB, XR = 16 * MB, SROWS = WR + XR;   // rows of a stage: W then X
     constexpr int NI = SROWS / 8;                                 // copies per stage (8 rows each)
+    constexpr int SLOT = SROWS * kKW;                             // floats per ring slot
     static_assert(D >= 2 && D <= 3, "ring depth");
     static_assert((D - 1) * NI <= 63, "vmcnt range");
-    __shared__ __align__(16) float ring[kLinWaves][D][SROWS * kKW];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int r = lane & 15, kk = lane >> 4;
-    const int n0 = blockIdx.x * WR;
-    const int ks = blockIdx.y;
     const int kper = a.K / a.KS;                       // a multiple of kKC (host-checked)
     const int ns = kper / kKC;                         // stages per wavefront, >= D - 1 (host-checked)
     const int kbeg = ks * kper + wave * (kper / kLinWaves);
+    float* myring = ring + wave * D * SLOT;
 
     // copy lane: row 8 i + lane / 8 of the stage, fetching chunk (lane % 8) ^ (row & 7)
     const int crow = lane >> 3, cch = (lane & 7) ^ crow;
@@ -92,7 +96,7 @@ __global__ void __launch_bounds__(kLinThreads) linear_skinny_kernel(const LinArg
                           : a.x + (int64_t)min(row - WR, a.M - 1) * a.x_rs + kbeg + 4 * cch;
     }
     auto issue = [&](int s) __attribute__((always_inline)) {
-        float* dst = &ring[wave][s % D][0];
+        float* dst = myring + (s % D) * SLOT;
         // the builtin exists for the device pass only; the host pass still
         // has to see the kernel to emit its launch stub
 #if defined(__HIP_DEVICE_COMPILE__)
@@ -110,7 +114,7 @@ __global__ void __launch_bounds__(kLinThreads) linear_skinny_kernel(const LinArg
 #pragma unroll
         for (int mb = 0; mb < MB; ++mb) acc[rb][mb] = F4v{0.f, 0.f, 0.f, 0.f};
     auto mma = [&](int s) __attribute__((always_inline)) {
-        const float* st = &ring[wave][s % D][0];
+        const float* st = myring + (s % D) * SLOT;
 #pragma unroll
         for (int kb = 0; kb < kKW / 16; ++kb) {
             const int c = 4 * kb + kk;
@@ -153,25 +157,45 @@ __global__ void __launch_bounds__(kLinThreads) linear_skinny_kernel(const LinArg
         mma(s + 1);
     }
 
-    // D[i][j] of an MFMA tile sits in lane j + 16 (i / 4), register i % 4:
-    // n = n0 + 16 rb + 4 (lane / 16) + reg, m = 16 mb + lane % 16.  The
-    // reduction reuses the ring once every wavefront is past its reads.
+    // the reduction space reuses the ring once every wavefront is past its reads
     __syncthreads();
-    F4v* s_acc = reinterpret_cast<F4v*>(&ring[0][0][0]);
-    static_assert(sizeof(ring) >= sizeof(F4v) * kLinWaves * RB * MB * 64, "reduction space");
+    F4v* s_acc = reinterpret_cast<F4v*>(ring);
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
         for (int mb = 0; mb < MB; ++mb) s_acc[(wave * RB * MB + rb * MB + mb) * 64 + lane] = acc[rb][mb];
     __syncthreads();
-    for (int t = tid; t < RB * MB * 64; t += kLinThreads) {
-        const int tile = t >> 6, ln = t & 63;
-        const int rb = tile / MB, mb = tile - rb * MB;
-        F4v sum = s_acc[tile * 64 + ln];
+}
+
+// Pair t < 64 RB MB of the tile: D[i][j] of an MFMA tile sits in lane
+// j + 16 (i / 4), register i % 4, so pair (tile, ln) holds outputs
+// n = n0 + 16 rb + 4 (ln / 16) + 0..3 of row m = 16 mb + ln % 16.
+template <int RB, int MB>
+__device__ __forceinline__ F4v tile_sum(const float* ring, int t, int& m, int& nl) {
+    const F4v* s_acc = reinterpret_cast<const F4v*>(ring);
+    const int tile = t >> 6, ln = t & 63;
+    const int rb = tile / MB, mb = tile - rb * MB;
+    F4v sum = s_acc[tile * 64 + ln];
 #pragma unroll
-        for (int w = 1; w < kLinWaves; ++w) sum += s_acc[(w * RB * MB + tile) * 64 + ln];
-        const int m = 16 * mb + (ln & 15);
-        const int n = n0 + 16 * rb + 4 * (ln >> 4);
+    for (int w = 1; w < kLinWaves; ++w) sum += s_acc[(w * RB * MB + tile) * 64 + ln];
+    m = 16 * mb + (ln & 15);
+    nl = 16 * rb + 4 * (ln >> 4);
+    return sum;
+}
+
+template <int RB, int MB, int D>
+constexpr int ring_floats() { return kLinWaves * D * (16 * RB + 16 * MB) * kKW; }
+
+template <int RB, int MB, int D>
+__global__ void __launch_bounds__(kLinThreads) linear_skinny_kernel(const LinArgs a) {
+    __shared__ __align__(16) float ring[ring_floats<RB, MB, D>()];
+    static_assert(sizeof(ring) >= sizeof(F4v) * kLinWaves * RB * MB * 64, "reduction space");
+    const int n0 = blockIdx.x * 16 * RB, ks = blockIdx.y;
+    skinny_tile<RB, MB, D>(a, ring, n0, ks);
+    for (int t = threadIdx.x; t < RB * MB * 64; t += kLinThreads) {
+        int m, nl;
+        F4v sum = tile_sum<RB, MB>(ring, t, m, nl);
+        const int n = n0 + nl;
         if (m < a.M && n < a.N) {
             if (a.bias && ks == 0) sum += ld4(a.bias + n);
             *reinterpret_cast<F4v*>(a.y + ks * a.y_ks + (int64_t)m * a.y_rs + n) = sum;
@@ -186,6 +210,191 @@ void launch_linear(const LinArgs& a, hipStream_t st) {
         hipLaunchKernelGGL((linear_skinny_kernel<RB, MB, 3>), grid, dim3(kLinThreads), 0, st, a);
     else
         hipLaunchKernelGGL((linear_skinny_kernel<RB, MB, 2>), grid, dim3(kLinThreads), 0, st, a);
+}
+
+// ------------------------------------------------------- in_proj + conv step + x_proj partials
+// The batched step's in_proj (model.py:261), conv step + SiLU (264-277) and
+// x_proj (279) as one launch.  in_proj's output rows [0, D) are the x half
+// and [D, 2D) the z half; a workgroup's tile of 16 RB rows lies in one half
+// (D % (16 RB) == 0).  A z tile stores z.  An x tile keeps its outputs
+// x[m][c] (c = its 16 RB channels, m = the b rows) and, as the epilogue:
+//   * the conv step of each (row, channel): window = the K - 1 history
+//     values of conv_state then x, xc = SiLU(window . conv_w[c] + conv_b[c]),
+//     history shifted by one in place; xc to global memory;
+//   * the x_proj partial of its channels: xpart[tile][m][j] = sum over its
+//     channels c, in order, of xc[m][c] W_xT[c][j].  The caller adds the
+//     D / (16 RB) partials in tile order.
+// The conv operands and the tile's W_xT rows are loaded before the GEMM
+// (they do not depend on it), so the epilogue waits on no memory.
+struct InConvArgs {
+    float* state;            // [b, D, K - 1], in place
+    const float* conv_w;     // [D, K]
+    const float* conv_b;     // [D] or null
+    const float* WxT;        // [D, J]
+    float* xc;               // [b, D]
+    float* z;                // [b, D] rows at stride z_rs
+    float* xpart;            // [D / (16 RB), b, J]
+    int64_t z_rs;
+    int D, J;
+};
+
+constexpr int kIcMaxJQ = 9;                       // J <= 32 * 9 = 288
+
+template <int RB, int MB, int D, int K, int JQ>
+__global__ void __launch_bounds__(kLinThreads) in_conv_xproj_kernel(const LinArgs a, const InConvArgs c) {
+    constexpr int CB = 16 * RB, XR = 16 * MB;         // channels of a tile, rows of x
+    constexpr int WLD = JQ * 32 * CB / kLinThreads;   // W_xT loads per thread
+    // the epilogue's buffers live in the ring too, past the reduction space:
+    // with a second LDS array in the kernel the compiler can no longer tell
+    // the ring reads from the copies' LDS writes and drains vmcnt to zero
+    // before every stage (measured at the mamba-1.4b width: 28.9 us against
+    // 17 us for the plain product)
+    __shared__ __align__(16) float ring[ring_floats<RB, MB, D>()];
+    constexpr int kAcc = kLinWaves * RB * MB * 64 * 4;          // floats of the reduction space
+    static_assert(kAcc + CB * JQ * 32 + XR * (CB + 1) <= ring_floats<RB, MB, D>(), "epilogue space");
+    float (*s_wx)[JQ * 32] = reinterpret_cast<float (*)[JQ * 32]>(ring + kAcc);
+    float (*s_xc)[CB + 1] = reinterpret_cast<float (*)[CB + 1]>(ring + kAcc + CB * JQ * 32);
+    static_assert(WLD * kLinThreads == JQ * 32 * CB, "W_xT tile split");
+
+    const int tid = threadIdx.x;
+    const int n0 = blockIdx.x * CB;
+    const bool xtile = n0 < c.D;                       // uniform
+    const int t = tid;                                 // this thread's output pair, if t < 64 RB MB
+    const bool has_pair = t < RB * MB * 64;
+    // the pair's row and first channel (same formula as tile_sum)
+    const int p_tile = t >> 6, p_ln = t & 63, p_rb = p_tile / MB, p_mb = p_tile - p_rb * MB;
+    const int pm = 16 * p_mb + (p_ln & 15), pc = 16 * p_rb + 4 * (p_ln >> 4);
+
+    F4v hist[K - 1], cw[K], cb = {0.f, 0.f, 0.f, 0.f};
+    float wl[WLD];
+    // only a thread that owns a pair reads conv operands: for t >= 64 RB MB
+    // the formula above gives channels past the tile (and, on the last x
+    // tile, past d_inner)
+    if (xtile && has_pair) {
+        const int mm = min(pm, a.M - 1), ch = n0 + pc;
+        const F4v* sp = reinterpret_cast<const F4v*>(c.state + ((int64_t)mm * c.D + ch) * (K - 1));
+#pragma unroll
+        for (int k = 0; k < K - 1; ++k) hist[k] = sp[k];
+        const F4v* wp = reinterpret_cast<const F4v*>(c.conv_w + (int64_t)ch * K);
+#pragma unroll
+        for (int k = 0; k < K; ++k) cw[k] = wp[k];
+        if (c.conv_b) cb = ld4(c.conv_b + ch);
+    }
+    if (xtile) {
+        // W_xT tile: element e = tid + 256 i of [CB][JQ * 32] (rows n0 + e / (32 JQ) < n0 + CB <= D),
+        // columns past J clamped (never used)
+#pragma unroll
+        for (int i = 0; i < WLD; ++i) {
+            const int e = tid + kLinThreads * i, cc = e / (JQ * 32), j = e - cc * (JQ * 32);
+            wl[i] = c.WxT[(int64_t)(n0 + cc) * c.J + min(j, c.J - 1)];
+        }
+    }
+
+    skinny_tile<RB, MB, D>(a, ring, n0, 0);
+
+    if (!xtile) {
+        if (has_pair) {
+            int m, nl;
+            F4v v = tile_sum<RB, MB>(ring, t, m, nl);
+            if (m < a.M) {
+                if (a.bias) v += ld4(a.bias + n0 + nl);
+                *reinterpret_cast<F4v*>(c.z + m * c.z_rs + (n0 + nl - c.D)) = v;
+            }
+        }
+        return;
+    }
+
+#pragma unroll
+    for (int i = 0; i < WLD; ++i) {
+        const int e = tid + kLinThreads * i, cc = e / (JQ * 32), j = e - cc * (JQ * 32);
+        s_wx[cc][j] = wl[i];
+    }
+    if (has_pair) {
+        int m, nl;
+        F4v v = tile_sum<RB, MB>(ring, t, m, nl);     // m == pm, nl == pc
+        if (a.bias) v += ld4(a.bias + n0 + nl);
+        // channel q of the four: history tap k is float q (K - 1) + k of the
+        // pair's history block, conv weight k float q K + k of its weight block
+        F4v xcv, nh[K - 1];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            float win[K];
+#pragma unroll
+            for (int k = 0; k < K - 1; ++k) win[k] = hist[(q * (K - 1) + k) / 4][(q * (K - 1) + k) % 4];
+            win[K - 1] = v[q];
+            float acc = 0.f;
+#pragma unroll
+            for (int k = 0; k < K; ++k) acc = fmaf(win[k], cw[(q * K + k) / 4][(q * K + k) % 4], acc);
+            acc += cb[q];
+            xcv[q] = silu_f(acc);
+#pragma unroll
+            for (int k = 0; k < K - 1; ++k) nh[(q * (K - 1) + k) / 4][(q * (K - 1) + k) % 4] = win[k + 1];
+        }
+        if (m < a.M) {
+            const int ch = n0 + nl;
+            F4v* sp = reinterpret_cast<F4v*>(c.state + ((int64_t)m * c.D + ch) * (K - 1));
+#pragma unroll
+            for (int k = 0; k < K - 1; ++k) sp[k] = nh[k];
+            *reinterpret_cast<F4v*>(c.xc + (int64_t)m * c.D + ch) = xcv;
+        }
+#pragma unroll
+        for (int q = 0; q < 4; ++q) s_xc[m][nl + q] = m < a.M ? xcv[q] : 0.f;
+    }
+    __syncthreads();
+
+    // x_proj partial: thread = (row group rg of TB rows, column lane jg),
+    // columns jg + 32 q; channels added in order
+    constexpr int TB = XR / 8;
+    const int rg = tid >> 5, jg = tid & 31;
+    float acc[TB][JQ];
+#pragma unroll
+    for (int i = 0; i < TB; ++i)
+#pragma unroll
+        for (int q = 0; q < JQ; ++q) acc[i][q] = 0.f;
+#pragma unroll 4
+    for (int cc = 0; cc < CB; ++cc) {
+        float xv[TB], wv[JQ];
+#pragma unroll
+        for (int i = 0; i < TB; ++i) xv[i] = s_xc[rg * TB + i][cc];
+#pragma unroll
+        for (int q = 0; q < JQ; ++q) wv[q] = s_wx[cc][jg + 32 * q];
+#pragma unroll
+        for (int q = 0; q < JQ; ++q)
+#pragma unroll
+            for (int i = 0; i < TB; ++i) acc[i][q] = fmaf(xv[i], wv[q], acc[i][q]);
+    }
+#pragma unroll
+    for (int i = 0; i < TB; ++i) {
+        const int m = rg * TB + i;
+        if (m >= a.M) continue;
+#pragma unroll
+        for (int q = 0; q < JQ; ++q) {
+            const int j = jg + 32 * q;
+            if (j < c.J) c.xpart[((int64_t)blockIdx.x * a.M + m) * c.J + j] = acc[i][q];
+        }
+    }
+}
+
+template <int RB, int MB, int K, int JQ>
+void launch_in_conv(const LinArgs& a, const InConvArgs& c, hipStream_t st) {
+    hipLaunchKernelGGL((in_conv_xproj_kernel<RB, MB, 3, K, JQ>), dim3((unsigned)(a.N / (16 * RB))), dim3(kLinThreads),
+                       0, st, a, c);
+}
+
+// JQ in {1, 3, 5, 9}: the smallest that covers J (columns past J are never stored)
+template <int RB, int MB, int K>
+void dispatch_in_conv_jq(int J, const LinArgs& a, const InConvArgs& c, hipStream_t st) {
+    if (J <= 32) launch_in_conv<RB, MB, K, 1>(a, c, st);
+    else if (J <= 96) launch_in_conv<RB, MB, K, 3>(a, c, st);
+    else if (J <= 160) launch_in_conv<RB, MB, K, 5>(a, c, st);
+    else launch_in_conv<RB, MB, K, 9>(a, c, st);
+}
+
+template <int RB, int MB>
+void dispatch_in_conv(int K, const LinArgs& a, const InConvArgs& c, hipStream_t st) {
+    if (K == 2) dispatch_in_conv_jq<RB, MB, 2>(c.J, a, c, st);
+    else if (K == 3) dispatch_in_conv_jq<RB, MB, 3>(c.J, a, c, st);
+    else dispatch_in_conv_jq<RB, MB, 4>(c.J, a, c, st);
 }
 
 }  // namespace
@@ -218,4 +427,38 @@ extern "C" int mtl_linear_skinny(const float* x, int64_t x_rs, const float* W, c
         if (two_m) launch_linear<1, 2>(a, st); else launch_linear<1, 1>(a, st);
     }
     return check_launch("linear_skinny_kernel");
+}
+
+extern "C" int mtl_in_proj_conv_xproj(const float* x, int64_t x_rs, const float* W_in, const float* b_in,
+                                      float* conv_state, const float* conv_w, const float* conv_b, int32_t d_conv,
+                                      const float* W_xT, int32_t J, float* xc, float* z, int64_t z_rs, float* xpart,
+                                      int64_t batch, int64_t d_model, int64_t d_inner, int32_t channels_per_part,
+                                      mtl_stream_t stream) {
+    clear_error();
+    MTL_REQUIRE(x && W_in && conv_state && conv_w && W_xT && xc && z && xpart, "null required pointer");
+    MTL_REQUIRE(batch >= 1 && batch <= 32, "batch must be in [1, 32]");
+    MTL_REQUIRE(d_model >= 2 * kKC && d_model % kKC == 0 && d_model < (int64_t(1) << 30),
+                "d_model must be a multiple of 128, at least 256");
+    MTL_REQUIRE(channels_per_part == 16 || channels_per_part == 32, "channels_per_part must be 16 or 32");
+    MTL_REQUIRE(d_inner >= channels_per_part && d_inner % channels_per_part == 0 && d_inner < (int64_t(1) << 29),
+                "d_inner must be a positive multiple of channels_per_part");
+    MTL_REQUIRE(d_conv >= 2 && d_conv <= 4, "d_conv must be 2, 3 or 4");
+    MTL_REQUIRE(J >= 1 && J <= 32 * kIcMaxJQ, "J (x_proj rows) must be in [1, 288]");
+    MTL_REQUIRE(x_rs >= d_model && x_rs % 4 == 0 && z_rs >= d_inner && z_rs % 4 == 0,
+                "row strides must cover a row and be multiples of 4");
+    MTL_REQUIRE((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(W_in) | reinterpret_cast<uintptr_t>(b_in) |
+                 reinterpret_cast<uintptr_t>(conv_state) | reinterpret_cast<uintptr_t>(conv_w) |
+                 reinterpret_cast<uintptr_t>(conv_b) | reinterpret_cast<uintptr_t>(xc) |
+                 reinterpret_cast<uintptr_t>(z)) % 16 == 0,
+                "x, W_in, b_in, conv_state, conv_w, conv_b, xc and z must be 16-byte aligned");
+    LinArgs a{x, W_in, b_in, nullptr, x_rs, 0, 0, (int)batch, (int)(2 * d_inner), (int)d_model, 1};
+    InConvArgs c{conv_state, conv_w, conv_b, W_xT, xc, z, xpart, z_rs, (int)d_inner, (int)J};
+    hipStream_t st = as_stream(stream);
+    const bool two_m = batch > 16;
+    if (channels_per_part == 32) {
+        if (two_m) dispatch_in_conv<2, 2>(d_conv, a, c, st); else dispatch_in_conv<2, 1>(d_conv, a, c, st);
+    } else {
+        if (two_m) dispatch_in_conv<1, 2>(d_conv, a, c, st); else dispatch_in_conv<1, 1>(d_conv, a, c, st);
+    }
+    return check_launch("in_conv_xproj_kernel");
 }

@@ -334,10 +334,19 @@ class MambaMixer(nn.Module):
     def _step_y(self, x_t: torch.Tensor, cache: LayerCache) -> torch.Tensor:
         """The step up to the gated SSM output y [b, d_inner] (before out_proj)."""
         Dm, R = self.cfg.d_inner, self.cfg.dt_rank
-        xz = self._in_proj_step(x_t)                             # [b, 2D]
         b = x_t.shape[0]
         J = R + 2 * self.cfg.d_state
         conv_w, conv_b = self._step_conv()
+        w_in = self.in_proj.weight
+        if ops.in_proj_conv_xproj_ok(x_t, w_in, cache.conv_state, conv_w.shape[-1], J):
+            # in_proj, the conv step and the x_proj partials of each channel
+            # block in one launch (measured at the mamba-1.4b width, 32 tokens:
+            # see in_proj_conv_xproj)
+            xc, z, xpart = ops.in_proj_conv_xproj(x_t, w_in, self.in_proj.bias, cache.conv_state, conv_w, conv_b,
+                                                  self._xproj_t())
+            return ops.selective_state_update(cache.ssm_state, xc, z, ops.sum_parts(xpart), _f32(self.dt_proj.weight),
+                                              _f32(self.dt_proj.bias), _f32(self.A_log), _f32(self.D), a_is_log=True)
+        xz = self._in_proj_step(x_t)                             # [b, 2D]
         if xz.dtype == torch.float32 and b <= 32 and J <= 288 and cache.conv_state.dtype == torch.float32:
             # conv step and the x_proj partials of 32-channel blocks in one kernel
             xc, xpart = ops.conv_step_xproj(cache.conv_state, xz[:, :Dm], conv_w, conv_b, self._xproj_t())

@@ -287,6 +287,55 @@ def conv_step_xproj(conv_state, x, weight, bias, W_xT, out=None, xpart=None):
     return out, xpart
 
 
+def in_proj_conv_xproj_ok(x, W_in, conv_state, d_conv, J) -> bool:
+    """Whether mtl_in_proj_conv_xproj takes this batched step: fp32 on the
+    GPU, 1..32 rows, d_model a multiple of 128 (at least 256), d_conv 2..4,
+    J <= 288, d_inner a multiple of 16."""
+    if x.dim() != 2 or W_in.dim() != 2 or x.dtype != torch.float32 or W_in.dtype != torch.float32:
+        return False
+    b, M = x.shape
+    D = W_in.shape[0] // 2
+    return (x.is_cuda and 1 <= b <= SKINNY_MAX_ROWS and M >= 256 and M % 128 == 0 and W_in.shape == (2 * D, M)
+            and D % 16 == 0 and 2 <= d_conv <= 4 and 1 <= J <= 288 and x.stride(1) == 1 and x.stride(0) % 4 == 0
+            and W_in.is_contiguous() and x.data_ptr() % 16 == 0 and W_in.data_ptr() % 16 == 0
+            and conv_state.dtype == torch.float32 and conv_state.is_contiguous()
+            and tuple(conv_state.shape) == (b, D, d_conv - 1))
+
+
+def in_proj_conv_xproj(x, W_in, b_in, conv_state, conv_w, conv_b, W_xT, channels_per_part=None):
+    """mtl_in_proj_conv_xproj: a batched step's in_proj (x [b, d_model] .
+    W_in [2D, d_model]^T + b_in), the conv step + SiLU of its x half (conv
+    history [b, D, K-1] updated in place) and the x_proj partials of each
+    channel block, in one launch.  Returns (xc [b, D], z [b, D], xpart
+    [D / channels_per_part, b, J]); ops.sum_parts(xpart) is x_dbl."""
+    b, M = x.shape
+    D = W_in.shape[0] // 2
+    w = conv_w.reshape(conv_w.shape[0], conv_w.shape[-1]) if conv_w.dim() == 3 else conv_w
+    K = w.shape[1]
+    J = W_xT.shape[1]
+    if not in_proj_conv_xproj_ok(x, W_in, conv_state, K, J):
+        raise ValueError("in_proj_conv_xproj: fp32 x [b<=32, d_model%128==0, >=256], contiguous W_in [2D, d_model] "
+                         "(D%16==0), conv_state [b, D, K-1] with K in 2..4, J <= 288")
+    _f32_mat(w, (D, K), "conv_w")
+    _f32_vec(conv_b, D, "conv_b")
+    _f32_vec(b_in, 2 * D, "b_in")
+    _f32_mat(W_xT, (D, J), "W_xT")
+    if channels_per_part is None:
+        # 32-channel tiles where they still give every CU a workgroup (the
+        # same rule as linear_skinny's rows_per_block)
+        channels_per_part = 32 if b > 16 and D % 32 == 0 and 2 * D // 32 >= 256 else 16
+    xc = torch.empty(b, D, device=x.device, dtype=torch.float32)
+    z = torch.empty(b, D, device=x.device, dtype=torch.float32)
+    xpart = torch.empty(D // channels_per_part, b, J, device=x.device, dtype=torch.float32)
+    _same_device(x, W_in, b_in, conv_state, w, conv_b, W_xT)
+    with _dev_guard(x):
+        _lib.check(_lib.load().mtl_in_proj_conv_xproj(_ptr(x), x.stride(0), _ptr(W_in), _ptr(b_in), _ptr(conv_state),
+                                                      _ptr(w), _ptr(conv_b), K, _ptr(W_xT), J, _ptr(xc), _ptr(z),
+                                                      z.stride(0), _ptr(xpart), b, M, D, channels_per_part,
+                                                      _stream(x)), "in_proj_conv_xproj")
+    return xc, z, xpart
+
+
 # --------------------------------------------------------------------------- step
 def selective_state_update(ssm_state, x, z, x_dbl, W_dt, b_dt, A, D=None, a_is_log=False, out=None):
     """In-place single-token SSM update (mtl_selective_state_update).

@@ -98,6 +98,14 @@ def test_invalid_arguments_are_rejected_without_a_gpu():
     ("mtl_linear_skinny", dict(N=6), b"multiple of 4"),
     ("mtl_linear_skinny", dict(rows_per_block=8), b"rows_per_block"),
     ("mtl_linear_skinny", dict(K=256, ksplit=2, y_ks=64), b"overlap"),
+    ("mtl_in_proj_conv_xproj", dict(batch=33), b"batch must be in [1, 32]"),
+    ("mtl_in_proj_conv_xproj", dict(d_model=128), b"at least 256"),
+    ("mtl_in_proj_conv_xproj", dict(d_model=320), b"multiple of 128"),
+    ("mtl_in_proj_conv_xproj", dict(cpp=8), b"channels_per_part"),
+    ("mtl_in_proj_conv_xproj", dict(d_inner=48, cpp=32), b"multiple of channels_per_part"),
+    ("mtl_in_proj_conv_xproj", dict(d_conv=5), b"d_conv"),
+    ("mtl_in_proj_conv_xproj", dict(d_conv=1), b"d_conv"),
+    ("mtl_in_proj_conv_xproj", dict(J=289), b"J (x_proj rows)"),
 ])
 def test_entry_points_validate_sizes_on_the_host(case):
     """Each entry point rejects sizes its kernels do not cover, with a message,
@@ -150,6 +158,11 @@ def test_entry_points_validate_sizes_on_the_host(case):
         a.update(over)
         rc = lib.mtl_linear_skinny(P, a["K"], P, None, P, a["N"], a["y_ks"], a["M"], a["N"], a["K"], a["ksplit"],
                                    a["rows_per_block"], None)
+    elif name == "mtl_in_proj_conv_xproj":
+        a = dict(batch=8, d_model=256, d_inner=64, cpp=16, d_conv=4, J=40)
+        a.update(over)
+        rc = lib.mtl_in_proj_conv_xproj(P, a["d_model"], P, None, P, P, None, a["d_conv"], P, a["J"], P, P,
+                                        a["d_inner"], P, a["batch"], a["d_model"], a["d_inner"], a["cpp"], None)
     else:
         a = dict(width=4)
         a.update(over)

@@ -207,14 +207,17 @@ def test_graph_replay_bit_identical_to_eager(small_lm, batch):
 
 @pytest.mark.parametrize("batch", [8, 32])
 def test_graph_replay_on_the_skinny_gemm_step(batch, monkeypatch):
-    """The batched per-op step with in_proj and out_proj on mtl_linear_skinny
-    (out_proj as 4 split-K parts summed by the residual add): graph replays
-    equal eager bit for bit, with eager work between replays, and the eager
-    step matches the float64 oracle."""
+    """The batched per-op step with in_proj fused with the conv step and the
+    x_proj partials (mtl_in_proj_conv_xproj) and out_proj on mtl_linear_skinny
+    (4 split-K parts summed by the residual add): graph replays equal eager
+    bit for bit, with eager work between replays, and the eager step matches
+    the float64 oracle."""
     from mamba_lite import ops as mops
     calls = []
     real = mops.linear_skinny
     monkeypatch.setattr(mops, "linear_skinny", lambda *a, **k: calls.append(k.get("ksplit", 1)) or real(*a, **k))
+    real_ic = mops.in_proj_conv_xproj
+    monkeypatch.setattr(mops, "in_proj_conv_xproj", lambda *a, **k: calls.append("fused") or real_ic(*a, **k))
     torch.manual_seed(6)
     cfg = MambaConfig(d_model=256, n_layer=2, vocab_size=512, d_state=16)
     model = MambaLM(cfg)
@@ -225,7 +228,7 @@ def test_graph_replay_on_the_skinny_gemm_step(batch, monkeypatch):
     with torch.no_grad():
         _, cache_e = model.prefill(ids)
         eager = [model.step(s, cache_e).clone() for s in steps]
-        assert 1 in calls and 4 in calls, calls      # in_proj whole, out_proj in 4 parts
+        assert "fused" in calls and 4 in calls and 1 not in calls, calls   # fused in_proj, out_proj in 4 parts
         ref_logits, rcache = om.lm_prefill(_lm_weights(model), ids.cpu().numpy(), dtype=np.float64)
         for k, s in enumerate(steps):
             ref = om.lm_step(_lm_weights(model), s.cpu().numpy(), rcache, dtype=np.float64)
