@@ -215,17 +215,22 @@ void launch_linear(const LinArgs& a, hipStream_t st) {
 // ------------------------------------------------------- in_proj + conv step + x_proj partials
 // The batched step's in_proj (model.py:261), conv step + SiLU (264-277) and
 // x_proj (279) as one launch.  in_proj's output rows [0, D) are the x half
-// and [D, 2D) the z half; a workgroup's tile of 16 RB rows lies in one half
-// (D % (16 RB) == 0).  A z tile stores z.  An x tile keeps its outputs
-// x[m][c] (c = its 16 RB channels, m = the b rows) and, as the epilogue:
+// and [D, 2D) the z half; a workgroup's tile of CB = 16 RB rows lies in one
+// half (D % CB == 0).  A z tile stores z.  An x tile keeps its outputs
+// x[m][c] (c = its CB channels, m = the b rows) and, as the epilogue:
 //   * the conv step of each (row, channel): window = the K - 1 history
 //     values of conv_state then x, xc = SiLU(window . conv_w[c] + conv_b[c]),
 //     history shifted by one in place; xc to global memory;
-//   * the x_proj partial of its channels: xpart[tile][m][j] = sum over its
-//     channels c, in order, of xc[m][c] W_xT[c][j].  The caller adds the
-//     D / (16 RB) partials in tile order.
-// The conv operands and the tile's W_xT rows are loaded before the GEMM
-// (they do not depend on it), so the epilogue waits on no memory.
+//   * the x_proj partial of its channels on the matrix cores:
+//     xpart[tile][m][j] = sum over its channels c of xc[m][c] W_xT[c][j],
+//     as 16 x 16 blocks of (m, j) with K = the channels in steps of 4.  The
+//     caller adds the D / CB partials in tile order.
+// The tile's W_xT rows are one contiguous block of CB J floats; the
+// workgroup copies it into LDS past the ring with global_load_lds before the
+// GEMM (the GEMM's last vmcnt(0) and barrier cover it).  The conv operands
+// are loaded after the GEMM: loaded before it (into registers), their
+// scattered history rows delayed the first stages by more than the memory
+// round trip they save (1.4b width, 32 tokens: 24.5 against 21.7 us).
 struct InConvArgs {
     float* state;            // [b, D, K - 1], in place
     const float* conv_w;     // [D, K]
@@ -233,65 +238,53 @@ struct InConvArgs {
     const float* WxT;        // [D, J]
     float* xc;               // [b, D]
     float* z;                // [b, D] rows at stride z_rs
-    float* xpart;            // [D / (16 RB), b, J]
+    float* xpart;            // [D / CB, b, J]
     int64_t z_rs;
     int D, J;
 };
 
-constexpr int kIcMaxJQ = 9;                       // J <= 32 * 9 = 288
+constexpr int kIcMaxJ = 288;
 
-template <int RB, int MB, int D, int K, int JQ>
+template <int RB, int MB, int D, int K, int NBJ>
 __global__ void __launch_bounds__(kLinThreads) in_conv_xproj_kernel(const LinArgs a, const InConvArgs c) {
-    constexpr int CB = 16 * RB, XR = 16 * MB;         // channels of a tile, rows of x
-    constexpr int WLD = JQ * 32 * CB / kLinThreads;   // W_xT loads per thread
-    // the epilogue's buffers live in the ring too, past the reduction space:
-    // with a second LDS array in the kernel the compiler can no longer tell
-    // the ring reads from the copies' LDS writes and drains vmcnt to zero
-    // before every stage (measured at the mamba-1.4b width: 28.9 us against
-    // 17 us for the plain product)
-    __shared__ __align__(16) float ring[ring_floats<RB, MB, D>()];
-    constexpr int kAcc = kLinWaves * RB * MB * 64 * 4;          // floats of the reduction space
-    static_assert(kAcc + CB * JQ * 32 + XR * (CB + 1) <= ring_floats<RB, MB, D>(), "epilogue space");
-    float (*s_wx)[JQ * 32] = reinterpret_cast<float (*)[JQ * 32]>(ring + kAcc);
-    float (*s_xc)[CB + 1] = reinterpret_cast<float (*)[CB + 1]>(ring + kAcc + CB * JQ * 32);
-    static_assert(WLD * kLinThreads == JQ * 32 * CB, "W_xT tile split");
+    constexpr int CB = 16 * RB, XR = 16 * MB;           // channels of a tile, rows of x
+    constexpr int RING = ring_floats<RB, MB, D>();
+    constexpr int WXF = (CB * 16 * NBJ + 255) / 256 * 256;   // W_xT tile space, whole 1 KB copies
+    // All of the kernel's LDS is one array: with a second LDS array the
+    // compiler can no longer tell the ring reads from the copies' LDS writes
+    // and drains vmcnt to zero before every stage (1.4b width: 28.9 us
+    // against 17 us for the plain product).
+    __shared__ __align__(16) float lds[RING + WXF];
+    float* ring = lds;
+    float* s_wx = lds + RING;                          // [CB][J]
+    constexpr int kAcc = kLinWaves * RB * MB * 64 * 4;  // floats of the reduction space
+    static_assert(kAcc + XR * (CB + 1) <= RING, "epilogue space");
+    float (*s_xc)[CB + 1] = reinterpret_cast<float (*)[CB + 1]>(ring + kAcc);
 
-    const int tid = threadIdx.x;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int n0 = blockIdx.x * CB;
     const bool xtile = n0 < c.D;                       // uniform
-    const int t = tid;                                 // this thread's output pair, if t < 64 RB MB
-    const bool has_pair = t < RB * MB * 64;
-    // the pair's row and first channel (same formula as tile_sum)
-    const int p_tile = t >> 6, p_ln = t & 63, p_rb = p_tile / MB, p_mb = p_tile - p_rb * MB;
-    const int pm = 16 * p_mb + (p_ln & 15), pc = 16 * p_rb + 4 * (p_ln >> 4);
+    const int J = c.J;
 
-    F4v hist[K - 1], cw[K], cb = {0.f, 0.f, 0.f, 0.f};
-    float wl[WLD];
-    // only a thread that owns a pair reads conv operands: for t >= 64 RB MB
-    // the formula above gives channels past the tile (and, on the last x
-    // tile, past d_inner)
-    if (xtile && has_pair) {
-        const int mm = min(pm, a.M - 1), ch = n0 + pc;
-        const F4v* sp = reinterpret_cast<const F4v*>(c.state + ((int64_t)mm * c.D + ch) * (K - 1));
-#pragma unroll
-        for (int k = 0; k < K - 1; ++k) hist[k] = sp[k];
-        const F4v* wp = reinterpret_cast<const F4v*>(c.conv_w + (int64_t)ch * K);
-#pragma unroll
-        for (int k = 0; k < K; ++k) cw[k] = wp[k];
-        if (c.conv_b) cb = ld4(c.conv_b + ch);
-    }
     if (xtile) {
-        // W_xT tile: element e = tid + 256 i of [CB][JQ * 32] (rows n0 + e / (32 JQ) < n0 + CB <= D),
-        // columns past J clamped (never used)
-#pragma unroll
-        for (int i = 0; i < WLD; ++i) {
-            const int e = tid + kLinThreads * i, cc = e / (JQ * 32), j = e - cc * (JQ * 32);
-            wl[i] = c.WxT[(int64_t)(n0 + cc) * c.J + min(j, c.J - 1)];
+        // the tile's W_xT block, 1 KB per copy, copies dealt to the wavefronts;
+        // lanes past the block re-read its last 16 bytes into the padding
+        const int nf = CB * J;                         // a multiple of 4
+        const float* src = c.WxT + (int64_t)n0 * J;
+        for (int ch = wave; ch * 256 < nf; ch += kLinWaves) {
+            const int f = min(ch * 256 + 4 * lane, nf - 4);
+#if defined(__HIP_DEVICE_COMPILE__)
+            __builtin_amdgcn_global_load_lds(src + f, s_wx + ch * 256, 16, 0, 0);
+#else
+            (void)f;
+#endif
         }
     }
 
     skinny_tile<RB, MB, D>(a, ring, n0, 0);
 
+    const int t = tid;                                 // this thread's output pair, if t < 64 RB MB
+    const bool has_pair = t < RB * MB * 64;
     if (!xtile) {
         if (has_pair) {
             int m, nl;
@@ -304,18 +297,27 @@ __global__ void __launch_bounds__(kLinThreads) in_conv_xproj_kernel(const LinArg
         return;
     }
 
-#pragma unroll
-    for (int i = 0; i < WLD; ++i) {
-        const int e = tid + kLinThreads * i, cc = e / (JQ * 32), j = e - cc * (JQ * 32);
-        s_wx[cc][j] = wl[i];
-    }
+    // the pair's conv results, stored after the x_proj phase: global stores
+    // issued before its LDS reads would be waited for there (the compiler
+    // orders LDS reads after every earlier vector-memory operation once the
+    // kernel has copied into LDS)
+    int m = 0, nl = 0, ch = 0;
+    F4v xcv = {0.f, 0.f, 0.f, 0.f}, nh[K - 1];
     if (has_pair) {
-        int m, nl;
-        F4v v = tile_sum<RB, MB>(ring, t, m, nl);     // m == pm, nl == pc
+        F4v v = tile_sum<RB, MB>(ring, t, m, nl);
         if (a.bias) v += ld4(a.bias + n0 + nl);
+        ch = n0 + nl;
+        const int mm = min(m, a.M - 1);
+        F4v hist[K - 1], cw[K], cb = {0.f, 0.f, 0.f, 0.f};
+        const F4v* sp = reinterpret_cast<const F4v*>(c.state + ((int64_t)mm * c.D + ch) * (K - 1));
+#pragma unroll
+        for (int k = 0; k < K - 1; ++k) hist[k] = sp[k];
+        const F4v* wp = reinterpret_cast<const F4v*>(c.conv_w + (int64_t)ch * K);
+#pragma unroll
+        for (int k = 0; k < K; ++k) cw[k] = wp[k];
+        if (c.conv_b) cb = ld4(c.conv_b + ch);
         // channel q of the four: history tap k is float q (K - 1) + k of the
         // pair's history block, conv weight k float q K + k of its weight block
-        F4v xcv, nh[K - 1];
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
             float win[K];
@@ -330,71 +332,81 @@ __global__ void __launch_bounds__(kLinThreads) in_conv_xproj_kernel(const LinArg
 #pragma unroll
             for (int k = 0; k < K - 1; ++k) nh[(q * (K - 1) + k) / 4][(q * (K - 1) + k) % 4] = win[k + 1];
         }
-        if (m < a.M) {
-            const int ch = n0 + nl;
-            F4v* sp = reinterpret_cast<F4v*>(c.state + ((int64_t)m * c.D + ch) * (K - 1));
-#pragma unroll
-            for (int k = 0; k < K - 1; ++k) sp[k] = nh[k];
-            *reinterpret_cast<F4v*>(c.xc + (int64_t)m * c.D + ch) = xcv;
-        }
 #pragma unroll
         for (int q = 0; q < 4; ++q) s_xc[m][nl + q] = m < a.M ? xcv[q] : 0.f;
     }
     __syncthreads();
 
-    // x_proj partial: thread = (row group rg of TB rows, column lane jg),
-    // columns jg + 32 q; channels added in order
-    constexpr int TB = XR / 8;
-    const int rg = tid >> 5, jg = tid & 31;
-    float acc[TB][JQ];
+    // x_proj partial on the matrix cores: wavefront w takes column blocks
+    // jb = w + 4 i (i < JPW); lane l = r + 16 kk feeds A = xc[16 mb + r][4 s + kk]
+    // (read once, shared by the blocks) and B = W_xT[4 s + kk][16 jb + r]
+    // (columns past J clamped, never stored); D[i][j] lands in lane
+    // j + 16 (i / 4), register i % 4.  The JPW MB accumulators are
+    // independent chains, interleaved step by step.
+    constexpr int JPW = (NBJ + kLinWaves - 1) / kLinWaves;
+    const int r = lane & 15, kk = lane >> 4;
+    float av[CB / 4][MB];
 #pragma unroll
-    for (int i = 0; i < TB; ++i)
+    for (int s4 = 0; s4 < CB / 4; ++s4)
 #pragma unroll
-        for (int q = 0; q < JQ; ++q) acc[i][q] = 0.f;
-#pragma unroll 4
-    for (int cc = 0; cc < CB; ++cc) {
-        float xv[TB], wv[JQ];
+        for (int mb = 0; mb < MB; ++mb) av[s4][mb] = s_xc[16 * mb + r][4 * s4 + kk];
+    F4v acc[JPW][MB];
 #pragma unroll
-        for (int i = 0; i < TB; ++i) xv[i] = s_xc[rg * TB + i][cc];
+    for (int i = 0; i < JPW; ++i)
 #pragma unroll
-        for (int q = 0; q < JQ; ++q) wv[q] = s_wx[cc][jg + 32 * q];
+        for (int mb = 0; mb < MB; ++mb) acc[i][mb] = F4v{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int q = 0; q < JQ; ++q)
+    for (int s4 = 0; s4 < CB / 4; ++s4) {
 #pragma unroll
-            for (int i = 0; i < TB; ++i) acc[i][q] = fmaf(xv[i], wv[q], acc[i][q]);
-    }
+        for (int i = 0; i < JPW; ++i) {
+            const int jr = min(16 * (wave + kLinWaves * i) + r, J - 1);
+            const float bv = s_wx[(4 * s4 + kk) * J + jr];
 #pragma unroll
-    for (int i = 0; i < TB; ++i) {
-        const int m = rg * TB + i;
-        if (m >= a.M) continue;
-#pragma unroll
-        for (int q = 0; q < JQ; ++q) {
-            const int j = jg + 32 * q;
-            if (j < c.J) c.xpart[((int64_t)blockIdx.x * a.M + m) * c.J + j] = acc[i][q];
+            for (int mb = 0; mb < MB; ++mb)
+                acc[i][mb] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[s4][mb], bv, acc[i][mb], 0, 0, 0);
         }
     }
+#pragma unroll
+    for (int i = 0; i < JPW; ++i) {
+        const int j = 16 * (wave + kLinWaves * i) + r;
+        if (j < J) {
+#pragma unroll
+            for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const int mo = 16 * mb + 4 * kk + q;
+                    if (mo < a.M) c.xpart[((int64_t)blockIdx.x * a.M + mo) * J + j] = acc[i][mb][q];
+                }
+        }
+    }
+    if (has_pair && m < a.M) {
+        F4v* spo = reinterpret_cast<F4v*>(c.state + ((int64_t)m * c.D + ch) * (K - 1));
+#pragma unroll
+        for (int k = 0; k < K - 1; ++k) spo[k] = nh[k];
+        *reinterpret_cast<F4v*>(c.xc + (int64_t)m * c.D + ch) = xcv;
+    }
 }
 
-template <int RB, int MB, int K, int JQ>
+template <int RB, int MB, int K, int NBJ>
 void launch_in_conv(const LinArgs& a, const InConvArgs& c, hipStream_t st) {
-    hipLaunchKernelGGL((in_conv_xproj_kernel<RB, MB, 3, K, JQ>), dim3((unsigned)(a.N / (16 * RB))), dim3(kLinThreads),
-                       0, st, a, c);
+    hipLaunchKernelGGL((in_conv_xproj_kernel<RB, MB, 3, K, NBJ>), dim3((unsigned)(a.N / (16 * RB))),
+                       dim3(kLinThreads), 0, st, a, c);
 }
 
-// JQ in {1, 3, 5, 9}: the smallest that covers J (columns past J are never stored)
+// NBJ = 16-column blocks of x_proj's output: the smallest of 2, 6, 10, 18 that covers J
 template <int RB, int MB, int K>
-void dispatch_in_conv_jq(int J, const LinArgs& a, const InConvArgs& c, hipStream_t st) {
-    if (J <= 32) launch_in_conv<RB, MB, K, 1>(a, c, st);
-    else if (J <= 96) launch_in_conv<RB, MB, K, 3>(a, c, st);
-    else if (J <= 160) launch_in_conv<RB, MB, K, 5>(a, c, st);
-    else launch_in_conv<RB, MB, K, 9>(a, c, st);
+void dispatch_in_conv_j(int J, const LinArgs& a, const InConvArgs& c, hipStream_t st) {
+    if (J <= 32) launch_in_conv<RB, MB, K, 2>(a, c, st);
+    else if (J <= 96) launch_in_conv<RB, MB, K, 6>(a, c, st);
+    else if (J <= 160) launch_in_conv<RB, MB, K, 10>(a, c, st);
+    else launch_in_conv<RB, MB, K, 18>(a, c, st);
 }
 
 template <int RB, int MB>
 void dispatch_in_conv(int K, const LinArgs& a, const InConvArgs& c, hipStream_t st) {
-    if (K == 2) dispatch_in_conv_jq<RB, MB, 2>(c.J, a, c, st);
-    else if (K == 3) dispatch_in_conv_jq<RB, MB, 3>(c.J, a, c, st);
-    else dispatch_in_conv_jq<RB, MB, 4>(c.J, a, c, st);
+    if (K == 2) dispatch_in_conv_j<RB, MB, 2>(c.J, a, c, st);
+    else if (K == 3) dispatch_in_conv_j<RB, MB, 3>(c.J, a, c, st);
+    else dispatch_in_conv_j<RB, MB, 4>(c.J, a, c, st);
 }
 
 }  // namespace
@@ -443,14 +455,14 @@ extern "C" int mtl_in_proj_conv_xproj(const float* x, int64_t x_rs, const float*
     MTL_REQUIRE(d_inner >= channels_per_part && d_inner % channels_per_part == 0 && d_inner < (int64_t(1) << 29),
                 "d_inner must be a positive multiple of channels_per_part");
     MTL_REQUIRE(d_conv >= 2 && d_conv <= 4, "d_conv must be 2, 3 or 4");
-    MTL_REQUIRE(J >= 1 && J <= 32 * kIcMaxJQ, "J (x_proj rows) must be in [1, 288]");
+    MTL_REQUIRE(J >= 1 && J <= kIcMaxJ, "J (x_proj rows) must be in [1, 288]");
     MTL_REQUIRE(x_rs >= d_model && x_rs % 4 == 0 && z_rs >= d_inner && z_rs % 4 == 0,
                 "row strides must cover a row and be multiples of 4");
     MTL_REQUIRE((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(W_in) | reinterpret_cast<uintptr_t>(b_in) |
                  reinterpret_cast<uintptr_t>(conv_state) | reinterpret_cast<uintptr_t>(conv_w) |
                  reinterpret_cast<uintptr_t>(conv_b) | reinterpret_cast<uintptr_t>(xc) |
-                 reinterpret_cast<uintptr_t>(z)) % 16 == 0,
-                "x, W_in, b_in, conv_state, conv_w, conv_b, xc and z must be 16-byte aligned");
+                 reinterpret_cast<uintptr_t>(z) | reinterpret_cast<uintptr_t>(W_xT)) % 16 == 0,
+                "x, W_in, b_in, conv_state, conv_w, conv_b, W_xT, xc and z must be 16-byte aligned");
     LinArgs a{x, W_in, b_in, nullptr, x_rs, 0, 0, (int)batch, (int)(2 * d_inner), (int)d_model, 1};
     InConvArgs c{conv_state, conv_w, conv_b, W_xT, xc, z, xpart, z_rs, (int)d_inner, (int)J};
     hipStream_t st = as_stream(stream);

@@ -1,9 +1,10 @@
 """mtl_in_proj_conv_xproj (a batched step's in_proj, conv step and x_proj
 partials in one launch, model.py:261-279) against a float64 reference of the
 same three steps, tolerance 1e-5 relative: xc, z, the shifted conv history
-and every channel block's x_proj partial; and, with 32-channel parts, bit for
-bit against the two launches it replaces (mtl_linear_skinny for in_proj, then
-mtl_conv_step_xproj), whose summation orders it keeps.  Shapes: the mamba-1.4b
+and every channel block's x_proj partial; and against the two launches it
+replaces (mtl_linear_skinny for in_proj, then mtl_conv_step_xproj): xc, z and
+the history bit for bit (same summation orders), the partials to 1e-5 (they
+are summed on the matrix cores here, channel by channel there).  Shapes: the mamba-1.4b
 and 130m widths at 32 tokens, small and odd batch sizes, conv widths 2..4, J
 up to 288, with and without the in_proj and conv biases."""
 import pytest
@@ -71,9 +72,10 @@ def test_in_proj_conv_xproj_vs_float64(b, M, D, K, J, cpp, biases):
 
 @pytest.mark.parametrize("b,M,D,K,J", [(32, 2048, 4096, 4, 160), (7, 768, 1536, 4, 80), (20, 256, 96, 3, 200)])
 def test_in_proj_conv_xproj_equals_the_two_launches(b, M, D, K, J):
-    """32-channel parts keep the unfused path's summation orders: in_proj
-    (mtl_linear_skinny, same tile product), the conv taps in order, the
-    x_proj channels of a block in order -- so the outputs match bit for bit."""
+    """With 32-channel parts the in_proj tile product (the same as
+    mtl_linear_skinny's) and the conv taps keep the unfused path's summation
+    orders, so xc, z and the history match bit for bit; the x_proj partials
+    of the same channel blocks agree to 1e-5."""
     print(f"\n[in_proj_conv_xproj == linear_skinny + conv_step_xproj b={b} d_model={M} d_inner={D}]", flush=True)
     x, W_in, b_in, state, conv_w, conv_b, W_xT = _operands(b, M, D, K, J, True, 7 * b + D)
     state2 = state.clone()
@@ -83,7 +85,7 @@ def test_in_proj_conv_xproj_equals_the_two_launches(b, M, D, K, J):
     assert torch.equal(z, xz[:, D:])
     assert torch.equal(xc, xc2)
     assert torch.equal(state, state2)
-    assert torch.equal(xpart, xpart2)
+    assert_rel(xpart.cpu().numpy(), xpart2.cpu().numpy(), TOL, "x_proj partials")
 
 
 def test_in_proj_conv_xproj_rejects_what_it_does_not_cover():
