@@ -3,12 +3,13 @@ models against the float64 oracle, fp32, tolerance 1e-4 (relative to each
 element plus the tensor's rms):
 
   * a 1024-token mixer prefill at batch 1 (model.py:184-241);
-  * MambaMixer.step and MambaLM.step at batch 32 (the per-op step: conv step
-    fused with the split-K x_proj partials, their ordered sum, the SSM
-    update; model.py:249-294, 343-353);
+  * MambaMixer.step and MambaLM.step at batch 32 (the per-op step: in_proj
+    fused with the conv step and the x_proj partials of each channel block,
+    their ordered sum, the SSM update; model.py:249-294, 343-353);
   * MambaLM.step on the fused decode path at batch 1, 2 and 4;
-  * d_model 2560 (d_inner 5120: 160 x_proj partial blocks, past the fused
-    path's 4096-channel limit) at batch 1 and 8;
+  * d_model 2560 (d_inner 5120, past the fused decode path's 4096-channel
+    limit: 320 x_proj partial blocks of 16 channels at batch 1 and 8, 160 of
+    32 at batch 32);
   * the full-size mamba-130m model (24 layers, vocab 50280) on the fused
     decode path at batch 1.
 
@@ -107,10 +108,11 @@ def test_lm_step_at_1p4b_width(b):
     _lm_steps_vs_oracle(lm, W, b, 8, 3, 2048, 46 + b, expect_fused=b in (1, 2, 4))
 
 
-@pytest.mark.parametrize("b", [1, 8])
+@pytest.mark.parametrize("b", [1, 8, 32])
 def test_lm_step_d_inner_5120(b):
-    """d_inner 5120: 160 x_proj partial blocks of 32 channels, summed by the
-    runtime-count form of mtl_sum_parts; the fused path stops at 4096."""
+    """d_inner 5120: 320 x_proj partial blocks of 16 channels (batch 1, 8) or
+    160 of 32 (batch 32), summed by the runtime-count form of mtl_sum_parts;
+    the fused decode path stops at 4096."""
     print(f"\n[wide: lm step d_model=2560 b={b}]", flush=True)
     lm, W = _lm(47, 2560, 1, 512)
     _lm_steps_vs_oracle(lm, W, b, 5, 2, 512, 48 + b, expect_fused=False)
