@@ -310,8 +310,9 @@ int mtl_in_proj_conv_xproj(const float* x, int64_t x_rs, const float* W_in, cons
  *   id outside [0, vocab) makes that batch row NaN instead of reading
  *   outside the table, where the reference's nn.Embedding raises) ->
  *   RMSNorm (norm_w, eps; model.py:130-135) -> in_proj rows W_in [2D, M]
- *   (+ b_in) of channel blocks of `channels_per_block` (must be 8: one
- *   workgroup per 8 channels, 4 in_proj rows per wavefront; model.py:261) ->
+ *   (+ b_in) of channel blocks of `channels_per_block` (8 or 4: one
+ *   workgroup per block of the x rows and one per block of the z rows, 2 or
+ *   1 in_proj rows per wavefront; model.py:261) ->
  *   conv step with the in-place history shift of conv_state [b, D, K-1]
  *   (conv_w [D, K], conv_b; model.py:264-274) -> xc = SiLU(conv)
  *   (model.py:277), gz = SiLU(z) [b, D] -> if W_xT (x_proj transposed

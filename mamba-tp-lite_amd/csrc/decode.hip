@@ -77,8 +77,8 @@ struct InArgs {
     float eps;
 };
 
-constexpr int kCB = 8;                             // channels per decode_in workgroup
-constexpr int kRowsPerWave = kCB / kWaves;         // in_proj rows per wavefront
+// channels per decode_in workgroup: 8 (2 in_proj rows per wavefront), or 4
+// (one row per wavefront, twice the workgroups on the weight stream)
 constexpr int kMaxConv = 8;                        // d_conv <= 8
 
 // PL = float4 runs per lane (M <= 256 * PL; lanes past M/4 in the last run
@@ -90,22 +90,23 @@ constexpr int kMaxConv = 8;                        // d_conv <= 8
 // partials), the second the z rows (then SiLU(z)).  Halving the rows per
 // workgroup puts the weight stream on twice as many CUs, so more of it is in
 // flight at once.
-template <int B, int PL>
+template <int B, int PL, int CB>
 __global__ void __launch_bounds__(kThreads) decode_in_kernel(const InArgs a) {
-    constexpr int G = kRowsPerWave;
+    constexpr int G = CB / kWaves;                // in_proj rows per wavefront
+    static_assert(G >= 1 && G * kWaves == CB, "channels per workgroup");
     extern __shared__ __align__(16) float s_xw[];  // [B][M]: norm_w * x (the rms scale is applied to the dots)
-    __shared__ float s_pre[kCB][B];
-    __shared__ float s_xc[kCB][B];
+    __shared__ float s_pre[CB][B];
+    __shared__ float s_xc[CB][B];
     __shared__ float s_red[B][kWaves];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int M = a.M, D = a.D, J = a.J, K = a.K;
     const int K4 = M >> 2;
-    const int nblk = (D + kCB - 1) / kCB;
+    const int nblk = (D + CB - 1) / CB;
     const bool zblk = (int)blockIdx.x >= nblk;     // uniform: this workgroup takes the z rows
     const int blk = zblk ? (int)blockIdx.x - nblk : (int)blockIdx.x;
-    const int c0 = blk * kCB;
-    const int nch = min(kCB, D - c0);
+    const int c0 = blk * CB;
+    const int nch = min(CB, D - c0);
 
     // ---- 0. every independent load, in one batch
     const float* rows[G];
@@ -140,12 +141,12 @@ __global__ void __launch_bounds__(kThreads) decode_in_kernel(const InArgs a) {
     const float cbias = a.conv_b ? a.conv_b[cv_c] : 0.f;
 
     // x_proj columns of (j, batch) pair tid over the block's channels
-    float wx[kCB];
+    float wx[CB];
     const int xt = min(tid, J * B - 1);
     const int xp_j = xt % J, xp_b = xt / J;
     if (a.W_xT) {
 #pragma unroll
-        for (int ch = 0; ch < kCB; ++ch) wx[ch] = a.W_xT[(int64_t)(c0 + min(ch, nch - 1)) * J + xp_j];
+        for (int ch = 0; ch < CB; ++ch) wx[ch] = a.W_xT[(int64_t)(c0 + min(ch, nch - 1)) * J + xp_j];
     }
 
     // activation rows and norm weights: element e = tid + 256 q
@@ -266,7 +267,7 @@ __global__ void __launch_bounds__(kThreads) decode_in_kernel(const InArgs a) {
     if (tid < J * B) {
         float xacc = 0.f;
 #pragma unroll
-        for (int ch = 0; ch < kCB; ++ch) xacc = ch < nch ? fmaf(wx[ch], s_xc[ch][xp_b], xacc) : xacc;
+        for (int ch = 0; ch < CB; ++ch) xacc = ch < nch ? fmaf(wx[ch], s_xc[ch][xp_b], xacc) : xacc;
         a.xpart[((int64_t)blk * B + xp_b) * J + xp_j] = xacc;
     }
     for (int t = tid + kThreads; t < J * B; t += kThreads) {   // pairs beyond the first 256
@@ -547,7 +548,7 @@ extern "C" int mtl_decode_in(const float* x, const float* emb, const int64_t* id
     MTL_REQUIRE(d_model >= 4 && d_model % 4 == 0 && d_model <= 256 * kMaxPL,
                 "d_model must be a multiple of 4 in [4, 4096]");
     MTL_REQUIRE(d_inner >= 1 && d_conv >= 2 && d_conv <= kMaxConv && xdbl_cols >= 1, "bad sizes");
-    MTL_REQUIRE(channels_per_block == kCB, "channels_per_block must be 8");
+    MTL_REQUIRE(channels_per_block == 8 || channels_per_block == 4, "channels_per_block must be 8 or 4");
     MTL_REQUIRE((x != nullptr) != (emb != nullptr && ids != nullptr), "give either x or (emb, ids)");
     MTL_REQUIRE(x != nullptr || vocab >= 1, "vocab must be >= 1 with (emb, ids)");
     MTL_REQUIRE(norm_w && W_in && conv_state && conv_w && xc && gz, "null required pointer");
@@ -557,11 +558,17 @@ extern "C" int mtl_decode_in(const float* x, const float* emb, const int64_t* id
     MTL_REQUIRE(smem <= 60 * 1024, "batch * d_model too large for the decode LDS tile");
     InArgs a{x, emb, ids, vocab, resid_out, norm_w, W_in, b_in, conv_state, conv_w, conv_b, W_xT, xc, gz, xpart,
              d_model, d_inner, d_conv, xdbl_cols, eps};
-    const dim3 grid((unsigned)(2 * ((d_inner + kCB - 1) / kCB)));   // x-row blocks, then z-row blocks
+    const int cb = channels_per_block;
+    const dim3 grid((unsigned)(2 * ((d_inner + cb - 1) / cb)));   // x-row blocks, then z-row blocks
     hipStream_t st = as_stream(stream);
     const int plv = round_runs((d_model / 4 + 63) / 64);
-    MTL_DISPATCH_B(batch, MTL_DISPATCH_RUNS(PL, plv, hipLaunchKernelGGL((decode_in_kernel<B, PL>), grid, dim3(kThreads),
-                                                                  smem, st, a)));
+    if (cb == 8) {
+        MTL_DISPATCH_B(batch, MTL_DISPATCH_RUNS(PL, plv, hipLaunchKernelGGL((decode_in_kernel<B, PL, 8>), grid,
+                                                                      dim3(kThreads), smem, st, a)));
+    } else {
+        MTL_DISPATCH_B(batch, MTL_DISPATCH_RUNS(PL, plv, hipLaunchKernelGGL((decode_in_kernel<B, PL, 4>), grid,
+                                                                      dim3(kThreads), smem, st, a)));
+    }
     return check_launch("decode_in");
 }
 

@@ -529,7 +529,7 @@ class MambaLM(nn.Module):
             return plan
         cfg = self.cfg
         J = cfg.dt_rank + 2 * cfg.d_state
-        cpb = 8  # channels per decode_in workgroup (fixed by the kernel)
+        cpb = 8  # channels per decode_in workgroup when it also forms the x_proj partials
         nblk = (cfg.d_inner + cpb - 1) // cpb
         # every decode_ssm workgroup sums the x_proj partials with Q threads
         # per (j, batch) pair and one batch of <= 64 loads per thread; when
@@ -568,6 +568,11 @@ class MambaLM(nn.Module):
         # (more workgroups on its 160 rows at the 1.4b width) that decode_ssm adds
         xp_parts = 1 if split_k else _XPROJ_PARTS if D % (4 * _XPROJ_PARTS) == 0 else 1
         xpart = torch.empty(plan["nblk"] if split_k else xp_parts, b, J, **f32)
+        # decode_in at batch 1 without the partials: 4 channels per workgroup,
+        # one in_proj row per wavefront, twice the workgroups on the weight
+        # stream (measured at d_model 2048: 12.87 -> 12.63 us; at batch 2 and 4
+        # the 8-channel blocks are faster)
+        cpb = 4 if b == 1 and not split_k else plan["cpb"]
         x_cur = None
         for i, blk in enumerate(self.layers):
             mx, lp, lc = blk.mixer, plan["layers"][i], cache.layers[i]
@@ -576,7 +581,7 @@ class MambaLM(nn.Module):
                           x=x_cur, emb=self.embedding.weight if i == 0 else None, ids=ids if i == 0 else None,
                           resid_out=xs[2] if i == 0 else None, b_in=mx.in_proj.bias, conv_b=mx.conv1d.bias,
                           W_xT=lp["W_xT"] if split_k else None, xpart=xpart if split_k else None,
-                          channels_per_block=plan["cpb"])
+                          channels_per_block=cpb)
             if not split_k:
                 ops.decode_gemv_parts(xc, mx.x_proj.weight, xpart)
             ops.decode_ssm(xpart, xc, gz, mx.dt_proj.weight, mx.dt_proj.bias, mx.A_log, mx.D, lc.ssm_state, y)

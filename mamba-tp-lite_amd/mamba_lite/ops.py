@@ -502,7 +502,8 @@ def decode_in(norm_w, eps, W_in, conv_state, conv_w, xc, gz, *, x=None, emb=None
               b_in=None, conv_b=None, W_xT=None, xpart=None, channels_per_block=8):
     """mtl_decode_in: RMSNorm -> in_proj rows -> conv step (conv_state in
     place) -> xc = SiLU(conv), gz = SiLU(z), and optionally the x_proj split-K
-    partials into xpart [nblk, b, J].  x [b, M] or (emb [V, M], ids [b])."""
+    partials into xpart [nblk, b, J], nblk = ceil(D / channels_per_block)
+    (8 or 4 channels per workgroup).  x [b, M] or (emb [V, M], ids [b])."""
     b, D = xc.shape
     M = norm_w.shape[0]
     K = conv_w.shape[1]

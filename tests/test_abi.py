@@ -68,6 +68,7 @@ def test_invalid_arguments_are_rejected_without_a_gpu():
     ("mtl_decode_in", dict(batch=3), b"batch must be 1, 2 or 4"),
     ("mtl_decode_in", dict(d_model=6), b"d_model"),
     ("mtl_decode_in", dict(channels_per_block=16), b"channels_per_block"),
+    ("mtl_decode_in", dict(channels_per_block=2), b"channels_per_block must be 8 or 4"),
     ("mtl_decode_in", dict(d_conv=9), b"bad sizes"),
     ("mtl_decode_in", dict(d_conv=1), b"bad sizes"),
     ("mtl_decode_in", dict(first_layer=True, vocab=0), b"vocab"),

@@ -9,6 +9,7 @@ import pytest
 import torch
 
 from _util import assert_rel
+from mamba_lite import ops
 from mamba_lite.cuda_graph import GraphedStepper
 from mamba_lite.model import MambaConfig, MambaLM, MambaMixer
 from oracle import mixer as om
@@ -208,7 +209,7 @@ def test_decode_norm_gemv_matches_rmsnorm_then_linear(b, cols, rows, with_bias):
     step in one launch) against torch fp32 RMSNorm followed by F.linear, at
     1e-4 relative: the lm_head shapes of the 130m and 1.4b widths, a ragged
     row count, the smallest width and the widest."""
-    from mamba_lite import ops
+
     print(f"decode_norm_gemv b={b} cols={cols} rows={rows} bias={with_bias}", flush=True)
     g = torch.Generator(device=DEV).manual_seed(cols + rows)
     v = 3.0 * torch.randn(b, cols, device=DEV, generator=g)
@@ -222,3 +223,36 @@ def test_decode_norm_gemv_matches_rmsnorm_then_linear(b, cols, rows, with_bias):
                                      bias.double() if with_bias else None)
     torch.cuda.synchronize()
     assert_rel(_np(out), ref.cpu().numpy(), 1e-4, "logits")
+
+
+@pytest.mark.parametrize("b", [1, 2, 4])
+@pytest.mark.parametrize("M,D", [(2048, 4096), (96, 192), (64, 100)])
+def test_decode_in_channel_blocks_of_4_and_8(b, M, D):
+    """mtl_decode_in with 4 and 8 channels per workgroup: every in_proj row is
+    one wavefront's dot product in the same order either way, so xc, SiLU(z)
+    and the shifted conv history match bit for bit; the x_proj partials of
+    4- and 8-channel blocks add up to the same x_dbl within fp32 rounding."""
+    print(f"decode_in blocks 4 vs 8: b={b} d_model={M} d_inner={D}", flush=True)
+    g = torch.Generator(device=DEV).manual_seed(b * 7 + M)
+    K, J = 4, 40
+    x = torch.randn(b, M, device=DEV, generator=g)
+    norm_w = torch.rand(M, device=DEV, generator=g) + 0.5
+    W_in = torch.randn(2 * D, M, device=DEV, generator=g) / M ** 0.5
+    conv_w = torch.randn(D, K, device=DEV, generator=g) / 2
+    conv_b = torch.randn(D, device=DEV, generator=g)
+    state0 = torch.randn(b, D, K - 1, device=DEV, generator=g)
+    W_xT = torch.randn(D, J, device=DEV, generator=g) / D ** 0.5
+    outs = {}
+    for cpb in (4, 8):
+        for with_xp in (False, True):
+            st = state0.clone()
+            xc = torch.empty(b, D, device=DEV)
+            gz = torch.empty(b, D, device=DEV)
+            xpart = torch.empty(-(-D // cpb), b, J, device=DEV) if with_xp else None
+            ops.decode_in(norm_w, 1e-5, W_in, st, conv_w, xc, gz, x=x, conv_b=conv_b,
+                          W_xT=W_xT if with_xp else None, xpart=xpart, channels_per_block=cpb)
+            outs[cpb, with_xp] = (xc, gz, st, None if xpart is None else xpart.sum(0))
+    for with_xp in (False, True):
+        for i in range(3):
+            assert torch.equal(outs[4, with_xp][i], outs[8, with_xp][i]), (with_xp, i)
+    assert_rel(_np(outs[4, True][3]), _np(outs[8, True][3]), 1e-5, "x_dbl")
