@@ -7,11 +7,14 @@ Same public surface as mamba-tp-lite's mamba_lite/model.py:
 Parameter names and shapes match the reference, so its state dicts (and HF
 `state-spaces/mamba-*-hf` checkpoints through from_pretrained) load as is.
 
-What runs where: in_proj / x_proj / dt_proj / out_proj / lm_head are torch
-GEMMs (hipBLASLt / rocBLAS); the causal conv + SiLU, the selective scan
-(with dt bias, softplus, D skip and SiLU gate fused), the single-token conv
-and SSM updates and the residual + RMSNorm are the libmtl HIP kernels.  The
-model runs on the GPU only.
+What runs where: the prefill's in_proj / x_proj / dt_proj / out_proj and the
+lm_head are torch GEMMs (hipBLASLt / rocBLAS).  The decode step's projections
+run on libmtl kernels: GEMVs fused with the norm and the residual at batch
+<= 4, matrix-core skinny GEMMs at <= 32 tokens (in_proj fused with the conv
+step and x_proj).  The causal conv + SiLU, the selective scan (with dt bias,
+softplus, D skip and SiLU gate fused), the single-token conv and SSM updates
+and the residual + RMSNorm are libmtl HIP kernels as well.  The model runs on
+the GPU only.
 
 Deliberate deviation: with bfloat16 activations the SSM state stays float32
 (the cache allocates it in float32 and prefill returns it in float32);
