@@ -296,6 +296,35 @@ struct GemvArgs {
 // NORM: out = (W . (norm_w * v)) * rsqrt(mean(v^2) + eps) + bias -- the final
 // RMSNorm folded into the lm_head rows (every workgroup recomputes the rms of
 // the few-kB vector instead of waiting for a separate norm kernel)
+// Batch 1 without the norm: one wavefront per workgroup and per row, v read
+// straight from global memory (it is a few KB and sits in L2 after the first
+// workgroups), so a row needs no LDS stage and no barrier.  Twice to four
+// times the workgroups of the form below on the same weight stream: the
+// mamba-1.4b decode step went 1410-1415 -> 1401-1406 us/token, the 130m one
+// 322.5-324 -> 320.5-321.5 (same dot-product order, the same bits).
+template <int PL>
+__global__ void __launch_bounds__(64) decode_gemv_row_kernel(const GemvArgs a) {
+    const int lane = threadIdx.x;
+    const int K = a.K, K4 = K >> 2;
+    const int m = blockIdx.x;
+    const float4* row = reinterpret_cast<const float4*>(a.W + (int64_t)m * K);
+    const float4* v4 = reinterpret_cast<const float4*>(a.v);
+    float4 w[PL];
+#pragma unroll
+    for (int p = 0; p < PL; ++p) w[p] = ntload4(row + min(p * 64 + lane, K4 - 1));
+    const float bias = a.bias ? a.bias[m] : 0.f;
+    const float xin = a.x_in ? a.x_in[m] : 0.f;
+    const bool tail_ok = (PL - 1) * 64 + lane < K4;
+    float acc = 0.f;
+#pragma unroll
+    for (int p = 0; p < PL; ++p) {
+        const float t = dot4(w[p], v4[min(p * 64 + lane, K4 - 1)], acc);
+        acc = p < PL - 1 || tail_ok ? t : acc;
+    }
+    acc = group_sum<64>(acc);
+    if (lane == 0) a.out[m] = a.x_in ? xin + (acc + bias) : acc + bias;
+}
+
 template <int B, int PL, bool NORM = false>
 __global__ void __launch_bounds__(kThreads) decode_gemv_kernel(const GemvArgs a) {
     extern __shared__ __align__(16) float s_v[];      // [B][K]
@@ -594,6 +623,9 @@ extern "C" int mtl_decode_gemv(const float* v, const float* W, const float* bias
         MTL_DISPATCH_B(batch, MTL_DISPATCH_RUNS(PLW, plw,
             if constexpr (PLW * kWaves <= kMaxPL) hipLaunchKernelGGL((decode_gemv_split_kernel<B, PLW>),
                 dim3((unsigned)rows), dim3(kThreads), smem, st, a)));
+    } else if (batch == 1) {
+        MTL_DISPATCH_RUNS(PL, round_runs(runs), hipLaunchKernelGGL((decode_gemv_row_kernel<PL>), dim3((unsigned)rows),
+                                                                   dim3(64), 0, st, a));
     } else {
         const dim3 grid((unsigned)((rows + kWaves - 1) / kWaves));
         MTL_DISPATCH_B(batch, MTL_DISPATCH_RUNS(PL, round_runs(runs), hipLaunchKernelGGL((decode_gemv_kernel<B, PL>),

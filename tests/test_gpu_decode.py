@@ -256,3 +256,49 @@ def test_decode_in_channel_blocks_of_4_and_8(b, M, D):
         for i in range(3):
             assert torch.equal(outs[4, with_xp][i], outs[8, with_xp][i]), (with_xp, i)
     assert_rel(_np(outs[4, True][3]), _np(outs[8, True][3]), 1e-5, "x_dbl")
+
+
+@pytest.mark.parametrize("b,cols,rows,with_bias,with_x", [(1, 4096, 2048, False, True), (1, 1536, 768, True, True),
+                                                          (2, 1536, 768, False, True), (4, 100, 9, True, False),
+                                                          (1, 4, 3, True, False), (1, 4096, 160, False, False),
+                                                          (4, 2048, 131, True, True)])
+def test_decode_gemv_vs_float64(b, cols, rows, with_bias, with_x):
+    """mtl_decode_gemv (the decode step's out_proj with the residual add, and
+    x_proj at the 1.4b width) against float64 out = x_in + W v + bias, 1e-5
+    relative: the out_proj shapes of the 1.4b and 130m widths at batch 1 (one
+    wavefront per row), batch 2 and 4 (four rows per workgroup), few long rows
+    (a workgroup per row split four ways), ragged widths and row counts."""
+    print(f"decode_gemv b={b} cols={cols} rows={rows} bias={with_bias} x_in={with_x}", flush=True)
+    g = torch.Generator(device=DEV).manual_seed(cols * 3 + rows + b)
+    v = torch.randn(b, cols, device=DEV, generator=g)
+    W = torch.randn(rows, cols, device=DEV, generator=g) / cols ** 0.5
+    bias = torch.randn(rows, device=DEV, generator=g) if with_bias else None
+    x_in = torch.randn(b, rows, device=DEV, generator=g) if with_x else None
+    out = torch.empty(b, rows, device=DEV)
+    ops.decode_gemv(v, W, out, bias=bias, x_in=x_in)
+    ref = v.double().cpu() @ W.double().cpu().T
+    if with_bias:
+        ref = ref + bias.double().cpu()
+    if with_x:
+        ref = ref + x_in.double().cpu()
+    assert_rel(_np(out), ref.numpy(), 1e-5, "out")
+
+
+@pytest.mark.parametrize("cols,rows", [(4096, 2048), (1536, 768), (100, 9)])
+def test_decode_gemv_batch1_rows_equal_batch2_rows(cols, rows):
+    """Batch 1 runs one wavefront per row, batch 2 four rows per workgroup
+    with v staged in LDS; both take each lane's four-wide dot products in
+    the same order and reduce over the wavefront the same way, so a row of
+    a batch-2 call equals the batch-1 call on that row's v bit for bit."""
+    print(f"decode_gemv b1 == b2 rows cols={cols} rows={rows}", flush=True)
+    g = torch.Generator(device=DEV).manual_seed(cols + 5 * rows)
+    v = torch.randn(2, cols, device=DEV, generator=g)
+    W = torch.randn(rows, cols, device=DEV, generator=g) / cols ** 0.5
+    bias = torch.randn(rows, device=DEV, generator=g)
+    x_in = torch.randn(2, rows, device=DEV, generator=g)
+    out2 = torch.empty(2, rows, device=DEV)
+    ops.decode_gemv(v, W, out2, bias=bias, x_in=x_in)
+    for i in range(2):
+        out1 = torch.empty(1, rows, device=DEV)
+        ops.decode_gemv(v[i:i + 1].clone(), W, out1, bias=bias, x_in=x_in[i:i + 1].clone())
+        assert torch.equal(out1[0], out2[i]), i
