@@ -464,7 +464,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--only", default="all", choices=["all", "scan", "decode", "quant", "shard", "prefill", "copy"])
+    ap.add_argument("--only", default="all",
+                    choices=["all", "scan", "decode", "quant", "shard", "prefill", "copy", "decode-counters"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--decode-shapes", default="130m,1.4b", help="comma list of 130m, 1.4b")
     args = ap.parse_args()
@@ -497,6 +498,24 @@ def main():
             dst.copy_(src)
         torch.cuda.synchronize()
         print(json.dumps({"copy_bytes_each_way": n * 4, "launches": 5}), flush=True)
+        return
+    if args.only == "decode-counters":
+        # a short workload for rocprofv3 --pmc runs over the decode kernels
+        # (counter collection serializes every dispatch, so the timed decode
+        # bench's replays take minutes there): the 1.4b shape, a 16-token
+        # prefill, then 4 eager steps at batch 1 (fused path) and batch 32
+        # (per-op path), the same kernels on the same shapes as the graphs
+        model = build_lm(MambaConfig(d_model=2048, n_layer=48, vocab_size=50280), dev)
+        for b in (1, 32):
+            g = torch.Generator(device=dev).manual_seed(1)
+            ids = torch.randint(0, 50280, (b, 16), device=dev, generator=g)
+            nxt = torch.zeros(b, 1, dtype=torch.long, device=dev)
+            with torch.no_grad():
+                _, cache = model.prefill(ids)
+                for s in range(4):
+                    model.step(nxt, cache)
+                    torch.cuda.synchronize()
+                    log(f"decode-counters 1.4b b={b}: step {s} done")
         return
     if want("scan"):
         log("scan: isolated selective scan fp32 [32,1536,1024]")
