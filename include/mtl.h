@@ -256,8 +256,9 @@ int mtl_quant_dequant_sum_fp16(const float* const* parts, int32_t nparts, int64_
  * Skinny fp32 GEMM on the matrix cores for the projections of a batched
  * decode step: y = x W^T (+ bias), nn.Linear on [b, K] with b <= 32 tokens --
  * in_proj (model.py:261), out_proj (model.py:293) and the tied lm_head
- * (model.py:326, 353) in MambaMixer.step / MambaLM.step.
- *   x: [M, K], row stride x_rs (>= K, multiple of 4), 1 <= M <= 32;
+ * (model.py:326, 353) in MambaMixer.step / MambaLM.step -- and of a prefill
+ * of at most 64 tokens (model.py:197, 214, 240, 339).
+ *   x: [M, K], row stride x_rs (>= K, multiple of 4), 1 <= M <= 64;
  *   W: [N, K] contiguous, N a multiple of 4; bias: [N] or NULL;
  *   y: [M, N] with row stride y_rs (>= N, multiple of 4).
  * K must be a multiple of 128 * ksplit.  With ksplit > 1 the K range is cut

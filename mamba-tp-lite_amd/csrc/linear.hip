@@ -1,11 +1,13 @@
 // Skinny fp32 GEMM on the matrix cores for the projections of a batched
-// decode step (gfx950).
+// decode step and of a short prefill (gfx950).
 //
-//   Y[m, n] = sum_k X[m, k] * W[n, k]  (+ bias[n]),   m < M <= 32
+//   Y[m, n] = sum_k X[m, k] * W[n, k]  (+ bias[n]),   m < M <= 64
 //
 // is nn.Linear on a [b, K] activation with b <= 32 tokens: in_proj
 // (model.py:261), out_proj (model.py:293) and the tied lm_head
-// (model.py:326, 353) of MambaMixer.step / MambaLM.step.  At these shapes the
+// (model.py:326, 353) of MambaMixer.step / MambaLM.step; and on the [b l, K]
+// activations of a prefill of b l <= 64 tokens (model.py:197, 214, 240,
+// 339).  At these shapes the
 // product streams the weight once and does 2*M flops per weight element, so
 // it is bound by HBM; a GEMM library tiles it for large M and leaves much of
 // the weight stream idle (fp32 M=32, weights cold in HBM, mamba-1.4b width:
@@ -206,7 +208,10 @@ __global__ void __launch_bounds__(kLinThreads) linear_skinny_kernel(const LinArg
 template <int RB, int MB>
 void launch_linear(const LinArgs& a, hipStream_t st) {
     dim3 grid((unsigned)((a.N + 16 * RB - 1) / (16 * RB)), (unsigned)a.KS);
-    if (a.K / a.KS >= 2 * kKC)
+    // 64 rows of x: a 2-stage ring (80 KB of LDS at 16 W rows, 96 KB at 32)
+    if constexpr (MB > 2)
+        hipLaunchKernelGGL((linear_skinny_kernel<RB, MB, 2>), grid, dim3(kLinThreads), 0, st, a);
+    else if (a.K / a.KS >= 2 * kKC)
         hipLaunchKernelGGL((linear_skinny_kernel<RB, MB, 3>), grid, dim3(kLinThreads), 0, st, a);
     else
         hipLaunchKernelGGL((linear_skinny_kernel<RB, MB, 2>), grid, dim3(kLinThreads), 0, st, a);
@@ -419,7 +424,7 @@ extern "C" int mtl_linear_skinny(const float* x, int64_t x_rs, const float* W, c
                                  int32_t rows_per_block, mtl_stream_t stream) {
     clear_error();
     MTL_REQUIRE(x && W && y, "null pointer");
-    MTL_REQUIRE(M >= 1 && M <= 32, "M (rows of x) must be in [1, 32]");
+    MTL_REQUIRE(M >= 1 && M <= 64, "M (rows of x) must be in [1, 64]");
     MTL_REQUIRE(N >= 1 && N % 4 == 0 && N < (int64_t(1) << 31), "N must be a positive multiple of 4");
     MTL_REQUIRE(ksplit >= 1 && ksplit <= 64, "ksplit must be in [1, 64]");
     MTL_REQUIRE(K >= 1 && K % (int64_t(kKC) * ksplit) == 0 && K < (int64_t(1) << 31),
@@ -432,11 +437,15 @@ extern "C" int mtl_linear_skinny(const float* x, int64_t x_rs, const float* W, c
     MTL_REQUIRE(y_ks % 4 == 0, "y_ks must be a multiple of 4");
     LinArgs a{x, W, bias, y, x_rs, y_rs, y_ks, (int)M, (int)N, (int)K, (int)ksplit};
     hipStream_t st = as_stream(stream);
-    const bool two_m = M > 16;
+    // 16-row MFMA blocks of x: 1, 2 or 4
     if (rows_per_block == 32) {
-        if (two_m) launch_linear<2, 2>(a, st); else launch_linear<2, 1>(a, st);
+        if (M > 32) launch_linear<2, 4>(a, st);
+        else if (M > 16) launch_linear<2, 2>(a, st);
+        else launch_linear<2, 1>(a, st);
     } else {
-        if (two_m) launch_linear<1, 2>(a, st); else launch_linear<1, 1>(a, st);
+        if (M > 32) launch_linear<1, 4>(a, st);
+        else if (M > 16) launch_linear<1, 2>(a, st);
+        else launch_linear<1, 1>(a, st);
     }
     return check_launch("linear_skinny_kernel");
 }

@@ -146,6 +146,33 @@ SMALL_PREFILL_BLAS: str | None = "cublas"
 # out_proj as this many split-K parts.
 SKINNY_OUT_SPLIT = 4
 
+# A prefill of at most 64 tokens (b l rows of the projections, fp32) runs
+# in_proj, x_proj and out_proj on mtl_linear_skinny as well: in_proj whole,
+# x_proj (few weight rows) split over K into up to 16 parts that
+# mtl_sum_parts adds, and, inside MambaLM.prefill, out_proj as
+# SKINNY_OUT_SPLIT parts that the residual add sums.  The tied lm_head stays
+# on the library GEMM (faster at 64 x 50280 x 768: 66 against 69 us).  An
+# eager MambaLM.prefill that takes the host-light rocBLAS path
+# (SMALL_PREFILL_BLAS) keeps the library GEMMs there as well: that path is
+# bound by host time per launch, which the split x_proj adds to.
+_SKINNY_PREFILL = True
+
+
+def _skinny_rows(x: torch.Tensor, w: torch.Tensor, enabled: bool = True) -> torch.Tensor | None:
+    """x [..., K] as the [rows, K] operand of mtl_linear_skinny, or None
+    where it does not apply."""
+    if not (enabled and _SKINNY_PREFILL) or not x.is_contiguous():
+        return None
+    x2 = x.reshape(-1, x.shape[-1])
+    return x2 if ops.linear_skinny_ok(x2, w) else None
+
+
+def _skinny_split(K: int, most: int = 16) -> int:
+    """The largest split of K into ranges of whole 128-column granules, at
+    most `most` parts."""
+    g = K // 128
+    return max(p for p in range(1, min(g, most) + 1) if g % p == 0)
+
 # column parts of the fused step's stand-alone x_proj GEMV
 _XPROJ_PARTS = 4
 
@@ -246,6 +273,13 @@ class MambaMixer(nn.Module):
         as the initial state and never written; new state tensors are returned,
         or, with `out` (a preallocated LayerCache, which may be `cache` itself),
         the final states are written into out's tensors and those are returned."""
+        return self._prefill(x, cache, out, parts_ok=False)
+
+    def _prefill(self, x: torch.Tensor, cache: LayerCache | None, out: LayerCache | None, parts_ok: bool,
+                 skinny: bool = True):
+        """prefill(); with parts_ok, out_proj of a short prefill may come back
+        as _Parts (split-K partial products for the residual add to sum);
+        skinny=False keeps every projection on torch's GEMMs."""
         b, l, _ = x.shape
         Dm, N, R, K = self.cfg.d_inner, self.cfg.d_state, self.cfg.dt_rank, self.cfg.d_conv
         if out is not None:
@@ -263,7 +297,9 @@ class MambaMixer(nn.Module):
             xs = F.linear(x, w_in[:Dm], b_in[:Dm] if b_in is not None else None).transpose(1, 2)   # [b, D, l]
             z = F.linear(x, w_in[Dm:], b_in[Dm:] if b_in is not None else None).transpose(1, 2)
         else:
-            xz = self.in_proj(x)                                 # [b, l, 2D]
+            x2 = _skinny_rows(x, self.in_proj.weight, skinny)
+            xz = (ops.linear_skinny(x2, self.in_proj.weight, self.in_proj.bias).view(b, l, 2 * Dm) if x2 is not None
+                  else self.in_proj(x))                          # [b, l, 2D]
             xs = xz[..., :Dm].transpose(1, 2)                    # [b, D, l] view, D-stride 1
             z = xz[..., Dm:].transpose(1, 2)
         conv_in_state = cache.conv_state if cache is not None else None
@@ -278,7 +314,13 @@ class MambaMixer(nn.Module):
                                           silu=True, out=u_store.transpose(1, 2),
                                           final_state=out.conv_state if out is not None else None)
         w_x = self.x_proj.weight
-        x_dbl = F.linear(u_store, w_x)                            # [b, l, R+2N]
+        u2 = _skinny_rows(u_store, w_x, skinny)
+        if u2 is not None:
+            ks = _skinny_split(Dm)
+            x_dbl = ops.linear_skinny(u2, w_x, ksplit=ks)
+            x_dbl = (ops.sum_parts(x_dbl) if ks > 1 else x_dbl).view(b, l, -1)
+        else:
+            x_dbl = F.linear(u_store, w_x)                        # [b, l, R+2N]
         dt_low = x_dbl[..., :R]
         if split:
             # B and C copied out of x_dbl into contiguous [b, l, N] (2 * b*l*N
@@ -298,8 +340,14 @@ class MambaMixer(nn.Module):
         _, h = ops.selective_scan(u, dt.transpose(1, 2), _f32(self.A_log), B, C, D=_f32(self.D), z=z,
                                   delta_bias=_f32(self.dt_proj.bias), h0=h0, delta_softplus=True, a_is_log=True,
                                   y=y_store.transpose(1, 2), h_out=out.ssm_state if out is not None else None)
-        y_out = self.out_proj(y_store)
-        return y_out, conv_state, h if out is not None else h.to(_state_dtype(x.dtype))
+        h = h if out is not None else h.to(_state_dtype(x.dtype))
+        if parts_ok:
+            w_out = self.out_proj.weight
+            y2 = _skinny_rows(y_store, w_out, skinny)
+            if y2 is not None and Dm % (128 * SKINNY_OUT_SPLIT) == 0:
+                parts = ops.linear_skinny(y2, w_out, self.out_proj.bias, ksplit=SKINNY_OUT_SPLIT)
+                return _Parts(parts.view(SKINNY_OUT_SPLIT, b, l, -1)), conv_state, h
+        return self.out_proj(y_store), conv_state, h
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         """No-cache forward (reference model.py:243-246)."""
@@ -463,14 +511,16 @@ class MambaLM(nn.Module):
         if out_cache is not None and len(out_cache.layers) != len(self.layers):
             raise ValueError("out_cache has the wrong number of layers")
 
+        small = input_ids.numel() <= SMALL_PREFILL_TOKENS and not torch.cuda.is_current_stream_capturing()
+        host_bound = small and SMALL_PREFILL_BLAS is not None
+
         def layer(i, xn):
             lc = cache.layers[i] if cache is not None else None
             oc = out_cache.layers[i] if out_cache is not None else None
-            y, cs, hs = self.layers[i].mixer.prefill(xn, lc, oc)
+            y, cs, hs = self.layers[i].mixer._prefill(xn, lc, oc, parts_ok=True, skinny=not host_bound)
             new_layers.append(LayerCache(conv_state=cs, ssm_state=hs))
             return y
 
-        small = input_ids.numel() <= SMALL_PREFILL_TOKENS and not torch.cuda.is_current_stream_capturing()
         with _prefer_blas(SMALL_PREFILL_BLAS if small else None):
             xf = self._run(x, layer)
         return self.lm_head(xf), (out_cache if out_cache is not None else MambaCache(new_layers))

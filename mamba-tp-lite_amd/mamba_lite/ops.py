@@ -295,7 +295,7 @@ def in_proj_conv_xproj_ok(x, W_in, conv_state, d_conv, J) -> bool:
         return False
     b, M = x.shape
     D = W_in.shape[0] // 2
-    return (x.is_cuda and 1 <= b <= SKINNY_MAX_ROWS and M >= 256 and M % 128 == 0 and W_in.shape == (2 * D, M)
+    return (x.is_cuda and 1 <= b <= IN_CONV_MAX_ROWS and M >= 256 and M % 128 == 0 and W_in.shape == (2 * D, M)
             and D % 16 == 0 and 2 <= d_conv <= 4 and 1 <= J <= 288 and x.stride(1) == 1 and x.stride(0) % 4 == 0
             and W_in.is_contiguous() and x.data_ptr() % 16 == 0 and W_in.data_ptr() % 16 == 0
             and conv_state.dtype == torch.float32 and conv_state.is_contiguous()
@@ -545,12 +545,13 @@ def decode_gemv(v, W, out, bias=None, x_in=None):
     return out
 
 
-SKINNY_MAX_ROWS = 32
+SKINNY_MAX_ROWS = 64     # mtl_linear_skinny: rows of x
+IN_CONV_MAX_ROWS = 32    # mtl_in_proj_conv_xproj: batch rows
 
 
 def linear_skinny_ok(x, W) -> bool:
     """Whether mtl_linear_skinny takes y = x W^T for these operands: fp32 on
-    the GPU, 1..32 rows of x, K a multiple of 128, W rows a multiple of 4,
+    the GPU, 1..64 rows of x, K a multiple of 128, W rows a multiple of 4,
     16-byte aligned rows."""
     if x.dim() != 2 or W.dim() != 2 or x.dtype != torch.float32 or W.dtype != torch.float32:
         return False
@@ -563,11 +564,12 @@ def linear_skinny_ok(x, W) -> bool:
 
 def linear_skinny(x, W, bias=None, out=None, ksplit=1, rows_per_block=None):
     """mtl_linear_skinny: out [M, N] = x [M, K] . W [N, K]^T (+ bias) on the
-    matrix cores, for M <= 32 (the projections of a batched decode step).
+    matrix cores, for M <= 64 (the projections of a batched decode step,
+    and of a prefill of at most 64 tokens).
     With ksplit > 1, out is [ksplit, M, N]: the partial products over K
     split into ksplit equal ranges (bias in part 0), to be added in order."""
     if not linear_skinny_ok(x, W):
-        raise ValueError("linear_skinny: fp32 x [M<=32, K%128==0] (unit column stride, 16B rows) and contiguous "
+        raise ValueError("linear_skinny: fp32 x [M<=64, K%128==0] (unit column stride, 16B rows) and contiguous "
                          "W [N%4==0, K] expected")
     M, K = x.shape
     N = W.shape[0]
@@ -583,7 +585,8 @@ def linear_skinny(x, W, bias=None, out=None, ksplit=1, rows_per_block=None):
     if rows_per_block is None:
         # 32-row tiles halve the re-reads of x where they still give every CU
         # a workgroup; at 16 rows or fewer of x the 16-row tiles stream faster
-        rows_per_block = 32 if M > 16 and (N + 31) // 32 * ksplit >= 256 else 16
+        # (past 32 rows of x, 32-row tiles need 96 KB of LDS: one workgroup per CU)
+        rows_per_block = 32 if 16 < M <= 32 and (N + 31) // 32 * ksplit >= 256 else 16
     _same_device(x, W, bias, out)
     with _dev_guard(x):
         _lib.check(_lib.load().mtl_linear_skinny(_ptr(x), x.stride(0), _ptr(W), _ptr(bias), _ptr(out), N, M * N,

@@ -92,7 +92,7 @@ def test_invalid_arguments_are_rejected_without_a_gpu():
     ("mtl_decode_gemv_parts", dict(cols=4100, nparts=4), b"multiple of 4 * nparts"),
     ("mtl_decode_gemv_parts", dict(cols=8192 * 4, nparts=4), b"at most 4096"),
     ("mtl_decode_gemv_parts", dict(batch=3), b"batch must be 1, 2 or 4"),
-    ("mtl_linear_skinny", dict(M=33), b"M (rows of x)"),
+    ("mtl_linear_skinny", dict(M=65), b"M (rows of x)"),
     ("mtl_linear_skinny", dict(M=0), b"M (rows of x)"),
     ("mtl_linear_skinny", dict(K=96), b"multiple of 128"),
     ("mtl_linear_skinny", dict(K=256, ksplit=4), b"multiple of 128 * ksplit"),

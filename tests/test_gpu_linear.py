@@ -1,8 +1,8 @@
 """mtl_linear_skinny (the matrix-core GEMM of the batched decode step's
 projections, model.py:261, 293, 326) against a float64 reference of
 y = x W^T + bias, tolerance 1e-5 relative (to each element plus the output's
-rms): row counts 1..32 (one and two 16-row MFMA blocks), the mamba-130m and
-1.4b projection shapes, both workgroup tilings, K ranges of 1, 2, 3 and more
+rms): row counts 1..64 (one, two and four 16-row MFMA blocks), the mamba-130m and
+1.4b projection shapes (and the 130m prefill's at 64 tokens), both workgroup tilings, K ranges of 1, 2, 3 and more
 32-column stages per wavefront (every branch of the copy pipeline), weight
 row counts that leave a tile partly filled, split K, strided x rows."""
 import pytest
@@ -23,7 +23,8 @@ def _ref(x, W, bias):
 
 @pytest.mark.parametrize("M,N,K", [(1, 64, 128), (5, 3072, 768), (16, 768, 1536), (17, 8192, 2048),
                                    (32, 2048, 4096), (32, 4, 128), (3, 50280, 256), (9, 1000, 384),
-                                   (24, 200, 640)])
+                                   (24, 200, 640), (33, 768, 1536), (48, 80, 1536), (64, 3072, 768),
+                                   (64, 50280, 768), (64, 4, 128), (57, 1000, 384)])
 @pytest.mark.parametrize("rows_per_block", [16, 32])
 @pytest.mark.parametrize("with_bias", [False, True])
 def test_linear_skinny_vs_float64(M, N, K, rows_per_block, with_bias):

@@ -227,6 +227,7 @@ def test_graph_replay_on_the_skinny_gemm_step(batch, monkeypatch):
     steps = [torch.randint(0, 512, (batch, 1), device=DEV) for _ in range(4)]
     with torch.no_grad():
         _, cache_e = model.prefill(ids)
+        calls.clear()                     # the prefill's own projections (<= 64 tokens) run there too
         eager = [model.step(s, cache_e).clone() for s in steps]
         assert "fused" in calls and 4 in calls and 1 not in calls, calls   # fused in_proj, out_proj in 4 parts
         ref_logits, rcache = om.lm_prefill(_lm_weights(model), ids.cpu().numpy(), dtype=np.float64)
@@ -464,3 +465,55 @@ def test_graphed_prefill_replays_match_eager_and_feed_the_stepper():
         mm.SMALL_PREFILL_BLAS = orig
     with pytest.raises(ValueError):
         gp.replay(torch.zeros(b, l + 1, dtype=torch.long, device=DEV))
+
+
+@pytest.mark.parametrize("b,l", [(1, 64), (2, 20), (1, 17), (1, 1)])
+def test_short_prefill_on_the_skinny_gemm_vs_oracle(b, l, monkeypatch):
+    """A prefill of at most 64 tokens at a width whose projections all fit
+    mtl_linear_skinny (K a multiple of 128): in_proj whole, x_proj split over
+    K and summed, out_proj as 4 parts summed by the residual add.  Logits and
+    final states against the float64 oracle at 1e-4, and against the same
+    prefill on torch's GEMMs at 1e-5; the mixer's own prefill (out_proj as
+    one tensor) against the oracle's mixer.  The skinny GEMMs run where a
+    captured prefill runs them (SMALL_PREFILL_BLAS off); an eager prefill on
+    the host-light rocBLAS path keeps the library GEMMs."""
+    import mamba_lite.model as mm
+    from mamba_lite import ops as mops
+    monkeypatch.setattr(mm, "SMALL_PREFILL_BLAS", None)
+    torch.manual_seed(11)
+    cfg = MambaConfig(d_model=256, n_layer=2, vocab_size=384, d_state=16)
+    with torch.device(DEV):
+        model = MambaLM(cfg).eval()
+    ids = torch.randint(0, cfg.vocab_size, (b, l), device=DEV)
+    calls = []
+    real = mops.linear_skinny
+    monkeypatch.setattr(mops, "linear_skinny", lambda *a, **k: calls.append(a[0].shape) or real(*a, **k))
+    with torch.no_grad():
+        logits, cache = model.prefill(ids)
+    assert all(s[0] == b * l for s in calls) and len(calls) == 3 * cfg.n_layer, calls
+    ref, rcache = om.lm_prefill(_lm_weights(model), ids.cpu().numpy(), dtype=np.float64)
+    assert_rel(logits.cpu().numpy(), ref, 1e-4, "logits")
+    for lc, (rc, rh) in zip(cache.layers, rcache):
+        assert_rel(lc.conv_state.cpu().numpy(), rc, 1e-4, "conv_state")
+        assert_rel(lc.ssm_state.cpu().numpy(), rh, 1e-4, "ssm_state")
+    monkeypatch.setattr(mm, "_SKINNY_PREFILL", False)
+    with torch.no_grad():
+        logits2, _ = model.prefill(ids)
+    assert_rel(logits.cpu().numpy(), logits2.cpu().numpy(), 1e-5, "skinny vs torch GEMMs")
+    monkeypatch.setattr(mm, "_SKINNY_PREFILL", True)
+    monkeypatch.setattr(mm, "SMALL_PREFILL_BLAS", "cublas")
+    calls.clear()
+    with torch.no_grad():
+        logits3, _ = model.prefill(ids)
+    assert calls == [], calls
+    assert_rel(logits3.cpu().numpy(), ref, 1e-4, "logits on the rocBLAS path")
+    monkeypatch.setattr(mm, "_SKINNY_PREFILL", True)
+    mx = model.layers[0].mixer
+    xin = torch.randn(b, l, cfg.d_model, device=DEV)
+    with torch.no_grad():
+        y, cs, hs = mx.prefill(xin)
+    w = _lm_weights(model)["layers"][0]
+    ry, rc, rh = om.mixer_prefill(w, xin.double().cpu().numpy(), None, None, np.float64)
+    assert isinstance(y, torch.Tensor) and y.shape == (b, l, cfg.d_model)
+    assert_rel(y.cpu().numpy(), ry, 1e-4, "mixer out")
+    assert_rel(hs.cpu().numpy(), rh, 1e-4, "mixer ssm_state")
