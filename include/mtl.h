@@ -226,6 +226,22 @@ int mtl_add_rmsnorm_parts(const float* x, const float* y_parts, int32_t nparts, 
 int mtl_sum_parts(const float* parts, int32_t nparts, int64_t n, float* out, mtl_stream_t stream);
 
 /* ------------------------------------------------------------------------
+ * x_proj's split-K parts summed, and dt_proj on the sum, in one launch
+ * (model.py:214-216 of MambaMixer.prefill, dt_proj without its bias, which
+ * the scan adds):
+ *   x_dbl[r][j] = ((parts[0][r][j] + parts[1][r][j]) + ...)   (part order,
+ *                 as mtl_sum_parts for nparts <= 32),
+ *   dt[r][c]    = sum over k < R, in order, of x_dbl[r][k] W_dt[c][k].
+ * parts: contiguous [nparts, rows, J] (x_proj of rows tokens by
+ * mtl_linear_skinny with ksplit = nparts); W_dt: contiguous [D, R], R <=
+ * min(J, 160); x_dbl: [rows, J] contiguous, or NULL to skip writing it
+ * (with nparts = 1 the caller reads parts itself); dt: [rows, D]
+ * contiguous.  1 <= nparts <= 16.  Deterministic.
+ * ---------------------------------------------------------------------- */
+int mtl_xproj_sum_dt(const float* parts, int32_t nparts, int64_t rows, int32_t J, const float* W_dt, int32_t R,
+                     int64_t D, float* x_dbl, float* dt, mtl_stream_t stream);
+
+/* ------------------------------------------------------------------------
  * Per-token int8 quantize -> dequantize-sum of an AllReduce payload,
  * local (the collective replaced by nparts partials resident on one GPU).
  * Replaces tp_utils.py:103-131 (_int8_gather, per_token=True, reached via

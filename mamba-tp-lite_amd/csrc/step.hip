@@ -176,6 +176,103 @@ __global__ void __launch_bounds__(256) sum_parts_kernel(const float* __restrict_
     if (i < n) out[i] = s;
 }
 
+// x_proj's split-K parts of a short prefill summed, with dt_proj applied to
+// the sum (model.py:214-216 without the bias, which the scan adds):
+//   x_dbl[r][j] = parts[0][r][j] + parts[1][r][j] + ... (part order, as
+//                 sum_parts_kernel adds them),
+//   dt[r][c]    = sum_{k < R} x_dbl[r][k] W_dt[c][k]   (k in order).
+// One workgroup per 64 channels x 4 rows.  It sums the dt_low columns of its
+// rows into LDS (workgroups of the first channel tile sum all J columns and
+// write x_dbl) and copies its 64 W_dt rows -- one contiguous block of 64 R
+// floats -- into LDS transposed; then wavefront w takes row w and lane l
+// channel l: a W_dt read per k that is conflict-free across the lanes and a
+// broadcast read of dt_low.  The loads are issued before their first use
+// (W_dt's first batch, then up to PMAX parts per element for 3 elements per
+// thread), so the workgroup waits for memory once.  Two launches (the sum
+// and a library GEMM of K = R) become one.
+constexpr int kXdCh = 64, kXdRows = 4, kXdMaxR = 160, kXdMaxParts = 16;
+template <int PMAX>
+__global__ void __launch_bounds__(256) xproj_sum_dt_kernel(const float* __restrict__ parts, int nparts, int rows,
+                                                           int J, int R, const float* __restrict__ Wdt, int D,
+                                                           float* __restrict__ xdbl, float* __restrict__ dt) {
+    __shared__ float s_lo[kXdRows][kXdMaxR + 1];
+    __shared__ float s_w[kXdMaxR][kXdCh + 1];
+    const int tid = threadIdx.x;
+    const int c0 = blockIdx.x * kXdCh, r0 = blockIdx.y * kXdRows;
+    const int64_t n = (int64_t)rows * J;
+    // the rows' x_dbl columns: all J in the first channel tile, else the R of dt_low
+    const int cols = (blockIdx.x == 0 && xdbl) ? J : R;
+    const int ne = kXdRows * cols;
+    const int nch = min(kXdCh, D - c0);
+    const int nw = nch * R;
+    const float* wb = Wdt + (int64_t)c0 * R;
+    constexpr int QE = 3, QW = 16;
+    // W_dt in batches of QW per thread (one batch covers R <= 64); the first
+    // batch's loads go out ahead of the parts' loads
+    float w[QW];
+    auto load_w = [&](int e0) __attribute__((always_inline)) {
+#pragma unroll
+        for (int q = 0; q < QW; ++q) w[q] = wb[min(e0 + tid + q * 256, nw - 1)];
+    };
+    auto store_w = [&](int e0) __attribute__((always_inline)) {
+#pragma unroll
+        for (int q = 0; q < QW; ++q) {
+            const int e = e0 + tid + q * 256;
+            if (e < nw) {
+                const int c = e / R, k = e - c * R;
+                s_w[k][c] = w[q];
+            }
+        }
+    };
+    load_w(0);
+    for (int e0 = 0; e0 < ne; e0 += QE * 256) {
+        float v[QE][PMAX];
+        int64_t idx[QE];
+#pragma unroll
+        for (int q = 0; q < QE; ++q) {
+            const int e = min(e0 + tid + q * 256, ne - 1);
+            const int rl = e / cols, j = e - rl * cols;
+            idx[q] = (int64_t)min(r0 + rl, rows - 1) * J + j;
+#pragma unroll
+            for (int p = 0; p < PMAX; ++p) v[q][p] = parts[min(p, nparts - 1) * n + idx[q]];
+        }
+#pragma unroll
+        for (int q = 0; q < QE; ++q) {
+            const int e = e0 + tid + q * 256;
+            float acc = v[q][0];
+#pragma unroll
+            for (int p = 1; p < PMAX; ++p) acc = p < nparts ? acc + v[q][p] : acc;
+            if (e < ne) {
+                const int rl = e / cols, j = e - rl * cols;
+                if (j < R) s_lo[rl][j] = acc;
+                if (cols == J && r0 + rl < rows) xdbl[idx[q]] = acc;
+            }
+        }
+    }
+    store_w(0);
+    for (int e0 = QW * 256; e0 < nw; e0 += QW * 256) {
+        load_w(e0);
+        store_w(e0);
+    }
+    __syncthreads();
+    // dt: k in order; LDS reads 8 k at a time ahead of their fmas
+    const int c = tid & (kXdCh - 1), rl = tid >> 6;
+    float acc = 0.f;
+    int k = 0;
+    for (; k + 8 <= R; k += 8) {
+        float a[8], b[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            a[u] = s_lo[rl][k + u];
+            b[u] = s_w[k + u][c];
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) acc = fmaf(a[u], b[u], acc);
+    }
+    for (; k < R; ++k) acc = fmaf(s_lo[rl][k], s_w[k][c], acc);
+    if (c < nch && r0 + rl < rows) dt[(int64_t)(r0 + rl) * D + c0 + c] = acc;
+}
+
 constexpr int kNormThreads = 256;
 
 // One workgroup per row.  RUNS elements per thread (cols <= 256 RUNS),
@@ -509,6 +606,32 @@ extern "C" int mtl_add_rmsnorm_parts(const float* x, const float* y_parts, int32
     if (rows == 0) return MTL_OK;
     MTL_REQUIRE(x && y_parts && w && normed, "null required pointer");
     return add_rmsnorm_launch(x, y_parts, nparts, rows * cols, x_out, w, normed, rows, cols, eps, as_stream(stream));
+}
+
+extern "C" int mtl_xproj_sum_dt(const float* parts, int32_t nparts, int64_t rows, int32_t J, const float* W_dt,
+                                int32_t R, int64_t D, float* x_dbl, float* dt, mtl_stream_t stream) {
+    using namespace mtl;
+    clear_error();
+    MTL_REQUIRE(nparts >= 1 && nparts <= kXdMaxParts, "nparts must be in [1, 16]");
+    MTL_REQUIRE(rows >= 0 && rows < (int64_t(1) << 24), "rows out of range");
+    MTL_REQUIRE(R >= 1 && R <= kXdMaxR && J >= R, "dt_rank must be in [1, 160] and at most J");
+    MTL_REQUIRE(D >= 1 && D < (int64_t(1) << 24), "d_inner out of range");
+    MTL_REQUIRE((int64_t)rows * J * nparts < (int64_t(1) << 31), "parts too large");
+    if (rows == 0) return MTL_OK;
+    MTL_REQUIRE(parts && W_dt && dt, "null required pointer");
+    MTL_REQUIRE(nparts > 1 || x_dbl == nullptr || x_dbl != parts, "x_dbl must not alias parts");
+    const dim3 grid((unsigned)((D + kXdCh - 1) / kXdCh), (unsigned)((rows + kXdRows - 1) / kXdRows));
+    hipStream_t st = as_stream(stream);
+    if (nparts <= 4)
+        hipLaunchKernelGGL((xproj_sum_dt_kernel<4>), grid, dim3(256), 0, st, parts, nparts, (int)rows, J, R, W_dt,
+                           (int)D, x_dbl, dt);
+    else if (nparts <= 8)
+        hipLaunchKernelGGL((xproj_sum_dt_kernel<8>), grid, dim3(256), 0, st, parts, nparts, (int)rows, J, R, W_dt,
+                           (int)D, x_dbl, dt);
+    else
+        hipLaunchKernelGGL((xproj_sum_dt_kernel<16>), grid, dim3(256), 0, st, parts, nparts, (int)rows, J, R, W_dt,
+                           (int)D, x_dbl, dt);
+    return check_launch("xproj_sum_dt");
 }
 
 extern "C" int mtl_sum_parts(const float* parts, int32_t nparts, int64_t n, float* out, mtl_stream_t stream) {

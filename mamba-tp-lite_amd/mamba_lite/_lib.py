@@ -64,6 +64,7 @@ SIGNATURES = {
     "mtl_add_rmsnorm": (ctypes.c_int, [_fp, _fp, _fp, _fp, _fp, _i64, _i64, ctypes.c_float, _vp]),
     "mtl_add_rmsnorm_parts": (ctypes.c_int, [_fp, _fp, _i32, _fp, _fp, _fp, _i64, _i64, ctypes.c_float, _vp]),
     "mtl_sum_parts": (ctypes.c_int, [_fp, _i32, _i64, _fp, _vp]),
+    "mtl_xproj_sum_dt": (ctypes.c_int, [_fp, _i32, _i64, _i32, _fp, _i32, _i64, _fp, _fp, _vp]),
     "mtl_conv_step_xproj": (ctypes.c_int, [_fp, _fp, _i64, _fp, _fp, _fp, _i64, _fp, _fp, _i64, _i64, _i32, _i32,
                                            _vp]),
     "mtl_conv_step_xproj_noalloc": (ctypes.c_int, [_fp, _fp, _i64, _fp, _fp, _fp, _i64, _fp, _fp, _i64, _i64, _i32,

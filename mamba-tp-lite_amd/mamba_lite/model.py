@@ -315,10 +315,18 @@ class MambaMixer(nn.Module):
                                           final_state=out.conv_state if out is not None else None)
         w_x = self.x_proj.weight
         u2 = _skinny_rows(u_store, w_x, skinny)
+        dt = None
         if u2 is not None:
+            # x_proj split over K; its parts summed and dt_proj applied to the
+            # sum in one launch (dt_proj's K = dt_rank is not the skinny GEMM's)
             ks = _skinny_split(Dm)
-            x_dbl = ops.linear_skinny(u2, w_x, ksplit=ks)
-            x_dbl = (ops.sum_parts(x_dbl) if ks > 1 else x_dbl).view(b, l, -1)
+            parts = ops.linear_skinny(u2, w_x, ksplit=ks).view(ks, b * l, -1)
+            if R <= ops.XPROJ_SUM_DT_MAX_R:
+                x_dbl, dt = ops.xproj_sum_dt(parts, self.dt_proj.weight, write_x_dbl=ks > 1)
+                dt = dt.view(b, l, Dm)
+            else:
+                x_dbl = ops.sum_parts(parts) if ks > 1 else parts[0]
+            x_dbl = x_dbl.view(b, l, -1)
         else:
             x_dbl = F.linear(u_store, w_x)                        # [b, l, R+2N]
         dt_low = x_dbl[..., :R]
@@ -331,7 +339,8 @@ class MambaMixer(nn.Module):
         else:
             B = x_dbl[..., R:R + N].transpose(1, 2)               # [b, N, l] view, row stride R+2N
             C = x_dbl[..., R + N:].transpose(1, 2)
-        dt = F.linear(dt_low, self.dt_proj.weight)                # [b, l, D]; bias fused in the scan
+        if dt is None:
+            dt = F.linear(dt_low, self.dt_proj.weight)            # [b, l, D]; bias fused in the scan
         h0 = None
         if cache is not None:
             h0 = cache.ssm_state.float().contiguous()

@@ -423,6 +423,39 @@ def sum_parts(parts, out=None):
     return out
 
 
+XPROJ_SUM_DT_MAX_R = 160
+
+
+def xproj_sum_dt(parts, W_dt, x_dbl=None, write_x_dbl=True):
+    """mtl_xproj_sum_dt: parts [P, rows, J] (x_proj split over K) ->
+    (x_dbl [rows, J] = the parts summed in order, dt [rows, D] = x_dbl[:, :R]
+    . W_dt^T), one launch.  With P = 1 and write_x_dbl False, x_dbl is
+    parts[0] itself."""
+    _f32c(parts, "parts")
+    _f32c(W_dt, "W_dt")
+    if parts.dim() != 3 or W_dt.dim() != 2:
+        raise ValueError("xproj_sum_dt: parts [P, rows, J] and W_dt [D, R] expected")
+    P, rows, J = parts.shape
+    D, R = W_dt.shape
+    if not 1 <= R <= min(J, XPROJ_SUM_DT_MAX_R):
+        raise ValueError(f"xproj_sum_dt: dt_rank must be in [1, min(J, {XPROJ_SUM_DT_MAX_R})]")
+    if not write_x_dbl and P != 1:
+        raise ValueError("xproj_sum_dt: x_dbl is written unless there is one part")
+    if write_x_dbl:
+        if x_dbl is None:
+            x_dbl = torch.empty(rows, J, device=parts.device, dtype=torch.float32)
+        _f32c(x_dbl, "x_dbl")
+        if tuple(x_dbl.shape) != (rows, J):
+            raise ValueError(f"xproj_sum_dt: x_dbl must be {(rows, J)}")
+    dt = torch.empty(rows, D, device=parts.device, dtype=torch.float32)
+    _same_device(parts, W_dt, x_dbl)
+    with _dev_guard(parts):
+        _lib.check(_lib.load().mtl_xproj_sum_dt(_ptr(parts), P, rows, J, _ptr(W_dt), R, D,
+                                                _ptr(x_dbl) if write_x_dbl else None, _ptr(dt), _stream(parts)),
+                   "xproj_sum_dt")
+    return (x_dbl if write_x_dbl else parts[0]), dt
+
+
 def _parts_array(parts):
     arr = (ctypes.c_void_p * len(parts))(*[p.data_ptr() for p in parts])
     return ctypes.cast(arr, ctypes.POINTER(ctypes.c_void_p)), arr

@@ -93,6 +93,9 @@ def test_invalid_arguments_are_rejected_without_a_gpu():
     ("mtl_decode_gemv_parts", dict(cols=8192 * 4, nparts=4), b"at most 4096"),
     ("mtl_decode_gemv_parts", dict(batch=3), b"batch must be 1, 2 or 4"),
     ("mtl_linear_skinny", dict(M=65), b"M (rows of x)"),
+    ("mtl_xproj_sum_dt", dict(R=161), b"dt_rank"),
+    ("mtl_xproj_sum_dt", dict(R=90, J=80), b"dt_rank"),
+    ("mtl_xproj_sum_dt", dict(nparts=0), b"nparts"),
     ("mtl_linear_skinny", dict(M=0), b"M (rows of x)"),
     ("mtl_linear_skinny", dict(K=96), b"multiple of 128"),
     ("mtl_linear_skinny", dict(K=256, ksplit=4), b"multiple of 128 * ksplit"),
@@ -154,6 +157,10 @@ def test_entry_points_validate_sizes_on_the_host(case):
         a = dict(batch=1, rows=8, cols=4096, nparts=4)
         a.update(over)
         rc = lib.mtl_decode_gemv_parts(P, P, P, a["batch"], a["rows"], a["cols"], a["nparts"], None)
+    elif name == "mtl_xproj_sum_dt":
+        a = dict(nparts=4, rows=64, J=80, R=48, D=1536)
+        a.update(over)
+        rc = lib.mtl_xproj_sum_dt(P, a["nparts"], a["rows"], a["J"], P, a["R"], a["D"], P, P, None)
     elif name == "mtl_linear_skinny":
         a = dict(M=8, N=64, K=128, ksplit=1, rows_per_block=16, y_ks=0)
         a.update(over)

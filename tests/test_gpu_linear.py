@@ -69,3 +69,24 @@ def test_linear_skinny_strided_rows_and_repeatability():
     y2 = ops.linear_skinny(x, W)
     assert torch.equal(y1, y2)
     assert_rel(y1.cpu().numpy(), _ref(x, W, None), TOL, "y")
+
+
+@pytest.mark.parametrize("P,rows,J,R,D", [(12, 64, 80, 48, 1536), (4, 37, 160, 128, 4096), (1, 5, 36, 4, 128),
+                                          (16, 64, 192, 160, 5120), (3, 17, 50, 7, 100)])
+def test_xproj_sum_dt_vs_float64(P, rows, J, R, D):
+    """mtl_xproj_sum_dt (x_proj's split-K parts summed, dt_proj on the sum,
+    one launch): x_dbl bit for bit against mtl_sum_parts (same part order),
+    dt against float64 at 1e-5; the mamba-130m, 1.4b and 2.8b widths, a
+    single part, ragged row and channel counts."""
+    print(f"\n[xproj_sum_dt P={P} rows={rows} J={J} R={R} D={D}]", flush=True)
+    g = torch.Generator(device=DEV).manual_seed(P * 31 + rows + D)
+    parts = torch.randn(P, rows, J, device=DEV, generator=g)
+    W_dt = torch.randn(D, R, device=DEV, generator=g) / R ** 0.5
+    x_dbl, dt = ops.xproj_sum_dt(parts, W_dt)
+    ref_x = ops.sum_parts(parts) if P > 1 else parts[0]
+    assert torch.equal(x_dbl, ref_x)
+    ref_dt = parts.double().sum(0)[:, :R].cpu() @ W_dt.double().cpu().T
+    assert_rel(dt.cpu().numpy(), ref_dt.numpy(), TOL, "dt")
+    if P == 1:
+        x1, dt1 = ops.xproj_sum_dt(parts, W_dt, write_x_dbl=False)
+        assert x1.data_ptr() == parts.data_ptr() and torch.equal(dt1, dt)
