@@ -289,6 +289,23 @@ int mtl_linear_skinny(const float* x, int64_t x_rs, const float* W, const float*
                       mtl_stream_t stream);
 
 /* ------------------------------------------------------------------------
+ * A short prefill's in_proj with the causal conv + SiLU in one launch
+ * (MambaMixer.prefill, model.py:197-212), fp32, batch * seqlen <= 64 token
+ * rows.  x: [batch * seqlen, d_model] (row m = token m % seqlen of batch row
+ * m / seqlen; row stride x_rs); W_in: [2 d_inner, d_model] contiguous; b_in:
+ * [2 d_inner] or NULL; conv_w: [d_inner, d_conv]; conv_b: [d_inner] or NULL;
+ * conv_state_in: [batch, d_inner, d_conv - 1] incoming history, or NULL for
+ * zeros.  Writes u [batch * seqlen, d_inner] = SiLU(causal depthwise conv of
+ * the x half + conv_b), z [batch * seqlen, d_inner] = the z half, and
+ * conv_state_out [batch, d_inner, d_conv - 1] = the last d_conv - 1 conv
+ * inputs (model.py:212), which must not alias conv_state_in.  The conv sums
+ * its taps in order and adds the bias last, as mtl_causal_conv1d_fwd does,
+ * and the in_proj product is mtl_linear_skinny's, so u, z and the state
+ * equal those two launches' bit for bit.  d_model a multiple of 128;
+ * d_inner a multiple of 16; d_conv 2, 3 or 4; x, W_in, b_in, z 16-byte
+ * aligned.  Deterministic.
+ * ---------------------------------------------------------------------- */
+/* ------------------------------------------------------------------------
  * A batched step's in_proj, conv step and x_proj partials in one launch:
  * model.py:261 (xz = in_proj(x)), 264-277 (conv step + SiLU of the x half,
  * the history shifted in place) and 279 (x_dbl = x_proj(xc)) for b <= 32
@@ -310,6 +327,10 @@ int mtl_linear_skinny(const float* x, int64_t x_rs, const float* W, const float*
  * conv_state, conv_w, conv_b, xc and z 16-byte aligned.  Deterministic.
  * Replaces mtl_linear_skinny (in_proj) + mtl_conv_step_xproj in the step.
  * ---------------------------------------------------------------------- */
+int mtl_in_proj_conv_prefill(const float* x, int64_t x_rs, const float* W_in, const float* b_in, const float* conv_w,
+                             const float* conv_b, int32_t d_conv, const float* conv_state_in, float* conv_state_out,
+                             float* u, float* z, int64_t batch, int64_t seqlen, int64_t d_model, int64_t d_inner,
+                             mtl_stream_t stream);
 int mtl_in_proj_conv_xproj(const float* x, int64_t x_rs, const float* W_in, const float* b_in, float* conv_state,
                            const float* conv_w, const float* conv_b, int32_t d_conv, const float* W_xT, int32_t J,
                            float* xc, float* z, int64_t z_rs, float* xpart, int64_t batch, int64_t d_model,

@@ -392,6 +392,91 @@ __global__ void __launch_bounds__(kLinThreads) in_conv_xproj_kernel(const LinArg
     }
 }
 
+// ------------------------------------------------------- a short prefill's in_proj + causal conv
+// MambaMixer.prefill's in_proj (model.py:197) for b l <= 64 tokens with, as
+// the x tiles' epilogue, the causal depthwise conv + SiLU and the final conv
+// state (198-212).  Row m of x is token t = m % l of batch row m / l, so a
+// tile holds every token of its 16 RB channels: its in_proj outputs (with
+// the in_proj bias) go to LDS, and pair (m, channel) takes the window of the
+// K - 1 tokens before t (from the tile, or, before the first token, from the
+// incoming history, or zeros) and t itself:
+//   u[m][c] = SiLU(sum_k window[k] conv_w[c][k] + conv_b[c])   (k in order,
+//   then the bias, as conv_fwd_kernel sums them), and the final history
+//   state_out[b][c][j] = the input at token l - (K - 1) + j (from the
+//   incoming history where that is before the first token).
+// z tiles store z.  Thread t's pairs all have channel t % (16 RB), so its
+// conv weights and bias are loaded once.
+struct PrefillConvArgs {
+    const float* state_in;   // [b, D, K - 1] or null (zeros)
+    float* state_out;        // [b, D, K - 1], not aliasing state_in
+    const float* conv_w;     // [D, K]
+    const float* conv_b;     // [D] or null
+    float* u;                // [b l, D]
+    float* z;                // [b l, D]
+    int D, L;                // L = tokens per batch row
+};
+
+template <int RB, int K>
+__global__ void __launch_bounds__(kLinThreads) in_conv_prefill_kernel(const LinArgs a, const PrefillConvArgs c) {
+    constexpr int MB = 4, DEPTH = 2;
+    constexpr int CB = 16 * RB, XR = 16 * MB;
+    constexpr int RING = ring_floats<RB, MB, DEPTH>();
+    __shared__ __align__(16) float ring[RING];
+    constexpr int kAcc = kLinWaves * RB * MB * 64 * 4;
+    static_assert(kAcc + XR * (CB + 1) <= RING, "epilogue space");
+    static_assert(kLinThreads % CB == 0, "a thread's pairs share one channel");
+    float (*s_x)[CB + 1] = reinterpret_cast<float (*)[CB + 1]>(ring + kAcc);
+    const int tid = threadIdx.x;
+    const int n0 = blockIdx.x * CB;
+    const bool xtile = n0 < c.D;                       // uniform
+
+    skinny_tile<RB, MB, DEPTH>(a, ring, n0, 0);
+
+    for (int t = tid; t < RB * MB * 64; t += kLinThreads) {
+        int m, nl;
+        F4v v = tile_sum<RB, MB>(ring, t, m, nl);
+        if (a.bias) v += ld4(a.bias + n0 + nl);
+        if (!xtile) {
+            if (m < a.M) *reinterpret_cast<F4v*>(c.z + (int64_t)m * c.D + (n0 + nl - c.D)) = v;
+        } else {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) s_x[m][nl + q] = v[q];
+        }
+    }
+    if (!xtile) return;
+    __syncthreads();
+
+    const int cl = tid % CB, ch = n0 + cl;
+    float w[K];
+#pragma unroll
+    for (int k = 0; k < K; ++k) w[k] = c.conv_w[(int64_t)ch * K + k];
+    const float cb = c.conv_b ? c.conv_b[ch] : 0.f;
+    const float* hin = c.state_in;
+    for (int p = tid; p < a.M * CB; p += kLinThreads) {
+        const int m = p / CB;
+        const int bi = m / c.L, tt = m - bi * c.L;
+        float acc = 0.f;
+#pragma unroll
+        for (int k = 0; k < K; ++k) {
+            const int tau = tt - (K - 1) + k;
+            const float xv = tau >= 0 ? s_x[m - (K - 1) + k][cl]
+                                      : (hin ? hin[((int64_t)bi * c.D + ch) * (K - 1) + tau + K - 1] : 0.f);
+            acc = fmaf(w[k], xv, acc);
+        }
+        acc += cb;
+        c.u[(int64_t)m * c.D + ch] = silu_f(acc);
+    }
+    const int nb = a.M / c.L;
+    for (int p = tid; p < nb * CB * (K - 1); p += kLinThreads) {
+        const int j = p % (K - 1), rest = p / (K - 1);
+        const int cj = rest % CB, bi = rest / CB, chj = n0 + cj;
+        const int tau = c.L - (K - 1) + j;
+        const float v = tau >= 0 ? s_x[bi * c.L + tau][cj]
+                                 : (hin ? hin[((int64_t)bi * c.D + chj) * (K - 1) + tau + K - 1] : 0.f);
+        c.state_out[((int64_t)bi * c.D + chj) * (K - 1) + j] = v;
+    }
+}
+
 template <int RB, int MB, int K, int NBJ>
 void launch_in_conv(const LinArgs& a, const InConvArgs& c, hipStream_t st) {
     hipLaunchKernelGGL((in_conv_xproj_kernel<RB, MB, 3, K, NBJ>), dim3((unsigned)(a.N / (16 * RB))),
@@ -448,6 +533,33 @@ extern "C" int mtl_linear_skinny(const float* x, int64_t x_rs, const float* W, c
         else launch_linear<1, 1>(a, st);
     }
     return check_launch("linear_skinny_kernel");
+}
+
+extern "C" int mtl_in_proj_conv_prefill(const float* x, int64_t x_rs, const float* W_in, const float* b_in,
+                                        const float* conv_w, const float* conv_b, int32_t d_conv,
+                                        const float* conv_state_in, float* conv_state_out, float* u, float* z,
+                                        int64_t batch, int64_t seqlen, int64_t d_model, int64_t d_inner,
+                                        mtl_stream_t stream) {
+    clear_error();
+    MTL_REQUIRE(x && W_in && conv_w && conv_state_out && u && z, "null required pointer");
+    MTL_REQUIRE(batch >= 1 && seqlen >= 1 && batch * seqlen <= 64, "batch * seqlen must be in [1, 64]");
+    MTL_REQUIRE(d_model >= kKC && d_model % kKC == 0 && d_model < (int64_t(1) << 30),
+                "d_model must be a positive multiple of 128");
+    MTL_REQUIRE(d_inner >= 16 && d_inner % 16 == 0 && d_inner < (int64_t(1) << 29), "d_inner must be a multiple of 16");
+    MTL_REQUIRE(d_conv >= 2 && d_conv <= 4, "d_conv must be 2, 3 or 4");
+    MTL_REQUIRE(x_rs >= d_model && x_rs % 4 == 0, "x row stride must cover a row and be a multiple of 4");
+    MTL_REQUIRE((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(W_in) | reinterpret_cast<uintptr_t>(b_in) |
+                 reinterpret_cast<uintptr_t>(z)) % 16 == 0, "x, W_in, b_in and z must be 16-byte aligned");
+    MTL_REQUIRE(conv_state_in != conv_state_out, "conv_state_out must not alias conv_state_in");
+    const int64_t M = batch * seqlen;
+    LinArgs a{x, W_in, b_in, nullptr, x_rs, 0, 0, (int)M, (int)(2 * d_inner), (int)d_model, 1};
+    const PrefillConvArgs c{conv_state_in, conv_state_out, conv_w, conv_b, u, z, (int)d_inner, (int)seqlen};
+    const dim3 grid((unsigned)(2 * d_inner / 16));
+    hipStream_t st = as_stream(stream);
+    if (d_conv == 2) hipLaunchKernelGGL((in_conv_prefill_kernel<1, 2>), grid, dim3(kLinThreads), 0, st, a, c);
+    else if (d_conv == 3) hipLaunchKernelGGL((in_conv_prefill_kernel<1, 3>), grid, dim3(kLinThreads), 0, st, a, c);
+    else hipLaunchKernelGGL((in_conv_prefill_kernel<1, 4>), grid, dim3(kLinThreads), 0, st, a, c);
+    return check_launch("in_conv_prefill_kernel");
 }
 
 extern "C" int mtl_in_proj_conv_xproj(const float* x, int64_t x_rs, const float* W_in, const float* b_in,

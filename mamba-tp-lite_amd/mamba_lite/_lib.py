@@ -77,6 +77,8 @@ SIGNATURES = {
     "mtl_decode_gemv": (ctypes.c_int, [_fp, _fp, _fp, _fp, _fp, _i32, _i32, _i32, _vp]),
     "mtl_decode_gemv_parts": (ctypes.c_int, [_fp, _fp, _fp, _i32, _i32, _i32, _i32, _vp]),
     "mtl_linear_skinny": (ctypes.c_int, [_fp, _i64, _fp, _fp, _fp, _i64, _i64, _i64, _i64, _i64, _i32, _i32, _vp]),
+    "mtl_in_proj_conv_prefill": (ctypes.c_int, [_fp, _i64, _fp, _fp, _fp, _fp, _i32, _fp, _fp, _fp, _fp, _i64, _i64,
+                                                _i64, _i64, _vp]),
     "mtl_in_proj_conv_xproj": (ctypes.c_int, [_fp, _i64, _fp, _fp, _fp, _fp, _fp, _i32, _fp, _i32, _fp, _fp, _i64, _fp,
                                               _i64, _i64, _i64, _i32, _vp]),
     "mtl_decode_norm_gemv": (ctypes.c_int, [_fp, _fp, ctypes.c_float, _fp, _fp, _fp, _i32, _i32, _i32, _vp]),

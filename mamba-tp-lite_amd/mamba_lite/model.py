@@ -290,14 +290,18 @@ class MambaMixer(nn.Module):
                     not out.ssm_state.is_contiguous():
                 raise ValueError(f"out.ssm_state must be contiguous float32 {(b, Dm, N)}")
         split = b * l >= SPLIT_PROJ_MIN_TOKENS
-        if split:
+        x2 = None if split else _skinny_rows(x, self.in_proj.weight, skinny)
+        # in_proj with the causal conv as its epilogue (<= 64 tokens)
+        fused_conv = x2 is not None and ops.in_proj_conv_prefill_ok(x2, self.in_proj.weight, K)
+        if fused_conv:
+            xs = z = None
+        elif split:
             # in_proj as two GEMMs (x rows, z rows) so the conv and the scan read
             # whole contiguous [b, l, D] rows rather than halves of [b, l, 2D] rows
             w_in, b_in = self.in_proj.weight, self.in_proj.bias
             xs = F.linear(x, w_in[:Dm], b_in[:Dm] if b_in is not None else None).transpose(1, 2)   # [b, D, l]
             z = F.linear(x, w_in[Dm:], b_in[Dm:] if b_in is not None else None).transpose(1, 2)
         else:
-            x2 = _skinny_rows(x, self.in_proj.weight, skinny)
             xz = (ops.linear_skinny(x2, self.in_proj.weight, self.in_proj.bias).view(b, l, 2 * Dm) if x2 is not None
                   else self.in_proj(x))                          # [b, l, 2D]
             xs = xz[..., :Dm].transpose(1, 2)                    # [b, D, l] view, D-stride 1
@@ -309,10 +313,19 @@ class MambaMixer(nn.Module):
             conv_in_state = conv_in_state.contiguous()
             if out is not None and conv_in_state.data_ptr() == out.conv_state.data_ptr():
                 conv_in_state = conv_in_state.clone()            # the conv reads and writes different runs
-        u_store = torch.empty(b, l, Dm, device=x.device, dtype=x.dtype)
-        u, conv_state = ops.causal_conv1d(xs, self._conv_w(), _f32(self.conv1d.bias), conv_state=conv_in_state,
-                                          silu=True, out=u_store.transpose(1, 2),
-                                          final_state=out.conv_state if out is not None else None)
+        if fused_conv:
+            conv_state = (out.conv_state if out is not None
+                          else torch.empty(b, Dm, K - 1, device=x.device, dtype=torch.float32))
+            u_flat, z_flat = ops.in_proj_conv_prefill(x2, self.in_proj.weight, self.in_proj.bias, self._conv_w(),
+                                                      _f32(self.conv1d.bias), conv_in_state, conv_state, b, l)
+            u_store = u_flat.view(b, l, Dm)
+            u = u_store.transpose(1, 2)                          # [b, D, l] views
+            z = z_flat.view(b, l, Dm).transpose(1, 2)
+        else:
+            u_store = torch.empty(b, l, Dm, device=x.device, dtype=x.dtype)
+            u, conv_state = ops.causal_conv1d(xs, self._conv_w(), _f32(self.conv1d.bias), conv_state=conv_in_state,
+                                              silu=True, out=u_store.transpose(1, 2),
+                                              final_state=out.conv_state if out is not None else None)
         w_x = self.x_proj.weight
         u2 = _skinny_rows(u_store, w_x, skinny)
         dt = None

@@ -287,6 +287,48 @@ def conv_step_xproj(conv_state, x, weight, bias, W_xT, out=None, xpart=None):
     return out, xpart
 
 
+def in_proj_conv_prefill_ok(x2, W_in, d_conv) -> bool:
+    """Whether mtl_in_proj_conv_prefill takes this prefill: fp32 on the GPU,
+    1..64 token rows, d_model a multiple of 128, d_inner a multiple of 16,
+    d_conv 2..4, 16-byte aligned rows."""
+    if x2.dim() != 2 or W_in.dim() != 2 or x2.dtype != torch.float32 or W_in.dtype != torch.float32:
+        return False
+    M, K = x2.shape
+    D = W_in.shape[0] // 2
+    return (x2.is_cuda and 1 <= M <= SKINNY_MAX_ROWS and K % 128 == 0 and W_in.shape == (2 * D, K) and D % 16 == 0
+            and 2 <= d_conv <= 4 and x2.stride(1) == 1 and x2.stride(0) % 4 == 0 and W_in.is_contiguous()
+            and x2.data_ptr() % 16 == 0 and W_in.data_ptr() % 16 == 0)
+
+
+def in_proj_conv_prefill(x2, W_in, b_in, conv_w, conv_b, conv_state_in, conv_state_out, batch, seqlen):
+    """mtl_in_proj_conv_prefill: x2 [b l, d_model] -> (u [b l, D] =
+    SiLU(causal conv of the x half), z [b l, D]); conv_state_out [b, D, K-1]
+    receives the final history (conv_state_in [b, D, K-1] or None: zeros)."""
+    M, K = x2.shape
+    D = W_in.shape[0] // 2
+    Kc = conv_w.shape[-1]
+    if not in_proj_conv_prefill_ok(x2, W_in, Kc) or M != batch * seqlen:
+        raise ValueError("in_proj_conv_prefill: fp32 x [b l <= 64, K%128==0], W_in [2D, K] (D%16==0), d_conv 2..4")
+    _f32_mat(conv_w, (D, Kc), "conv_w")
+    _f32_vec(b_in, 2 * D, "b_in")
+    _f32_vec(conv_b, D, "conv_b")
+    for name, t in (("conv_state_in", conv_state_in), ("conv_state_out", conv_state_out)):
+        if t is not None and (tuple(t.shape) != (batch, D, Kc - 1) or t.dtype != torch.float32
+                              or not t.is_contiguous()):
+            raise ValueError(f"{name} must be contiguous float32 {(batch, D, Kc - 1)}")
+    if conv_state_out is None:
+        raise ValueError("conv_state_out is required")
+    u = torch.empty(M, D, device=x2.device, dtype=torch.float32)
+    z = torch.empty(M, D, device=x2.device, dtype=torch.float32)
+    _same_device(x2, W_in, b_in, conv_w, conv_b, conv_state_in, conv_state_out)
+    with _dev_guard(x2):
+        _lib.check(_lib.load().mtl_in_proj_conv_prefill(_ptr(x2), x2.stride(0), _ptr(W_in), _ptr(b_in), _ptr(conv_w),
+                                                        _ptr(conv_b), Kc, _ptr(conv_state_in), _ptr(conv_state_out),
+                                                        _ptr(u), _ptr(z), batch, seqlen, K, D, _stream(x2)),
+                   "in_proj_conv_prefill")
+    return u, z
+
+
 def in_proj_conv_xproj_ok(x, W_in, conv_state, d_conv, J) -> bool:
     """Whether mtl_in_proj_conv_xproj takes this batched step: fp32 on the
     GPU, 1..32 rows, d_model a multiple of 128 (at least 256), d_conv 2..4,

@@ -93,6 +93,10 @@ def test_invalid_arguments_are_rejected_without_a_gpu():
     ("mtl_decode_gemv_parts", dict(cols=8192 * 4, nparts=4), b"at most 4096"),
     ("mtl_decode_gemv_parts", dict(batch=3), b"batch must be 1, 2 or 4"),
     ("mtl_linear_skinny", dict(M=65), b"M (rows of x)"),
+    ("mtl_in_proj_conv_prefill", dict(batch=5, seqlen=13), b"batch * seqlen"),
+    ("mtl_in_proj_conv_prefill", dict(d_conv=5), b"d_conv"),
+    ("mtl_in_proj_conv_prefill", dict(d_inner=40), b"multiple of 16"),
+    ("mtl_in_proj_conv_prefill", dict(alias=True), b"alias"),
     ("mtl_xproj_sum_dt", dict(R=161), b"dt_rank"),
     ("mtl_xproj_sum_dt", dict(R=90, J=80), b"dt_rank"),
     ("mtl_xproj_sum_dt", dict(nparts=0), b"nparts"),
@@ -157,6 +161,12 @@ def test_entry_points_validate_sizes_on_the_host(case):
         a = dict(batch=1, rows=8, cols=4096, nparts=4)
         a.update(over)
         rc = lib.mtl_decode_gemv_parts(P, P, P, a["batch"], a["rows"], a["cols"], a["nparts"], None)
+    elif name == "mtl_in_proj_conv_prefill":
+        a = dict(batch=1, seqlen=64, d_model=256, d_inner=512, d_conv=4, alias=False)
+        a.update(over)
+        Q = ctypes.c_void_p(32)
+        rc = lib.mtl_in_proj_conv_prefill(P, a["d_model"], P, None, P, None, a["d_conv"], Q if a["alias"] else P, Q,
+                                          P, P, a["batch"], a["seqlen"], a["d_model"], a["d_inner"], None)
     elif name == "mtl_xproj_sum_dt":
         a = dict(nparts=4, rows=64, J=80, R=48, D=1536)
         a.update(over)

@@ -94,3 +94,49 @@ def test_in_proj_conv_xproj_rejects_what_it_does_not_cover():
         ops.in_proj_conv_xproj(x[:, :128].contiguous(), W_in[:, :128].contiguous(), None, state, conv_w, None, W_xT)
     with pytest.raises(ValueError):   # conv history of the wrong width
         ops.in_proj_conv_xproj(x, W_in, None, state[:, :, :2].contiguous(), conv_w, None, W_xT)
+
+
+PREFILL_CASES = [  # b, l, d_model, d_inner, d_conv, with history, biases
+    (1, 64, 768, 1536, 4, False, False),
+    (2, 20, 256, 512, 3, True, False),
+    (4, 16, 128, 64, 2, True, True),
+    (1, 1, 256, 32, 4, True, False),
+    (3, 2, 128, 48, 4, True, True),
+    (64, 1, 256, 96, 4, True, False),
+    (2, 32, 2048, 4096, 4, True, False),
+]
+
+
+@pytest.mark.parametrize("b,l,M,D,K,hist,biases", PREFILL_CASES)
+def test_in_proj_conv_prefill(b, l, M, D, K, hist, biases):
+    """mtl_in_proj_conv_prefill (a short prefill's in_proj with the causal
+    conv + SiLU and the final history as the epilogue, model.py:197-212):
+    u, z and the final conv state bit for bit against mtl_linear_skinny +
+    mtl_causal_conv1d_fwd, and against float64 at 1e-5; prompts shorter
+    than the conv window (history and tokens mixed in the final state), one
+    token per batch row, the 130m and 1.4b widths."""
+    print(f"\n[in_proj_conv_prefill b={b} l={l} d_model={M} d_inner={D} d_conv={K} hist={hist} biases={biases}]",
+          flush=True)
+    g = torch.Generator(device=DEV).manual_seed(b * 97 + l + D + K)
+    x = torch.randn(b * l, M, device=DEV, generator=g)
+    W_in = torch.randn(2 * D, M, device=DEV, generator=g) / M ** 0.5
+    b_in = torch.randn(2 * D, device=DEV, generator=g) if biases else None
+    conv_w = torch.randn(D, K, device=DEV, generator=g) / K ** 0.5
+    conv_b = torch.randn(D, device=DEV, generator=g) if biases else None
+    h_in = torch.randn(b, D, K - 1, device=DEV, generator=g) if hist else None
+    h_out = torch.empty(b, D, K - 1, device=DEV)
+    u, z = ops.in_proj_conv_prefill(x, W_in, b_in, conv_w, conv_b, h_in, h_out, b, l)
+    xz = ops.linear_skinny(x, W_in, b_in).view(b, l, 2 * D)
+    u2, h2 = ops.causal_conv1d(xz[..., :D].transpose(1, 2), conv_w, conv_b, conv_state=h_in, silu=True)
+    assert torch.equal(z.view(b, l, D), xz[..., D:])
+    assert torch.equal(u.view(b, l, D), u2.transpose(1, 2))
+    assert torch.equal(h_out, h2)
+    xd = x.double().cpu().view(b, l, M)
+    xzd = xd @ W_in.double().cpu().T + (b_in.double().cpu() if biases else 0)
+    xsd = xzd[..., :D].transpose(1, 2)                                              # [b, D, l]
+    pad = h_in.double().cpu() if hist else torch.zeros(b, D, K - 1, dtype=torch.float64)
+    win = torch.cat([pad, xsd], dim=2)                                             # [b, D, K-1+l]
+    pre = sum(win[..., k:k + l] * conv_w.double().cpu()[None, :, k, None] for k in range(K))
+    pre = pre + (conv_b.double().cpu()[None, :, None] if biases else 0)
+    assert_rel(u.view(b, l, D).cpu().numpy(), F.silu(pre).transpose(1, 2).numpy(), TOL, "u")
+    assert_rel(h_out.cpu().numpy(), win[..., -(K - 1):].numpy(), TOL, "final history")

@@ -470,8 +470,9 @@ def test_graphed_prefill_replays_match_eager_and_feed_the_stepper():
 @pytest.mark.parametrize("b,l", [(1, 64), (2, 20), (1, 17), (1, 1)])
 def test_short_prefill_on_the_skinny_gemm_vs_oracle(b, l, monkeypatch):
     """A prefill of at most 64 tokens at a width whose projections all fit
-    mtl_linear_skinny (K a multiple of 128): in_proj whole, x_proj split over
-    K and summed, out_proj as 4 parts summed by the residual add.  Logits and
+    mtl_linear_skinny (K a multiple of 128): in_proj whole with the causal
+    conv as its epilogue, x_proj split over K and summed, out_proj as 4 parts
+    summed by the residual add.  Logits and
     final states against the float64 oracle at 1e-4, and against the same
     prefill on torch's GEMMs at 1e-5; the mixer's own prefill (out_proj as
     one tensor) against the oracle's mixer.  The skinny GEMMs run where a
@@ -488,8 +489,11 @@ def test_short_prefill_on_the_skinny_gemm_vs_oracle(b, l, monkeypatch):
     calls = []
     real = mops.linear_skinny
     monkeypatch.setattr(mops, "linear_skinny", lambda *a, **k: calls.append(a[0].shape) or real(*a, **k))
+    real_ipc = mops.in_proj_conv_prefill
+    monkeypatch.setattr(mops, "in_proj_conv_prefill", lambda *a, **k: calls.append(a[0].shape) or real_ipc(*a, **k))
     with torch.no_grad():
         logits, cache = model.prefill(ids)
+    # in_proj (with the conv), x_proj and out_proj of every layer
     assert all(s[0] == b * l for s in calls) and len(calls) == 3 * cfg.n_layer, calls
     ref, rcache = om.lm_prefill(_lm_weights(model), ids.cpu().numpy(), dtype=np.float64)
     assert_rel(logits.cpu().numpy(), ref, 1e-4, "logits")
