@@ -405,7 +405,8 @@ __global__ void __launch_bounds__(kLinThreads) in_conv_xproj_kernel(const LinArg
 //   state_out[b][c][j] = the input at token l - (K - 1) + j (from the
 //   incoming history where that is before the first token).
 // z tiles store z.  Thread t's pairs all have channel t % (16 RB), so its
-// conv weights and bias are loaded once.
+// conv weights and bias are loaded once, with the history taps its pairs
+// need, before the product.
 struct PrefillConvArgs {
     const float* state_in;   // [b, D, K - 1] or null (zeros)
     float* state_out;        // [b, D, K - 1], not aliasing state_in
@@ -430,6 +431,29 @@ __global__ void __launch_bounds__(kLinThreads) in_conv_prefill_kernel(const LinA
     const int n0 = blockIdx.x * CB;
     const bool xtile = n0 < c.D;                       // uniform
 
+    // the thread's conv operands, requested ahead of the product: its
+    // channel's weights and bias, and the incoming history taps of its pairs
+    // that fall before their sequence's first token
+    constexpr int IT = XR * CB / kLinThreads;          // pairs per thread
+    const int cl = tid % CB, ch = n0 + cl;
+    const float* hin = c.state_in;
+    float w[K], cb = 0.f, hv[IT][K - 1];
+    if (xtile) {
+#pragma unroll
+        for (int k = 0; k < K; ++k) w[k] = c.conv_w[(int64_t)ch * K + k];
+        cb = c.conv_b ? c.conv_b[ch] : 0.f;
+#pragma unroll
+        for (int i = 0; i < IT; ++i) {
+            const int m = (tid + i * kLinThreads) / CB;
+            const int bi = m / c.L, tt = m - bi * c.L;
+#pragma unroll
+            for (int k = 0; k < K - 1; ++k) {
+                const int tau = tt - (K - 1) + k;
+                hv[i][k] = (hin && m < a.M && tau < 0) ? hin[((int64_t)bi * c.D + ch) * (K - 1) + tau + K - 1] : 0.f;
+            }
+        }
+    }
+
     skinny_tile<RB, MB, DEPTH>(a, ring, n0, 0);
 
     for (int t = tid; t < RB * MB * 64; t += kLinThreads) {
@@ -446,21 +470,16 @@ __global__ void __launch_bounds__(kLinThreads) in_conv_prefill_kernel(const LinA
     if (!xtile) return;
     __syncthreads();
 
-    const int cl = tid % CB, ch = n0 + cl;
-    float w[K];
 #pragma unroll
-    for (int k = 0; k < K; ++k) w[k] = c.conv_w[(int64_t)ch * K + k];
-    const float cb = c.conv_b ? c.conv_b[ch] : 0.f;
-    const float* hin = c.state_in;
-    for (int p = tid; p < a.M * CB; p += kLinThreads) {
-        const int m = p / CB;
-        const int bi = m / c.L, tt = m - bi * c.L;
+    for (int i = 0; i < IT; ++i) {
+        const int m = (tid + i * kLinThreads) / CB;
+        if (m >= a.M) break;
+        const int tt = m % c.L;
         float acc = 0.f;
 #pragma unroll
         for (int k = 0; k < K; ++k) {
             const int tau = tt - (K - 1) + k;
-            const float xv = tau >= 0 ? s_x[m - (K - 1) + k][cl]
-                                      : (hin ? hin[((int64_t)bi * c.D + ch) * (K - 1) + tau + K - 1] : 0.f);
+            const float xv = tau >= 0 ? s_x[m - (K - 1) + k][cl] : hv[i][k < K - 1 ? k : K - 2];
             acc = fmaf(w[k], xv, acc);
         }
         acc += cb;
