@@ -1,6 +1,7 @@
 """Benchmark of the Mamba mixer hot path on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--only scan|decode|quant|shard|prefill|all]
+    python bench.py [--gpus 1] [--steps K] [--warmup W]
+                   [--only scan|decode|quant|shard|prefill|copy|decode-counters|all]
 
 Headline (`value`): fused selective-scan prefill throughput, fp32, on the
 isolated-op workload u, delta, z [32, 1536, 1024], B, C [32, 16, 1024],
@@ -12,7 +13,8 @@ materialize-then-loop scan on the host cores, same workload).
 Reported beside it in the same JSON line, each with its own parity check:
   decode_us_per_token  hipGraph-replayed MambaLM.step, 130m shape b=1 and
                        1.4b shape b=1 / b=32 (random-init fp32 weights)
-  prefill_tok_s        MambaLM.prefill, 130m shape (b=1 x 64, b=32 x 1024)
+  prefill_tok_s        MambaLM.prefill, 130m shape (b=1 x 64, b=32 x 1024) and
+                       1.4b shape (b=1 x 1024, b=32 x 1024)
   prefill_graph_tok_s  the b=1 x 64 prefill captured once (GraphedPrefill)
                        and replayed per prompt
   quant                per-token int8 and fp16 quantize->dequantize-sum of
@@ -593,8 +595,16 @@ def main():
             log(f"prefill graph: {extra['prefill_graph_tok_s']}")
             del model
             torch.cuda.empty_cache()
+            # the 1.4b shape's 1024-token prompts (48 layers, d_inner 4096)
+            model = build_lm(MambaConfig(d_model=2048, n_layer=48, vocab_size=50280), dev)
+            extra["prefill_tok_s"]["1p4b_b1_l1024"] = bench_prefill(model, 1, 1024, dev, iters=5)
+            extra["prefill_tok_s"]["1p4b_b32_l1024"] = bench_prefill(model, 32, 1024, dev, iters=2)
+            log(f"prefill 1.4b: b=1 x 1024 {extra['prefill_tok_s']['1p4b_b1_l1024']:.0f} tok/s, "
+                f"b=32 x 1024 {extra['prefill_tok_s']['1p4b_b32_l1024']:.0f} tok/s")
+            del model
+            torch.cuda.empty_cache()
         except Exception as e:
-            extra["prefill_tok_s"] = {"error": repr(e)}
+            extra.setdefault("prefill_tok_s", {})["error"] = repr(e)
 
     if want("quant"):
         try:

@@ -521,3 +521,30 @@ def test_short_prefill_on_the_skinny_gemm_vs_oracle(b, l, monkeypatch):
     assert isinstance(y, torch.Tensor) and y.shape == (b, l, cfg.d_model)
     assert_rel(y.cpu().numpy(), ry, 1e-4, "mixer out")
     assert_rel(hs.cpu().numpy(), rh, 1e-4, "mixer ssm_state")
+
+
+def test_short_prefill_continues_into_its_own_cache(monkeypatch):
+    """A prompt of <= 64 tokens continued from a cache and written back into
+    that same cache (out_cache=cache, as GraphedPrefill serves prompts) on
+    the fused short-prefill kernels: the conv history read and the one
+    written are the same tensor.  Logits and states against the float64
+    oracle's continuation at 1e-4."""
+    import mamba_lite.model as mm
+    monkeypatch.setattr(mm, "SMALL_PREFILL_BLAS", None)
+    torch.manual_seed(21)
+    cfg = MambaConfig(d_model=256, n_layer=2, vocab_size=384, d_state=16)
+    with torch.device(DEV):
+        model = MambaLM(cfg).eval()
+    ids1 = torch.randint(0, cfg.vocab_size, (2, 13), device=DEV)
+    ids2 = torch.randint(0, cfg.vocab_size, (2, 9), device=DEV)
+    W = _lm_weights(model)
+    with torch.no_grad():
+        _, cache = model.prefill(ids1)
+        logits, same = model.prefill(ids2, cache=cache, out_cache=cache)
+    assert same is cache
+    _, rc1 = om.lm_prefill(W, ids1.cpu().numpy(), dtype=np.float64)
+    ref, rc2 = om.lm_prefill(W, ids2.cpu().numpy(), cache=rc1, dtype=np.float64)
+    assert_rel(_np(logits), ref, 1e-4, "continued logits")
+    for lc, (rcs, rhs) in zip(cache.layers, rc2):
+        assert_rel(_np(lc.conv_state), rcs, 1e-4, "conv_state")
+        assert_rel(_np(lc.ssm_state), rhs, 1e-4, "ssm_state")
