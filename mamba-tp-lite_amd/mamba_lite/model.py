@@ -176,6 +176,13 @@ def _skinny_split(K: int, most: int = 16) -> int:
 # column parts of the fused step's stand-alone x_proj GEMV
 _XPROJ_PARTS = 4
 
+# Largest batch that takes the fused decode step (its kernels take 1, 2 or
+# 4 rows).  At 4 rows the per-op step on the matrix-core skinny GEMMs is as
+# fast or faster (graph replays, A/B in one run: 130m 542 -> 501 us/step,
+# 1.4b 2406 against 2414); at 2 rows the fused step is well ahead (130m 407
+# against 475, 1.4b 1730 against 2343).
+FUSED_STEP_MAX_BATCH = 2
+
 
 @contextlib.contextmanager
 def _prefer_blas(lib: str | None):
@@ -549,9 +556,10 @@ class MambaLM(nn.Module):
 
     def step(self, input_ids: torch.Tensor, cache: MambaCache):
         """input_ids [b, 1] -> logits [b, 1, vocab]; cache updated in place
-        (reference model.py:343-353).  fp32 models at batch 1, 2 or 4 take
-        the fused decode path (3-4 launches per layer); others run the
-        per-op path (GEMMs + conv-step and SSM-update kernels)."""
+        (reference model.py:343-353).  fp32 models at batch 1 and 2
+        (FUSED_STEP_MAX_BATCH) take the fused decode path (3-4 launches per
+        layer); others run the per-op path (the matrix-core skinny GEMMs or
+        the library's, the conv-step and SSM-update kernels)."""
         if self._fused_step_ok(input_ids, cache):
             return self._step_fused(input_ids, cache)
         x = self.embedding(input_ids).squeeze(1)
@@ -569,8 +577,9 @@ class MambaLM(nn.Module):
     def _fused_step_ok(self, input_ids, cache) -> bool:
         cfg = self.cfg
         b = input_ids.shape[0]
-        if b not in (1, 2, 4) or cfg.d_state > 16 or cfg.d_model % 4 or cfg.d_inner % 4 or \
-                b * cfg.d_model > 15 * 1024 or cfg.d_inner > 4096 or cfg.dt_rank > 256 or not 2 <= cfg.d_conv <= 8:
+        if b not in (1, 2, 4) or b > FUSED_STEP_MAX_BATCH or cfg.d_state > 16 or cfg.d_model % 4 or \
+                cfg.d_inner % 4 or b * cfg.d_model > 15 * 1024 or cfg.d_inner > 4096 or cfg.dt_rank > 256 or \
+                not 2 <= cfg.d_conv <= 8:
             return False
         if self.embedding.weight.dtype != torch.float32 or not input_ids.is_cuda:
             return False

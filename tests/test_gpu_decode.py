@@ -18,6 +18,15 @@ pytestmark = pytest.mark.gpu
 DEV = "cuda"
 
 
+@pytest.fixture(autouse=True)
+def _fused_up_to_batch_4(monkeypatch):
+    """The fused kernels take 1, 2 or 4 rows; MambaLM.step sends batch 4 to
+    the per-op path by default (faster there), so these tests raise the
+    limit to keep the fused path covered at batch 4."""
+    import mamba_lite.model as mm
+    monkeypatch.setattr(mm, "FUSED_STEP_MAX_BATCH", 4)
+
+
 def _np(t):
     return t.detach().float().cpu().numpy()
 

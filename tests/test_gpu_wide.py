@@ -99,13 +99,16 @@ def _lm_steps_vs_oracle(lm, W, b, plen, steps, vocab, seed, expect_fused):
             assert_rel(_n(lc.ssm_state), rh, TOL, f"layer {i} ssm_state")
 
 
-@pytest.mark.parametrize("b", [1, 2, 4, 32])
-def test_lm_step_at_1p4b_width(b):
-    """b = 1, 2, 4: the fused decode path (x_proj as its own row GEMV at this
-    width); b = 32: the per-op path."""
-    print(f"\n[wide: lm step d_model=2048 b={b}]", flush=True)
+@pytest.mark.parametrize("b,fused_max", [(1, 2), (2, 2), (4, 4), (4, 2), (32, 2)])
+def test_lm_step_at_1p4b_width(b, fused_max, monkeypatch):
+    """b = 1, 2 (and 4 with the fused limit raised): the fused decode path
+    (x_proj as its own row GEMV at this width); b = 4 by default and 32:
+    the per-op path."""
+    import mamba_lite.model as mm
+    monkeypatch.setattr(mm, "FUSED_STEP_MAX_BATCH", fused_max)
+    print(f"\n[wide: lm step d_model=2048 b={b} fused up to {fused_max}]", flush=True)
     lm, W = _lm(45, 2048, 2, 2048, dt_rank=128)
-    _lm_steps_vs_oracle(lm, W, b, 8, 3, 2048, 46 + b, expect_fused=b in (1, 2, 4))
+    _lm_steps_vs_oracle(lm, W, b, 8, 3, 2048, 46 + b, expect_fused=b <= fused_max)
 
 
 @pytest.mark.parametrize("b", [1, 8, 32])
