@@ -187,7 +187,7 @@ __global__ void __launch_bounds__(256) sum_parts_kernel(const float* __restrict_
 // floats -- into LDS transposed; then wavefront w takes row w and lane l
 // channel l: a W_dt read per k that is conflict-free across the lanes and a
 // broadcast read of dt_low.  The loads are issued before their first use
-// (W_dt's first batch, then up to PMAX parts per element for 3 elements per
+// (W_dt's first batch, then up to PMAX parts per element for 2 elements per
 // thread), so the workgroup waits for memory once.  Two launches (the sum
 // and a library GEMM of K = R) become one.
 constexpr int kXdCh = 64, kXdRows = 4, kXdMaxR = 160, kXdMaxParts = 16;
@@ -206,7 +206,7 @@ __global__ void __launch_bounds__(256) xproj_sum_dt_kernel(const float* __restri
     const int nch = min(kXdCh, D - c0);
     const int nw = nch * R;
     const float* wb = Wdt + (int64_t)c0 * R;
-    constexpr int QE = 3, QW = 16;
+    constexpr int QE = 2, QW = 16;
     // W_dt in batches of QW per thread (one batch covers R <= 64); the first
     // batch's loads go out ahead of the parts' loads
     float w[QW];
@@ -231,10 +231,12 @@ __global__ void __launch_bounds__(256) xproj_sum_dt_kernel(const float* __restri
 #pragma unroll
         for (int q = 0; q < QE; ++q) {
             const int e = min(e0 + tid + q * 256, ne - 1);
+            const bool live = e0 + tid + q * 256 < ne;
             const int rl = e / cols, j = e - rl * cols;
             idx[q] = (int64_t)min(r0 + rl, rows - 1) * J + j;
+            // lanes past the elements and parts past nparts request nothing
 #pragma unroll
-            for (int p = 0; p < PMAX; ++p) v[q][p] = parts[min(p, nparts - 1) * n + idx[q]];
+            for (int p = 0; p < PMAX; ++p) v[q][p] = (live && p < nparts) ? parts[p * n + idx[q]] : 0.f;
         }
 #pragma unroll
         for (int q = 0; q < QE; ++q) {
@@ -627,6 +629,9 @@ extern "C" int mtl_xproj_sum_dt(const float* parts, int32_t nparts, int64_t rows
                            (int)D, x_dbl, dt);
     else if (nparts <= 8)
         hipLaunchKernelGGL((xproj_sum_dt_kernel<8>), grid, dim3(256), 0, st, parts, nparts, (int)rows, J, R, W_dt,
+                           (int)D, x_dbl, dt);
+    else if (nparts <= 12)
+        hipLaunchKernelGGL((xproj_sum_dt_kernel<12>), grid, dim3(256), 0, st, parts, nparts, (int)rows, J, R, W_dt,
                            (int)D, x_dbl, dt);
     else
         hipLaunchKernelGGL((xproj_sum_dt_kernel<16>), grid, dim3(256), 0, st, parts, nparts, (int)rows, J, R, W_dt,
