@@ -548,3 +548,33 @@ def test_short_prefill_continues_into_its_own_cache(monkeypatch):
     for lc, (rcs, rhs) in zip(cache.layers, rc2):
         assert_rel(_np(lc.conv_state), rcs, 1e-4, "conv_state")
         assert_rel(_np(lc.ssm_state), rhs, 1e-4, "ssm_state")
+
+
+@pytest.mark.parametrize("d_model", [64, 256])
+def test_bf16_lm_prefill_step_generate(d_model):
+    """MambaLM cast to bfloat16 (the reference's from_pretrained(dtype=...),
+    model.py:368-372): prefill, teacher-forced steps and generate run on the
+    per-op path with bf16 activations and caches, and track the same weights
+    in float32 within bf16 rounding (2e-2 relative on the logits)."""
+    torch.manual_seed(31 + d_model)
+    cfg = MambaConfig(d_model=d_model, n_layer=2, vocab_size=300, d_state=16)
+    with torch.device(DEV):
+        m32 = MambaLM(cfg).eval()
+    _init_dt_bias(m32, 31)
+    with torch.device(DEV):
+        m16 = MambaLM(cfg).eval()
+    m16.load_state_dict(m32.state_dict())
+    m16 = m16.to(torch.bfloat16)
+    ids = torch.randint(0, cfg.vocab_size, (2, 11), device=DEV)
+    with torch.no_grad():
+        l32, c32 = m32.prefill(ids[:, :8])
+        l16, c16 = m16.prefill(ids[:, :8])
+        assert l16.dtype == torch.bfloat16 and c16.layers[0].conv_state.dtype == torch.bfloat16
+        assert_rel(_np(l16), _np(l32), 2e-2, "bf16 prefill logits")
+        for t in range(8, 11):
+            s32 = m32.step(ids[:, t:t + 1], c32)
+            s16 = m16.step(ids[:, t:t + 1], c16)
+            assert s16.dtype == torch.bfloat16
+            assert_rel(_np(s16), _np(s32), 2e-2, f"bf16 step {t}")
+        toks = m16.generate(ids[:, :4], max_new_tokens=3)
+    assert toks.shape == (2, 7) and torch.equal(toks[:, :4], ids[:, :4])
