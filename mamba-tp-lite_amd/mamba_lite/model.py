@@ -680,7 +680,13 @@ class MambaLM(nn.Module):
     @torch.no_grad()
     def generate(self, input_ids: torch.Tensor, max_new_tokens: int, greedy: bool = True):
         """Prefill once, then greedy decode through the cache (reference
-        model.py:355-365).  Returns the full token sequence."""
+        model.py:355-365).  Returns the full token sequence.  The reference
+        has no sampling path: with greedy=False it sets the first token to
+        None (model.py:359) and its first step fails; here that is a clear
+        error before any work."""
+        if not greedy:
+            raise NotImplementedError("generate: only greedy decoding exists (the reference's greedy=False "
+                                      "path has no sampler)")
         logits, cache = self.prefill(input_ids)
         next_id = logits[:, -1:].argmax(dim=-1)
         tokens = [input_ids, next_id]

@@ -225,3 +225,13 @@ def test_local_tp_mixer_needs_a_divisible_world_size():
         LocalTPMixer(cfg, world_size=3)
     with pytest.raises(RuntimeError, match="no shards"):
         LocalTPMixer(cfg, world_size=2).prefill(torch.randn(1, 2, 32))
+
+
+def test_generate_has_no_sampling_path():
+    """The reference's generate(greedy=False) leaves the first token None
+    (model.py:359) and fails in its first step; here it is a clear error
+    raised before any work (no GPU needed)."""
+    cfg = MambaConfig(d_model=32, n_layer=1, vocab_size=64, d_state=8)
+    model = MambaLM(cfg)
+    with pytest.raises(NotImplementedError):
+        model.generate(torch.zeros(1, 3, dtype=torch.long), 2, greedy=False)
