@@ -578,3 +578,30 @@ def test_bf16_lm_prefill_step_generate(d_model):
             assert_rel(_np(s16), _np(s32), 2e-2, f"bf16 step {t}")
         toks = m16.generate(ids[:, :4], max_new_tokens=3)
     assert toks.shape == (2, 7) and torch.equal(toks[:, :4], ids[:, :4])
+
+
+@pytest.mark.parametrize("d_conv,bias,b,l", [(2, False, 2, 32), (3, True, 4, 9), (4, True, 1, 64)])
+def test_short_prefill_conv_widths_and_biases(d_conv, bias, b, l, monkeypatch):
+    """The fused short-prefill path (in_proj with the conv epilogue, split
+    x_proj with dt_proj, out_proj parts) at conv widths 2, 3, 4, with the
+    in_proj / out_proj biases, against the float64 oracle at 1e-4."""
+    import mamba_lite.model as mm
+    from mamba_lite import ops as mops
+    monkeypatch.setattr(mm, "SMALL_PREFILL_BLAS", None)
+    torch.manual_seed(40 + d_conv)
+    cfg = MambaConfig(d_model=128, n_layer=2, vocab_size=256, d_state=16, d_conv=d_conv, bias=bias)
+    with torch.device(DEV):
+        model = MambaLM(cfg).eval()
+    _init_dt_bias(model, 40)
+    calls = []
+    real = mops.in_proj_conv_prefill
+    monkeypatch.setattr(mops, "in_proj_conv_prefill", lambda *a, **k: calls.append(1) or real(*a, **k))
+    ids = torch.randint(0, cfg.vocab_size, (b, l), device=DEV)
+    with torch.no_grad():
+        logits, cache = model.prefill(ids)
+    assert len(calls) == cfg.n_layer
+    ref, rcache = om.lm_prefill(_lm_weights(model), ids.cpu().numpy(), dtype=np.float64)
+    assert_rel(_np(logits), ref, 1e-4, "logits")
+    for lc, (rcs, rhs) in zip(cache.layers, rcache):
+        assert_rel(_np(lc.conv_state), rcs, 1e-4, "conv_state")
+        assert_rel(_np(lc.ssm_state), rhs, 1e-4, "ssm_state")
