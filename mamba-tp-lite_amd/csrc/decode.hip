@@ -400,10 +400,12 @@ __global__ void __launch_bounds__(kThreads) decode_gemv_kernel(const GemvArgs a)
 // and column part (blockIdx.y: columns [p K, (p + 1) K) of rows of length
 // ld), the 4 wavefronts take quarters of it (PLW float4 runs per lane each,
 // K <= 1024 PLW) and their sums are added in wavefront order; part p writes
-// its partial product to out + p * out_ps (bias and x_in in part 0).
+// its partial product to out + p * out_ps (bias and x_in in part 0).  The
+// products are the LDS-staged form's, in the same order, so the bits are
+// unchanged (1.4b b=1 x_proj: one barrier instead of three).
 template <int B, int PLW>
 __global__ void __launch_bounds__(kThreads) decode_gemv_split_kernel(const GemvArgs a) {
-    extern __shared__ __align__(16) float s_v[];      // [B][K], then the [kWaves][B] wavefront sums
+    __shared__ float s_sum[kWaves][B];                // the wavefront sums
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int K = a.K, K4 = K >> 2;
     const int m = blockIdx.x, part = blockIdx.y;
@@ -417,41 +419,36 @@ __global__ void __launch_bounds__(kThreads) decode_gemv_split_kernel(const GemvA
     float xin[B];
 #pragma unroll
     for (int bi = 0; bi < B; ++bi) xin[bi] = add_x ? a.x_in[(int64_t)bi * a.Mrows + m] : 0.f;
-    constexpr int PL = kWaves * PLW;
-    float vv[B][PL];
+    // v straight from global memory (a few KB, in L2 after the first
+    // workgroups): each lane reads the float4 runs it multiplies, so there
+    // is no LDS stage and no barrier before the products
+    float4 xv[B][PLW];
 #pragma unroll
-    for (int q = 0; q < PL; ++q)
+    for (int p = 0; p < PLW; ++p)
 #pragma unroll
-        for (int bi = 0; bi < B; ++bi) vv[bi][q] = a.v[(int64_t)bi * a.ld + k0 + min(tid + q * kThreads, K - 1)];
-#pragma unroll
-    for (int q = 0; q < PL; ++q)
-        if (tid + q * kThreads < K)
-#pragma unroll
-            for (int bi = 0; bi < B; ++bi) s_v[bi * K + tid + q * kThreads] = vv[bi][q];
-    __syncthreads();
+        for (int bi = 0; bi < B; ++bi)
+            xv[bi][p] = reinterpret_cast<const float4*>(a.v + (int64_t)bi * a.ld + k0)
+                [min((wave * PLW + p) * 64 + lane, K4 - 1)];
 
     float acc[B];
 #pragma unroll
     for (int bi = 0; bi < B; ++bi) acc[bi] = 0.f;
 #pragma unroll
     for (int p = 0; p < PLW; ++p) {
-        const int k4 = (wave * PLW + p) * 64 + lane;
-        const bool ok = k4 < K4;
+        const bool ok = (wave * PLW + p) * 64 + lane < K4;
 #pragma unroll
         for (int bi = 0; bi < B; ++bi) {
-            const float4 x4 = reinterpret_cast<const float4*>(s_v + (size_t)bi * K)[min(k4, K4 - 1)];
-            const float t = dot4(w[p], x4, acc[bi]);
+            const float t = dot4(w[p], xv[bi][p], acc[bi]);
             acc[bi] = ok ? t : acc[bi];
         }
     }
     wave_sum<B>(acc);
-    __syncthreads();                                  // every wavefront is done reading s_v
     if (lane == 0)
 #pragma unroll
-        for (int bi = 0; bi < B; ++bi) s_v[wave * B + bi] = acc[bi];
+        for (int bi = 0; bi < B; ++bi) s_sum[wave][bi] = acc[bi];
     __syncthreads();
     if (tid < B) {
-        const float o = ((s_v[tid] + s_v[B + tid]) + (s_v[2 * B + tid] + s_v[3 * B + tid])) + bias;
+        const float o = ((s_sum[0][tid] + s_sum[1][tid]) + (s_sum[2][tid] + s_sum[3][tid])) + bias;
         a.out[part * a.out_ps + (int64_t)tid * a.Mrows + m] = add_x ? xin[tid] + o : o;
     }
 }
@@ -622,7 +619,7 @@ extern "C" int mtl_decode_gemv(const float* v, const float* W, const float* bias
         MTL_REQUIRE(plw * kWaves <= kMaxPL, "internal: split GEMV run count");
         MTL_DISPATCH_B(batch, MTL_DISPATCH_RUNS(PLW, plw,
             if constexpr (PLW * kWaves <= kMaxPL) hipLaunchKernelGGL((decode_gemv_split_kernel<B, PLW>),
-                dim3((unsigned)rows), dim3(kThreads), smem, st, a)));
+                dim3((unsigned)rows), dim3(kThreads), 0, st, a)));
     } else if (batch == 1) {
         MTL_DISPATCH_RUNS(PL, round_runs(runs), hipLaunchKernelGGL((decode_gemv_row_kernel<PL>), dim3((unsigned)rows),
                                                                    dim3(64), 0, st, a));
@@ -647,13 +644,11 @@ extern "C" int mtl_decode_gemv_parts(const float* v, const float* W, float* out_
     MTL_REQUIRE(plw * kWaves <= kMaxPL, "cols / nparts must be at most 4096");
     MTL_REQUIRE(v && W && out_parts, "null required pointer");
     MTL_REQUIRE(((uintptr_t)W % 16) == 0 && ((uintptr_t)v % 16) == 0, "W and v must be 16-byte aligned");
-    const size_t smem = sizeof(float) * (size_t)batch * K;
-    MTL_REQUIRE(smem <= 64 * 1024, "batch * cols / nparts too large for the decode LDS tile");
     GemvArgs a{v, W, nullptr, nullptr, out_parts, rows, K, nullptr, 0.f, cols, (int64_t)batch * rows};
     hipStream_t st = as_stream(stream);
     MTL_DISPATCH_B(batch, MTL_DISPATCH_RUNS(PLW, plw,
         if constexpr (PLW * kWaves <= kMaxPL) hipLaunchKernelGGL((decode_gemv_split_kernel<B, PLW>),
-            dim3((unsigned)rows, (unsigned)nparts), dim3(kThreads), smem, st, a)));
+            dim3((unsigned)rows, (unsigned)nparts), dim3(kThreads), 0, st, a)));
     return check_launch("decode_gemv_parts");
 }
 
