@@ -296,33 +296,43 @@ struct GemvArgs {
 // NORM: out = (W . (norm_w * v)) * rsqrt(mean(v^2) + eps) + bias -- the final
 // RMSNorm folded into the lm_head rows (every workgroup recomputes the rms of
 // the few-kB vector instead of waiting for a separate norm kernel)
-// Batch 1 without the norm: one wavefront per workgroup and per row, v read
-// straight from global memory (it is a few KB and sits in L2 after the first
-// workgroups), so a row needs no LDS stage and no barrier.  Twice to four
+// Batch 1 and 2 without the norm: one wavefront per workgroup and per row,
+// v read straight from global memory (a few KB per batch row, in L2 after
+// the first workgroups), so a row needs no LDS stage and no barrier.  Four
 // times the workgroups of the form below on the same weight stream: the
-// mamba-1.4b decode step went 1410-1415 -> 1401-1406 us/token, the 130m one
-// 322.5-324 -> 320.5-321.5 (same dot-product order, the same bits).
-template <int PL>
+// mamba-1.4b decode step went 1410-1415 -> 1401-1406 us/token at batch 1 and
+// 1712 -> 1664 us/step at batch 2, the 130m one 322.5-324 -> 320.5-321.5
+// and 414 -> 403 (same dot-product order, the same bits).
+template <int B, int PL>
 __global__ void __launch_bounds__(64) decode_gemv_row_kernel(const GemvArgs a) {
     const int lane = threadIdx.x;
     const int K = a.K, K4 = K >> 2;
     const int m = blockIdx.x;
     const float4* row = reinterpret_cast<const float4*>(a.W + (int64_t)m * K);
-    const float4* v4 = reinterpret_cast<const float4*>(a.v);
     float4 w[PL];
 #pragma unroll
     for (int p = 0; p < PL; ++p) w[p] = ntload4(row + min(p * 64 + lane, K4 - 1));
     const float bias = a.bias ? a.bias[m] : 0.f;
-    const float xin = a.x_in ? a.x_in[m] : 0.f;
-    const bool tail_ok = (PL - 1) * 64 + lane < K4;
-    float acc = 0.f;
+    float xin[B];
 #pragma unroll
-    for (int p = 0; p < PL; ++p) {
-        const float t = dot4(w[p], v4[min(p * 64 + lane, K4 - 1)], acc);
-        acc = p < PL - 1 || tail_ok ? t : acc;
-    }
-    acc = group_sum<64>(acc);
-    if (lane == 0) a.out[m] = a.x_in ? xin + (acc + bias) : acc + bias;
+    for (int bi = 0; bi < B; ++bi) xin[bi] = a.x_in ? a.x_in[(int64_t)bi * a.Mrows + m] : 0.f;
+    const bool tail_ok = (PL - 1) * 64 + lane < K4;
+    float acc[B];
+#pragma unroll
+    for (int bi = 0; bi < B; ++bi) acc[bi] = 0.f;
+#pragma unroll
+    for (int p = 0; p < PL; ++p)
+#pragma unroll
+        for (int bi = 0; bi < B; ++bi) {
+            const float4* v4 = reinterpret_cast<const float4*>(a.v + (int64_t)bi * K);
+            const float t = dot4(w[p], v4[min(p * 64 + lane, K4 - 1)], acc[bi]);
+            acc[bi] = p < PL - 1 || tail_ok ? t : acc[bi];
+        }
+    wave_sum<B>(acc);
+    if (lane == 0)
+#pragma unroll
+        for (int bi = 0; bi < B; ++bi)
+            a.out[(int64_t)bi * a.Mrows + m] = a.x_in ? xin[bi] + (acc[bi] + bias) : acc[bi] + bias;
 }
 
 template <int B, int PL, bool NORM = false>
@@ -620,9 +630,14 @@ extern "C" int mtl_decode_gemv(const float* v, const float* W, const float* bias
         MTL_DISPATCH_B(batch, MTL_DISPATCH_RUNS(PLW, plw,
             if constexpr (PLW * kWaves <= kMaxPL) hipLaunchKernelGGL((decode_gemv_split_kernel<B, PLW>),
                 dim3((unsigned)rows), dim3(kThreads), 0, st, a)));
-    } else if (batch == 1) {
-        MTL_DISPATCH_RUNS(PL, round_runs(runs), hipLaunchKernelGGL((decode_gemv_row_kernel<PL>), dim3((unsigned)rows),
-                                                                   dim3(64), 0, st, a));
+    } else if (batch <= 2) {
+        if (batch == 1) {
+            MTL_DISPATCH_RUNS(PL, round_runs(runs), hipLaunchKernelGGL((decode_gemv_row_kernel<1, PL>),
+                                                                       dim3((unsigned)rows), dim3(64), 0, st, a));
+        } else {
+            MTL_DISPATCH_RUNS(PL, round_runs(runs), hipLaunchKernelGGL((decode_gemv_row_kernel<2, PL>),
+                                                                       dim3((unsigned)rows), dim3(64), 0, st, a));
+        }
     } else {
         const dim3 grid((unsigned)((rows + kWaves - 1) / kWaves));
         MTL_DISPATCH_B(batch, MTL_DISPATCH_RUNS(PL, round_runs(runs), hipLaunchKernelGGL((decode_gemv_kernel<B, PL>),

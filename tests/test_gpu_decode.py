@@ -274,8 +274,8 @@ def test_decode_in_channel_blocks_of_4_and_8(b, M, D):
 def test_decode_gemv_vs_float64(b, cols, rows, with_bias, with_x):
     """mtl_decode_gemv (the decode step's out_proj with the residual add, and
     x_proj at the 1.4b width) against float64 out = x_in + W v + bias, 1e-5
-    relative: the out_proj shapes of the 1.4b and 130m widths at batch 1 (one
-    wavefront per row), batch 2 and 4 (four rows per workgroup), few long rows
+    relative: the out_proj shapes of the 1.4b and 130m widths at batch 1 and 2
+    (one wavefront per row), batch 4 (four rows per workgroup), few long rows
     (a workgroup per row split four ways), ragged widths and row counts."""
     print(f"decode_gemv b={b} cols={cols} rows={rows} bias={with_bias} x_in={with_x}", flush=True)
     g = torch.Generator(device=DEV).manual_seed(cols * 3 + rows + b)
@@ -294,20 +294,25 @@ def test_decode_gemv_vs_float64(b, cols, rows, with_bias, with_x):
 
 
 @pytest.mark.parametrize("cols,rows", [(4096, 2048), (1536, 768), (100, 9)])
-def test_decode_gemv_batch1_rows_equal_batch2_rows(cols, rows):
-    """Batch 1 runs one wavefront per row, batch 2 four rows per workgroup
-    with v staged in LDS; both take each lane's four-wide dot products in
-    the same order and reduce over the wavefront the same way, so a row of
-    a batch-2 call equals the batch-1 call on that row's v bit for bit."""
-    print(f"decode_gemv b1 == b2 rows cols={cols} rows={rows}", flush=True)
+def test_decode_gemv_row_kernel_equals_the_staged_kernel(cols, rows):
+    """Batch 1 and 2 run one wavefront per row with v read from global
+    memory, batch 4 four rows per workgroup with v staged in LDS; all take
+    each lane's four-wide dot products in the same order and reduce over the
+    wavefront the same way, so the rows of a batch-4 call equal batch-1 and
+    batch-2 calls on the same v bit for bit."""
+    print(f"decode_gemv b1, b2 == b4 rows cols={cols} rows={rows}", flush=True)
     g = torch.Generator(device=DEV).manual_seed(cols + 5 * rows)
-    v = torch.randn(2, cols, device=DEV, generator=g)
+    v = torch.randn(4, cols, device=DEV, generator=g)
     W = torch.randn(rows, cols, device=DEV, generator=g) / cols ** 0.5
     bias = torch.randn(rows, device=DEV, generator=g)
-    x_in = torch.randn(2, rows, device=DEV, generator=g)
-    out2 = torch.empty(2, rows, device=DEV)
-    ops.decode_gemv(v, W, out2, bias=bias, x_in=x_in)
-    for i in range(2):
+    x_in = torch.randn(4, rows, device=DEV, generator=g)
+    out4 = torch.empty(4, rows, device=DEV)
+    ops.decode_gemv(v, W, out4, bias=bias, x_in=x_in)
+    for i in range(4):
         out1 = torch.empty(1, rows, device=DEV)
         ops.decode_gemv(v[i:i + 1].clone(), W, out1, bias=bias, x_in=x_in[i:i + 1].clone())
-        assert torch.equal(out1[0], out2[i]), i
+        assert torch.equal(out1[0], out4[i]), i
+    for i in (0, 2):
+        out2 = torch.empty(2, rows, device=DEV)
+        ops.decode_gemv(v[i:i + 2].clone(), W, out2, bias=bias, x_in=x_in[i:i + 2].clone())
+        assert torch.equal(out2, out4[i:i + 2]), i
