@@ -140,3 +140,20 @@ def test_in_proj_conv_prefill(b, l, M, D, K, hist, biases):
     pre = pre + (conv_b.double().cpu()[None, :, None] if biases else 0)
     assert_rel(u.view(b, l, D).cpu().numpy(), F.silu(pre).transpose(1, 2).numpy(), TOL, "u")
     assert_rel(h_out.cpu().numpy(), win[..., -(K - 1):].numpy(), TOL, "final history")
+
+
+def test_in_proj_conv_prefill_strided_rows():
+    """x as a row-strided view (row stride 2 d_model): the same u, z and
+    history as from a contiguous copy, bit for bit."""
+    print("\n[in_proj_conv_prefill strided x]", flush=True)
+    g = torch.Generator(device=DEV).manual_seed(5)
+    b, l, M, D, K = 2, 24, 256, 128, 4
+    wide = torch.randn(b * l, 2 * M, device=DEV, generator=g)
+    x = wide[:, M:]
+    W_in = torch.randn(2 * D, M, device=DEV, generator=g) / M ** 0.5
+    conv_w = torch.randn(D, K, device=DEV, generator=g)
+    h_in = torch.randn(b, D, K - 1, device=DEV, generator=g)
+    h1, h2 = torch.empty(b, D, K - 1, device=DEV), torch.empty(b, D, K - 1, device=DEV)
+    u1, z1 = ops.in_proj_conv_prefill(x, W_in, None, conv_w, None, h_in, h1, b, l)
+    u2, z2 = ops.in_proj_conv_prefill(x.contiguous(), W_in, None, conv_w, None, h_in, h2, b, l)
+    assert torch.equal(u1, u2) and torch.equal(z1, z2) and torch.equal(h1, h2)
