@@ -331,6 +331,75 @@ int mtl_in_proj_conv_prefill(const float* x, int64_t x_rs, const float* W_in, co
                              const float* conv_b, int32_t d_conv, const float* conv_state_in, float* conv_state_out,
                              float* u, float* z, int64_t batch, int64_t seqlen, int64_t d_model, int64_t d_inner,
                              mtl_stream_t stream);
+/* ------------------------------------------------------------------------
+ * A short prompt's whole layer stack in one call: MambaLM.prefill
+ * (model.py:328-341) over MambaBlock.prefill (303-306) and
+ * MambaMixer.prefill (184-241), fp32, batch * seqlen <= 64 token rows, with
+ * the kernels the per-op entry points above launch, in the same order:
+ *   xn = RMSNorm_0(h);  per layer i:
+ *     mtl_in_proj_conv_prefill(xn) -> u, z, conv_state_out
+ *     mtl_linear_skinny(u, W_x, ksplit = the largest split of d_inner / 128
+ *       into at most 16 parts) -> x_parts
+ *     mtl_xproj_sum_dt(x_parts, W_dt) -> x_dbl, dt
+ *     mtl_selective_scan_fwd(u, dt + dt_bias (softplus), A = -exp(A_log),
+ *       B, C = columns of x_dbl, D, z, h0) -> y, h_out
+ *     mtl_linear_skinny(y, W_out, b_out, ksplit = 4) -> y_parts
+ *     h += the y_parts in order, xn = RMSNorm_{i+1}(h) (norm_f after the
+ *       last layer, into normed_out)    (mtl_add_rmsnorm_parts)
+ * h: [b seqlen, d_model], the embedded tokens in, the final residual out.
+ * Workspace (all contiguous fp32): xn [rows, d_model]; u, z, dt, y [rows,
+ * d_inner]; x_parts [16, rows, J]; x_dbl [rows, J] (J = dt_rank +
+ * 2 d_state); y_parts [4, rows, d_model]; normed_out [rows, d_model].
+ * layers[i]: the layer's weights (as the per-op entry points take them) and
+ * its cache: conv_state_in / h0 (NULL: zeros) and conv_state_out / h_out
+ * ([b, d_inner, d_conv - 1] and [b, d_inner, d_state]; conv_state_out must
+ * not alias conv_state_in, h_out may alias h0).  d_model a multiple of 128
+ * (at least 256), d_inner a multiple of 512, d_state <= 16, dt_rank <= 160,
+ * dt_rank + 2 d_state a multiple of 4, d_conv 2..4.  Every layer is checked
+ * before the first launch.  The bits equal those of the per-op launches.
+ * ---------------------------------------------------------------------- */
+typedef struct {
+    const float* norm_w;       /* [d_model] the block's RMSNorm */
+    float eps;
+    int32_t reserved;
+    const float* W_in;         /* [2 d_inner, d_model] */
+    const float* b_in;         /* [2 d_inner] or NULL */
+    const float* conv_w;       /* [d_inner, d_conv] */
+    const float* conv_b;       /* [d_inner] or NULL */
+    const float* W_x;          /* [J, d_inner] */
+    const float* W_dt;         /* [d_inner, dt_rank] */
+    const float* dt_bias;      /* [d_inner] */
+    const float* A_log;        /* [d_inner, d_state] */
+    const float* Dv;           /* [d_inner] or NULL */
+    const float* W_out;        /* [d_model, d_inner] */
+    const float* b_out;        /* [d_model] or NULL */
+    const float* conv_state_in;
+    float* conv_state_out;
+    const float* h0;
+    float* h_out;
+} mtl_prefill_layer;
+
+typedef struct {
+    float* h;
+    float* xn;
+    float* u;
+    float* z;
+    float* dt;
+    float* y;
+    float* x_parts;
+    float* x_dbl;
+    float* y_parts;
+    const float* norm_f;
+    float* normed_out;
+    float eps_f;
+    int32_t d_conv;
+    int32_t n_layers;
+    int32_t reserved;
+    int64_t batch, seqlen, d_model, d_inner, d_state, dt_rank;
+} mtl_prefill_short_args;
+
+int mtl_prefill_short(const mtl_prefill_short_args* args, const mtl_prefill_layer* layers, mtl_stream_t stream);
+
 int mtl_in_proj_conv_xproj(const float* x, int64_t x_rs, const float* W_in, const float* b_in, float* conv_state,
                            const float* conv_w, const float* conv_b, int32_t d_conv, const float* W_xT, int32_t J,
                            float* xc, float* z, int64_t z_rs, float* xpart, int64_t batch, int64_t d_model,

@@ -52,6 +52,27 @@ class ConvParams(ctypes.Structure):
     ]
 
 
+class PrefillLayer(ctypes.Structure):
+    """mirror of mtl_prefill_layer"""
+    _fields_ = [
+        ("norm_w", _vp), ("eps", ctypes.c_float), ("reserved", _i32),
+        ("W_in", _vp), ("b_in", _vp), ("conv_w", _vp), ("conv_b", _vp), ("W_x", _vp), ("W_dt", _vp),
+        ("dt_bias", _vp), ("A_log", _vp), ("Dv", _vp), ("W_out", _vp), ("b_out", _vp),
+        ("conv_state_in", _vp), ("conv_state_out", _vp), ("h0", _vp), ("h_out", _vp),
+    ]
+
+
+class PrefillShortArgs(ctypes.Structure):
+    """mirror of mtl_prefill_short_args"""
+    _fields_ = [
+        ("h", _vp), ("xn", _vp), ("u", _vp), ("z", _vp), ("dt", _vp), ("y", _vp), ("x_parts", _vp),
+        ("x_dbl", _vp), ("y_parts", _vp), ("norm_f", _vp), ("normed_out", _vp),
+        ("eps_f", ctypes.c_float), ("d_conv", _i32), ("n_layers", _i32), ("reserved", _i32),
+        ("batch", _i64), ("seqlen", _i64), ("d_model", _i64), ("d_inner", _i64), ("d_state", _i64),
+        ("dt_rank", _i64),
+    ]
+
+
 # name -> (restype, argtypes); every symbol of include/mtl.h
 SIGNATURES = {
     "mtl_last_error": (ctypes.c_char_p, []),
@@ -65,6 +86,7 @@ SIGNATURES = {
     "mtl_add_rmsnorm_parts": (ctypes.c_int, [_fp, _fp, _i32, _fp, _fp, _fp, _i64, _i64, ctypes.c_float, _vp]),
     "mtl_sum_parts": (ctypes.c_int, [_fp, _i32, _i64, _fp, _vp]),
     "mtl_xproj_sum_dt": (ctypes.c_int, [_fp, _i32, _i64, _i32, _fp, _i32, _i64, _fp, _fp, _vp]),
+    "mtl_prefill_short": (ctypes.c_int, [ctypes.POINTER(PrefillShortArgs), ctypes.POINTER(PrefillLayer), _vp]),
     "mtl_conv_step_xproj": (ctypes.c_int, [_fp, _fp, _i64, _fp, _fp, _fp, _i64, _fp, _fp, _i64, _i64, _i32, _i32,
                                            _vp]),
     "mtl_conv_step_xproj_noalloc": (ctypes.c_int, [_fp, _fp, _i64, _fp, _fp, _fp, _i64, _fp, _fp, _i64, _i64, _i32,

@@ -31,7 +31,7 @@ import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
-from . import ops
+from . import _lib, ops
 
 
 def load_hf_state_dict(hf_path: str) -> dict[str, torch.Tensor]:
@@ -156,6 +156,12 @@ SKINNY_OUT_SPLIT = 4
 # (SMALL_PREFILL_BLAS) keeps the library GEMMs there as well: that path is
 # bound by host time per launch, which the split x_proj adds to.
 _SKINNY_PREFILL = True
+
+# A prompt of at most 64 tokens on an fp32 model runs its whole layer stack
+# as one C call (mtl_prefill_short) launching the same kernels, in the same
+# order, as the per-op path above: the bits are the same, and the ~100 us of
+# Python per layer that bounds an eager short prefill goes away.
+SHORT_PREFILL_NATIVE = True
 
 
 def _skinny_rows(x: torch.Tensor, w: torch.Tensor, enabled: bool = True) -> torch.Tensor | None:
@@ -535,10 +541,13 @@ class MambaLM(nn.Module):
         GraphedStepper captured, or `cache` itself) the final states are
         written into its tensors in place and out_cache is returned, so a
         captured decode graph can serve the next prompt without re-capture."""
-        x = self.embedding(input_ids)
-        new_layers: list[LayerCache] = []
         if out_cache is not None and len(out_cache.layers) != len(self.layers):
             raise ValueError("out_cache has the wrong number of layers")
+        native = self._prefill_short(input_ids, cache, out_cache)
+        if native is not None:
+            return native
+        x = self.embedding(input_ids)
+        new_layers: list[LayerCache] = []
 
         small = input_ids.numel() <= SMALL_PREFILL_TOKENS and not torch.cuda.is_current_stream_capturing()
         host_bound = small and SMALL_PREFILL_BLAS is not None
@@ -553,6 +562,74 @@ class MambaLM(nn.Module):
         with _prefer_blas(SMALL_PREFILL_BLAS if small else None):
             xf = self._run(x, layer)
         return self.lm_head(xf), (out_cache if out_cache is not None else MambaCache(new_layers))
+
+    # ---- short prompt as one C call ----
+    def _short_prefill_plan(self):
+        """ctypes array of mtl_prefill_layer holding every layer's weight
+        pointers, or None when a weight is not a contiguous float32 GPU
+        tensor.  Rebuilt whenever any weight tensor's address changes."""
+        ws = []
+        for blk in self.layers:
+            mx = blk.mixer
+            ws += [blk.norm.weight, mx.in_proj.weight, mx.in_proj.bias, mx.conv1d.weight, mx.conv1d.bias,
+                   mx.x_proj.weight, mx.dt_proj.weight, mx.dt_proj.bias, mx.A_log, mx.D, mx.out_proj.weight,
+                   mx.out_proj.bias]
+        ws.append(self.norm_f.weight)
+        key = tuple(0 if t is None else t.data_ptr() for t in ws)
+        plan = getattr(self, "_short_plan", None)
+        if plan is not None and plan[0] == key:
+            return plan[1]
+        arr = None
+        if all(t is None or (t.is_cuda and t.dtype == torch.float32 and t.is_contiguous()) for t in ws):
+            arr = (_lib.PrefillLayer * len(self.layers))()
+            for i, L in enumerate(arr):
+                (L.norm_w, L.W_in, L.b_in, L.conv_w, L.conv_b, L.W_x, L.W_dt, L.dt_bias, L.A_log, L.Dv, L.W_out,
+                 L.b_out) = key[12 * i:12 * i + 12]
+                L.eps = self.layers[i].norm.eps
+        self._short_plan = (key, arr)
+        return arr
+
+    def _prefill_short(self, input_ids, cache, out_cache):
+        """prefill() through mtl_prefill_short, or None where it does not
+        apply (more than 64 tokens, a layer shape or dtype it does not take,
+        caches that are not contiguous float32)."""
+        cfg = self.cfg
+        if not (SHORT_PREFILL_NATIVE and _SKINNY_PREFILL) or input_ids.dim() != 2 or not input_ids.is_cuda:
+            return None
+        b, l = input_ids.shape
+        D, N, K = cfg.d_inner, cfg.d_state, cfg.d_conv
+        if not ops.prefill_short_ok(b * l, cfg.d_model, D, N, cfg.dt_rank, K) or \
+                self.embedding.weight.dtype != torch.float32:
+            return None
+        for c in (cache, out_cache):
+            if c is not None and not all(
+                    tuple(lc.conv_state.shape) == (b, D, K - 1) and lc.conv_state.dtype == torch.float32 and
+                    lc.conv_state.is_contiguous() and tuple(lc.ssm_state.shape) == (b, D, N) and
+                    lc.ssm_state.dtype == torch.float32 and lc.ssm_state.is_contiguous() for lc in c.layers):
+                return None
+        arr = self._short_prefill_plan()
+        if arr is None:
+            return None
+        new_layers, held = [], []
+        for i, L in enumerate(arr):
+            lc = cache.layers[i] if cache is not None else None
+            if out_cache is not None:
+                conv_out, h_out = out_cache.layers[i].conv_state, out_cache.layers[i].ssm_state
+            else:
+                conv_out = torch.empty(b, D, K - 1, device=input_ids.device, dtype=torch.float32)
+                h_out = torch.empty(b, D, N, device=input_ids.device, dtype=torch.float32)
+                new_layers.append(LayerCache(conv_state=conv_out, ssm_state=h_out))
+            conv_in = lc.conv_state if lc is not None else None
+            if conv_in is not None and conv_in.data_ptr() == conv_out.data_ptr():
+                conv_in = conv_in.clone()        # the conv reads and writes different runs
+                held.append(conv_in)
+            L.conv_state_in = conv_in.data_ptr() if conv_in is not None else None
+            L.conv_state_out = conv_out.data_ptr()
+            L.h0 = lc.ssm_state.data_ptr() if lc is not None else None   # h_out may be h0
+            L.h_out = h_out.data_ptr()
+        h = self.embedding(input_ids).contiguous()
+        normed = ops.prefill_short(h, arr, self.norm_f.weight, self.norm_f.eps, D, N, cfg.dt_rank, K)
+        return self.lm_head(normed), (out_cache if out_cache is not None else MambaCache(new_layers))
 
     def step(self, input_ids: torch.Tensor, cache: MambaCache):
         """input_ids [b, 1] -> logits [b, 1, vocab]; cache updated in place

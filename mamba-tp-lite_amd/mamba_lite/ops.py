@@ -498,6 +498,47 @@ def xproj_sum_dt(parts, W_dt, x_dbl=None, write_x_dbl=True):
     return (x_dbl if write_x_dbl else parts[0]), dt
 
 
+def prefill_short_ok(rows, d_model, d_inner, d_state, dt_rank, d_conv) -> bool:
+    """Whether mtl_prefill_short takes a prompt of `rows` = b l tokens of this
+    layer shape."""
+    return (1 <= rows <= SKINNY_MAX_ROWS and d_model >= 256 and d_model % 128 == 0 and d_inner >= 512
+            and d_inner % 512 == 0 and 1 <= d_state <= 16 and 1 <= dt_rank <= XPROJ_SUM_DT_MAX_R
+            and (dt_rank + 2 * d_state) % 4 == 0 and 2 <= d_conv <= 4)
+
+
+def prefill_short(h, layers, norm_f, eps_f, d_inner, d_state, dt_rank, d_conv):
+    """mtl_prefill_short: a short prompt's whole layer stack in one call.
+    h [b, l, d_model] float32 holds the embedded tokens and is overwritten
+    with the final residual stream; `layers` is a ctypes array of
+    _lib.PrefillLayer (weights plus this call's cache pointers).  Returns
+    norm_f(h) [b, l, d_model]."""
+    _f32c(h, "h")
+    _f32c(norm_f, "norm_f")
+    b, l, M = h.shape
+    rows, J = b * l, dt_rank + 2 * d_state
+    if not prefill_short_ok(rows, M, d_inner, d_state, dt_rank, d_conv):
+        raise ValueError("prefill_short: sizes outside mtl_prefill_short")
+    # one workspace, every buffer on a 256-byte boundary
+    sizes = [rows * M, rows * d_inner, rows * d_inner, rows * d_inner, rows * d_inner, 16 * rows * J, rows * J,
+             4 * rows * M]
+    offs, n = [], 0
+    for s in sizes:
+        offs.append(n)
+        n += -(-s // 64) * 64
+    ws = torch.empty(n + rows * M, device=h.device, dtype=torch.float32)
+    normed = ws[n:].view(b, l, M)
+    base = ws.data_ptr()
+    a = _lib.PrefillShortArgs()
+    a.h = h.data_ptr()
+    a.xn, a.u, a.z, a.dt, a.y, a.x_parts, a.x_dbl, a.y_parts = [base + 4 * o for o in offs]
+    a.norm_f, a.normed_out, a.eps_f = norm_f.data_ptr(), normed.data_ptr(), float(eps_f)
+    a.d_conv, a.n_layers = d_conv, len(layers)
+    a.batch, a.seqlen, a.d_model, a.d_inner, a.d_state, a.dt_rank = b, l, M, d_inner, d_state, dt_rank
+    with _dev_guard(h):
+        _lib.check(_lib.load().mtl_prefill_short(ctypes.byref(a), layers, _stream(h)), "prefill_short")
+    return normed
+
+
 def _parts_array(parts):
     arr = (ctypes.c_void_p * len(parts))(*[p.data_ptr() for p in parts])
     return ctypes.cast(arr, ctypes.POINTER(ctypes.c_void_p)), arr

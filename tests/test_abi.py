@@ -44,6 +44,12 @@ def test_struct_layouts_match_header():
 
     assert ctypes.sizeof(_lib.ScanParams) == 8 * (6 * 4 + 5 + 4) + 4 * 4
     assert ctypes.sizeof(_lib.ConvParams) == 8 * (2 * 4 + 4 + 3) + 4 * 4
+    # mtl_prefill_layer: norm_w, eps + reserved, 15 pointers
+    assert ctypes.sizeof(_lib.PrefillLayer) == 8 + 4 + 4 + 15 * 8
+    assert _lib.PrefillLayer.W_in.offset == 16
+    # mtl_prefill_short_args: 11 pointers, eps_f and three int32, six int64 sizes
+    assert ctypes.sizeof(_lib.PrefillShortArgs) == 11 * 8 + 4 * 4 + 6 * 8
+    assert _lib.PrefillShortArgs.batch.offset == 104
 
 
 def test_invalid_arguments_are_rejected_without_a_gpu():
@@ -106,6 +112,16 @@ def test_invalid_arguments_are_rejected_without_a_gpu():
     ("mtl_linear_skinny", dict(N=6), b"multiple of 4"),
     ("mtl_linear_skinny", dict(rows_per_block=8), b"rows_per_block"),
     ("mtl_linear_skinny", dict(K=256, ksplit=2, y_ks=64), b"overlap"),
+    ("mtl_prefill_short", dict(batch=5, seqlen=13), b"batch * seqlen"),
+    ("mtl_prefill_short", dict(d_model=320), b"d_model"),
+    ("mtl_prefill_short", dict(d_inner=768), b"d_inner"),
+    ("mtl_prefill_short", dict(d_state=17), b"d_state"),
+    ("mtl_prefill_short", dict(d_conv=5), b"d_conv"),
+    ("mtl_prefill_short", dict(n_layers=0), b"n_layers"),
+    ("mtl_prefill_short", dict(null_ws=True), b"null workspace"),
+    ("mtl_prefill_short", dict(null_layer=True), b"layer 1: null required pointer"),
+    ("mtl_prefill_short", dict(alias=True), b"layer 1: conv_state_out must not alias"),
+    ("mtl_prefill_short", dict(d_state=15), b"multiple of 4"),
     ("mtl_in_proj_conv_xproj", dict(batch=33), b"batch must be in [1, 32]"),
     ("mtl_in_proj_conv_xproj", dict(d_model=128), b"at least 256"),
     ("mtl_in_proj_conv_xproj", dict(d_model=320), b"multiple of 128"),
@@ -176,6 +192,26 @@ def test_entry_points_validate_sizes_on_the_host(case):
         a.update(over)
         rc = lib.mtl_linear_skinny(P, a["K"], P, None, P, a["N"], a["y_ks"], a["M"], a["N"], a["K"], a["ksplit"],
                                    a["rows_per_block"], None)
+    elif name == "mtl_prefill_short":
+        a = dict(batch=1, seqlen=64, d_model=256, d_inner=512, d_state=16, d_conv=4, n_layers=2, null_ws=False,
+                 null_layer=False, alias=False)
+        a.update(over)
+        args = _lib.PrefillShortArgs()
+        for f, *_ in _lib.PrefillShortArgs._fields_[:11]:
+            setattr(args, f, None if a["null_ws"] and f == "y" else 16)
+        args.eps_f, args.d_conv, args.n_layers = 1e-5, a["d_conv"], a["n_layers"]
+        args.batch, args.seqlen, args.d_model, args.d_inner = a["batch"], a["seqlen"], a["d_model"], a["d_inner"]
+        args.d_state, args.dt_rank = a["d_state"], 16
+        layers = (_lib.PrefillLayer * 2)()
+        for i, L in enumerate(layers):
+            for f, *_ in _lib.PrefillLayer._fields_:
+                if f not in ("eps", "reserved"):
+                    setattr(L, f, 16 * (len(f) + 1))
+            L.conv_state_out = 32
+            L.conv_state_in = 32 if a["alias"] and i == 1 else 48
+            if a["null_layer"] and i == 1:
+                L.W_dt = None
+        rc = lib.mtl_prefill_short(ctypes.byref(args), layers, None)
     elif name == "mtl_in_proj_conv_xproj":
         a = dict(batch=8, d_model=256, d_inner=64, cpp=16, d_conv=4, J=40)
         a.update(over)

@@ -481,6 +481,7 @@ def test_short_prefill_on_the_skinny_gemm_vs_oracle(b, l, monkeypatch):
     import mamba_lite.model as mm
     from mamba_lite import ops as mops
     monkeypatch.setattr(mm, "SMALL_PREFILL_BLAS", None)
+    monkeypatch.setattr(mm, "SHORT_PREFILL_NATIVE", False)    # the per-op launches themselves
     torch.manual_seed(11)
     cfg = MambaConfig(d_model=256, n_layer=2, vocab_size=384, d_state=16)
     with torch.device(DEV):
@@ -605,3 +606,57 @@ def test_short_prefill_conv_widths_and_biases(d_conv, bias, b, l, monkeypatch):
     for lc, (rcs, rhs) in zip(cache.layers, rcache):
         assert_rel(_np(lc.conv_state), rcs, 1e-4, "conv_state")
         assert_rel(_np(lc.ssm_state), rhs, 1e-4, "ssm_state")
+
+
+@pytest.mark.parametrize("d_conv,bias,b,l", [(4, False, 1, 64), (4, False, 2, 20), (3, True, 4, 9), (2, False, 1, 1),
+                                             (4, True, 2, 32)])
+def test_native_short_prefill_equals_the_per_op_path(d_conv, bias, b, l, monkeypatch):
+    """mtl_prefill_short (a short prompt's layer stack as one C call) against
+    the per-op path it replaces (the same kernels launched one by one from
+    Python): logits and every final state bit for bit, for a fresh prompt
+    and for one continued from a cache into that same cache; against the
+    float64 oracle at 1e-4; and again after a weight is replaced by a tensor
+    at another address (the call's pointer table is rebuilt)."""
+    import mamba_lite.model as mm
+    from mamba_lite import ops as mops
+    monkeypatch.setattr(mm, "SMALL_PREFILL_BLAS", None)
+    print(f"native short prefill d_conv={d_conv} bias={bias} b={b} l={l}", flush=True)
+    torch.manual_seed(50 + d_conv + l)
+    cfg = MambaConfig(d_model=256, n_layer=3, vocab_size=320, d_state=16, d_conv=d_conv, bias=bias)
+    with torch.device(DEV):
+        model = MambaLM(cfg).eval()
+    _init_dt_bias(model, 50)
+    calls = []
+    real = mops.prefill_short
+    monkeypatch.setattr(mops, "prefill_short", lambda *a, **k: calls.append(1) or real(*a, **k))
+    ids = torch.randint(0, cfg.vocab_size, (b, l), device=DEV)
+    ids2 = torch.randint(0, cfg.vocab_size, (b, l), device=DEV)
+
+    def run():
+        with torch.no_grad():
+            lg, c = model.prefill(ids)
+            snap = [(x.conv_state.clone(), x.ssm_state.clone()) for x in c.layers]
+            lg2, same = model.prefill(ids2, cache=c, out_cache=c)
+        assert same is c
+        return [lg, lg2] + [t for pair in snap for t in pair] + [t for x in c.layers for t in (x.conv_state,
+                                                                                                x.ssm_state)]
+
+    nat = run()
+    assert len(calls) == 2
+    monkeypatch.setattr(mm, "SHORT_PREFILL_NATIVE", False)
+    per = run()
+    assert len(calls) == 2
+    for k, (x, y) in enumerate(zip(nat, per)):
+        assert torch.equal(x, y), k
+    ref, rcache = om.lm_prefill(_lm_weights(model), ids.cpu().numpy(), dtype=np.float64)
+    assert_rel(_np(nat[0]), ref, 1e-4, "logits")
+    for i, (rcs, rhs) in enumerate(rcache):
+        assert_rel(_np(nat[2 + 2 * i]), rcs, 1e-4, "conv_state")
+        assert_rel(_np(nat[3 + 2 * i]), rhs, 1e-4, "ssm_state")
+    w = model.layers[1].mixer.out_proj.weight
+    w.data = (0.5 * w.data).clone()
+    with torch.no_grad():
+        lp, _ = model.prefill(ids)
+        monkeypatch.setattr(mm, "SHORT_PREFILL_NATIVE", True)
+        ln, _ = model.prefill(ids)
+    assert len(calls) == 3 and torch.equal(ln, lp) and not torch.equal(ln, nat[0])
