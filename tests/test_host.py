@@ -235,3 +235,31 @@ def test_generate_has_no_sampling_path():
     model = MambaLM(cfg)
     with pytest.raises(NotImplementedError):
         model.generate(torch.zeros(1, 3, dtype=torch.long), 2, greedy=False)
+
+
+@pytest.mark.parametrize("rows,M,D,N,R,K,ok", [
+    (64, 768, 1536, 16, 48, 4, True),       # 130m shape, 64 tokens
+    (1, 2048, 4096, 16, 128, 4, True),      # 1.4b shape, one token
+    (65, 768, 1536, 16, 48, 4, False),      # more than 64 token rows
+    (64, 128, 512, 16, 8, 4, False),        # d_model below 256
+    (64, 320, 1024, 16, 20, 4, False),      # d_model not a multiple of 128
+    (64, 384, 768, 16, 24, 4, False),       # d_inner not a multiple of 512
+    (64, 768, 1536, 17, 48, 4, False),      # d_state above 16
+    (64, 768, 1536, 15, 48, 4, False),      # dt_rank + 2 d_state not a multiple of 4
+    (64, 768, 1536, 16, 161, 4, False),     # dt_rank above 160
+    (64, 768, 1536, 16, 48, 5, False),      # conv width 5
+    (64, 768, 1536, 16, 48, 1, False),      # conv width 1
+])
+def test_prefill_short_covers_the_sizes_its_kernels_take(rows, M, D, N, R, K, ok):
+    """ops.prefill_short_ok admits exactly the sizes mtl_prefill_short
+    checks on the host (the same bounds the C-ABI rejection tests hold)."""
+    assert ops.prefill_short_ok(rows, M, D, N, R, K) is ok
+
+
+def test_prefill_short_is_not_taken_off_the_gpu():
+    """MambaLM._prefill_short declines CPU token ids and non-fp32 models
+    before touching the library, so prefill() keeps its other paths there."""
+    cfg = MambaConfig(d_model=256, n_layer=1, vocab_size=64, d_state=16)
+    model = MambaLM(cfg)
+    assert model._prefill_short(torch.zeros(1, 8, dtype=torch.long), None, None) is None
+    assert not hasattr(model, "_short_plan")
