@@ -1,7 +1,7 @@
 """Benchmark of the Mamba mixer hot path on one MI355X.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W]
-                   [--only scan|decode|quant|shard|prefill|copy|decode-counters|all]
+                   [--only scan|decode|quant|shard|prefill|prefill-short|copy|decode-counters|all]
 
 Headline (`value`): fused selective-scan prefill throughput, fp32, on the
 isolated-op workload u, delta, z [32, 1536, 1024], B, C [32, 16, 1024],
@@ -467,7 +467,8 @@ def main():
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--only", default="all",
-                    choices=["all", "scan", "decode", "quant", "shard", "prefill", "copy", "decode-counters"])
+                    choices=["all", "scan", "decode", "quant", "shard", "prefill", "prefill-short", "copy",
+                             "decode-counters"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--decode-shapes", default="130m,1.4b", help="comma list of 130m, 1.4b")
     args = ap.parse_args()
@@ -500,6 +501,15 @@ def main():
             dst.copy_(src)
         torch.cuda.synchronize()
         print(json.dumps({"copy_bytes_each_way": n * 4, "launches": 5}), flush=True)
+        return
+    if args.only == "prefill-short":
+        # the eager 64-token prompt alone (130m shape, b=1, fp32), for a
+        # rocprofv3 trace of the one-call short prefill: 3 warmup prompts, then
+        # the 20 timed ones of the prefill_tok_s entry
+        model = build_lm(MambaConfig(d_model=768, n_layer=24, vocab_size=50280), dev)
+        tok_s = bench_prefill(model, 1, 64, dev)
+        log(f"prefill-short 130m b=1 x 64 eager: {tok_s:.0f} tok/s, {64 / tok_s * 1e6:.1f} us per prompt")
+        print(json.dumps({"prefill_tok_s": {"130m_b1_l64": tok_s}}), flush=True)
         return
     if args.only == "decode-counters":
         # a short workload for rocprofv3 --pmc runs over the decode kernels
