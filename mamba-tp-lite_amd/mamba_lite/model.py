@@ -607,9 +607,12 @@ class MambaLM(nn.Module):
                     lc.conv_state.is_contiguous() and tuple(lc.ssm_state.shape) == (b, D, N) and
                     lc.ssm_state.dtype == torch.float32 and lc.ssm_state.is_contiguous() for lc in c.layers):
                 return None
-        arr = self._short_prefill_plan()
-        if arr is None:
+        tmpl = self._short_prefill_plan()
+        if tmpl is None:
             return None
+        # a copy per call: the library reads it while ctypes has released the
+        # GIL, so another thread's prefill must not rewrite its cache pointers
+        arr = type(tmpl).from_buffer_copy(tmpl)
         new_layers, held = [], []
         for i, L in enumerate(arr):
             lc = cache.layers[i] if cache is not None else None
