@@ -135,10 +135,12 @@ SPLIT_PROJ_MIN_TOKENS = 16384
 # host is the bottleneck (measured on MI355X at the 130m shape, 64 tokens: 4
 # projections per layer, device time 3-13 us each).  The tied lm_head stays on
 # hipBLASLt, whose kernel is faster there (54 us against 91 us for 64 x 50280).
-# Set SMALL_PREFILL_BLAS to None to leave torch's backend choice alone.  A
-# prefill being captured into a HIP graph (cuda_graph.GraphedPrefill) has no
-# host cost per launch, so it keeps hipBLASLt (a 64-token 130m prefill replays
-# in 1.42 ms that way against 1.64 ms on rocBLAS).
+# An fp32 prompt of <= 64 tokens that mtl_prefill_short takes (below) never
+# reaches these GEMMs.  Set SMALL_PREFILL_BLAS to None to leave torch's backend
+# choice alone.  A prefill being captured into a HIP graph
+# (cuda_graph.GraphedPrefill) has no host cost per launch, so it keeps
+# hipBLASLt (a 64-token 130m prefill on library GEMMs replayed in 1.42 ms that
+# way against 1.64 ms on rocBLAS).
 SMALL_PREFILL_TOKENS = 256
 SMALL_PREFILL_BLAS: str | None = "cublas"
 
