@@ -459,6 +459,63 @@ int mtl_decode_ssm(const float* xpart, int32_t nblk, const float* xc, const floa
                    const float* b_dt, const float* A_log, const float* Dv, float* ssm_state, float* y,
                    int32_t batch, int32_t d_inner, int32_t d_state, int32_t dt_rank, mtl_stream_t stream);
 
+/* ------------------------------------------------------------------------
+ * mtl_decode_step: one fused decode step of the whole layer stack in one
+ * call -- MambaLM.step (model.py:343-353) over MambaBlock.step (308-311)
+ * and MambaMixer.step (249-294) -- fp32, batch 1, 2 or 4: per layer
+ * mtl_decode_in, [mtl_decode_gemv_parts], mtl_decode_ssm, mtl_decode_gemv,
+ * then mtl_decode_norm_gemv into logits [b, vocab].  The same launches with
+ * the same arguments as calling those entry points one by one, so the same
+ * bits.  With split_k, decode_in forms the x_proj partials from W_xT
+ * ([d_inner, J], x_proj transposed) in blocks of channels_per_block, and
+ * xpart holds ceil(d_inner / channels_per_block) of them; without it, x_proj
+ * (W_x [J, d_inner]) runs as xproj_parts column parts.  Each layer's
+ * conv_state [b, d_inner, d_conv - 1] and ssm_state [b, d_inner, d_state]
+ * are updated in place.  Workspace: xc, gz, y [b, d_inner]; x0, x1, resid
+ * [b, d_model]; xpart [parts, b, J].  Every layer's pointers are checked
+ * before the first launch.
+ * ---------------------------------------------------------------------- */
+typedef struct {
+    const float* norm_w;       /* [d_model] the block's RMSNorm */
+    float eps;
+    int32_t reserved;
+    const float* W_in;         /* [2 d_inner, d_model] */
+    const float* b_in;         /* [2 d_inner] or NULL */
+    const float* conv_w;       /* [d_inner, d_conv] */
+    const float* conv_b;       /* [d_inner] or NULL */
+    const float* W_xT;         /* [d_inner, J] (split_k) or NULL */
+    const float* W_x;          /* [J, d_inner] (without split_k) or NULL */
+    const float* W_dt;         /* [d_inner, dt_rank] */
+    const float* dt_bias;      /* [d_inner] or NULL */
+    const float* A_log;        /* [d_inner, d_state] */
+    const float* Dv;           /* [d_inner] or NULL */
+    const float* W_out;        /* [d_model, d_inner] */
+    const float* b_out;        /* [d_model] or NULL */
+    float* conv_state;
+    float* ssm_state;
+} mtl_decode_layer;
+
+typedef struct {
+    const int64_t* ids;        /* [b] token ids */
+    const float* emb;          /* [vocab, d_model], also the tied lm_head */
+    const float* norm_f;       /* [d_model] */
+    float* logits;             /* [b, vocab] */
+    float* xc;
+    float* gz;
+    float* y;
+    float* x0;
+    float* x1;
+    float* resid;
+    float* xpart;
+    float eps_f;
+    int32_t vocab;
+    int32_t n_layers;
+    int32_t batch;
+    int32_t d_model, d_inner, d_state, dt_rank, d_conv, channels_per_block, split_k, xproj_parts;
+} mtl_decode_step_args;
+
+int mtl_decode_step(const mtl_decode_step_args* args, const mtl_decode_layer* layers, mtl_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

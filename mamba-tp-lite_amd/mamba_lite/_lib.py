@@ -73,6 +73,27 @@ class PrefillShortArgs(ctypes.Structure):
     ]
 
 
+class DecodeLayer(ctypes.Structure):
+    """mirror of mtl_decode_layer"""
+    _fields_ = [
+        ("norm_w", _vp), ("eps", ctypes.c_float), ("reserved", _i32),
+        ("W_in", _vp), ("b_in", _vp), ("conv_w", _vp), ("conv_b", _vp), ("W_xT", _vp), ("W_x", _vp),
+        ("W_dt", _vp), ("dt_bias", _vp), ("A_log", _vp), ("Dv", _vp), ("W_out", _vp), ("b_out", _vp),
+        ("conv_state", _vp), ("ssm_state", _vp),
+    ]
+
+
+class DecodeStepArgs(ctypes.Structure):
+    """mirror of mtl_decode_step_args"""
+    _fields_ = [
+        ("ids", _vp), ("emb", _vp), ("norm_f", _vp), ("logits", _vp), ("xc", _vp), ("gz", _vp), ("y", _vp),
+        ("x0", _vp), ("x1", _vp), ("resid", _vp), ("xpart", _vp),
+        ("eps_f", ctypes.c_float), ("vocab", _i32), ("n_layers", _i32), ("batch", _i32),
+        ("d_model", _i32), ("d_inner", _i32), ("d_state", _i32), ("dt_rank", _i32), ("d_conv", _i32),
+        ("channels_per_block", _i32), ("split_k", _i32), ("xproj_parts", _i32),
+    ]
+
+
 # name -> (restype, argtypes); every symbol of include/mtl.h
 SIGNATURES = {
     "mtl_last_error": (ctypes.c_char_p, []),
@@ -87,6 +108,7 @@ SIGNATURES = {
     "mtl_sum_parts": (ctypes.c_int, [_fp, _i32, _i64, _fp, _vp]),
     "mtl_xproj_sum_dt": (ctypes.c_int, [_fp, _i32, _i64, _i32, _fp, _i32, _i64, _fp, _fp, _vp]),
     "mtl_prefill_short": (ctypes.c_int, [ctypes.POINTER(PrefillShortArgs), ctypes.POINTER(PrefillLayer), _vp]),
+    "mtl_decode_step": (ctypes.c_int, [ctypes.POINTER(DecodeStepArgs), ctypes.POINTER(DecodeLayer), _vp]),
     "mtl_conv_step_xproj": (ctypes.c_int, [_fp, _fp, _i64, _fp, _fp, _fp, _i64, _fp, _fp, _i64, _i64, _i32, _i32,
                                            _vp]),
     "mtl_conv_step_xproj_noalloc": (ctypes.c_int, [_fp, _fp, _i64, _fp, _fp, _fp, _i64, _fp, _fp, _i64, _i64, _i32,

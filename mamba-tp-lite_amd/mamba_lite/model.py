@@ -165,6 +165,12 @@ _SKINNY_PREFILL = True
 # Python per layer that bounds an eager short prefill goes away.
 SHORT_PREFILL_NATIVE = True
 
+# The fused decode step (fp32, batch 1 and 2) runs its whole layer stack as
+# one C call (mtl_decode_step) launching the same kernels with the same
+# arguments as the per-layer Python loop: the same bits, without the Python
+# per launch that bounds an eager step.
+DECODE_STEP_NATIVE = True
+
 
 def _skinny_rows(x: torch.Tensor, w: torch.Tensor, enabled: bool = True) -> torch.Tensor | None:
     """x [..., K] as the [rows, K] operand of mtl_linear_skinny, or None
@@ -718,6 +724,30 @@ class MambaLM(nn.Module):
                       "split_k_max_b": split_k_max_b}
         return self._plan
 
+    def _decode_step_template(self, plan, split_k):
+        """ctypes array of mtl_decode_layer with every layer's weight pointers
+        (x_proj transposed from the decode plan with split_k, as is without),
+        rebuilt whenever any of those tensors' addresses change."""
+        ws = []
+        for blk, lp in zip(self.layers, plan["layers"]):
+            mx = blk.mixer
+            ws += [blk.norm.weight, mx.in_proj.weight, mx.in_proj.bias, lp["conv_w"], mx.conv1d.bias,
+                   lp["W_xT"] if split_k else None, None if split_k else mx.x_proj.weight, mx.dt_proj.weight,
+                   mx.dt_proj.bias, mx.A_log, mx.D, mx.out_proj.weight, mx.out_proj.bias]
+        key = tuple(0 if t is None else t.data_ptr() for t in ws)
+        cached = getattr(self, "_step_tmpl", {}).get(split_k)
+        if cached is not None and cached[0] == key:
+            return cached[1]
+        arr = (_lib.DecodeLayer * len(self.layers))()
+        for i, L in enumerate(arr):
+            (L.norm_w, L.W_in, L.b_in, L.conv_w, L.conv_b, L.W_xT, L.W_x, L.W_dt, L.dt_bias, L.A_log, L.Dv, L.W_out,
+             L.b_out) = key[13 * i:13 * i + 13]
+            L.eps = self.layers[i].norm.eps
+        if not hasattr(self, "_step_tmpl"):
+            self._step_tmpl = {}
+        self._step_tmpl[split_k] = (key, arr)
+        return arr
+
     def _step_fused(self, input_ids, cache):
         cfg = self.cfg
         plan = self._decode_plan()
@@ -739,6 +769,15 @@ class MambaLM(nn.Module):
         # stream (measured at d_model 2048: 12.87 -> 12.63 us; at batch 2 and 4
         # the 8-channel blocks are faster)
         cpb = 4 if b == 1 and not split_k else plan["cpb"]
+        if DECODE_STEP_NATIVE:
+            logits = torch.empty(b, self.embedding.weight.shape[0], **f32)
+            tmpl = self._decode_step_template(plan, split_k)
+            arr = type(tmpl).from_buffer_copy(tmpl)     # per call: read by the library without the GIL
+            for L, lc in zip(arr, cache.layers):
+                L.conv_state, L.ssm_state = lc.conv_state.data_ptr(), lc.ssm_state.data_ptr()
+            ops.decode_step(arr, ids, self.embedding.weight, _f32(self.norm_f.weight), self.norm_f.eps, logits,
+                            xc, gz, y, xs, xpart, cfg, cpb, split_k, xp_parts)
+            return logits.unsqueeze(1)
         x_cur = None
         for i, blk in enumerate(self.layers):
             mx, lp, lc = blk.mixer, plan["layers"][i], cache.layers[i]

@@ -539,6 +539,34 @@ def prefill_short(h, layers, norm_f, eps_f, d_inner, d_state, dt_rank, d_conv):
     return normed
 
 
+def decode_step(layers, ids, emb, norm_f, eps_f, logits, xc, gz, y, xs, xpart, cfg, channels_per_block, split_k,
+                xproj_parts):
+    """mtl_decode_step: one fused decode step of every layer in one call.
+    `layers` is a ctypes array of _lib.DecodeLayer (weights and this call's
+    cache pointers); ids [b] int64; logits [b, vocab] receives norm_f + the
+    tied lm_head; xc, gz, y [b, d_inner], xs three [b, d_model] and xpart
+    [parts, b, J] are the workspace, all float32 contiguous on one device."""
+    for t, name in ((emb, "emb"), (norm_f, "norm_f"), (logits, "logits"), (xc, "xc"), (gz, "gz"), (y, "y"),
+                    (xpart, "xpart"), *((x, "xs") for x in xs)):
+        _f32c(t, name)
+    if ids.dtype != torch.int64 or not ids.is_contiguous():
+        raise ValueError("decode_step: ids must be contiguous int64")
+    b, D = xc.shape
+    J = cfg.dt_rank + 2 * cfg.d_state
+    if ids.numel() != b or tuple(logits.shape) != (b, emb.shape[0]) or xpart.shape[1:] != (b, J):
+        raise ValueError("decode_step: ids [b], logits [b, vocab], xpart [parts, b, J] expected")
+    a = _lib.DecodeStepArgs()
+    a.ids, a.emb, a.norm_f, a.logits = ids.data_ptr(), emb.data_ptr(), norm_f.data_ptr(), logits.data_ptr()
+    a.xc, a.gz, a.y, a.xpart = xc.data_ptr(), gz.data_ptr(), y.data_ptr(), xpart.data_ptr()
+    a.x0, a.x1, a.resid = xs[0].data_ptr(), xs[1].data_ptr(), xs[2].data_ptr()
+    a.eps_f, a.vocab, a.n_layers, a.batch = float(eps_f), emb.shape[0], len(layers), b
+    a.d_model, a.d_inner, a.d_state, a.dt_rank, a.d_conv = emb.shape[1], D, cfg.d_state, cfg.dt_rank, cfg.d_conv
+    a.channels_per_block, a.split_k, a.xproj_parts = channels_per_block, int(split_k), xproj_parts
+    with _dev_guard(xc):
+        _lib.check(_lib.load().mtl_decode_step(ctypes.byref(a), layers, _stream(xc)), "decode_step")
+    return logits
+
+
 def _parts_array(parts):
     arr = (ctypes.c_void_p * len(parts))(*[p.data_ptr() for p in parts])
     return ctypes.cast(arr, ctypes.POINTER(ctypes.c_void_p)), arr

@@ -50,6 +50,11 @@ def test_struct_layouts_match_header():
     # mtl_prefill_short_args: 11 pointers, eps_f and three int32, six int64 sizes
     assert ctypes.sizeof(_lib.PrefillShortArgs) == 11 * 8 + 4 * 4 + 6 * 8
     assert _lib.PrefillShortArgs.batch.offset == 104
+    # mtl_decode_layer: norm_w, eps + reserved, 14 pointers
+    assert ctypes.sizeof(_lib.DecodeLayer) == 8 + 4 + 4 + 14 * 8
+    # mtl_decode_step_args: 11 pointers, eps_f, then eleven int32
+    assert ctypes.sizeof(_lib.DecodeStepArgs) == 11 * 8 + 4 + 11 * 4
+    assert _lib.DecodeStepArgs.eps_f.offset == 88
 
 
 def test_invalid_arguments_are_rejected_without_a_gpu():
@@ -122,6 +127,13 @@ def test_invalid_arguments_are_rejected_without_a_gpu():
     ("mtl_prefill_short", dict(null_layer=True), b"layer 1: null required pointer"),
     ("mtl_prefill_short", dict(alias=True), b"layer 1: conv_state_out must not alias"),
     ("mtl_prefill_short", dict(d_state=15), b"multiple of 4"),
+    ("mtl_decode_step", dict(batch=3), b"batch must be 1, 2 or 4"),
+    ("mtl_decode_step", dict(cpb=16), b"channels_per_block"),
+    ("mtl_decode_step", dict(n_layers=0), b"n_layers"),
+    ("mtl_decode_step", dict(split_k=0, xproj_parts=0), b"xproj_parts"),
+    ("mtl_decode_step", dict(null_ws=True), b"null workspace"),
+    ("mtl_decode_step", dict(null_layer=True), b"layer 1: null required pointer"),
+    ("mtl_decode_step", dict(split_k=0, xproj_parts=4, null_layer=False), b"layer 0: null required pointer"),
     ("mtl_in_proj_conv_xproj", dict(batch=33), b"batch must be in [1, 32]"),
     ("mtl_in_proj_conv_xproj", dict(d_model=128), b"at least 256"),
     ("mtl_in_proj_conv_xproj", dict(d_model=320), b"multiple of 128"),
@@ -212,6 +224,23 @@ def test_entry_points_validate_sizes_on_the_host(case):
             if a["null_layer"] and i == 1:
                 L.W_dt = None
         rc = lib.mtl_prefill_short(ctypes.byref(args), layers, None)
+    elif name == "mtl_decode_step":
+        a = dict(batch=1, cpb=8, n_layers=2, split_k=1, xproj_parts=1, null_ws=False, null_layer=False)
+        a.update(over)
+        args = _lib.DecodeStepArgs()
+        for f, *_ in _lib.DecodeStepArgs._fields_[:11]:
+            setattr(args, f, None if a["null_ws"] and f == "gz" else 16)
+        args.eps_f, args.vocab, args.n_layers, args.batch = 1e-5, 64, a["n_layers"], a["batch"]
+        args.d_model, args.d_inner, args.d_state, args.dt_rank, args.d_conv = 256, 512, 16, 16, 4
+        args.channels_per_block, args.split_k, args.xproj_parts = a["cpb"], a["split_k"], a["xproj_parts"]
+        layers = (_lib.DecodeLayer * 2)()
+        for i, L in enumerate(layers):
+            for f, *_ in _lib.DecodeLayer._fields_:
+                if f not in ("eps", "reserved", "W_x"):       # W_x unset: only split_k layers are complete
+                    setattr(L, f, 16)
+            if a["null_layer"] and i == 1:
+                L.A_log = None
+        rc = lib.mtl_decode_step(ctypes.byref(args), layers, None)
     elif name == "mtl_in_proj_conv_xproj":
         a = dict(batch=8, d_model=256, d_inner=64, cpp=16, d_conv=4, J=40)
         a.update(over)

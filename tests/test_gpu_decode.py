@@ -316,3 +316,40 @@ def test_decode_gemv_row_kernel_equals_the_staged_kernel(cols, rows):
         out2 = torch.empty(2, rows, device=DEV)
         ops.decode_gemv(v[i:i + 2].clone(), W, out2, bias=bias, x_in=x_in[i:i + 2].clone())
         assert torch.equal(out2, out4[i:i + 2]), i
+
+
+@pytest.mark.parametrize("d_model,b,fused_max", [(256, 1, 2), (256, 2, 2), (256, 4, 4), (2048, 1, 2), (2048, 2, 2)])
+def test_native_decode_step_equals_the_per_layer_loop(d_model, b, fused_max, monkeypatch):
+    """mtl_decode_step (every layer of a fused decode step in one C call)
+    against the per-layer Python loop it replaces: logits and every layer's
+    conv and SSM state bit for bit over three steps, at a width where
+    decode_in forms the x_proj partials (d_model 256) and one where x_proj
+    runs as its own column-part GEMV (d_model 2048)."""
+    import mamba_lite.model as mm
+    from mamba_lite import ops as mops
+    from mamba_lite.model import MambaCache, MambaConfig, MambaLM
+    monkeypatch.setattr(mm, "FUSED_STEP_MAX_BATCH", fused_max)
+    print(f"native decode step d_model={d_model} b={b}", flush=True)
+    torch.manual_seed(70 + b)
+    cfg = MambaConfig(d_model=d_model, n_layer=2, vocab_size=320, d_state=16)
+    with torch.device("cuda"):
+        model = MambaLM(cfg).eval()
+    calls = []
+    real = mops.decode_step
+    monkeypatch.setattr(mops, "decode_step", lambda *a, **k: calls.append(1) or real(*a, **k))
+    ids = torch.randint(0, cfg.vocab_size, (b, 6), device="cuda")
+    steps = [torch.randint(0, cfg.vocab_size, (b, 1), device="cuda") for _ in range(3)]
+
+    def run():
+        with torch.no_grad():
+            _, cache = model.prefill(ids)
+            out = [model.step(s, cache).clone() for s in steps]
+        return out + [t for lc in cache.layers for t in (lc.conv_state, lc.ssm_state)]
+
+    nat = run()
+    assert len(calls) == 3
+    monkeypatch.setattr(mm, "DECODE_STEP_NATIVE", False)
+    per = run()
+    assert len(calls) == 3
+    for k, (x, y) in enumerate(zip(nat, per)):
+        assert torch.equal(x, y), k
