@@ -472,8 +472,9 @@ int mtl_decode_ssm(const float* xpart, int32_t nblk, const float* xc, const floa
  * (W_x [J, d_inner]) runs as xproj_parts column parts.  Each layer's
  * conv_state [b, d_inner, d_conv - 1] and ssm_state [b, d_inner, d_state]
  * are updated in place.  Workspace: xc, gz, y [b, d_inner]; x0, x1, resid
- * [b, d_model]; xpart [parts, b, J].  Every layer's pointers are checked
- * before the first launch.
+ * [b, d_model]; xpart [parts, b, J].  d_model and d_inner multiples of 4 up
+ * to 4096, d_state <= 16, dt_rank <= 256, d_conv 2..8.  Every layer's
+ * pointers and these sizes are checked before the first launch.
  * ---------------------------------------------------------------------- */
 typedef struct {
     const float* norm_w;       /* [d_model] the block's RMSNorm */
@@ -486,7 +487,7 @@ typedef struct {
     const float* W_xT;         /* [d_inner, J] (split_k) or NULL */
     const float* W_x;          /* [J, d_inner] (without split_k) or NULL */
     const float* W_dt;         /* [d_inner, dt_rank] */
-    const float* dt_bias;      /* [d_inner] or NULL */
+    const float* dt_bias;      /* [d_inner] */
     const float* A_log;        /* [d_inner, d_state] */
     const float* Dv;           /* [d_inner] or NULL */
     const float* W_out;        /* [d_model, d_inner] */

@@ -33,12 +33,19 @@ extern "C" int mtl_decode_step(const mtl_decode_step_args* a, const mtl_decode_l
     MTL_REQUIRE(a->vocab >= 1, "vocab must be >= 1");
     MTL_REQUIRE(cpb == 4 || cpb == 8, "channels_per_block must be 8 or 4");
     MTL_REQUIRE(split_k || a->xproj_parts >= 1, "xproj_parts must be >= 1 without W_xT");
+    // the sizes the per-layer entry points take, checked here so that a bad
+    // size fails before the first layer's conv history is updated
+    MTL_REQUIRE(M >= 4 && M % 4 == 0 && M <= 4096, "d_model must be a multiple of 4, at most 4096");
+    MTL_REQUIRE(D >= 4 && D % 4 == 0 && D <= 4096, "d_inner must be a multiple of 4, at most 4096");
+    MTL_REQUIRE(N >= 1 && N <= 16 && R >= 1 && R <= 256, "d_state must be in [1, 16] and dt_rank in [1, 256]");
+    MTL_REQUIRE(K >= 2 && K <= 8, "d_conv must be in [2, 8]");
     MTL_REQUIRE(a->ids && a->emb && a->norm_f && a->logits && a->xc && a->gz && a->y && a->x0 && a->x1 &&
                 a->resid && a->xpart, "null workspace pointer");
     // every layer is checked before the first launch
     for (int32_t i = 0; i < a->n_layers; ++i) {
         const mtl_decode_layer& L = layers[i];
-        MTL_REQUIRE(L.norm_w && L.W_in && L.conv_w && L.W_dt && L.A_log && L.W_out && L.conv_state && L.ssm_state &&
+        MTL_REQUIRE(L.norm_w && L.W_in && L.conv_w && L.W_dt && L.dt_bias && L.A_log && L.W_out && L.conv_state &&
+                    L.ssm_state &&
                     (split_k ? L.W_xT != nullptr : L.W_x != nullptr),
                     "layer " + std::to_string(i) + ": null required pointer");
     }

@@ -129,6 +129,9 @@ def test_invalid_arguments_are_rejected_without_a_gpu():
     ("mtl_prefill_short", dict(d_state=15), b"multiple of 4"),
     ("mtl_decode_step", dict(batch=3), b"batch must be 1, 2 or 4"),
     ("mtl_decode_step", dict(cpb=16), b"channels_per_block"),
+    ("mtl_decode_step", dict(d_state=17), b"d_state"),
+    ("mtl_decode_step", dict(d_inner=8192), b"d_inner"),
+    ("mtl_decode_step", dict(d_conv=9), b"d_conv"),
     ("mtl_decode_step", dict(n_layers=0), b"n_layers"),
     ("mtl_decode_step", dict(split_k=0, xproj_parts=0), b"xproj_parts"),
     ("mtl_decode_step", dict(null_ws=True), b"null workspace"),
@@ -225,13 +228,15 @@ def test_entry_points_validate_sizes_on_the_host(case):
                 L.W_dt = None
         rc = lib.mtl_prefill_short(ctypes.byref(args), layers, None)
     elif name == "mtl_decode_step":
-        a = dict(batch=1, cpb=8, n_layers=2, split_k=1, xproj_parts=1, null_ws=False, null_layer=False)
+        a = dict(batch=1, cpb=8, n_layers=2, split_k=1, xproj_parts=1, null_ws=False, null_layer=False, d_state=16,
+                 d_inner=512, d_conv=4)
         a.update(over)
         args = _lib.DecodeStepArgs()
         for f, *_ in _lib.DecodeStepArgs._fields_[:11]:
             setattr(args, f, None if a["null_ws"] and f == "gz" else 16)
         args.eps_f, args.vocab, args.n_layers, args.batch = 1e-5, 64, a["n_layers"], a["batch"]
-        args.d_model, args.d_inner, args.d_state, args.dt_rank, args.d_conv = 256, 512, 16, 16, 4
+        args.d_model, args.d_inner, args.d_state, args.dt_rank, args.d_conv = 256, a["d_inner"], a["d_state"], 16, \
+            a["d_conv"]
         args.channels_per_block, args.split_k, args.xproj_parts = a["cpb"], a["split_k"], a["xproj_parts"]
         layers = (_lib.DecodeLayer * 2)()
         for i, L in enumerate(layers):
