@@ -41,15 +41,43 @@ extern "C" int mtl_decode_step(const mtl_decode_step_args* a, const mtl_decode_l
     MTL_REQUIRE(K >= 2 && K <= 8, "d_conv must be in [2, 8]");
     MTL_REQUIRE(a->ids && a->emb && a->norm_f && a->logits && a->xc && a->gz && a->y && a->x0 && a->x1 &&
                 a->resid && a->xpart, "null workspace pointer");
-    // every layer is checked before the first launch
+    // the LDS tiles of decode_in (b d_model), of the out_proj GEMV (b d_inner)
+    // and of the norm + lm_head GEMV (b d_model)
+    MTL_REQUIRE((size_t)b * M * sizeof(float) <= 60 * 1024, "batch * d_model too large for the decode LDS tile");
+    MTL_REQUIRE((size_t)b * D * sizeof(float) <= 64 * 1024, "batch * d_inner too large for the decode LDS tile");
+    const int32_t nblk = split_k ? (D + cpb - 1) / cpb : a->xproj_parts;
+    if (!split_k) {
+        // mtl_decode_gemv_parts: d_inner in xproj_parts column parts of whole
+        // float4 runs, each at most 4096 columns
+        MTL_REQUIRE(a->xproj_parts <= 64, "xproj_parts must be in [1, 64]");
+        MTL_REQUIRE(D % (4 * a->xproj_parts) == 0, "d_inner must be a multiple of 4 * xproj_parts");
+    }
+    {
+        // mtl_decode_ssm: Q threads per (j, batch) pair sum at most 64 partials each
+        const int32_t pairs = J * b;
+        const int32_t Q = std::max(1, std::min(256 / pairs, 8));
+        MTL_REQUIRE((nblk + Q - 1) / Q <= 64,
+                    "too many x_proj partial blocks for this batch and width (use split_k = 0)");
+        MTL_REQUIRE((size_t)pairs * (1 + Q) * sizeof(float) <= 64 * 1024, "x_dbl too wide");
+    }
+    // the GEMVs' vector operands (xc for x_proj, y for out_proj, the
+    // residual for the lm_head) and their weights are read as float4 runs
+    auto al16 = [](const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; };
+    MTL_REQUIRE(al16(a->xc) && al16(a->y) && al16(a->emb), "xc, y and emb must be 16-byte aligned");
+    // out_proj writes x0 / x1 while reading the residual in the other one
+    MTL_REQUIRE(a->x0 != a->x1 && a->x0 != a->resid && a->x1 != a->resid, "x0, x1 and resid must be distinct");
+    // every layer is checked before the first launch, so a bad layer leaves
+    // no conv history or SSM state half stepped
     for (int32_t i = 0; i < a->n_layers; ++i) {
         const mtl_decode_layer& L = layers[i];
+        const std::string at = "layer " + std::to_string(i) + ": ";
         MTL_REQUIRE(L.norm_w && L.W_in && L.conv_w && L.W_dt && L.dt_bias && L.A_log && L.W_out && L.conv_state &&
                     L.ssm_state &&
                     (split_k ? L.W_xT != nullptr : L.W_x != nullptr),
-                    "layer " + std::to_string(i) + ": null required pointer");
+                    at + "null required pointer");
+        MTL_REQUIRE(al16(L.W_in) && al16(L.W_out) && (split_k || al16(L.W_x)),
+                    at + "W_in, W_out and W_x must be 16-byte aligned");
     }
-    const int32_t nblk = split_k ? (D + cpb - 1) / cpb : a->xproj_parts;
     const float* x_cur = nullptr;
     int rc;
     for (int32_t i = 0; i < a->n_layers; ++i) {

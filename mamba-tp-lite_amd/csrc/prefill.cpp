@@ -57,7 +57,14 @@ extern "C" int mtl_prefill_short(const mtl_prefill_short_args* a, const mtl_pref
     MTL_REQUIRE(a->d_conv >= 2 && a->d_conv <= 4, "d_conv must be 2, 3 or 4");
     MTL_REQUIRE(a->h && a->xn && a->u && a->z && a->dt && a->y && a->x_parts && a->x_dbl && a->y_parts &&
                 a->norm_f && a->normed_out, "null workspace pointer");
-    // every layer is checked before the first launch, so a bad layer leaves nothing half written
+    // the 16-byte alignment the skinny GEMMs and the fused in_proj take of
+    // their operands (mtl_linear_skinny, mtl_in_proj_conv_prefill)
+    auto al16 = [](const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; };
+    MTL_REQUIRE(al16(a->xn) && al16(a->u) && al16(a->z) && al16(a->y) && al16(a->x_parts) && al16(a->y_parts),
+                "workspace xn, u, z, y, x_parts and y_parts must be 16-byte aligned");
+    // every layer is checked before the first launch, so a bad layer leaves
+    // nothing half written: pointers, aliasing and alignment are the checks
+    // that differ from layer to layer (the sizes are common to all layers)
     for (int32_t i = 0; i < a->n_layers; ++i) {
         const mtl_prefill_layer& L = layers[i];
         MTL_REQUIRE(L.norm_w && L.W_in && L.conv_w && L.W_x && L.W_dt && L.A_log && L.W_out && L.conv_state_out &&
@@ -66,6 +73,8 @@ extern "C" int mtl_prefill_short(const mtl_prefill_short_args* a, const mtl_pref
         // conv history is read and written in different runs
         MTL_REQUIRE(L.conv_state_in != L.conv_state_out,
                     "layer " + std::to_string(i) + ": conv_state_out must not alias conv_state_in");
+        MTL_REQUIRE(al16(L.W_in) && al16(L.b_in) && al16(L.W_x) && al16(L.W_out) && al16(L.b_out),
+                    "layer " + std::to_string(i) + ": W_in, b_in, W_x, W_out and b_out must be 16-byte aligned");
     }
     const int32_t xs = skinny_split(D), os = 4;
     const int rpb_x = skinny_rows_per_block(rows, J, xs), rpb_o = skinny_rows_per_block(rows, M, os);

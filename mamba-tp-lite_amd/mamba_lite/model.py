@@ -672,8 +672,34 @@ class MambaLM(nn.Module):
         if self.embedding.weight.dtype != torch.float32 or not input_ids.is_cuda:
             return False
         lc = cache.layers[0]
-        return lc.conv_state.dtype == torch.float32 and lc.ssm_state.dtype == torch.float32 and \
-            lc.conv_state.is_contiguous() and lc.ssm_state.is_contiguous()
+        if not (lc.conv_state.dtype == torch.float32 and lc.ssm_state.dtype == torch.float32 and
+                lc.conv_state.is_contiguous() and lc.ssm_state.is_contiguous()):
+            return False
+        if DECODE_STEP_NATIVE:
+            plan = self._decode_plan()
+            split_k = b <= plan["split_k_max_b"]
+            if self._decode_step_template(plan, split_k, input_ids.device) is None:
+                return False
+        return True
+
+    def _check_step_cache(self, cache, b: int, device):
+        """Every layer's conv_state [b, D, K-1] and ssm_state [b, D, N] must be
+        contiguous float32 on the ids' device before the one-call step hands
+        their addresses to the kernels (the reference fails in torch.cat on a
+        mismatched cache, model.py:264-266)."""
+        cfg = self.cfg
+        if len(cache.layers) != len(self.layers):
+            raise ValueError(f"step: cache has {len(cache.layers)} layers, the model {len(self.layers)}")
+        cs_shape = (b, cfg.d_inner, cfg.d_conv - 1)
+        h_shape = (b, cfg.d_inner, cfg.d_state)
+        for i, lc in enumerate(cache.layers):
+            cs, hs = lc.conv_state, lc.ssm_state
+            if cs.shape != cs_shape or cs.dtype != torch.float32 or not cs.is_contiguous() or cs.device != device:
+                raise ValueError(f"step: layer {i} conv_state must be contiguous float32 {cs_shape} on {device}, "
+                                 f"got {tuple(cs.shape)} {cs.dtype} on {cs.device}")
+            if hs.shape != h_shape or hs.dtype != torch.float32 or not hs.is_contiguous() or hs.device != device:
+                raise ValueError(f"step: layer {i} ssm_state must be contiguous float32 {h_shape} on {device}, "
+                                 f"got {tuple(hs.shape)} {hs.dtype} on {hs.device}")
 
     def _derived_key(self):
         """(address, version) of the parameters that derived weight copies are
@@ -724,10 +750,12 @@ class MambaLM(nn.Module):
                       "split_k_max_b": split_k_max_b}
         return self._plan
 
-    def _decode_step_template(self, plan, split_k):
+    def _decode_step_template(self, plan, split_k, device):
         """ctypes array of mtl_decode_layer with every layer's weight pointers
         (x_proj transposed from the decode plan with split_k, as is without),
-        rebuilt whenever any of those tensors' addresses change."""
+        or None when a weight is not a contiguous float32 tensor on `device`
+        (the step then runs op by op).  Rebuilt whenever any of those
+        tensors' addresses change."""
         ws = []
         for blk, lp in zip(self.layers, plan["layers"]):
             mx = blk.mixer
@@ -736,16 +764,18 @@ class MambaLM(nn.Module):
                    mx.dt_proj.bias, mx.A_log, mx.D, mx.out_proj.weight, mx.out_proj.bias]
         key = tuple(0 if t is None else t.data_ptr() for t in ws)
         cached = getattr(self, "_step_tmpl", {}).get(split_k)
-        if cached is not None and cached[0] == key:
+        if cached is not None and cached[0] == key and cached[2] == device:
             return cached[1]
-        arr = (_lib.DecodeLayer * len(self.layers))()
-        for i, L in enumerate(arr):
-            (L.norm_w, L.W_in, L.b_in, L.conv_w, L.conv_b, L.W_xT, L.W_x, L.W_dt, L.dt_bias, L.A_log, L.Dv, L.W_out,
-             L.b_out) = key[13 * i:13 * i + 13]
-            L.eps = self.layers[i].norm.eps
+        arr = None
+        if all(t is None or (t.device == device and t.dtype == torch.float32 and t.is_contiguous()) for t in ws):
+            arr = (_lib.DecodeLayer * len(self.layers))()
+            for i, L in enumerate(arr):
+                (L.norm_w, L.W_in, L.b_in, L.conv_w, L.conv_b, L.W_xT, L.W_x, L.W_dt, L.dt_bias, L.A_log, L.Dv,
+                 L.W_out, L.b_out) = key[13 * i:13 * i + 13]
+                L.eps = self.layers[i].norm.eps
         if not hasattr(self, "_step_tmpl"):
             self._step_tmpl = {}
-        self._step_tmpl[split_k] = (key, arr)
+        self._step_tmpl[split_k] = (key, arr, device)
         return arr
 
     def _step_fused(self, input_ids, cache):
@@ -770,8 +800,9 @@ class MambaLM(nn.Module):
         # the 8-channel blocks are faster)
         cpb = 4 if b == 1 and not split_k else plan["cpb"]
         if DECODE_STEP_NATIVE:
+            self._check_step_cache(cache, b, dev)
             logits = torch.empty(b, self.embedding.weight.shape[0], **f32)
-            tmpl = self._decode_step_template(plan, split_k)
+            tmpl = self._decode_step_template(plan, split_k, dev)
             arr = type(tmpl).from_buffer_copy(tmpl)     # per call: read by the library without the GIL
             for L, lc in zip(arr, cache.layers):
                 L.conv_state, L.ssm_state = lc.conv_state.data_ptr(), lc.ssm_state.data_ptr()

@@ -137,6 +137,16 @@ def test_invalid_arguments_are_rejected_without_a_gpu():
     ("mtl_decode_step", dict(null_ws=True), b"null workspace"),
     ("mtl_decode_step", dict(null_layer=True), b"layer 1: null required pointer"),
     ("mtl_decode_step", dict(split_k=0, xproj_parts=4, null_layer=False), b"layer 0: null required pointer"),
+    # rejected before any launch: limits the per-layer calls would only meet
+    # after layer 0's conv history had moved on
+    ("mtl_decode_step", dict(batch=2, d_model=768, d_inner=1536, dt_rank=48), b"partial blocks"),
+    ("mtl_decode_step", dict(split_k=0, xproj_parts=3), b"multiple of 4 * xproj_parts"),
+    ("mtl_decode_step", dict(split_k=0, xproj_parts=65, d_inner=4096), b"xproj_parts must be in [1, 64]"),
+    ("mtl_decode_step", dict(misaligned_layer=True), b"layer 1: W_in, W_out and W_x must be 16-byte aligned"),
+    ("mtl_decode_step", dict(same_ws=True), b"x0, x1 and resid must be distinct"),
+    ("mtl_decode_step", dict(batch=4, d_model=4096), b"batch * d_model too large"),
+    ("mtl_prefill_short", dict(misaligned_layer=True),
+     b"layer 1: W_in, b_in, W_x, W_out and b_out must be 16-byte aligned"),
     ("mtl_in_proj_conv_xproj", dict(batch=33), b"batch must be in [1, 32]"),
     ("mtl_in_proj_conv_xproj", dict(d_model=128), b"at least 256"),
     ("mtl_in_proj_conv_xproj", dict(d_model=320), b"multiple of 128"),
@@ -209,7 +219,7 @@ def test_entry_points_validate_sizes_on_the_host(case):
                                    a["rows_per_block"], None)
     elif name == "mtl_prefill_short":
         a = dict(batch=1, seqlen=64, d_model=256, d_inner=512, d_state=16, d_conv=4, n_layers=2, null_ws=False,
-                 null_layer=False, alias=False)
+                 null_layer=False, alias=False, misaligned_layer=False)
         a.update(over)
         args = _lib.PrefillShortArgs()
         for f, *_ in _lib.PrefillShortArgs._fields_[:11]:
@@ -226,17 +236,20 @@ def test_entry_points_validate_sizes_on_the_host(case):
             L.conv_state_in = 32 if a["alias"] and i == 1 else 48
             if a["null_layer"] and i == 1:
                 L.W_dt = None
+            if a["misaligned_layer"] and i == 1:
+                L.W_out = 24
         rc = lib.mtl_prefill_short(ctypes.byref(args), layers, None)
     elif name == "mtl_decode_step":
         a = dict(batch=1, cpb=8, n_layers=2, split_k=1, xproj_parts=1, null_ws=False, null_layer=False, d_state=16,
-                 d_inner=512, d_conv=4)
+                 d_inner=512, d_conv=4, d_model=256, dt_rank=16, misaligned_layer=False, same_ws=False)
         a.update(over)
         args = _lib.DecodeStepArgs()
-        for f, *_ in _lib.DecodeStepArgs._fields_[:11]:
-            setattr(args, f, None if a["null_ws"] and f == "gz" else 16)
+        for k, (f, *_) in enumerate(_lib.DecodeStepArgs._fields_[:11]):
+            # distinct 16-byte aligned placeholders, never dereferenced
+            setattr(args, f, None if a["null_ws"] and f == "gz" else 16 if a["same_ws"] else 16 * (k + 1))
         args.eps_f, args.vocab, args.n_layers, args.batch = 1e-5, 64, a["n_layers"], a["batch"]
-        args.d_model, args.d_inner, args.d_state, args.dt_rank, args.d_conv = 256, a["d_inner"], a["d_state"], 16, \
-            a["d_conv"]
+        args.d_model, args.d_inner, args.d_state, args.dt_rank, args.d_conv = a["d_model"], a["d_inner"], \
+            a["d_state"], a["dt_rank"], a["d_conv"]
         args.channels_per_block, args.split_k, args.xproj_parts = a["cpb"], a["split_k"], a["xproj_parts"]
         layers = (_lib.DecodeLayer * 2)()
         for i, L in enumerate(layers):
@@ -245,6 +258,8 @@ def test_entry_points_validate_sizes_on_the_host(case):
                     setattr(L, f, 16)
             if a["null_layer"] and i == 1:
                 L.A_log = None
+            if a["misaligned_layer"] and i == 1:
+                L.W_out = 24
         rc = lib.mtl_decode_step(ctypes.byref(args), layers, None)
     elif name == "mtl_in_proj_conv_xproj":
         a = dict(batch=8, d_model=256, d_inner=64, cpp=16, d_conv=4, J=40)

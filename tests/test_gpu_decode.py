@@ -353,3 +353,33 @@ def test_native_decode_step_equals_the_per_layer_loop(d_model, b, fused_max, mon
     assert len(calls) == 3
     for k, (x, y) in enumerate(zip(nat, per)):
         assert torch.equal(x, y), k
+
+
+@pytest.mark.parametrize("bad", ["batch", "dtype", "strided", "layers"])
+def test_fused_step_rejects_a_mismatched_cache_before_any_launch(bad):
+    """A cache that does not match the step (a batch-1 cache stepped with
+    batch-2 ids, a bfloat16 or strided state in a layer after the first, a
+    cache with a layer missing) raises ValueError before any kernel runs: no
+    layer's conv history or SSM state moves (the reference fails in
+    torch.cat, model.py:264-266)."""
+    print(f"fused step, mismatched cache: {bad}", flush=True)
+    model = _model(768, 3, 512, seed=11)
+    with torch.no_grad():
+        _, cache = model.prefill(torch.randint(0, 512, (1, 6), device=DEV))
+        ids = torch.randint(0, 512, (1, 1), device=DEV)
+        if bad == "batch":
+            ids = torch.randint(0, 512, (2, 1), device=DEV)
+        elif bad == "dtype":
+            cache.layers[1].ssm_state = cache.layers[1].ssm_state.bfloat16()
+        elif bad == "strided":
+            cs = cache.layers[2].conv_state
+            cache.layers[2].conv_state = torch.zeros(cs.shape[0], cs.shape[2], cs.shape[1], device=DEV).transpose(1, 2)
+        else:
+            cache.layers.pop()
+        before = [(l.conv_state.clone(), l.ssm_state.clone()) for l in cache.layers]
+        assert model._fused_step_ok(ids, cache)
+        with pytest.raises(ValueError, match="step:"):
+            model.step(ids, cache)
+        torch.cuda.synchronize()
+        for (c0, h0), l in zip(before, cache.layers):
+            assert torch.equal(c0, l.conv_state) and torch.equal(h0, l.ssm_state)
