@@ -22,6 +22,7 @@
 #ifndef MTL_H
 #define MTL_H
 
+#include <stddef.h>
 #include <stdint.h>
 
 #ifdef __cplusplus
@@ -516,6 +517,45 @@ typedef struct {
 } mtl_decode_step_args;
 
 int mtl_decode_step(const mtl_decode_step_args* args, const mtl_decode_layer* layers, mtl_stream_t stream);
+
+/* ------------------------------------------------------------------------
+ * mtl_decode_step_persist: the same step -- MambaLM.step (model.py:343-353)
+ * over MambaBlock.step (308-311) and MambaMixer.step (249-294) -- for batch
+ * 1 as ONE persistent launch over every layer, then the norm_f + tied
+ * lm_head GEMV of mtl_decode_norm_gemv into logits [1, vocab].  Its
+ * workgroups stay resident and exchange the x_proj partials, y and the new
+ * residual through the workspace three times per layer instead of ending
+ * three kernels per layer.
+ *   args     as mtl_decode_step (batch 1; x0 receives the final residual;
+ *            xc, gz, y, x1, resid, xpart, channels_per_block, split_k and
+ *            xproj_parts are not used).
+ *   layers   host array [n_layers]: validated here; each layer's
+ *            conv_state [1, D, K-1] and ssm_state [1, D, N] are updated in
+ *            place.  W_xT ([d_inner, J], x_proj transposed) is required.
+ *   layers_dev  a device copy of the same array (its weight pointers are
+ *            read by the kernel; its cache fields are not).
+ *   workspace   device memory of mtl_decode_persist_workspace_bytes(),
+ *            256-byte aligned, zero-filled before its first use and then
+ *            left to the library: it carries an epoch from call to call
+ *            (word 0) and an error word (word 1, nonzero after a wait timed
+ *            out; the logits of that call are then NaN).  Calls that share a
+ *            workspace must be ordered (one stream); concurrent calls race.
+ *   blocking 0 picks the register blocking (workgroups per launch) itself;
+ *            1 and 2 force 6 or 3 channels per compute wavefront pair.
+ * Shapes: d_model a multiple of 4 up to 1024, d_inner a multiple of 4 up to
+ * 2 d_model, d_state <= 16, dt_rank <= 64 with dt_rank + 2 d_state <= 128,
+ * d_conv 2..4, n_layers <= 64.  All workgroups must be co-resident: the grid
+ * is at most the device's CU count (checked) and the GPU must not be shared
+ * with other long kernels meanwhile (a wait then times out, see above).
+ * ---------------------------------------------------------------------- */
+size_t mtl_decode_persist_workspace_bytes(int32_t d_model, int32_t d_inner, int32_t d_state, int32_t dt_rank);
+/* Workgroups mtl_decode_step_persist launches for this shape and blocking on
+ * a device of 256 or more CUs, or 0 when it does not take the shape. */
+int32_t mtl_decode_persist_grid(int32_t d_model, int32_t d_inner, int32_t d_state, int32_t dt_rank, int32_t d_conv,
+                                int32_t n_layers, int32_t blocking);
+int mtl_decode_step_persist(const mtl_decode_step_args* args, const mtl_decode_layer* layers,
+                            const mtl_decode_layer* layers_dev, void* workspace, size_t workspace_bytes,
+                            int32_t blocking, mtl_stream_t stream);
 
 #ifdef __cplusplus
 }

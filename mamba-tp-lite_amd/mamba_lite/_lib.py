@@ -109,6 +109,10 @@ SIGNATURES = {
     "mtl_xproj_sum_dt": (ctypes.c_int, [_fp, _i32, _i64, _i32, _fp, _i32, _i64, _fp, _fp, _vp]),
     "mtl_prefill_short": (ctypes.c_int, [ctypes.POINTER(PrefillShortArgs), ctypes.POINTER(PrefillLayer), _vp]),
     "mtl_decode_step": (ctypes.c_int, [ctypes.POINTER(DecodeStepArgs), ctypes.POINTER(DecodeLayer), _vp]),
+    "mtl_decode_persist_workspace_bytes": (ctypes.c_size_t, [_i32, _i32, _i32, _i32]),
+    "mtl_decode_persist_grid": (_i32, [_i32, _i32, _i32, _i32, _i32, _i32, _i32]),
+    "mtl_decode_step_persist": (ctypes.c_int, [ctypes.POINTER(DecodeStepArgs), ctypes.POINTER(DecodeLayer), _vp, _vp,
+                                               ctypes.c_size_t, _i32, _vp]),
     "mtl_conv_step_xproj": (ctypes.c_int, [_fp, _fp, _i64, _fp, _fp, _fp, _i64, _fp, _fp, _i64, _i64, _i32, _i32,
                                            _vp]),
     "mtl_conv_step_xproj_noalloc": (ctypes.c_int, [_fp, _fp, _i64, _fp, _fp, _fp, _i64, _fp, _fp, _i64, _i64, _i32,

@@ -171,6 +171,24 @@ SHORT_PREFILL_NATIVE = True
 # per launch that bounds an eager step.
 DECODE_STEP_NATIVE = True
 
+# With DECODE_PERSIST, the batch-1 fused decode of a model that fits its
+# register blocking (d_model <= 1024, d_inner <= 2 d_model, dt_rank <= 64,
+# d_conv <= 4, <= 64 layers) runs as one persistent launch,
+# mtl_decode_step_persist, instead of three kernels per layer.  It is off:
+# at the 130m shape, graph replays, it measured 449 us/token against 317-321
+# us for the three-kernel layers (its three exchanges per layer cost 2-2.5
+# us each on this part, and its 64 workgroups stream the weights at ~56 GB/s
+# per CU).  PERSIST_BLOCKING 0 lets the library pick its grid.
+DECODE_PERSIST = False
+PERSIST_BLOCKING = 0
+
+
+def _persist_ok(cfg: MambaConfig) -> bool:
+    """Whether mtl_decode_step_persist takes this shape (asked of the library:
+    a register blocking must fit it)."""
+    return _lib.load().mtl_decode_persist_grid(cfg.d_model, cfg.d_inner, cfg.d_state, cfg.dt_rank, cfg.d_conv,
+                                               cfg.n_layer, PERSIST_BLOCKING) > 0
+
 
 def _skinny_rows(x: torch.Tensor, w: torch.Tensor, enabled: bool = True) -> torch.Tensor | None:
     """x [..., K] as the [rows, K] operand of mtl_linear_skinny, or None
@@ -712,7 +730,8 @@ class MambaLM(nn.Module):
     def _derived_tensors(self):
         """The derived copies a step reads now (held by a captured graph so a
         rebuild cannot free memory the graph still addresses)."""
-        held = [getattr(self, "_plan", None)]
+        held = [getattr(self, "_plan", None), getattr(self, "_persist_tab", None),
+                getattr(self, "_persist_ws", None)]
         for m in self.layers:
             held += [getattr(m.mixer, "_xproj_cache", None), getattr(m.mixer, "_unit_conv_w", None)]
         return held
@@ -736,19 +755,48 @@ class MambaLM(nn.Module):
             q = max(1, min(256 // (J * b), 8))
             return -(-nblk // q) <= 64
         split_k_max_b = max([b for b in (1, 2, 4) if _fits(b)], default=0)
-        split_k = split_k_max_b > 0
+        persist = _persist_ok(cfg)
+        need_xt = split_k_max_b > 0 or persist    # the persistent step reads x_proj transposed too
         layers = []
         with torch.no_grad():
             for m in self.layers:
                 mx = m.mixer
                 w = mx.conv1d.weight
                 layers.append({
-                    "W_xT": mx.x_proj.weight.detach().t().contiguous() if split_k else None,
+                    "W_xT": mx.x_proj.weight.detach().t().contiguous() if need_xt else None,
                     "conv_w": w.detach().reshape(w.shape[0], w.shape[-1]).contiguous(),
                 })
         self._plan = {"key": key, "layers": layers, "cpb": cpb, "nblk": nblk, "J": J,
-                      "split_k_max_b": split_k_max_b}
+                      "split_k_max_b": split_k_max_b, "persist": persist}
         return self._plan
+
+    def _persist_table(self, tmpl, device):
+        """Device copy of the weight records in `tmpl` for the persistent step,
+        rebuilt when the template changes; None when it would have to be
+        uploaded inside a graph capture (that step then runs kernel by
+        kernel)."""
+        cached = getattr(self, "_persist_tab", None)
+        if cached is not None and cached[0] is tmpl:
+            return cached[1]
+        if torch.cuda.is_current_stream_capturing():
+            return None
+        host = torch.frombuffer(bytearray(bytes(tmpl)), dtype=torch.uint8)
+        dev_tab = host.to(device)
+        self._persist_tab = (tmpl, dev_tab)
+        return dev_tab
+
+    def _persist_workspace(self, device):
+        """The persistent step's workspace on `device` (exchange slots, epoch,
+        error word), zero-filled once and kept."""
+        ws = getattr(self, "_persist_ws", {})
+        t = ws.get(device)
+        if t is None:
+            if torch.cuda.is_current_stream_capturing():
+                return None
+            t = ops.decode_persist_workspace(self.cfg, device)
+            ws[device] = t
+            self._persist_ws = ws
+        return t
 
     def _decode_step_template(self, plan, split_k, device):
         """ctypes array of mtl_decode_layer with every layer's weight pointers
@@ -799,6 +847,19 @@ class MambaLM(nn.Module):
         # stream (measured at d_model 2048: 12.87 -> 12.63 us; at batch 2 and 4
         # the 8-channel blocks are faster)
         cpb = 4 if b == 1 and not split_k else plan["cpb"]
+        if DECODE_STEP_NATIVE and DECODE_PERSIST and b == 1 and plan["persist"]:
+            self._check_step_cache(cache, b, dev)
+            tmpl = self._decode_step_template(plan, True, dev)
+            tab = self._persist_table(tmpl, dev) if tmpl is not None else None
+            wsp = self._persist_workspace(dev) if tab is not None else None
+            if wsp is not None:
+                arr = type(tmpl).from_buffer_copy(tmpl)
+                for L, lc in zip(arr, cache.layers):
+                    L.conv_state, L.ssm_state = lc.conv_state.data_ptr(), lc.ssm_state.data_ptr()
+                logits = torch.empty(1, self.embedding.weight.shape[0], **f32)
+                ops.decode_step_persist(arr, tab, ids, self.embedding.weight, _f32(self.norm_f.weight),
+                                        self.norm_f.eps, logits, xs[0], wsp, cfg, PERSIST_BLOCKING)
+                return logits.unsqueeze(1)
         if DECODE_STEP_NATIVE:
             self._check_step_cache(cache, b, dev)
             logits = torch.empty(b, self.embedding.weight.shape[0], **f32)

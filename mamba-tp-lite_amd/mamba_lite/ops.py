@@ -567,6 +567,44 @@ def decode_step(layers, ids, emb, norm_f, eps_f, logits, xc, gz, y, xs, xpart, c
     return logits
 
 
+def decode_persist_workspace(cfg, device) -> torch.Tensor:
+    """A zero-filled workspace for mtl_decode_step_persist (its exchange slots,
+    epoch and error word), to be kept and reused by every call on `device`."""
+    n = _lib.load().mtl_decode_persist_workspace_bytes(cfg.d_model, cfg.d_inner, cfg.d_state, cfg.dt_rank)
+    return torch.zeros(n, dtype=torch.uint8, device=device)
+
+
+def decode_step_persist(layers, layers_dev, ids, emb, norm_f, eps_f, logits, x0, workspace, cfg, blocking=0):
+    """mtl_decode_step_persist: the batch-1 decode step of every layer as one
+    persistent launch, then norm_f + the tied lm_head into logits [1, vocab].
+    `layers` is the host ctypes array of _lib.DecodeLayer (weights with W_xT,
+    and this call's cache pointers), `layers_dev` a uint8 device tensor
+    holding a copy of its weight records; x0 [1, d_model] receives the final
+    residual; workspace from decode_persist_workspace()."""
+    for t, name in ((emb, "emb"), (norm_f, "norm_f"), (logits, "logits"), (x0, "x0")):
+        _f32c(t, name)
+    if ids.dtype != torch.int64 or not ids.is_contiguous() or ids.numel() != 1:
+        raise ValueError("decode_step_persist: ids must be one contiguous int64 id")
+    if tuple(logits.shape) != (1, emb.shape[0]) or tuple(x0.shape) != (1, emb.shape[1]):
+        raise ValueError("decode_step_persist: logits [1, vocab] and x0 [1, d_model] expected")
+    if layers_dev.dtype != torch.uint8 or layers_dev.numel() != ctypes.sizeof(layers) or not layers_dev.is_contiguous():
+        raise ValueError("decode_step_persist: layers_dev must hold the layer records as contiguous uint8")
+    if workspace.dtype != torch.uint8 or not workspace.is_contiguous():
+        raise ValueError("decode_step_persist: workspace must be contiguous uint8")
+    _same_device(x0, ids, emb, norm_f, logits, layers_dev, workspace)
+    a = _lib.DecodeStepArgs()
+    a.ids, a.emb, a.norm_f, a.logits, a.x0 = ids.data_ptr(), emb.data_ptr(), norm_f.data_ptr(), logits.data_ptr(), \
+        x0.data_ptr()
+    a.eps_f, a.vocab, a.n_layers, a.batch = float(eps_f), emb.shape[0], len(layers), 1
+    a.d_model, a.d_inner, a.d_state, a.dt_rank, a.d_conv = emb.shape[1], cfg.d_inner, cfg.d_state, cfg.dt_rank, \
+        cfg.d_conv
+    with _dev_guard(x0):
+        _lib.check(_lib.load().mtl_decode_step_persist(ctypes.byref(a), layers, layers_dev.data_ptr(),
+                                                       workspace.data_ptr(), workspace.numel(), int(blocking),
+                                                       _stream(x0)), "decode_step_persist")
+    return logits
+
+
 def _parts_array(parts):
     arr = (ctypes.c_void_p * len(parts))(*[p.data_ptr() for p in parts])
     return ctypes.cast(arr, ctypes.POINTER(ctypes.c_void_p)), arr

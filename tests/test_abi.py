@@ -145,6 +145,14 @@ def test_invalid_arguments_are_rejected_without_a_gpu():
     ("mtl_decode_step", dict(misaligned_layer=True), b"layer 1: W_in, W_out and W_x must be 16-byte aligned"),
     ("mtl_decode_step", dict(same_ws=True), b"x0, x1 and resid must be distinct"),
     ("mtl_decode_step", dict(batch=4, d_model=4096), b"batch * d_model too large"),
+    ("mtl_decode_step_persist", dict(batch=2), b"batch must be 1"),
+    ("mtl_decode_step_persist", dict(d_model=2048, d_inner=4096), b"d_model"),
+    ("mtl_decode_step_persist", dict(n_layers=65), b"n_layers"),
+    ("mtl_decode_step_persist", dict(dt_rank=80), b"dt_rank"),
+    ("mtl_decode_step_persist", dict(d_conv=5), b"d_conv"),
+    ("mtl_decode_step_persist", dict(ws_bytes=1024), b"workspace too small"),
+    ("mtl_decode_step_persist", dict(blocking=3), b"blocking"),
+    ("mtl_decode_step_persist", dict(null_xt=True), b"layer 1: null required pointer"),
     ("mtl_prefill_short", dict(misaligned_layer=True),
      b"layer 1: W_in, b_in, W_x, W_out and b_out must be 16-byte aligned"),
     ("mtl_in_proj_conv_xproj", dict(batch=33), b"batch must be in [1, 32]"),
@@ -261,6 +269,25 @@ def test_entry_points_validate_sizes_on_the_host(case):
             if a["misaligned_layer"] and i == 1:
                 L.W_out = 24
         rc = lib.mtl_decode_step(ctypes.byref(args), layers, None)
+    elif name == "mtl_decode_step_persist":
+        a = dict(batch=1, n_layers=2, d_model=256, d_inner=512, d_state=16, dt_rank=16, d_conv=4, ws_bytes=1 << 20,
+                 blocking=0, null_xt=False)
+        a.update(over)
+        args = _lib.DecodeStepArgs()
+        for k, (f, *_) in enumerate(_lib.DecodeStepArgs._fields_[:11]):
+            setattr(args, f, 16 * (k + 1))
+        args.eps_f, args.vocab, args.n_layers, args.batch = 1e-5, 64, a["n_layers"], a["batch"]
+        args.d_model, args.d_inner, args.d_state, args.dt_rank, args.d_conv = a["d_model"], a["d_inner"], \
+            a["d_state"], a["dt_rank"], a["d_conv"]
+        layers = (_lib.DecodeLayer * max(2, a["n_layers"]))()
+        for i, L in enumerate(layers):
+            for f, *_ in _lib.DecodeLayer._fields_:
+                if f not in ("eps", "reserved", "W_x"):
+                    setattr(L, f, 16)
+            if a["null_xt"] and i == 1:
+                L.W_xT = None
+        rc = lib.mtl_decode_step_persist(ctypes.byref(args), layers, ctypes.c_void_p(256), ctypes.c_void_p(256),
+                                         a["ws_bytes"], a["blocking"], None)
     elif name == "mtl_in_proj_conv_xproj":
         a = dict(batch=8, d_model=256, d_inner=64, cpp=16, d_conv=4, J=40)
         a.update(over)

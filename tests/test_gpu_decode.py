@@ -383,3 +383,99 @@ def test_fused_step_rejects_a_mismatched_cache_before_any_launch(bad):
         torch.cuda.synchronize()
         for (c0, h0), l in zip(before, cache.layers):
             assert torch.equal(c0, l.conv_state) and torch.equal(h0, l.ssm_state)
+
+
+def _persist_err_word(model):
+    ws = getattr(model, "_persist_ws", {})
+    return [int(t[4:8].view(torch.int32).item()) for t in ws.values()]
+
+
+@pytest.mark.parametrize("d_model,n_layer,blocking", [(64, 2, 0), (64, 2, 1), (64, 2, 2), (768, 3, 1), (768, 3, 2),
+                                                      (512, 2, 0)])
+def test_persistent_step_matches_the_three_kernel_step(d_model, n_layer, blocking, monkeypatch):
+    """mtl_decode_step_persist (one launch for every layer) against the
+    three-kernel fused step on the same weights: logits and both caches
+    within 1e-4 over four steps (its x_proj partials are summed over
+    different channel blocks), caches updated in place, no wait timed out."""
+    import mamba_lite.model as mm
+    print(f"persistent decode d_model={d_model} layers={n_layer} blocking={blocking}", flush=True)
+    model = _model(d_model, n_layer, 512, seed=d_model + blocking)
+    assert model._decode_plan()["persist"]
+    ids = torch.randint(0, 512, (1, 6), device=DEV)
+    toks = [torch.randint(0, 512, (1, 1), device=DEV) for _ in range(4)]
+    with torch.no_grad():
+        _, c_ref = model.prefill(ids)
+        _, c = model.prefill(ids)
+        monkeypatch.setattr(mm, "DECODE_PERSIST", False)
+        refs = [model.step(t, c_ref).clone() for t in toks]
+        monkeypatch.setattr(mm, "DECODE_PERSIST", True)
+        monkeypatch.setattr(mm, "PERSIST_BLOCKING", blocking)
+        ptrs = [(l.conv_state.data_ptr(), l.ssm_state.data_ptr()) for l in c.layers]
+        for i, (t, r) in enumerate(zip(toks, refs)):
+            assert_rel(_np(model.step(t, c)), _np(r), 1e-4, f"logits step {i}")
+    for a, b in zip(c.layers, c_ref.layers):
+        assert_rel(_np(a.ssm_state), _np(b.ssm_state), 1e-4, "ssm_state")
+        assert_rel(_np(a.conv_state), _np(b.conv_state), 1e-5, "conv_state")
+    assert ptrs == [(l.conv_state.data_ptr(), l.ssm_state.data_ptr()) for l in c.layers]
+    assert _persist_err_word(model) == [0]
+
+
+@pytest.mark.parametrize("kw", [dict(d_state=8, d_conv=3, bias=True, conv_bias=False),
+                                dict(d_state=4, d_conv=2, dt_rank=5)])
+def test_persistent_step_config_variants(kw, monkeypatch):
+    """In/out_proj biases, no conv bias, N < 16, d_conv 2 and 3, a dt_rank
+    that is not a multiple of 16: persistent step vs the three-kernel step."""
+    import mamba_lite.model as mm
+    print(f"persistent decode variant {kw}", flush=True)
+    torch.manual_seed(3)
+    cfg = MambaConfig(d_model=96, n_layer=2, vocab_size=200, **kw)
+    with torch.device(DEV):
+        model = MambaLM(cfg)
+    with torch.no_grad():
+        for mx in model.modules():
+            if isinstance(mx, MambaMixer) and mx.in_proj.bias is not None:
+                mx.in_proj.bias.normal_(0, 0.1)
+                mx.out_proj.bias.normal_(0, 0.1)
+    model.eval()
+    ids = torch.randint(0, 200, (1, 5), device=DEV)
+    with torch.no_grad():
+        _, c_ref = model.prefill(ids)
+        _, c = model.prefill(ids)
+        for i in range(3):
+            t = torch.randint(0, 200, (1, 1), device=DEV)
+            monkeypatch.setattr(mm, "DECODE_PERSIST", False)
+            ref = model.step(t, c_ref)
+            monkeypatch.setattr(mm, "DECODE_PERSIST", True)
+            assert_rel(_np(model.step(t, c)), _np(ref), 1e-4, f"step {i}")
+    assert _persist_err_word(model) == [0]
+
+
+def test_persistent_step_vs_oracle(monkeypatch):
+    """The persistent step at the 130m width against the float64 oracle."""
+    import mamba_lite.model as mm
+    monkeypatch.setattr(mm, "DECODE_PERSIST", True)
+    test_fused_step_vs_oracle()
+
+
+def test_persistent_step_graph_replay_bit_identical(monkeypatch):
+    """Captured as a HIP graph, the persistent launch (its epoch in the
+    workspace advancing every replay) gives eager's bits, step after step,
+    with eager steps between replays on the same workspace."""
+    import mamba_lite.model as mm
+    monkeypatch.setattr(mm, "DECODE_PERSIST", True)
+    test_fused_step_graph_replay_bit_identical()
+
+
+def test_persistent_step_out_of_range_id_gives_nan(monkeypatch):
+    import mamba_lite.model as mm
+    monkeypatch.setattr(mm, "DECODE_PERSIST", True)
+    model = _model(64, 2, 128, seed=6)
+    ids = torch.randint(0, 128, (1, 4), device=DEV)
+    with torch.no_grad():
+        _, c1 = model.prefill(ids)
+        _, c2 = model.prefill(ids)
+        got = model.step(torch.full((1, 1), 128, dtype=torch.long, device=DEV), c1)
+        ok = model.step(torch.zeros((1, 1), dtype=torch.long, device=DEV), c2)
+    # the NaN row also enters c1's states, as on every path; c2 is untouched
+    assert torch.isnan(got).all() and torch.isfinite(ok).all()
+    assert _persist_err_word(model) == [0]

@@ -263,3 +263,18 @@ def test_prefill_short_is_not_taken_off_the_gpu():
     model = MambaLM(cfg)
     assert model._prefill_short(torch.zeros(1, 8, dtype=torch.long), None, None) is None
     assert not hasattr(model, "_short_plan")
+
+
+def test_persistent_decode_grid_query():
+    """mtl_decode_persist_grid: the 130m shape takes 64 workgroups with the
+    first blocking and 128 with the second; shapes outside the kernel's
+    register blocking return 0 (the step then runs kernel by kernel)."""
+    from mamba_lite import _lib
+    lib = _lib.load()
+    assert lib.mtl_decode_persist_grid(768, 1536, 16, 48, 4, 24, 0) == 64
+    assert lib.mtl_decode_persist_grid(768, 1536, 16, 48, 4, 24, 1) == 64
+    assert lib.mtl_decode_persist_grid(768, 1536, 16, 48, 4, 24, 2) == 128
+    assert lib.mtl_decode_persist_grid(2048, 4096, 16, 128, 4, 48, 0) == 0     # 1.4b: too wide
+    assert lib.mtl_decode_persist_grid(1024, 2048, 16, 64, 4, 48, 0) == 0      # partials exceed the exchange lanes
+    assert lib.mtl_decode_persist_grid(768, 1536, 16, 48, 4, 65, 0) == 0       # cache pointers: 64 layers at most
+    assert lib.mtl_decode_persist_grid(768, 1536, 16, 48, 8, 24, 0) == 0       # d_conv 8
