@@ -168,28 +168,38 @@ def _linear(x, w, b=None):
     return y + b if b is not None else y
 
 
-def mixer_prefill(p, x, conv_state=None, ssm_state=None, dtype=np.float32):
+def mixer_prefill(p, x, conv_state=None, ssm_state=None, dtype=np.float32, act=None):
     """MambaMixer.prefill, model.py:184-241.  p holds numpy weights:
     in_proj_w [2D,M] (+in_proj_b), conv_w [D,K], conv_b [D], x_proj_w [R+2N,D],
     dt_proj_w [D,R], dt_proj_b [D], A_log [D,N], D [D], out_proj_w [M,D]
-    (+out_proj_b).  x: [b,l,M].  Returns (out [b,l,M], conv_state, ssm_state)."""
+    (+out_proj_b).  x: [b,l,M].  Returns (out [b,l,M], conv_state, ssm_state).
+
+    act, if given, is applied to each activation tensor as an op stores it,
+    modelling a model whose activations are held in a narrower type (e.g. a
+    round to bfloat16) while the scan state keeps `dtype`: the in_proj output
+    (model.py:197), SiLU of the conv (206-209; conv and SiLU as one op), the
+    x_proj output (214), the dt_proj output (216), the gated scan output
+    (233-238; the scan as one op) and out_proj's output (239).  Each op
+    computes in `dtype` from its rounded inputs."""
     P = {k: (np.asarray(v, dtype) if v is not None else None) for k, v in p.items()}
     x = np.asarray(x, dtype)
+    store = (lambda t: np.asarray(act(t), dtype)) if act is not None else (lambda t: t)
     Dm = P["D"].shape[0]
     N = P["A_log"].shape[1]
     R = P["dt_proj_w"].shape[1]
-    xz = _linear(x, P["in_proj_w"], P.get("in_proj_b"))                # model.py:197
+    xz = store(_linear(x, P["in_proj_w"], P.get("in_proj_b")))         # model.py:197
     xs, z = xz[..., :Dm], xz[..., Dm:]                                  # model.py:198
     xs = np.ascontiguousarray(xs.transpose(0, 2, 1))                     # model.py:199
     conv, fstate = causal_conv1d(xs, P["conv_w"], P.get("conv_b"), conv_state, dtype)
-    xs = silu(conv)                                                     # model.py:209
-    x_dbl = _linear(xs.transpose(0, 2, 1), P["x_proj_w"])                # model.py:214
+    xs = store(silu(conv))                                              # model.py:209
+    x_dbl = store(_linear(xs.transpose(0, 2, 1), P["x_proj_w"]))         # model.py:214
     dt, B, C = x_dbl[..., :R], x_dbl[..., R:R + N], x_dbl[..., R + N:]   # model.py:215
-    dt = P["dt_proj_w"] @ dt.transpose(0, 2, 1)                          # model.py:216
+    dt = store(P["dt_proj_w"] @ dt.transpose(0, 2, 1))                   # model.py:216
     A = -np.exp(P["A_log"])                                             # model.py:220
     y, h = selective_scan(xs, dt, A, B, C, P["D"], z.transpose(0, 2, 1),
                           delta_bias=P["dt_proj_b"], h0=ssm_state, delta_softplus=True, dtype=dtype)
-    out = _linear(y.transpose(0, 2, 1), P["out_proj_w"], P.get("out_proj_b"))  # model.py:239
+    y = store(y)
+    out = store(_linear(y.transpose(0, 2, 1), P["out_proj_w"], P.get("out_proj_b")))  # model.py:239
     return out.astype(dtype), fstate, h
 
 
