@@ -278,3 +278,23 @@ def test_persistent_decode_grid_query():
     assert lib.mtl_decode_persist_grid(1024, 2048, 16, 64, 4, 48, 0) == 0      # partials exceed the exchange lanes
     assert lib.mtl_decode_persist_grid(768, 1536, 16, 48, 4, 65, 0) == 0       # cache pointers: 64 layers at most
     assert lib.mtl_decode_persist_grid(768, 1536, 16, 48, 8, 24, 0) == 0       # d_conv 8
+
+
+def test_from_pretrained_loads_in_proj_bias_of_a_bias_snapshot(tmp_path):
+    """A `use_bias: true` snapshot: the in_proj and out_proj biases are both
+    loaded.  (The reference's loader remaps out_proj.bias only, so its strict
+    load of such a snapshot stops on the missing in_proj.bias, model.py:
+    392-396; loading it is this build's deliberate deviation.)"""
+    import _golden as G
+    import torch
+    from _util import write_hf_snapshot
+    from mamba_lite.model import MambaConfig, MambaLM
+    cfg = MambaConfig(d_model=64, n_layer=2, vocab_size=128, bias=True)
+    sd = G.lm_weights(12, 64, 2, 128, bias=True)
+    write_hf_snapshot(tmp_path, cfg, {k: torch.from_numpy(v) for k, v in sd.items()})
+    lm = MambaLM.from_pretrained(str(tmp_path))
+    got = lm.state_dict()
+    assert set(got) == set(sd)
+    for k, v in sd.items():
+        assert torch.equal(got[k], torch.from_numpy(v)), k
+    assert lm.layers[1].mixer.in_proj.bias is not None and lm.layers[1].mixer.out_proj.bias is not None

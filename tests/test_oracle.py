@@ -336,3 +336,49 @@ def test_mixer_prefill_activation_rounding_hook():
     assert not np.array_equal(hb, bf16_round(hb))
     rms = np.sqrt(np.mean(o0 ** 2))
     assert 2.0 ** -9 * rms < np.abs(ob - o0).max() < 3e-2 * rms
+
+
+def _fl32(fr):
+    """A Fraction rounded once to the nearest float32 (ties to even), from
+    exact rational comparisons -- independent of numpy's float32 division."""
+    from fractions import Fraction
+    c = np.float32(float(fr))
+    cands = [np.nextafter(c, np.float32(-np.inf)), c, np.nextafter(c, np.float32(np.inf))]
+    return min(cands, key=lambda v: (abs(Fraction(float(v)) - fr),
+                                     int(np.frombuffer(np.float32(v).tobytes(), np.uint32)[0]) & 1))
+
+
+def test_int8_row_with_a_scale_off_the_power_of_two_grid():
+    """amax = 100: s = fl(100 / 127) = 0.7874016, not a power of two.  The
+    codes are round-half-even of the correctly rounded fp32 quotient x / s
+    (tp_utils.py:111-112), computed here by exact rational arithmetic; for
+    these inputs the reciprocal form x * fl(1 / s) rounds to the code below,
+    so an oracle slip to it fails."""
+    from fractions import Fraction
+    row = np.array([[100.0, 0.39370080828666687, 2.7559053897857666, 3.543307304382324, -4.3307085037231445,
+                     -100.0]], np.float32)
+    s, q = oq.quantize_int8_per_token(row)
+    s_exact = _fl32(Fraction(100) / Fraction(127))
+    assert s[0] == s_exact and s_exact not in (0.5, 1.0)
+    want = [int(np.rint(_fl32(Fraction(float(x)) / Fraction(float(s_exact))))) for x in row[0]]
+    assert q[0].tolist() == want == [127, 1, 4, 5, -6, -127]
+    inv = np.float32(np.float32(1.0) / s_exact)
+    recip = [int(np.rint(np.float32(x * inv))) for x in row[0]]
+    assert recip[1:5] == [0, 3, 4, -5]
+
+
+def test_inv_softplus_inverts_softplus():
+    """inv_softplus builds every test's dt_bias: softplus(inv_softplus(y))
+    returns y (float64, relative 1e-12) over the dt range [1e-3, 0.1] and
+    beyond, and inv_softplus(log 2) = 0 (softplus(0) = log 2)."""
+    y = np.exp(np.linspace(np.log(1e-6), np.log(30.0), 400))
+    x = om.inv_softplus(y)
+    back = np.log1p(np.exp(x))
+    np.testing.assert_allclose(back, y, rtol=1e-12)
+    lo = y <= 20
+    np.testing.assert_allclose(om.softplus(x[lo]), y[lo], rtol=1e-12)
+    # above 20 the oracle's softplus is the identity (torch's threshold), which
+    # differs from log1p(exp(x)) by under e^-20 relative
+    np.testing.assert_allclose(om.softplus(x[~lo]), y[~lo], rtol=np.exp(-20.0))
+    assert abs(om.inv_softplus(np.log(2.0))) < 1e-15
+    assert np.all(np.diff(x) > 0)                    # increasing, as softplus is
