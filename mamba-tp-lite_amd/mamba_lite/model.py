@@ -22,7 +22,6 @@ the reference casts it to the activation dtype (model.py:241).
 """
 from __future__ import annotations
 
-import contextlib
 import json
 import os
 from dataclasses import dataclass
@@ -129,20 +128,6 @@ class MambaCache:
 # is kept and the scan reads the slices through their strides.
 SPLIT_PROJ_MIN_TOKENS = 16384
 
-# Prefills of at most this many tokens run their per-layer projections on
-# torch's rocBLAS path instead of hipBLASLt: each hipBLASLt call costs about
-# 18.6 us of host time against 7.3 us for rocBLAS, and at these sizes the
-# host is the bottleneck (measured on MI355X at the 130m shape, 64 tokens: 4
-# projections per layer, device time 3-13 us each).  The tied lm_head stays on
-# hipBLASLt, whose kernel is faster there (54 us against 91 us for 64 x 50280).
-# An fp32 prompt of <= 64 tokens that mtl_prefill_short takes (below) never
-# reaches these GEMMs.  Set SMALL_PREFILL_BLAS to None to leave torch's backend
-# choice alone.  A prefill being captured into a HIP graph
-# (cuda_graph.GraphedPrefill) has no host cost per launch, so it keeps
-# hipBLASLt (a 64-token 130m prefill on library GEMMs replayed in 1.42 ms that
-# way against 1.64 ms on rocBLAS).
-SMALL_PREFILL_TOKENS = 256
-SMALL_PREFILL_BLAS: str | None = "cublas"
 
 # Batched step projections run on mtl_linear_skinny (fp32, <= 32 tokens);
 # out_proj as this many split-K parts.
@@ -153,10 +138,9 @@ SKINNY_OUT_SPLIT = 4
 # x_proj (few weight rows) split over K into up to 16 parts that
 # mtl_sum_parts adds, and, inside MambaLM.prefill, out_proj as
 # SKINNY_OUT_SPLIT parts that the residual add sums.  The tied lm_head stays
-# on the library GEMM (faster at 64 x 50280 x 768: 66 against 69 us).  An
-# eager MambaLM.prefill that takes the host-light rocBLAS path
-# (SMALL_PREFILL_BLAS) keeps the library GEMMs there as well: that path is
-# bound by host time per launch, which the split x_proj adds to.
+# on the library GEMM (faster at 64 x 50280 x 768: 66 against 69 us).
+# Prefills of more tokens keep torch's GEMMs on torch's own backend choice:
+# the library never changes that process-wide setting.
 _SKINNY_PREFILL = True
 
 # A prompt of at most 64 tokens on an fp32 model runs its whole layer stack
@@ -214,27 +198,6 @@ _XPROJ_PARTS = 4
 # 1.4b 2406 against 2414); at 2 rows the fused step is well ahead (130m 407
 # against 475, 1.4b 1730 against 2343).
 FUSED_STEP_MAX_BATCH = 2
-
-
-@contextlib.contextmanager
-def _prefer_blas(lib: str | None):
-    """Selects torch's BLAS backend for the enclosed GEMMs and restores the
-    caller's choice afterwards.  It is a process-wide torch setting: GEMMs
-    another thread issues meanwhile run on the same backend, which can change
-    their speed and the rounding of their sums (each library is a correct
-    fp32 GEMM; they differ in summation order)."""
-    if lib is None or not torch.cuda.is_available():
-        yield
-        return
-    prev = torch.backends.cuda.preferred_blas_library()
-    if str(prev).lower().endswith(lib):
-        yield
-        return
-    torch.backends.cuda.preferred_blas_library(lib)
-    try:
-        yield
-    finally:
-        torch.backends.cuda.preferred_blas_library(prev)
 
 
 def _f32(t: torch.Tensor | None) -> torch.Tensor | None:
@@ -575,18 +538,14 @@ class MambaLM(nn.Module):
         x = self.embedding(input_ids)
         new_layers: list[LayerCache] = []
 
-        small = input_ids.numel() <= SMALL_PREFILL_TOKENS and not torch.cuda.is_current_stream_capturing()
-        host_bound = small and SMALL_PREFILL_BLAS is not None
-
         def layer(i, xn):
             lc = cache.layers[i] if cache is not None else None
             oc = out_cache.layers[i] if out_cache is not None else None
-            y, cs, hs = self.layers[i].mixer._prefill(xn, lc, oc, parts_ok=True, skinny=not host_bound)
+            y, cs, hs = self.layers[i].mixer._prefill(xn, lc, oc, parts_ok=True)
             new_layers.append(LayerCache(conv_state=cs, ssm_state=hs))
             return y
 
-        with _prefer_blas(SMALL_PREFILL_BLAS if small else None):
-            xf = self._run(x, layer)
+        xf = self._run(x, layer)
         return self.lm_head(xf), (out_cache if out_cache is not None else MambaCache(new_layers))
 
     # ---- short prompt as one C call ----

@@ -405,27 +405,27 @@ def test_kernels_run_on_the_callers_current_stream():
         assert torch.equal(a.ssm_state, r.ssm_state) and torch.equal(a.conv_state, r.conv_state)
 
 
-def test_small_prefill_restores_the_blas_backend():
-    """A prefill of at most SMALL_PREFILL_TOKENS tokens runs its projections on
-    rocBLAS and leaves torch's backend choice as it found it."""
-    from mamba_lite import model as mm
+def test_prefill_leaves_the_blas_backend_alone():
+    """No library call changes torch's process-wide BLAS backend choice (a
+    GEMM another thread issues meanwhile keeps its backend and rounding)."""
     torch.manual_seed(6)
     cfg = MambaConfig(d_model=64, n_layer=1, vocab_size=128, d_state=16)
     with torch.device(DEV):
         model = MambaLM(cfg).eval()
     before = torch.backends.cuda.preferred_blas_library()
-    ids = torch.randint(0, cfg.vocab_size, (1, 16), device=DEV)
     with torch.no_grad():
-        model.prefill(ids)
-    assert torch.backends.cuda.preferred_blas_library() == before
-    assert ids.numel() <= mm.SMALL_PREFILL_TOKENS
+        for l in (16, 100, 300):
+            ids = torch.randint(0, cfg.vocab_size, (1, l), device=DEV)
+            _, cache = model.prefill(ids)
+            assert torch.backends.cuda.preferred_blas_library() == before
+            model.step(ids[:, :1], cache)
+            assert torch.backends.cuda.preferred_blas_library() == before
 
 
 def test_graphed_prefill_replays_match_eager_and_feed_the_stepper():
     """GraphedPrefill: every replay equals an eager prefill on the graph's BLAS
     backend bit for bit (logits, and every layer's final states written into
-    the shared cache), and the default eager prefill within fp32 tolerance;
-    between replays the program runs its own eager work.  A GraphedStepper
+    the shared cache); between replays the program runs its own eager work.  A GraphedStepper
     captured on the same cache then decodes from the graphed prompt exactly
     as eager steps decode from the eager prompt."""
     from mamba_lite import model as mm
@@ -441,29 +441,21 @@ def test_graphed_prefill_replays_match_eager_and_feed_the_stepper():
     st = GraphedStepper(model, cache, b, DEV)
     st.capture()
     g = torch.Generator(device=DEV).manual_seed(3)
-    orig = mm.SMALL_PREFILL_BLAS
-    try:
-        with torch.no_grad():
-            for k in range(3):
-                print(f"graphed prefill replay {k}", flush=True)
-                ids = torch.randint(0, cfg.vocab_size, (b, l), device=DEV, generator=g)
-                logits = gp.replay(ids).clone()
-                mm.SMALL_PREFILL_BLAS = None                 # the backend a capture uses
-                ref, rc = model.prefill(ids)
-                mm.SMALL_PREFILL_BLAS = orig
-                assert torch.equal(logits, ref), k
-                for a, r in zip(cache.layers, rc.layers):
-                    assert torch.equal(a.conv_state, r.conv_state) and torch.equal(a.ssm_state, r.ssm_state)
-                dflt, _ = model.prefill(ids)
-                torch.testing.assert_close(logits, dflt, atol=1e-4, rtol=1e-4)
-                nxt = ref[:, -1:].argmax(-1)
-                for _ in range(4):
-                    got = st.replay(nxt).clone()
-                    exp = model.step(nxt, rc)
-                    assert torch.equal(got, exp)
-                    nxt = exp[:, -1].argmax(-1, keepdim=True)
-    finally:
-        mm.SMALL_PREFILL_BLAS = orig
+    with torch.no_grad():
+        for k in range(3):
+            print(f"graphed prefill replay {k}", flush=True)
+            ids = torch.randint(0, cfg.vocab_size, (b, l), device=DEV, generator=g)
+            logits = gp.replay(ids).clone()
+            ref, rc = model.prefill(ids)
+            assert torch.equal(logits, ref), k
+            for a, r in zip(cache.layers, rc.layers):
+                assert torch.equal(a.conv_state, r.conv_state) and torch.equal(a.ssm_state, r.ssm_state)
+            nxt = ref[:, -1:].argmax(-1)
+            for _ in range(4):
+                got = st.replay(nxt).clone()
+                exp = model.step(nxt, rc)
+                assert torch.equal(got, exp)
+                nxt = exp[:, -1].argmax(-1, keepdim=True)
     with pytest.raises(ValueError):
         gp.replay(torch.zeros(b, l + 1, dtype=torch.long, device=DEV))
 
@@ -476,12 +468,9 @@ def test_short_prefill_on_the_skinny_gemm_vs_oracle(b, l, monkeypatch):
     summed by the residual add.  Logits and
     final states against the float64 oracle at 1e-4, and against the same
     prefill on torch's GEMMs at 1e-5; the mixer's own prefill (out_proj as
-    one tensor) against the oracle's mixer.  The skinny GEMMs run where a
-    captured prefill runs them (SMALL_PREFILL_BLAS off); an eager prefill on
-    the host-light rocBLAS path keeps the library GEMMs."""
+    one tensor) against the oracle's mixer."""
     import mamba_lite.model as mm
     from mamba_lite import ops as mops
-    monkeypatch.setattr(mm, "SMALL_PREFILL_BLAS", None)
     monkeypatch.setattr(mm, "SHORT_PREFILL_NATIVE", False)    # the per-op launches themselves
     torch.manual_seed(11)
     cfg = MambaConfig(d_model=256, n_layer=2, vocab_size=384, d_state=16)
@@ -507,13 +496,6 @@ def test_short_prefill_on_the_skinny_gemm_vs_oracle(b, l, monkeypatch):
         logits2, _ = model.prefill(ids)
     assert_rel(logits.cpu().numpy(), logits2.cpu().numpy(), 1e-5, "skinny vs torch GEMMs")
     monkeypatch.setattr(mm, "_SKINNY_PREFILL", True)
-    monkeypatch.setattr(mm, "SMALL_PREFILL_BLAS", "cublas")
-    calls.clear()
-    with torch.no_grad():
-        logits3, _ = model.prefill(ids)
-    assert calls == [], calls
-    assert_rel(logits3.cpu().numpy(), ref, 1e-4, "logits on the rocBLAS path")
-    monkeypatch.setattr(mm, "_SKINNY_PREFILL", True)
     mx = model.layers[0].mixer
     xin = torch.randn(b, l, cfg.d_model, device=DEV)
     with torch.no_grad():
@@ -532,7 +514,6 @@ def test_short_prefill_continues_into_its_own_cache(monkeypatch):
     written are the same tensor.  Logits and states against the float64
     oracle's continuation at 1e-4."""
     import mamba_lite.model as mm
-    monkeypatch.setattr(mm, "SMALL_PREFILL_BLAS", None)
     torch.manual_seed(21)
     cfg = MambaConfig(d_model=256, n_layer=2, vocab_size=384, d_state=16)
     with torch.device(DEV):
@@ -590,7 +571,6 @@ def test_short_prefill_conv_widths_and_biases(d_conv, bias, b, l, monkeypatch):
     in_proj / out_proj biases, against the float64 oracle at 1e-4."""
     import mamba_lite.model as mm
     from mamba_lite import ops as mops
-    monkeypatch.setattr(mm, "SMALL_PREFILL_BLAS", None)
     torch.manual_seed(40 + d_conv)
     cfg = MambaConfig(d_model=128, n_layer=2, vocab_size=256, d_state=16, d_conv=d_conv, bias=bias)
     with torch.device(DEV):
@@ -621,7 +601,6 @@ def test_native_short_prefill_equals_the_per_op_path(d_conv, bias, b, l, monkeyp
     at another address (the call's pointer table is rebuilt)."""
     import mamba_lite.model as mm
     from mamba_lite import ops as mops
-    monkeypatch.setattr(mm, "SMALL_PREFILL_BLAS", None)
     print(f"native short prefill d_conv={d_conv} bias={bias} b={b} l={l}", flush=True)
     torch.manual_seed(50 + d_conv + l)
     cfg = MambaConfig(d_model=256, n_layer=3, vocab_size=320, d_state=16, d_conv=d_conv, bias=bias)
