@@ -604,7 +604,8 @@ def main():
                          "algorithmic_bytes": SCAN_BYTES,
                          "limiter": "VALU issue and the access pattern together: 102 VALU instructions per 64 "
                                     "(channel, step) pairs, 80 of them the 16-state recurrence, 76% VALU busy "
-                                    "(rocprofv3 counters; 170 us of VALU work at 100%); the same channel-major "
+                                    "(rocprofv3 counters; 156 us of VALU issue at 100% and the 2.4 GHz peak "
+                                    "clock, scan_valu_roofline); the same channel-major "
                                     "u/delta/z/y stream with no arithmetic takes 173 us (4.65 TB/s)"},
         })
         extra["scan_valu_roofline"] = valu_roofline("fp32_b32_d1536_l1024", ms * 1e3)
