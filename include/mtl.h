@@ -167,7 +167,9 @@ int mtl_conv_step_xproj(float* conv_state, const float* x, int64_t x_sb, const f
  * it -- but the partials live in a fixed device array inside the library
  * (2^20 floats = 4 MiB per GPU, held until the process ends) instead of a
  * caller buffer.  Rejects ceil(D / 32) * b * J > 2^20 with MTL_EINVAL.
- * Allocates and frees nothing.  Every call on one GPU shares that GPU's
+ * The array used is the one of the device `stream` belongs to (the current
+ * device for the null stream), whichever device the calling thread has
+ * current.  Allocates and frees nothing.  Every call on one GPU shares that GPU's
  * array: calls that overlap on one GPU (different streams, threads or
  * processes sharing a context) race and must be serialized by the caller.
  * ---------------------------------------------------------------------- */

@@ -459,14 +459,26 @@ constexpr int kMaxScratchDevices = 64;
 std::mutex g_scratch_mu;
 float* g_scratch_ptr[kMaxScratchDevices] = {};
 
-// Device address of `scratch` on the current device (looked up on the first
-// call on each device).
-int scratch_on_current_device(float** out) {
-    int dev = -1;
-    hipError_t e = hipGetDevice(&dev);
+// Device address of `scratch` on the device that `stream` belongs to (looked
+// up on the first call on each device).  The lookup needs that device to be
+// the current one, so when the calling thread has another device current it
+// is switched for the lookup and switched back.
+int scratch_for_stream(hipStream_t stream, float** out) {
+    int cur = -1;
+    hipError_t e = hipGetDevice(&cur);
     if (e != hipSuccess) {
         set_error(std::string("hipGetDevice: ") + hipGetErrorString(e));
         return MTL_EHIP;
+    }
+    int dev = cur;
+    if (stream != nullptr) {
+        hipDevice_t sd = -1;
+        e = hipStreamGetDevice(stream, &sd);
+        if (e != hipSuccess) {
+            set_error(std::string("hipStreamGetDevice: ") + hipGetErrorString(e));
+            return MTL_EHIP;
+        }
+        dev = static_cast<int>(sd);
     }
     if (dev < 0 || dev >= kMaxScratchDevices) {
         set_error("device index beyond the scratch table");
@@ -474,10 +486,19 @@ int scratch_on_current_device(float** out) {
     }
     std::lock_guard<std::mutex> lock(g_scratch_mu);
     if (g_scratch_ptr[dev] == nullptr) {
+        if (dev != cur && (e = hipSetDevice(dev)) != hipSuccess) {
+            set_error(std::string("hipSetDevice: ") + hipGetErrorString(e));
+            return MTL_EHIP;
+        }
         void* p = nullptr;
         e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        const hipError_t back = dev != cur ? hipSetDevice(cur) : hipSuccess;
         if (e != hipSuccess || p == nullptr) {
             set_error(std::string("hipGetSymbolAddress(scratch): ") + hipGetErrorString(e));
+            return MTL_EHIP;
+        }
+        if (back != hipSuccess) {
+            set_error(std::string("hipSetDevice (restoring the caller's device): ") + hipGetErrorString(back));
             return MTL_EHIP;
         }
         g_scratch_ptr[dev] = static_cast<float*>(p);
@@ -518,10 +539,10 @@ extern "C" int mtl_conv_step_xproj_noalloc(float* conv_state, const float* x, in
                 "ceil(dim / 32) * batch * xdbl_cols exceeds the 2^20-float scratch; use mtl_conv_step_xproj with "
                 "a caller buffer");
     MTL_REQUIRE((conv_state || width == 1) && x && w && out && W_xT && x_dbl, "null required pointer");
-    float* part = nullptr;
-    const int rc = scratch_on_current_device(&part);
-    if (rc != MTL_OK) return rc;
     hipStream_t st = as_stream(stream);
+    float* part = nullptr;
+    const int rc = scratch_for_stream(st, &part);
+    if (rc != MTL_OK) return rc;
     // every [block, row, column] of the partials is written before it is read:
     // nothing in the scratch needs clearing between calls
     const int r1 = launch_conv_step_xproj(conv_state, x, x_sb, w, bias, out, out_sb, W_xT, part, batch, dim, width,

@@ -55,6 +55,20 @@ def test_noalloc_matches_caller_buffer_entry_point(shapes):
         assert torch.equal(xd1, xd2), "x_dbl"
 
 
+def test_noalloc_on_a_side_stream_takes_that_streams_device():
+    """A non-null stream: the scratch is looked up from the stream's device."""
+    rng = np.random.default_rng(8)
+    c = _case(rng, 4, 2048, 160, 4)
+    s1, xc1, xd1 = _existing(c)
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream()
+    with torch.cuda.stream(side):
+        print("\n[noalloc on a side stream b=4 D=2048 J=160]", flush=True)
+        s2, xc2, xd2 = _noalloc(c)
+    side.synchronize()
+    assert torch.equal(xc1, xc2) and torch.equal(s1, s2) and torch.equal(xd1, xd2)
+
+
 def test_noalloc_rejects_sizes_beyond_its_scratch():
     lib = _lib.load()
     P = ctypes.c_void_p(256)     # never dereferenced: the size check comes first
