@@ -17,7 +17,9 @@
  *   - Strides are in ELEMENTS of the tensor they describe.
  *   - Activations are fp32 or bf16 (`dtype`); weights, A, D, biases and the
  *     SSM state are always fp32.
- *   - Calls are stateless and re-entrant; calls on one stream are ordered.
+ *   - Calls are re-entrant; calls on one stream are ordered.  Two keep device
+ *     state between calls: mtl_decode_step_persist in the caller's workspace
+ *     and mtl_conv_step_xproj_noalloc in a per-GPU array of the library.
  */
 #ifndef MTL_H
 #define MTL_H
@@ -540,8 +542,12 @@ int mtl_decode_step(const mtl_decode_step_args* args, const mtl_decode_layer* la
  *            256-byte aligned, zero-filled before its first use and then
  *            left to the library: it carries an epoch from call to call
  *            (word 0) and an error word (word 1, nonzero after a wait timed
- *            out; the logits of that call are then NaN).  Calls that share a
- *            workspace must be ordered (one stream); concurrent calls race.
+ *            out; the logits of that call are then NaN and its layer caches
+ *            partly advanced).  After a nonzero error word the workspace
+ *            must be zero-filled again before the next call: a workgroup of
+ *            the failed launch that started late may have left slots tagged
+ *            for the next one.  Calls that share a workspace must be ordered
+ *            (one stream); concurrent calls race.
  *   blocking 0 picks the register blocking (workgroups per launch) itself;
  *            1 and 2 force 6 or 3 channels per compute wavefront pair.
  * Shapes: d_model a multiple of 4 up to 1024, d_inner a multiple of 4 up to

@@ -46,7 +46,10 @@
 // Waits are bounded: a wait that exceeds kSpinLimit polls writes a code
 // naming this launch into the error word of the workspace, stops waiting for
 // later exchanges and lets the launch finish; the final residual, and so
-// the logits, of that launch are then NaN.  All G
+// the logits, of that launch are then NaN.  A workgroup of such a launch
+// that started after workgroup 0 advanced the epoch tags its slots for the
+// next launch, so the caller zero-fills the workspace again before reusing
+// it (the host API says so).  All G
 // workgroups must be resident at once: the host keeps G at most the CU count
 // and checks the occupancy.
 

@@ -574,6 +574,21 @@ def decode_persist_workspace(cfg, device) -> torch.Tensor:
     return torch.zeros(n, dtype=torch.uint8, device=device)
 
 
+def decode_persist_error(workspace) -> int:
+    """The error word of a persistent-step workspace (synchronizes with the
+    device): 0, or the code of a launch whose wait timed out.  After a
+    nonzero word, reset_decode_persist_workspace() before the next call."""
+    if workspace.dtype != torch.uint8 or workspace.numel() < 8:
+        raise ValueError("decode_persist_error: not a persistent-step workspace")
+    return int(workspace[4:8].view(torch.int32).item()) & 0xFFFFFFFF
+
+
+def reset_decode_persist_workspace(workspace) -> None:
+    """Zero-fill a persistent-step workspace (epoch, error word and slots), as
+    after a call whose error word was nonzero.  Stream-ordered, no sync."""
+    workspace.zero_()
+
+
 def decode_step_persist(layers, layers_dev, ids, emb, norm_f, eps_f, logits, x0, workspace, cfg, blocking=0):
     """mtl_decode_step_persist: the batch-1 decode step of every layer as one
     persistent launch, then norm_f + the tied lm_head into logits [1, vocab].

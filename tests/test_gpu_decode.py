@@ -386,8 +386,9 @@ def test_fused_step_rejects_a_mismatched_cache_before_any_launch(bad):
 
 
 def _persist_err_word(model):
+    from mamba_lite import ops
     ws = getattr(model, "_persist_ws", {})
-    return [int(t[4:8].view(torch.int32).item()) for t in ws.values()]
+    return [ops.decode_persist_error(t) for t in ws.values()]
 
 
 @pytest.mark.parametrize("d_model,n_layer,blocking", [(64, 2, 0), (64, 2, 1), (64, 2, 2), (768, 3, 1), (768, 3, 2),

@@ -280,6 +280,24 @@ def test_persistent_decode_grid_query():
     assert lib.mtl_decode_persist_grid(768, 1536, 16, 48, 8, 24, 0) == 0       # d_conv 8
 
 
+def test_persistent_workspace_error_word_and_reset():
+    """The error word is bytes 4..8 of the workspace (an unsigned code, 0 when
+    no wait timed out); the reset zero-fills epoch, error word and slots."""
+    from mamba_lite import ops
+    cfg = MambaConfig(d_model=768, n_layer=1, vocab_size=8)
+    ws = ops.decode_persist_workspace(cfg, "cpu")
+    assert ws.numel() == 256 + 8 * (288 * 80 + 2048 + 1024) and int(ws.sum()) == 0
+    assert ops.decode_persist_error(ws) == 0
+    ws[0:4].view(torch.int32)[0] = 7                       # an epoch
+    ws[4:8].view(torch.int32)[0] = -3                      # code 0xFFFFFFFD
+    ws[300] = 9                                           # a slot byte
+    assert ops.decode_persist_error(ws) == 0xFFFFFFFD
+    ops.reset_decode_persist_workspace(ws)
+    assert int(ws.sum()) == 0 and ops.decode_persist_error(ws) == 0
+    with pytest.raises(ValueError):
+        ops.decode_persist_error(torch.zeros(4, dtype=torch.uint8))
+
+
 def test_from_pretrained_loads_in_proj_bias_of_a_bias_snapshot(tmp_path):
     """A `use_bias: true` snapshot: the in_proj and out_proj biases are both
     loaded.  (The reference's loader remaps out_proj.bias only, so its strict
