@@ -167,11 +167,16 @@ DECODE_PERSIST = False
 PERSIST_BLOCKING = 0
 
 
-def _persist_ok(cfg: MambaConfig) -> bool:
-    """Whether mtl_decode_step_persist takes this shape (asked of the library:
-    a register blocking must fit it)."""
-    return _lib.load().mtl_decode_persist_grid(cfg.d_model, cfg.d_inner, cfg.d_state, cfg.dt_rank, cfg.d_conv,
-                                               cfg.n_layer, PERSIST_BLOCKING) > 0
+def _persist_grid(cfg: MambaConfig) -> int:
+    """Workgroups mtl_decode_step_persist would launch for this shape, or 0
+    when it does not take it (asked of the library: a register blocking must
+    fit it)."""
+    return int(_lib.load().mtl_decode_persist_grid(cfg.d_model, cfg.d_inner, cfg.d_state, cfg.dt_rank, cfg.d_conv,
+                                                   cfg.n_layer, PERSIST_BLOCKING))
+
+
+def _cu_count(device) -> int:
+    return torch.cuda.get_device_properties(device).multi_processor_count
 
 
 def _skinny_rows(x: torch.Tensor, w: torch.Tensor, enabled: bool = True) -> torch.Tensor | None:
@@ -714,8 +719,8 @@ class MambaLM(nn.Module):
             q = max(1, min(256 // (J * b), 8))
             return -(-nblk // q) <= 64
         split_k_max_b = max([b for b in (1, 2, 4) if _fits(b)], default=0)
-        persist = _persist_ok(cfg)
-        need_xt = split_k_max_b > 0 or persist    # the persistent step reads x_proj transposed too
+        persist = _persist_grid(cfg)
+        need_xt = split_k_max_b > 0 or persist > 0    # the persistent step reads x_proj transposed too
         layers = []
         with torch.no_grad():
             for m in self.layers:
@@ -806,7 +811,9 @@ class MambaLM(nn.Module):
         # stream (measured at d_model 2048: 12.87 -> 12.63 us; at batch 2 and 4
         # the 8-channel blocks are faster)
         cpb = 4 if b == 1 and not split_k else plan["cpb"]
-        if DECODE_STEP_NATIVE and DECODE_PERSIST and b == 1 and plan["persist"]:
+        # its workgroups must all be resident at once: a device with fewer CUs
+        # than its grid (a partitioned GPU) runs the three-kernel step
+        if DECODE_STEP_NATIVE and DECODE_PERSIST and b == 1 and 0 < plan["persist"] <= _cu_count(dev):
             self._check_step_cache(cache, b, dev)
             tmpl = self._decode_step_template(plan, True, dev)
             tab = self._persist_table(tmpl, dev) if tmpl is not None else None
