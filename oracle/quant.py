@@ -82,8 +82,10 @@ def quant_dequant_sum_int8_tok(parts):
 def fp16_sum(parts):
     """tp_utils.py:37-42 locally: low_r = fp16(part_r); SUM in fp16; back to
     fp32.  Returns (out float32, list of fp16 payloads)."""
-    lows = [np.ascontiguousarray(p, np.float32).astype(np.float16) for p in parts]
-    acc = lows[0]
-    for lo in lows[1:]:
-        acc = (acc + lo).astype(np.float16)   # numpy half add: fp32 add rounded to fp16 (RNE)
+    # values beyond the fp16 range become +-inf, as torch's .half() makes them
+    with np.errstate(over="ignore"):
+        lows = [np.ascontiguousarray(p, np.float32).astype(np.float16) for p in parts]
+        acc = lows[0]
+        for lo in lows[1:]:
+            acc = (acc + lo).astype(np.float16)   # numpy half add: fp32 add rounded to fp16 (RNE)
     return acc.astype(np.float32), lows
