@@ -1,7 +1,8 @@
 """Benchmark of the Mamba mixer hot path on one MI355X.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W]
-                   [--only scan|decode|quant|shard|prefill|prefill-short|copy|decode-counters|all]
+                   [--only scan|decode|quant|shard|prefill|prefill-short|prefill-long|copy|decode-counters|all]
+                   [--decode-shapes 130m,1.4b] [--decode-persist] [--no-cpu-baseline]
 
 Headline (`value`): fused selective-scan prefill throughput, fp32, on the
 isolated-op workload u, delta, z [32, 1536, 1024], B, C [32, 16, 1024],
@@ -513,6 +514,9 @@ def main():
                              "copy", "decode-counters"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--decode-shapes", default="130m,1.4b", help="comma list of 130m, 1.4b")
+    ap.add_argument("--decode-persist", action="store_true",
+                    help="decode batch 1 through the persistent single-launch step (off by default in MambaLM); "
+                         "the shapes it does not take run their usual step")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU and has no multi-GPU mode (asked for --gpus {args.gpus}); "
@@ -627,6 +631,10 @@ def main():
 
     if want("decode"):
         dec = {}
+        if args.decode_persist:
+            import mamba_lite.model as mm
+            mm.DECODE_PERSIST = True
+            extra["decode_persist"] = True
         for name, cfg_kw, batches, prompt, ntok in (
                 ("130m", dict(d_model=768, n_layer=24, vocab_size=50280), (1,), 64, 256),
                 ("1.4b", dict(d_model=2048, n_layer=48, vocab_size=50280), (1, 32), 1024, 256)):
