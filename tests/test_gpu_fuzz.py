@@ -1,0 +1,107 @@
+"""Seeded random configurations of MambaLM against the float64 oracle.
+
+Each case draws a model shape (d_model among sizes that do and do not take
+the matrix-core paths, d_state 1-16, d_conv 1-4, expand 1-2, dt_rank, the
+in/out and conv biases, 1-3 layers), a batch and two prompt lengths, then
+checks at 1e-4 (relative to each element plus the tensor's rms):
+  * the prefill logits and every layer's final conv and SSM states
+    (reference model.py:328-341 over 184-241);
+  * a continuation prefill from that cache (334-341 with a cache);
+  * two teacher-forced steps from the continuation's cache, logits and the
+    states after them (343-353 over 249-294).
+The draws reach the matrix-core short-prompt projections (at most 64 token
+rows, d_model a multiple of 128), the fused decode (batch 1 and 2) and the
+per-op step (batch 3 and 5), the chunked and the tiled scan, and the
+d_conv = 1 step that skips the conv; four fixed cases add the one-call short
+prefill (d_inner a multiple of 512 as well).
+"""
+import numpy as np
+import pytest
+import torch
+
+import _golden as G
+from _util import assert_rel
+from mamba_lite.model import MambaConfig, MambaLM
+from oracle import mixer as om
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+N_CASES = 96
+
+
+def _draw(seed):
+    r = np.random.default_rng(1000 + seed)
+    d_model = int(r.choice([32, 48, 64, 96, 128, 256, 384, 512]))
+    cfg = dict(d_model=d_model, n_layer=int(r.integers(1, 4)), vocab_size=int(r.choice([64, 100])),
+               d_state=int(r.choice([1, 4, 8, 13, 16])), d_conv=int(r.choice([1, 2, 3, 4])),
+               expand=int(r.choice([1, 2])), bias=bool(r.integers(0, 2)), conv_bias=bool(r.integers(0, 2)))
+    if r.integers(0, 2):
+        cfg["dt_rank"] = int(r.integers(1, min(64, d_model) + 1))
+    batch = int(r.choice([1, 2, 3, 5]))
+    l0 = int(r.choice([1, 7, 33, 64, 65, 130]))
+    if r.integers(0, 2):
+        l0 = max(1, min(l0, 64 // batch))      # a short prompt: the one-call prefill where the shape allows
+    l1 = int(r.choice([1, 5, 40]))
+    return cfg, batch, l0, l1
+
+
+# drawn so that the one-call short prefill takes them (fp32, at most 64 token
+# rows, d_model a multiple of 128, d_inner a multiple of 512, J a multiple of 4)
+SHORT_CASES = [
+    (dict(d_model=512, n_layer=2, vocab_size=64, d_state=16, d_conv=4, expand=1, bias=True, conv_bias=False), 2, 17, 5),
+    (dict(d_model=256, n_layer=1, vocab_size=100, d_state=8, d_conv=2, expand=2, dt_rank=16, bias=False,
+          conv_bias=True), 1, 64, 1),
+    (dict(d_model=512, n_layer=3, vocab_size=64, d_state=4, d_conv=3, expand=2, bias=False, conv_bias=True), 3, 21,
+     40),
+    (dict(d_model=384, n_layer=1, vocab_size=64, d_state=12, d_conv=4, expand=4, dt_rank=24, bias=True,
+          conv_bias=True), 1, 1, 5),
+]
+
+
+def _case(i):
+    return _draw(i) if i < N_CASES else SHORT_CASES[i - N_CASES]
+
+
+def _cache_np(cache):
+    return [(lc.conv_state.detach().float().cpu().numpy(), lc.ssm_state.detach().float().cpu().numpy())
+            for lc in cache.layers]
+
+
+def _check_cache(got, ref, what):
+    for i, ((gc, gh), (rc, rh)) in enumerate(zip(got, ref)):
+        assert_rel(gc, rc, 1e-4, f"{what} layer {i} conv_state")
+        assert_rel(gh, rh, 1e-4, f"{what} layer {i} ssm_state")
+
+
+@pytest.mark.parametrize("seed", range(N_CASES + len(SHORT_CASES)))
+def test_random_config_prefill_continue_step_vs_oracle(seed):
+    cfg_kw, batch, l0, l1 = _case(seed)
+    print(f"\n[fuzz {seed}: {cfg_kw} batch={batch} prompt={l0} continuation={l1}]", flush=True)
+    cfg = MambaConfig(**cfg_kw)
+    extra = {k: cfg_kw[k] for k in ("d_state", "d_conv", "expand", "bias", "conv_bias", "dt_rank") if k in cfg_kw}
+    sd = G.lm_weights(2000 + seed, cfg.d_model, cfg.n_layer, cfg.vocab_size, **extra)
+    lm = MambaLM(cfg)
+    lm.load_state_dict({k: torch.from_numpy(v) for k, v in sd.items()}, strict=True)
+    lm = lm.to(DEV).eval()
+    W = G.oracle_lm_dict(sd, cfg.n_layer)
+    ids = np.random.default_rng(3000 + seed).integers(0, cfg.vocab_size, (batch, l0 + l1 + 2), dtype=np.int64)
+    tids = torch.from_numpy(ids).to(DEV)
+
+    ref0, rc0 = om.lm_prefill(W, ids[:, :l0], dtype=np.float64)
+    ref1, rc1 = om.lm_prefill(W, ids[:, l0:l0 + l1], cache=[(c.copy(), h.copy()) for c, h in rc0], dtype=np.float64)
+    with torch.no_grad():
+        if seed >= N_CASES:
+            assert lm._prefill_short(tids[:, :l0], None, None) is not None, "the one-call short prefill"
+        got0, c0 = lm.prefill(tids[:, :l0])
+        assert_rel(got0.float().cpu().numpy(), ref0, 1e-4, "prefill logits")
+        _check_cache(_cache_np(c0), rc0, "prefill")
+        got1, c1 = lm.prefill(tids[:, l0:l0 + l1], c0)
+        assert_rel(got1.float().cpu().numpy(), ref1, 1e-4, "continuation logits")
+        _check_cache(_cache_np(c1), rc1, "continuation")
+        ocache = [(c.copy(), h.copy()) for c, h in rc1]
+        for k in range(2):
+            t = l0 + l1 + k
+            ref = om.lm_step(W, ids[:, t:t + 1], ocache, dtype=np.float64)
+            got = lm.step(tids[:, t:t + 1], c1)
+            assert_rel(got.float().cpu().numpy(), ref, 1e-4, f"step {k} logits")
+    _check_cache(_cache_np(c1), ocache, "after the steps")
