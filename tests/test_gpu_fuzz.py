@@ -14,14 +14,20 @@ rows, d_model a multiple of 128), the fused decode (batch 1 and 2) and the
 per-op step (batch 3 and 5), the chunked and the tiled scan, and the
 d_conv = 1 step that skips the conv; four fixed cases add the one-call short
 prefill (d_inner a multiple of 512 as well).
+
+A second sweep runs the mixer with bf16 activations and fp32 state (the
+tensor-parallel shard's precision, tp_model.py:85-135) on random shapes,
+both projection layouts, a prefill and a continuation from its cache,
+against the oracle on the same bf16-rounded weights and inputs with its
+activations rounded to bf16 where each op stores them, at 1e-2.
 """
 import numpy as np
 import pytest
 import torch
 
 import _golden as G
-from _util import assert_rel
-from mamba_lite.model import MambaConfig, MambaLM
+from _util import assert_rel, bf16_round
+from mamba_lite.model import LayerCache, MambaConfig, MambaLM, MambaMixer
 from oracle import mixer as om
 
 pytestmark = pytest.mark.gpu
@@ -105,3 +111,50 @@ def test_random_config_prefill_continue_step_vs_oracle(seed):
             got = lm.step(tids[:, t:t + 1], c1)
             assert_rel(got.float().cpu().numpy(), ref, 1e-4, f"step {k} logits")
     _check_cache(_cache_np(c1), ocache, "after the steps")
+
+
+N_BF16 = 32
+
+
+def _draw_bf16(seed):
+    r = np.random.default_rng(5000 + seed)
+    d_model = int(r.choice([64, 96, 128, 256, 512]))
+    cfg = dict(d_model=d_model, n_layer=1, vocab_size=8, d_state=int(r.choice([4, 8, 16])),
+               d_conv=int(r.choice([2, 3, 4])), expand=int(r.choice([1, 2])), bias=bool(r.integers(0, 2)),
+               conv_bias=bool(r.integers(0, 2)))
+    if r.integers(0, 2):
+        cfg["dt_rank"] = int(r.integers(1, min(64, d_model) + 1))
+    return cfg, int(r.choice([1, 2, 3, 4])), int(r.choice([1, 17, 64, 100, 300])), int(r.choice([1, 9, 40])), \
+        bool(r.integers(0, 2))
+
+
+@pytest.mark.parametrize("seed", range(N_BF16))
+def test_random_bf16_mixer_prefill_and_continuation_vs_oracle(seed, monkeypatch):
+    import mamba_lite.model as mm
+    cfg_kw, batch, l0, l1, split = _draw_bf16(seed)
+    print(f"\n[fuzz bf16 {seed}: {cfg_kw} batch={batch} prompt={l0} continuation={l1} split={split}]", flush=True)
+    monkeypatch.setattr(mm, "SPLIT_PROJ_MIN_TOKENS", 0 if split else 1 << 40)
+    cfg = MambaConfig(**cfg_kw)
+    extra = {k: cfg_kw[k] for k in ("d_state", "d_conv", "expand", "bias", "conv_bias", "dt_rank") if k in cfg_kw}
+    sd = {k: bf16_round(v) for k, v in G.mixer_case_weights(6000 + seed, cfg.d_model, **extra).items()}
+    m = MambaMixer(cfg, 0)
+    m.load_state_dict({k: torch.from_numpy(v) for k, v in sd.items()}, strict=True)
+    m = m.to(DEV).to(torch.bfloat16).eval()
+    p = G.oracle_mixer_dict(sd)
+    rng = np.random.default_rng(7000 + seed)
+    x0 = bf16_round(rng.standard_normal((batch, l0, cfg.d_model)).astype(np.float32))
+    x1 = bf16_round(rng.standard_normal((batch, l1, cfg.d_model)).astype(np.float32))
+    ro, rc, rh = om.mixer_prefill(p, x0, dtype=np.float64, act=bf16_round)
+    with torch.no_grad():
+        out, cs, hs = m.prefill(torch.from_numpy(x0).to(DEV).bfloat16())
+        assert out.dtype == torch.bfloat16 and hs.dtype == torch.float32
+        _n = lambda t: t.detach().float().cpu().numpy()
+        assert_rel(_n(out), ro, 1e-2, "prefill out")
+        assert_rel(_n(cs), rc, 1e-2, "prefill conv_state")
+        assert_rel(_n(hs), rh, 1e-2, "prefill ssm_state")
+        # the continuation from this build's own states (bf16 history, fp32 state)
+        ro1, rc1, rh1 = om.mixer_prefill(p, x1, conv_state=_n(cs), ssm_state=_n(hs), dtype=np.float64, act=bf16_round)
+        out1, cs1, hs1 = m.prefill(torch.from_numpy(x1).to(DEV).bfloat16(), LayerCache(cs, hs))
+        assert_rel(_n(out1), ro1, 1e-2, "continuation out")
+        assert_rel(_n(cs1), rc1, 1e-2, "continuation conv_state")
+        assert_rel(_n(hs1), rh1, 1e-2, "continuation ssm_state")
