@@ -15,8 +15,12 @@
 // taken on the bit patterns of |x| as unsigned words, so a NaN in the row
 // makes amax NaN, as torch's amax does (tp_utils.py:111); the clamp at 1e-8
 // keeps the NaN (torch.clamp does), the row's scale is NaN and its outputs
-// are NaN.  The codes of such a row are -127 here; the reference's
-// float -> int8 conversion of NaN has no defined value.
+// are NaN.  An infinite element makes the row's scale inf: its finite
+// elements quantize to 0, its own quotient inf / inf is NaN, and every
+// output of the row is 0 * inf = NaN, as in the reference.  The clamp of the
+// codes keeps a NaN quotient NaN (torch.clamp does), and a NaN code is
+// written as byte 0: the reference's float -> int8 conversion of NaN has no
+// defined value, and 0 is what x86 and GPU conversions give for it.
 
 #include "common.h"
 
@@ -28,6 +32,16 @@ namespace {
 // past the caches took two [32768, 768] partials from 64.8 to 57.2 us (int8)
 // and from 73.0 to 56.3 us (fp16).
 constexpr int kMaxParts = 8;
+
+// clamp(round_half_even(x / s), -127, 127), a NaN quotient kept NaN
+__device__ __forceinline__ float int8_code(float x, float s) {
+    const float r = rintf(x / s);
+    return r < -127.f ? -127.f : (r > 127.f ? 127.f : r);
+}
+// the payload byte of a code; a NaN code is written as 0
+__device__ __forceinline__ uint32_t int8_byte(float q) {
+    return q == q ? (uint32_t)(uint8_t)(int8_t)(int)q : 0u;
+}
 constexpr int kQThreads = 256;          // 4 wavefronts, one row each
 constexpr int kRowsPerBlock = kQThreads / 64;
 constexpr int kMaxColsPerLane = 32;     // cols <= 2048 keeps the row in registers
@@ -68,9 +82,9 @@ quant_int8_tok_kernel(PartPtrs pp, int nparts, int64_t rows, int cols, float* __
 #pragma unroll
         for (int j = 0; j < PER_LANE; ++j) {
             const int col = lane + 64 * j;
-            const float q = fminf(fmaxf(rintf(v[j] / scale), -127.f), 127.f);
+            const float q = int8_code(v[j], scale);
             if (col < cols) {
-                if (pay) __builtin_nontemporal_store((uint8_t)(int8_t)q, pay + 4 * rows + base + col);
+                if (pay) __builtin_nontemporal_store((uint8_t)int8_byte(q), pay + 4 * rows + base + col);
                 acc[j] = acc[j] + q * scale;
             }
         }
@@ -125,8 +139,8 @@ quant_int8_tok_vec_kernel(PartPtrs pp, int nparts, int64_t rows, int cols, float
                 uint32_t packed = 0;
 #pragma unroll
                 for (int k = 0; k < 4; ++k) {
-                    q[k] = fminf(fmaxf(rintf(v[j][k] / scale), -127.f), 127.f);
-                    packed |= (uint32_t)(uint8_t)(int8_t)q[k] << (8 * k);
+                    q[k] = int8_code(v[j][k], scale);
+                    packed |= int8_byte(q[k]) << (8 * k);
                     acc[j][k] = acc[j][k] + q[k] * scale;
                 }
                 if (pay) __builtin_nontemporal_store(packed, reinterpret_cast<uint32_t*>(pay + 4 * rows + base) + c4);
@@ -160,8 +174,8 @@ quant_int8_tok_wide_kernel(PartPtrs pp, int nparts, int64_t rows, int cols, floa
         uint8_t* pay = pp.pay[r];
         if (pay && lane == 0) reinterpret_cast<float*>(pay)[row] = scale;
         for (int col = lane; col < cols; col += 64) {
-            const float q = fminf(fmaxf(rintf(src[col] / scale), -127.f), 127.f);
-            if (pay) pay[4 * rows + base + col] = (uint8_t)(int8_t)q;
+            const float q = int8_code(src[col], scale);
+            if (pay) pay[4 * rows + base + col] = (uint8_t)int8_byte(q);
             const float prev = r == 0 ? 0.f : out[base + col];
             out[base + col] = prev + q * scale;
         }

@@ -85,9 +85,9 @@ def test_fp16_full_payload_shape():
 @pytest.mark.parametrize("cols", [768, 770, 4097])
 def test_int8_nan_row_propagates(cols):
     """A NaN in a row makes that row's scale NaN and its outputs NaN, as
-    torch's amax and clamp do in the reference (tp_utils.py:111); the other
-    rows stay bit-exact.  (The codes of the NaN row are left unchecked: the
-    reference converts NaN to int8, which has no defined value.)"""
+    torch's amax and clamp do in the reference (tp_utils.py:111); its codes
+    are 0, as numpy's and torch's CPU float -> int8 conversions turn NaN (the
+    oracle's codes); the other rows stay bit-exact."""
     rng = np.random.default_rng(cols)
     parts = [_student(rng, (6, cols)) for _ in range(2)]
     parts[0][2, 5] = np.nan
@@ -104,6 +104,35 @@ def test_int8_nan_row_propagates(cols):
     rs, rq = oq.unpack_payload(ref_pays[0], 5, cols)
     g_s, g_q = oq.unpack_payload(pays[0].cpu().numpy(), 6, cols)
     assert np.array_equal(g_s[keep], rs) and np.array_equal(g_q[keep], rq)
+    with np.errstate(invalid="ignore"):
+        _, nan_codes = oq.quantize_int8_per_token(parts[0][2:3])
+    assert (nan_codes == 0).all() and (g_q[2] == 0).all()
+
+
+@pytest.mark.parametrize("cols", [768, 13])
+def test_int8_inf_row_gives_an_infinite_scale_and_nan_outputs(cols):
+    """An inf in a row: the reference's absmax is inf, so its scale is inf
+    (tp_utils.py:111-112), every finite element quantizes to 0 and the inf
+    element's quotient inf / inf is NaN, kept by torch.clamp and converted to
+    int8 as 0; every output of the row is 0 * inf = NaN.  The same here:
+    codes all 0, as the oracle's, scale inf, outputs NaN; the other rows stay
+    bit-exact."""
+    rng = np.random.default_rng(100 + cols)
+    parts = [_student(rng, (6, cols)) for _ in range(2)]
+    parts[1][4, 3] = -np.inf
+    out, pays = ops.quant_dequant_sum_int8_tok([torch.from_numpy(p).to(DEV) for p in parts])
+    got = out.cpu().numpy()
+    s1, q1 = oq.unpack_payload(pays[1].cpu().numpy(), 6, cols)
+    assert np.isposinf(s1[4])
+    with np.errstate(invalid="ignore"):
+        ref_s, ref_q = oq.quantize_int8_per_token(parts[1][4:5])
+    assert np.isposinf(ref_s[0]) and (ref_q == 0).all() and (q1[4] == 0).all()
+    assert np.isnan(got[4]).all()
+    keep = [0, 1, 2, 3, 5]
+    ref_out, ref_pays = oq.quant_dequant_sum_int8_tok([p[keep] for p in parts])
+    assert np.array_equal(got[keep], ref_out)
+    rs, rq = oq.unpack_payload(ref_pays[1], 5, cols)
+    assert np.array_equal(s1[keep], rs) and np.array_equal(q1[keep], rq)
 
 
 @pytest.mark.parametrize("n", [1, 1000, 65536 + 3, 4096])
