@@ -20,6 +20,12 @@ tensor-parallel shard's precision, tp_model.py:85-135) on random shapes,
 both projection layouts, a prefill and a continuation from its cache,
 against the oracle on the same bf16-rounded weights and inputs with its
 activations rounded to bf16 where each op stores them, at 1e-2.
+
+A third sweep splits random mixers over 2 or 4 ranks on the one GPU
+(tp_model.LocalTPMixer): the prefill output and each rank's states equal
+the dense mixer's and its channel slices, and two steps the dense step, at
+1e-4, with two all-reduces per call (tp_model.py:85-175, the reference's
+tests/test_tp_correctness.py:76-80).
 """
 import numpy as np
 import pytest
@@ -28,6 +34,7 @@ import torch
 import _golden as G
 from _util import assert_rel, bf16_round
 from mamba_lite.model import LayerCache, MambaConfig, MambaLM, MambaMixer
+from mamba_lite.tp_model import LocalTPMixer
 from oracle import mixer as om
 
 pytestmark = pytest.mark.gpu
@@ -158,3 +165,53 @@ def test_random_bf16_mixer_prefill_and_continuation_vs_oracle(seed, monkeypatch)
         assert_rel(_n(out1), ro1, 1e-2, "continuation out")
         assert_rel(_n(cs1), rc1, 1e-2, "continuation conv_state")
         assert_rel(_n(hs1), rh1, 1e-2, "continuation ssm_state")
+
+
+N_TP = 16
+
+
+def _draw_tp(seed):
+    r = np.random.default_rng(8000 + seed)
+    ws = int(r.choice([2, 4]))
+    d_model = int(r.choice([32, 64, 96, 128, 256, 512]))
+    cfg = dict(d_model=d_model, n_layer=1, vocab_size=8, d_state=int(r.choice([1, 4, 8, 16])),
+               d_conv=int(r.choice([2, 3, 4])), expand=int(r.choice([1, 2])), bias=bool(r.integers(0, 2)),
+               conv_bias=bool(r.integers(0, 2)))
+    if r.integers(0, 2):
+        cfg["dt_rank"] = int(r.integers(1, min(64, d_model) + 1))
+    return cfg, ws, int(r.choice([1, 2, 3])), int(r.choice([1, 9, 40, 70]))
+
+
+@pytest.mark.parametrize("seed", range(N_TP))
+def test_random_tp_shards_match_the_dense_mixer(seed):
+    cfg_kw, ws, batch, l = _draw_tp(seed)
+    print(f"\n[fuzz tp {seed}: {cfg_kw} ws={ws} batch={batch} l={l}]", flush=True)
+    cfg = MambaConfig(**cfg_kw)
+    assert cfg.d_inner % ws == 0
+    extra = {k: cfg_kw[k] for k in ("d_state", "d_conv", "expand", "bias", "conv_bias", "dt_rank") if k in cfg_kw}
+    sd = G.mixer_case_weights(9000 + seed, cfg.d_model, **extra)
+    dense = MambaMixer(cfg, 0)
+    dense.load_state_dict({k: torch.from_numpy(v) for k, v in sd.items()}, strict=True)
+    dense = dense.to(DEV).eval()
+    tp = LocalTPMixer.from_dense(dense, ws)
+    g = torch.Generator(device=DEV).manual_seed(10000 + seed)
+    x = torch.randn(batch, l + 2, cfg.d_model, device=DEV, generator=g)
+    _n = lambda t: t.detach().float().cpu().numpy()
+    S = cfg.d_inner // ws
+    with torch.no_grad():
+        ref, ref_conv, ref_ssm = dense.prefill(x[:, :l])
+        out, conv, ssm = tp.prefill(x[:, :l])
+        assert tp.comm.count == 2
+        assert_rel(_n(out), _n(ref), 1e-4, "prefill out")
+        for r in range(ws):
+            sl = slice(r * S, (r + 1) * S)
+            assert_rel(_n(conv[r]), _n(ref_conv[:, sl]), 1e-4, f"rank {r} conv_state")
+            assert_rel(_n(ssm[r]), _n(ref_ssm[:, sl]), 1e-4, f"rank {r} ssm_state")
+        caches = [LayerCache(c.clone(), h.clone()) for c, h in zip(conv, ssm)]
+        dcache = LayerCache(ref_conv.clone(), ref_ssm.clone())
+        for t in range(l, l + 2):
+            o = tp.step(x[:, t], caches)
+            od = dense.step(x[:, t], dcache)
+            assert_rel(_n(o), _n(od), 1e-4, f"step {t - l}")
+        assert tp.comm.count == 2 + 2 * 2
+        assert_rel(_n(torch.cat([c.ssm_state for c in caches], 1)), _n(dcache.ssm_state), 1e-4, "states after steps")
