@@ -21,6 +21,10 @@ both projection layouts, a prefill and a continuation from its cache,
 against the oracle on the same bf16-rounded weights and inputs with its
 activations rounded to bf16 where each op stores them, at 1e-2.
 
+The first 24 random model shapes are also captured with GraphedStepper:
+four replays equal four eager steps bit for bit, logits and caches
+(reference cuda_graph.py:34-131).
+
 A third sweep splits random mixers over 2 or 4 ranks on the one GPU
 (tp_model.LocalTPMixer): the prefill output and each rank's states equal
 the dense mixer's and its channel slices, and two steps the dense step, at
@@ -33,6 +37,7 @@ import torch
 
 import _golden as G
 from _util import assert_rel, bf16_round
+from mamba_lite.cuda_graph import GraphedStepper
 from mamba_lite.model import LayerCache, MambaConfig, MambaLM, MambaMixer
 from mamba_lite.tp_model import LocalTPMixer
 from oracle import mixer as om
@@ -215,3 +220,30 @@ def test_random_tp_shards_match_the_dense_mixer(seed):
             assert_rel(_n(o), _n(od), 1e-4, f"step {t - l}")
         assert tp.comm.count == 2 + 2 * 2
         assert_rel(_n(torch.cat([c.ssm_state for c in caches], 1)), _n(dcache.ssm_state), 1e-4, "states after steps")
+
+
+@pytest.mark.parametrize("seed", range(24))
+def test_random_config_graph_replay_equals_eager(seed):
+    cfg_kw, batch, l0, _ = _draw(seed)
+    print(f"\n[fuzz graph {seed}: {cfg_kw} batch={batch} prompt={l0}]", flush=True)
+    cfg = MambaConfig(**cfg_kw)
+    extra = {k: cfg_kw[k] for k in ("d_state", "d_conv", "expand", "bias", "conv_bias", "dt_rank") if k in cfg_kw}
+    sd = G.lm_weights(2000 + seed, cfg.d_model, cfg.n_layer, cfg.vocab_size, **extra)
+    lm = MambaLM(cfg)
+    lm.load_state_dict({k: torch.from_numpy(v) for k, v in sd.items()}, strict=True)
+    lm = lm.to(DEV).eval()
+    g = torch.Generator(device=DEV).manual_seed(11000 + seed)
+    ids = torch.randint(0, cfg.vocab_size, (batch, l0), device=DEV, generator=g)
+    toks = [torch.randint(0, cfg.vocab_size, (batch, 1), device=DEV, generator=g) for _ in range(4)]
+    with torch.no_grad():
+        _, ce = lm.prefill(ids)
+        eager = [lm.step(t, ce).clone() for t in toks]
+        _, cg = lm.prefill(ids)
+        st = GraphedStepper(lm, cg, batch, "cuda")
+        st.capture()
+        for k, t in enumerate(toks):
+            got = st.replay(t).clone()
+            torch.cuda.synchronize()
+            assert torch.equal(got, eager[k]), f"replay {k}"
+    for i, (le, lg) in enumerate(zip(ce.layers, cg.layers)):
+        assert torch.equal(le.conv_state, lg.conv_state) and torch.equal(le.ssm_state, lg.ssm_state), f"layer {i}"
