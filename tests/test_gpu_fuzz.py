@@ -23,7 +23,9 @@ activations rounded to bf16 where each op stores them, at 1e-2.
 
 The first 24 random model shapes are also captured with GraphedStepper:
 four replays equal four eager steps bit for bit, logits and caches
-(reference cuda_graph.py:34-131).
+(reference cuda_graph.py:34-131); 12 more capture the prompt prefill
+(GraphedPrefill): three replays of different prompts, eager work between
+them, each equal to an eager prefill bit for bit.
 
 A third sweep splits random mixers over 2 or 4 ranks on the one GPU
 (tp_model.LocalTPMixer): the prefill output and each rank's states equal
@@ -37,8 +39,8 @@ import torch
 
 import _golden as G
 from _util import assert_rel, bf16_round
-from mamba_lite.cuda_graph import GraphedStepper
-from mamba_lite.model import LayerCache, MambaConfig, MambaLM, MambaMixer
+from mamba_lite.cuda_graph import GraphedPrefill, GraphedStepper
+from mamba_lite.model import LayerCache, MambaCache, MambaConfig, MambaLM, MambaMixer
 from mamba_lite.tp_model import LocalTPMixer
 from oracle import mixer as om
 
@@ -247,3 +249,29 @@ def test_random_config_graph_replay_equals_eager(seed):
             assert torch.equal(got, eager[k]), f"replay {k}"
     for i, (le, lg) in enumerate(zip(ce.layers, cg.layers)):
         assert torch.equal(le.conv_state, lg.conv_state) and torch.equal(le.ssm_state, lg.ssm_state), f"layer {i}"
+
+
+@pytest.mark.parametrize("seed", range(24, 36))
+def test_random_config_graphed_prefill_equals_eager(seed):
+    cfg_kw, batch, l0, _ = _draw(seed)
+    print(f"\n[fuzz graphed prefill {seed}: {cfg_kw} batch={batch} prompt={l0}]", flush=True)
+    cfg = MambaConfig(**cfg_kw)
+    extra = {k: cfg_kw[k] for k in ("d_state", "d_conv", "expand", "bias", "conv_bias", "dt_rank") if k in cfg_kw}
+    sd = G.lm_weights(2000 + seed, cfg.d_model, cfg.n_layer, cfg.vocab_size, **extra)
+    lm = MambaLM(cfg)
+    lm.load_state_dict({k: torch.from_numpy(v) for k, v in sd.items()}, strict=True)
+    lm = lm.to(DEV).eval()
+    cache = MambaCache.allocate(cfg, batch, DEV, torch.float32)
+    gp = GraphedPrefill(lm, cache, batch, l0, DEV)
+    gp.capture()
+    g = torch.Generator(device=DEV).manual_seed(12000 + seed)
+    with torch.no_grad():
+        for k in range(3):
+            ids = torch.randint(0, cfg.vocab_size, (batch, l0), device=DEV, generator=g)
+            got = gp.replay(ids).clone()
+            ref, rc = lm.prefill(ids)                       # eager work between the replays
+            torch.cuda.synchronize()
+            assert torch.equal(got, ref), f"replay {k} logits"
+            for i, (a, r) in enumerate(zip(cache.layers, rc.layers)):
+                assert torch.equal(a.conv_state, r.conv_state) and torch.equal(a.ssm_state, r.ssm_state), \
+                    f"replay {k} layer {i}"
