@@ -718,8 +718,9 @@ def main():
     result.update(extra)
     result["device"] = torch.cuda.get_device_name(dev)
     result["gemm_table"] = {"loaded": gemm_ok, "file": "mamba-tp-lite_amd/mamba_lite/gemm_table_gfx950.csv",
-                            "covers": "prefill projection and lm_head shapes of the 130m model at 32 x 1024 tokens, "
-                                      "and the lm_head of a 64-token prompt"}
+                            "covers": "prefill projection and lm_head shapes of the 130m model at 32 x 1024 tokens "
+                                      "and the lm_head of its 64-token prompt; of the 1.4b model at 1 x 1024 and "
+                                      "32 x 1024 tokens"}
     print(json.dumps(result), flush=True)
 
 

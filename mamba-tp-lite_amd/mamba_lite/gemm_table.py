@@ -2,13 +2,15 @@
 
 The projections (in_proj, x_proj, dt_proj, out_proj, the tied lm_head) are
 torch fp32 GEMMs on hipBLASLt / rocBLAS.  `gemm_table_gfx950.csv` is a torch
-TunableOp results table: for each prefill projection shape of the mamba-130m
-model at batch 32 x 1024 tokens, and the lm_head of a 64-token prompt, it
-names the
-hipBLASLt or rocBLAS solution that measured fastest on MI355X, among all
-solutions both libraries offer.  It was recorded by running the prefill
-benchmark once with TunableOp tuning on (10 iterations or 10 ms per
-candidate).
+TunableOp results table: for each prefill projection and lm_head shape of the
+mamba-130m model at batch 32 x 1024 tokens (and the lm_head of its 64-token
+prompt) and of the mamba-1.4b model at 1 x 1024 and 32 x 1024 tokens, it
+names the hipBLASLt or rocBLAS solution that measured fastest on MI355X,
+among all solutions both libraries offer.  It was recorded by running the
+prefill benchmark with TunableOp tuning on (10 iterations or 10 ms per
+candidate).  Against hipBLASLt's defaults, the 1.4b entries took the
+1024-token prefill from 42.8 K to 43.4-43.5 K tok/s at batch 1 and from
+50.4 K to 51.5-51.6 K tok/s at batch 32 (A/B in one run, twice).
 
 `enable()` turns TunableOp on with tuning off and loads the table.  Shapes in
 the table then run their tuned solution; every other GEMM keeps torch's
