@@ -355,19 +355,21 @@ def test_graph_serves_a_second_prompt_after_prefill_into_its_cache(b):
             assert torch.equal(g, e)
 
 
-def test_tuned_gemm_table_loads_and_keeps_prefill_results():
+@pytest.mark.parametrize("d_model,b", [(768, 32), (2048, 1), (2048, 32)])
+def test_tuned_gemm_table_loads_and_keeps_prefill_results(d_model, b):
     """mamba_lite.gemm_table: torch accepts the committed TunableOp table on
-    this build, and a 130m-width mixer prefill of 32 x 1024 tokens (whose
-    in_proj halves, x_proj, dt_proj and out_proj shapes are in the table)
-    gives the same output and states within 1e-4 relative as the default
-    GEMM paths."""
+    this build, and a mixer prefill of b x 1024 tokens at the 130m and 1.4b
+    widths (whose projection shapes are in the table: in_proj whole at 1 x
+    1024, its halves at 32 x 1024, x_proj, dt_proj, out_proj) gives the same
+    output and states within 1e-4 relative as the default GEMM paths."""
     import torch.cuda.tunable as tunable
     from mamba_lite import gemm_table
+    print(f"\n[tuned table: mixer d_model={d_model} b={b} x 1024]", flush=True)
     torch.manual_seed(3)
-    cfg = MambaConfig(d_model=768, n_layer=1, vocab_size=50280, d_state=16)
+    cfg = MambaConfig(d_model=d_model, n_layer=1, vocab_size=50280, d_state=16)
     with torch.device(DEV):
         mixer = MambaMixer(cfg, 0).eval()
-    x = torch.randn(32, 1024, 768, device=DEV)
+    x = torch.randn(b, 1024, d_model, device=DEV)
     with torch.no_grad():
         ref, _, ref_h = mixer.prefill(x)
         try:
