@@ -720,7 +720,7 @@ def main():
     result["gemm_table"] = {"loaded": gemm_ok, "file": "mamba-tp-lite_amd/mamba_lite/gemm_table_gfx950.csv",
                             "covers": "prefill projection and lm_head shapes of the 130m model at 32 x 1024 tokens "
                                       "and the lm_head of its 64-token prompt; of the 1.4b model at 1 x 1024 and "
-                                      "32 x 1024 tokens"}
+                                      "32 x 1024 tokens; the 1.4b batch-32 decode step's lm_head"}
     print(json.dumps(result), flush=True)
 
 

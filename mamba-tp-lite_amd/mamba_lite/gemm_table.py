@@ -19,8 +19,11 @@ rejects it (and `enable` returns False) when torch, HIP, hipBLASLt or rocBLAS
 versions or the GPU architecture differ, and every GEMM then keeps the
 default path.  TunableOp is a process-wide torch setting, so this is opt-in.
 
-Decode shapes are left out: at 32 rows the tuner preferred solutions that
-ran slower inside the captured decode graph than hipBLASLt's default.  So
+Of the decode shapes only the 1.4b batch-32 step's tied lm_head (32 x 50280
+x 2048, the one torch GEMM left in that step) is in the table: its pick took
+the captured step from 2335-2336 to 2321 us.  The 32-row projections, when
+they were torch GEMMs, ran slower inside the captured decode graph with the
+tuner's picks than with hipBLASLt's default.  So
 are the 64-token prompt's projections: the tuner's rocBLAS picks ran 1.528
 ms per prompt inside a captured 130m prefill against 1.418 ms with
 hipBLASLt's defaults (they now run on the library's own skinny GEMM).  The
