@@ -101,6 +101,7 @@ __device__ __forceinline__ float lane_read(float v, int lane) {
     return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
 }
 constexpr int kDppXor1 = 0xB1, kDppXor2 = 0x4E, kDppRowMirror = 0x140, kDppHalfMirror = 0x141;
+constexpr int kDppWaveShr1 = 0x138;   // lane i takes lane i - 1 (gfx9 wave_shr:1); lane 0 keeps its old value
 
 template <int WIDTH>
 __device__ __forceinline__ float group_sum(float v) {

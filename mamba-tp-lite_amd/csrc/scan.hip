@@ -796,10 +796,228 @@ __global__ void __launch_bounds__(kLaneChannels * 64) scan_lanes_kernel(const Sc
     }
 }
 
+// Long sequences on the same grids: each lane holds kLaneSteps consecutive
+// steps, so a chunk is 64 kLaneSteps steps.  Per state, a lane first folds
+// its steps into one affine map (pass 1: the product of their dA and the h
+// they make from a zero start), the six DPP levels scan those maps across
+// the lanes as above, lane l takes lane l - 1's end state (wave_shr:1; lane
+// 0 the chunk's incoming state) and walks its steps again from it (pass 2),
+// accumulating C . h per step.  The scan's 12 DPP instructions per state are
+// then spent once per kLaneSteps steps, and a chunk's barriers and staging
+// once per 256 steps.  Fixed order throughout: deterministic, within fp32
+// rounding of the step-by-step loop.
+// It holds more registers (NS = 16: 214 VGPRs, one 8-wavefront workgroup per
+// CU), so it is taken where the grid is one workgroup per CU at most, for
+// sequences over 128 steps and more than 4 states.  Measured against the
+// kernel above (mixer layout, HIP events): D 1536, batch 1, 1024 steps 35.5
+// -> 28.6 us, 256 steps 11.0 -> 8.4 us; bf16 D 2048, 2048 steps 81.1 -> 59.9
+// us; at 512 workgroups (D 4096) 60.7 -> 58.8 us but 104.6 -> 111.2 us at
+// batch 2, D 2048; with 4 states 13.0 -> 14.5 us.
+constexpr int kLaneSteps = 4;
+constexpr int kLanesLongMinSteps = 128;
+constexpr int64_t kLanesLongMaxWorkgroups = 256;
+constexpr int kLanesLongMinStates = 5;
+
+template <typename T, int NS>
+__global__ void __launch_bounds__(kLaneChannels * 64) scan_lanes_long_kernel(const ScanArgs a) {
+    constexpr int CW = kLaneChannels, NT = CW * 64, S = kLaneSteps, CH = 64 * S;
+    constexpr int RS = CH + 4;                          // LDS row stride: 16-byte aligned, a state-fastest fill spreads over banks
+    static_assert(S == 4, "a lane's steps are one float4 of an LDS row");
+    __shared__ __align__(16) float s_B[NS][RS];
+    __shared__ __align__(16) float s_C[NS][RS];
+    __shared__ __align__(16) float s_x[3][CW][RS];       // u, delta, z of the workgroup's channels, then y
+    // each wavefront's A and carried state per state: the state-group loop
+    // stays rolled (one group's S x 4 maps live at a time), so they are read
+    // from LDS per group rather than held in registers
+    __shared__ __align__(16) float s_A[CW][NS];
+    __shared__ __align__(16) float s_h[CW][NS];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int b = blockIdx.y;
+    const int L = a.L, D = a.D, N = a.N;
+    const int c0 = blockIdx.x * CW;
+    const int c_raw = c0 + wave;
+    const bool c_ok = c_raw < D;                       // waves past D still take part in the barriers
+    const int c = c_ok ? c_raw : D - 1;
+    const bool has_z = a.z != nullptr;
+
+    // u, delta, z (and y) tiles of CW channels x CH steps, moved cooperatively:
+    // element e of the tile is (channel, step) = (e / CH, e % CH) with unit step
+    // stride, else (e % CW, e / CW), so consecutive threads touch consecutive
+    // addresses either way
+    constexpr int XE = CW * CH / NT;                   // tile elements per thread
+    const bool x_t_fast = a.u_sl == 1;
+    const T* ub = static_cast<const T*>(a.u) + b * a.u_sb;
+    const T* db = static_cast<const T*>(a.delta) + b * a.d_sb;
+    const T* zb = has_z ? static_cast<const T*>(a.z) + b * a.z_sb : ub;
+    const int64_t z_sd = has_z ? a.z_sd : a.u_sd, z_sl = has_z ? a.z_sl : a.u_sl;
+    T* yb = static_cast<T*>(a.y) + b * a.y_sb;
+    const T* Bp = static_cast<const T*>(a.B) + b * a.B_sb;
+    const T* Cp = static_cast<const T*>(a.C) + b * a.C_sb;
+    auto xe_ct = [&](int q, int& ce, int& te) __attribute__((always_inline)) {
+        const int e = tid + q * NT;
+        ce = x_t_fast ? e / CH : e % CW;
+        te = x_t_fast ? e % CH : e / CW;
+    };
+
+    constexpr int kFill = (NS * CH + NT - 1) / NT;     // B and C values each thread stages per chunk
+    const bool bc_t_fast = a.B_sl == 1;
+    struct Chunk { float fb[kFill], fc[kFill], u[XE], d[XE], z[XE]; };
+    auto load_chunk = [&](Chunk& k, int t0) __attribute__((always_inline)) {
+#pragma unroll
+        for (int q = 0; q < kFill; ++q) {
+            const int e = min(tid + q * NT, NS * CH - 1);
+            const int n = bc_t_fast ? e / CH : e % NS, tl = bc_t_fast ? e % CH : e / NS;
+            const int tcq = min(t0 + tl, L - 1), nn = min(n, N - 1);
+            k.fb[q] = Act<T>::load(Bp + (int64_t)nn * a.B_sn + (int64_t)tcq * a.B_sl);
+            k.fc[q] = Act<T>::load(Cp + (int64_t)nn * a.C_sn + (int64_t)tcq * a.C_sl);
+        }
+#pragma unroll
+        for (int q = 0; q < XE; ++q) {
+            int ce, te;
+            xe_ct(q, ce, te);
+            const int64_t cc = min(c0 + ce, D - 1), tc = min(t0 + te, L - 1);
+            k.u[q] = Act<T>::load(ub + cc * a.u_sd + tc * a.u_sl);
+            k.d[q] = Act<T>::load(db + cc * a.d_sd + tc * a.d_sl);
+            k.z[q] = Act<T>::load(zb + cc * z_sd + tc * z_sl);
+        }
+    };
+    Chunk cur, nxt;
+    load_chunk(cur, 0);
+
+    const float bias_l2 = (a.dbias ? a.dbias[c] : 0.f) * kLog2e;
+    const float D_c = a.Dv ? a.Dv[c] : 0.f;
+    const int nl = min(lane, N - 1);
+    float a_lane = a.A[(int64_t)c * N + nl];
+    if (a.a_is_log) a_lane = -expf(a_lane);
+    a_lane = lane < N ? a_lane : 0.f;
+    float h_lane = a.h0 ? a.h0[((int64_t)b * D + c) * N + nl] : 0.f;
+    h_lane = lane < N ? h_lane : 0.f;
+    if (lane < NS) {
+        s_A[wave][lane] = a_lane;
+        s_h[wave][lane] = h_lane;
+    }
+
+    for (int t0 = 0; t0 < L; t0 += CH) {
+#pragma unroll
+        for (int q = 0; q < kFill; ++q) {
+            const int e = tid + q * NT;
+            if (NS * CH % NT == 0 || e < NS * CH) {
+                const int n = bc_t_fast ? e / CH : e % NS, tl = bc_t_fast ? e % CH : e / NS;
+                s_B[n][tl] = n < N ? cur.fb[q] : 0.f;  // padded states: identity, no output
+                s_C[n][tl] = n < N ? cur.fc[q] : 0.f;
+            }
+        }
+#pragma unroll
+        for (int q = 0; q < XE; ++q) {
+            int ce, te;
+            xe_ct(q, ce, te);
+            s_x[0][ce][te] = cur.u[q];
+            s_x[1][ce][te] = cur.d[q];
+            s_x[2][ce][te] = cur.z[q];
+        }
+        if (t0 + CH < L) load_chunk(nxt, t0 + CH);
+        __syncthreads();
+        // this lane's steps t0 + S lane + s
+        const float4 u4 = *reinterpret_cast<const float4*>(&s_x[0][wave][S * lane]);
+        const float4 d4 = *reinterpret_cast<const float4*>(&s_x[1][wave][S * lane]);
+        const float4 z4 = *reinterpret_cast<const float4*>(&s_x[2][wave][S * lane]);
+        const float uv[S] = {u4.x, u4.y, u4.z, u4.w}, dv[S] = {d4.x, d4.y, d4.z, d4.w},
+                    zv[S] = {z4.x, z4.y, z4.z, z4.w};
+        float dt[S], dx[S], yacc[S];
+#pragma unroll
+        for (int s = 0; s < S; ++s) {
+            float v = fmaf(dv[s], kLog2e, bias_l2);     // log2 units
+            if (a.softplus) v = softplus_l2_f(v);
+            v = t0 + S * lane + s < L ? v : 0.f;        // identity map past the end
+            dt[s] = v;
+            dx[s] = v * kLn2 * uv[s];                   // dt (natural units) * u
+            yacc[s] = 0.f;
+        }
+#pragma unroll 1
+        for (int n0 = 0; n0 < NS; n0 += 4) {
+            const float4 A4 = *reinterpret_cast<const float4*>(&s_A[wave][n0]);
+            const float4 H4 = *reinterpret_cast<const float4*>(&s_h[wave][n0]);
+            const float Ag[4] = {A4.x, A4.y, A4.z, A4.w}, Hg[4] = {H4.x, H4.y, H4.z, H4.w};
+            // pass 1: each state's S steps folded into one map (av, bv)
+            float dA[4][S], dB[4][S], av[4], bv[4];
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const float4 B4 = *reinterpret_cast<const float4*>(&s_B[n0 + k][S * lane]);
+                const float Bs[S] = {B4.x, B4.y, B4.z, B4.w};
+#pragma unroll
+                for (int s = 0; s < S; ++s) {
+                    dA[k][s] = __builtin_amdgcn_exp2f(dt[s] * Ag[k]);
+                    dB[k][s] = dx[s] * Bs[s];
+                }
+                float pa = dA[k][0], pb = dB[k][0];
+#pragma unroll
+                for (int s = 1; s < S; ++s) {
+                    pb = fmaf(dA[k][s], pb, dB[k][s]);
+                    pa = pa * dA[k][s];
+                }
+                av[k] = pa;
+                bv[k] = pb;
+            }
+            asm volatile("s_nop 2" ::: "memory");
+            MTL_SCAN_LEVEL4("row_shr:1 row_mask:0xf bank_mask:0xf");
+            MTL_SCAN_LEVEL4("row_shr:2 row_mask:0xf bank_mask:0xf");
+            MTL_SCAN_LEVEL4("row_shr:4 row_mask:0xf bank_mask:0xf");
+            MTL_SCAN_LEVEL4("row_shr:8 row_mask:0xf bank_mask:0xf");
+            MTL_SCAN_LEVEL4("row_bcast:15 row_mask:0xa bank_mask:0xf");
+            MTL_SCAN_LEVEL4("row_bcast:31 row_mask:0xc bank_mask:0xf");
+            asm volatile("s_nop 1" ::: "memory");
+            // pass 2: from the end state of lane l - 1 (the chunk's incoming
+            // state for lane 0) through this lane's steps
+            float hnext[4];
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const float h_end = fmaf(av[k], Hg[k], bv[k]);
+                float h = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
+                    __builtin_bit_cast(int, Hg[k]), __builtin_bit_cast(int, h_end), kDppWaveShr1, 0xf, 0xf,
+                    false));
+                const float4 C4 = *reinterpret_cast<const float4*>(&s_C[n0 + k][S * lane]);
+                const float Cs[S] = {C4.x, C4.y, C4.z, C4.w};
+#pragma unroll
+                for (int s = 0; s < S; ++s) {
+                    h = fmaf(dA[k][s], h, dB[k][s]);
+                    yacc[s] = fmaf(Cs[s], h, yacc[s]);
+                }
+                hnext[k] = lane_read(h_end, 63);
+            }
+            // every lane has read the group's old states above (LDS operations
+            // of one wavefront complete in order)
+            if (lane == 0)
+                *reinterpret_cast<float4*>(&s_h[wave][n0]) = make_float4(hnext[0], hnext[1], hnext[2], hnext[3]);
+        }
+        float yv[S];
+#pragma unroll
+        for (int s = 0; s < S; ++s) yv[s] = fmaf(D_c, uv[s], yacc[s]) * (has_z ? silu_f(zv[s]) : 1.f);
+        __syncthreads();                               // every wavefront has read its u, delta, z
+        *reinterpret_cast<float4*>(&s_x[0][wave][S * lane]) = make_float4(yv[0], yv[1], yv[2], yv[3]);
+        __syncthreads();
+#pragma unroll
+        for (int q = 0; q < XE; ++q) {
+            int ce, te;
+            xe_ct(q, ce, te);
+            if (c0 + ce < D && t0 + te < L)
+                Act<T>::store(yb + (int64_t)(c0 + ce) * a.y_sd + (int64_t)(t0 + te) * a.y_sl, s_x[0][ce][te]);
+        }
+        cur = nxt;
+    }
+    if (a.h_out && c_ok && lane < N) a.h_out[((int64_t)b * D + c) * N + lane] = s_h[wave][lane];
+}
+
 template <typename T>
 void launch_scan_lanes(const ScanArgs& a, int64_t batch, hipStream_t st) {
     dim3 grid((unsigned)((a.D + kLaneChannels - 1) / kLaneChannels), (unsigned)batch);
     dim3 block(kLaneChannels * 64);
+    if (a.L > kLanesLongMinSteps && a.N >= kLanesLongMinStates &&
+        (int64_t)grid.x * grid.y <= kLanesLongMaxWorkgroups) {
+        if (a.N <= 8) hipLaunchKernelGGL((scan_lanes_long_kernel<T, 8>), grid, block, 0, st, a);
+        else if (a.N <= 16) hipLaunchKernelGGL((scan_lanes_long_kernel<T, 16>), grid, block, 0, st, a);
+        else hipLaunchKernelGGL((scan_lanes_long_kernel<T, 32>), grid, block, 0, st, a);
+        return;
+    }
     if (a.N <= 4) hipLaunchKernelGGL((scan_lanes_kernel<T, 4>), grid, block, 0, st, a);
     else if (a.N <= 8) hipLaunchKernelGGL((scan_lanes_kernel<T, 8>), grid, block, 0, st, a);
     else if (a.N <= 16) hipLaunchKernelGGL((scan_lanes_kernel<T, 16>), grid, block, 0, st, a);

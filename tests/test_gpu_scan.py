@@ -357,20 +357,23 @@ def test_scan_large_ragged_grid(dtype, L, Lp, N, full_ops):
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-def test_chunked_matches_tiled_and_continues(dtype):
+@pytest.mark.parametrize("b,L,k", [(2, 300, 77), (1, 300, 133), (1, 1000, 300)])
+def test_chunked_matches_tiled_and_continues(dtype, b, L, k):
     """The two kernels on one mid-size mixer-layout input agree (fp32 1e-4,
     bf16 outputs within 1e-2), and the chunked kernel continued from its own
     state at a step that is not a chunk boundary reproduces its one-pass
-    result."""
-    b, D, L, N = 2, 1536, 300, 16
-    print(f"scan chunked vs tiled {dtype} b={b} D={D} L={L}", flush=True)
+    result.  At batch 1 (192 workgroups) sequences over 128 steps take the
+    chunked kernel's long form (256-step chunks, 4 steps per lane), both
+    parts of the 133 / 167 and 300 / 700 splits included; at batch 2 (384
+    workgroups) the 64-step form."""
+    D, N = 1536, 16
+    print(f"scan chunked vs tiled {dtype} b={b} D={D} L={L} k={k}", flush=True)
     c = scan_case(np.random.default_rng(31), b, D, L, N)
     y1, h1 = _run(c, "tm", dtype=dtype, algo="tiled")
     y2, h2 = _run(c, "tm", dtype=dtype, algo="chunked")
     tol = 1e-4 if dtype == torch.float32 else 1e-2
     assert_rel(y2, y1, tol, "y chunked vs tiled")
     assert_rel(h2, h1, 1e-4, "h chunked vs tiled")
-    k = 77
     cut = lambda a, sl: {**c, "u": a["u"][..., sl], "delta": a["delta"][..., sl], "z": a["z"][..., sl],
                          "B": a["B"][..., sl], "C": a["C"][..., sl]}
     ya, ha = _run(cut(c, slice(0, k)), "tm", dtype=dtype, algo="chunked")
