@@ -411,6 +411,48 @@ int mtl_in_proj_conv_xproj(const float* x, int64_t x_rs, const float* W_in, cons
                            int64_t d_inner, int32_t channels_per_part, mtl_stream_t stream);
 
 /* ------------------------------------------------------------------------
+ * A batched step's out_proj with the block's residual add and the next
+ * block's RMSNorm inputs, so no add + norm launch runs between two blocks:
+ * model.py:293 (out = out_proj(y)), 311 (x + mixer(...)) and the input side
+ * of 130-135 (the next block's norm).  The product is mtl_linear_skinny's
+ * with ksplit parts written to parts [ksplit, M, N] (bias in part 0); the
+ * last workgroup of each n-tile to finish then adds the parts in order and
+ * the residual, exactly as mtl_add_rmsnorm_parts does:
+ *   h[m][n] += ((parts[0][m][n] + parts[1][m][n]) + ...)      (in place)
+ * and writes x_next[m][n] = h[m][n] * w_next[n] and, per n-tile t of
+ * rows_per_block columns, sq[t][m] = the sum over its columns, in order, of
+ * h[m][n]^2.  mtl_in_proj_conv_xproj_normed takes x_next and sq as the next
+ * block's input.  counters [N / rows_per_block] must be zero on entry (each
+ * counts its tile's ksplit workgroups; none is reset), so every call needs
+ * zeroed counters of its own.
+ *   x: [M, K] (row stride x_rs), 1 <= M <= 32; W: [N, K] contiguous; bias:
+ *   [N] or NULL; h, x_next: [M, N] contiguous, not aliasing; w_next: [N];
+ *   sq: [N / rows_per_block, M].
+ * N a multiple of rows_per_block (16 or 32); 1 <= ksplit <= 4; K a multiple
+ * of 128 * ksplit.
+ * x, W, bias, parts, h, w_next, x_next 16-byte aligned.  Deterministic.
+ * ---------------------------------------------------------------------- */
+int mtl_linear_skinny_residual(const float* x, int64_t x_rs, const float* W, const float* bias, float* parts,
+                               int64_t M, int64_t N, int64_t K, int32_t ksplit, int32_t rows_per_block, float* h,
+                               const float* w_next, float* x_next, float* sq, uint32_t* counters,
+                               mtl_stream_t stream);
+
+/* ------------------------------------------------------------------------
+ * mtl_in_proj_conv_xproj on a block input left by
+ * mtl_linear_skinny_residual: x = h * w (the block norm's weight applied to
+ * the residual rows h) and sq [sq_tiles, batch] the per-tile sums of h^2;
+ * the in_proj outputs are scaled by rsqrt(sum over tiles / d_model + eps)
+ * before b_in, which is in_proj(RMSNorm(h)) (model.py:130-135, 261) with the
+ * norm applied to the dot products.  1 <= sq_tiles <= 128; other arguments
+ * and rules as mtl_in_proj_conv_xproj.  Deterministic.
+ * ---------------------------------------------------------------------- */
+int mtl_in_proj_conv_xproj_normed(const float* x, int64_t x_rs, const float* W_in, const float* b_in,
+                                  float* conv_state, const float* conv_w, const float* conv_b, int32_t d_conv,
+                                  const float* W_xT, int32_t J, float* xc, float* z, int64_t z_rs, float* xpart,
+                                  int64_t batch, int64_t d_model, int64_t d_inner, int32_t channels_per_part,
+                                  const float* sq, int32_t sq_tiles, float eps, mtl_stream_t stream);
+
+/* ------------------------------------------------------------------------
  * Fused single-token decode step, fp32, batch 1, 2 or 4.
  * Together these replace one MambaBlock.step (model.py:308-311) around
  * MambaMixer.step (model.py:249-294): 3 launches per layer (4 when x_proj

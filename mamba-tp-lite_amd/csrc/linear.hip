@@ -217,6 +217,128 @@ void launch_linear(const LinArgs& a, hipStream_t st) {
         hipLaunchKernelGGL((linear_skinny_kernel<RB, MB, 2>), grid, dim3(kLinThreads), 0, st, a);
 }
 
+// ------------------------------------------------------- out_proj + residual add + the next norm's inputs
+// A batched step's out_proj split over K (model.py:293), the block's residual
+// add (model.py:311) and what the next block's RMSNorm (model.py:130-135)
+// needs from its input, without the add + norm launch between the blocks.
+// Every workgroup writes its split's partial tile, then counts its arrival on
+// its n-tile's counter; the last of the KS arrivals adds the KS partials in
+// split order, then the residual, exactly as mtl_add_rmsnorm_parts does:
+//   h[m][n] += ((part0 + part1) + part2) + ...,
+// stores h, xn[m][n] = h[m][n] * w[n] (the next in_proj's operand) and, per
+// row, the sum of h^2 over the tile's 16 RB columns into sq[tile][m] (the
+// columns added in order).  The next in_proj adds the sq row of every tile
+// and scales its dot products by rsqrt(mean h^2 + eps).
+// The partials move between workgroups (and XCDs) as agent-scope atomic
+// stores and loads, which the L2 of either XCD does not hold back; each
+// wavefront waits for its stores (vmcnt(0)) before the workgroup counts its
+// arrival, and the last arrival loads them only after its count returned.
+// Agent-scope fences instead (an L2 write-back per wavefront and an L2
+// invalidate in the last arrival) took the launch from 10.9 to 27.8 us at
+// the mamba-1.4b width, 32 rows.  h and w come from earlier launches, so
+// every workgroup loads its pairs' h and w before it counts.  Counters start
+// at zero and each is taken by exactly KS workgroups of one launch; nothing
+// is reset, so a call needs its own zeroed counters.
+struct ResidArgs {
+    float* h;          // [M, N] residual rows, in place
+    const float* w;    // [N] next RMSNorm's weight
+    float* xn;         // [M, N]
+    float* sq;         // [N / (16 RB), M]
+    unsigned* cnt;     // [N / (16 RB)], zero on entry
+};
+
+constexpr int kResidMaxSplit = 4;
+
+__device__ __forceinline__ void store_coherent(float* p, F4v v) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) __hip_atomic_store(p + q, v[q], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ F4v load_coherent(const float* p) {
+    F4v v;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) v[q] = __hip_atomic_load(p + q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return v;
+}
+
+template <int RB, int MB, int D>
+__global__ void __launch_bounds__(kLinThreads) linear_resid_kernel(const LinArgs a, const ResidArgs r) {
+    constexpr int WR = 16 * RB, NPAIR = RB * MB * 64;
+    __shared__ __align__(16) float ring[ring_floats<RB, MB, D>()];
+    static_assert(sizeof(ring) >= sizeof(float) * (16 * MB * 4 * RB + 4), "epilogue space");
+    const int n0 = blockIdx.x * WR, ks = blockIdx.y, tid = threadIdx.x;
+    // this thread's pair: 4 columns n0 + nl .. n0 + nl + 3 of row m (the
+    // layout tile_sum hands out); its bias, h and w do not depend on the
+    // product, so their loads are issued ahead of the product's copies and
+    // the first stage's wait covers them
+    const bool has_pair = tid < NPAIR;
+    int m, nl;
+    {
+        const int tile = tid >> 6, ln = tid & 63;
+        m = 16 * (tile % MB) + (ln & 15);
+        nl = 16 * (tile / MB) + 4 * (ln >> 4);
+    }
+    F4v bv = {0.f, 0.f, 0.f, 0.f}, hv = bv, wv = bv;
+    if (has_pair) {
+        if (a.bias && ks == 0) bv = ld4(a.bias + n0 + nl);
+        hv = ld4(r.h + (int64_t)min(m, a.M - 1) * a.N + n0 + nl);
+        wv = ld4(r.w + n0 + nl);
+    }
+    skinny_tile<RB, MB, D>(a, ring, n0, ks);
+    asm volatile("" : "+v"(bv), "+v"(hv), "+v"(wv));   // consumed after the product only
+    F4v own = {0.f, 0.f, 0.f, 0.f};
+    if (has_pair) {
+        int mt, nt;
+        own = tile_sum<RB, MB>(ring, tid, mt, nt);
+        if (a.bias && ks == 0) own += bv;
+        if (m < a.M) store_coherent(a.y + ks * a.y_ks + (int64_t)m * a.y_rs + n0 + nl, own);
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // this wavefront's partial stores are done
+    __syncthreads();                                     // every wavefront's; s_acc reads done
+    int* s_last = reinterpret_cast<int*>(ring);
+    if (tid == 0)
+        *s_last = __hip_atomic_fetch_add(r.cnt + blockIdx.x, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                  (unsigned)(a.KS - 1);
+    __syncthreads();
+    if (!*s_last) return;                                // uniform
+
+    float* s_sq = ring + 4;                              // [16 MB][4 RB]: row m's squares, by column group
+    if (has_pair && m < a.M) {
+        const float* pp = a.y + (int64_t)m * a.y_rs + n0 + nl;
+        F4v pv[kResidMaxSplit];                          // one batch of loads, no branches
+#pragma unroll
+        for (int p = 0; p < kResidMaxSplit; ++p) pv[p] = load_coherent(pp + min(p, a.KS - 1) * a.y_ks);
+        F4v t = ks == 0 ? own : pv[0];
+#pragma unroll
+        for (int p = 1; p < kResidMaxSplit; ++p)
+            if (p < a.KS) t += p == ks ? own : pv[p];
+        hv += t;
+        const int64_t o = (int64_t)m * a.N + n0 + nl;
+        *reinterpret_cast<F4v*>(r.h + o) = hv;
+        *reinterpret_cast<F4v*>(r.xn + o) = hv * wv;
+        float s = 0.f;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) s = fmaf(hv[q], hv[q], s);
+        s_sq[m * 4 * RB + (nl >> 2)] = s;
+    }
+    __syncthreads();
+    if (tid < a.M && tid < 16 * MB) {
+        float s = 0.f;
+#pragma unroll
+        for (int j = 0; j < 4 * RB; ++j) s += s_sq[tid * 4 * RB + j];
+        r.sq[(int64_t)blockIdx.x * a.M + tid] = s;
+    }
+}
+
+template <int RB, int MB>
+void launch_resid(const LinArgs& a, const ResidArgs& r, hipStream_t st) {
+    dim3 grid((unsigned)(a.N / (16 * RB)), (unsigned)a.KS);
+    if (a.K / a.KS >= 2 * kKC)
+        hipLaunchKernelGGL((linear_resid_kernel<RB, MB, 3>), grid, dim3(kLinThreads), 0, st, a, r);
+    else
+        hipLaunchKernelGGL((linear_resid_kernel<RB, MB, 2>), grid, dim3(kLinThreads), 0, st, a, r);
+}
+
 // ------------------------------------------------------- in_proj + conv step + x_proj partials
 // The batched step's in_proj (model.py:261), conv step + SiLU (264-277) and
 // x_proj (279) as one launch.  in_proj's output rows [0, D) are the x half
@@ -236,6 +358,11 @@ void launch_linear(const LinArgs& a, hipStream_t st) {
 // are loaded after the GEMM: loaded before it (into registers), their
 // scattered history rows delayed the first stages by more than the memory
 // round trip they save (1.4b width, 32 tokens: 24.5 against 21.7 us).
+// With sq set, x holds h * w (the block's RMSNorm weight applied to the
+// residual rows h, as linear_resid_kernel leaves them) and sq [nsq, b] the
+// per-tile sums of h^2 of each row: the tile's in_proj outputs are scaled by
+// rsqrt(sum / d_model + eps) before the bias, which is in_proj applied to
+// RMSNorm(h) (model.py:130-135), the norm taken on the dot products.
 struct InConvArgs {
     float* state;            // [b, D, K - 1], in place
     const float* conv_w;     // [D, K]
@@ -244,11 +371,14 @@ struct InConvArgs {
     float* xc;               // [b, D]
     float* z;                // [b, D] rows at stride z_rs
     float* xpart;            // [D / CB, b, J]
+    const float* sq;         // [nsq, b] or null
     int64_t z_rs;
-    int D, J;
+    int D, J, nsq;
+    float eps;
 };
 
 constexpr int kIcMaxJ = 288;
+constexpr int kSqPerThread = 16;                 // nsq <= 8 kSqPerThread
 
 template <int RB, int MB, int D, int K, int NBJ>
 __global__ void __launch_bounds__(kLinThreads) in_conv_xproj_kernel(const LinArgs a, const InConvArgs c) {
@@ -263,8 +393,10 @@ __global__ void __launch_bounds__(kLinThreads) in_conv_xproj_kernel(const LinArg
     float* ring = lds;
     float* s_wx = lds + RING;                          // [CB][J]
     constexpr int kAcc = kLinWaves * RB * MB * 64 * 4;  // floats of the reduction space
-    static_assert(kAcc + XR * (CB + 1) <= RING, "epilogue space");
+    static_assert(kAcc + XR * (CB + 1) + 8 * 32 <= RING, "epilogue space");
+    static_assert(XR <= 32, "row scales for at most 32 rows");
     float (*s_xc)[CB + 1] = reinterpret_cast<float (*)[CB + 1]>(ring + kAcc);
+    float* s_rs = ring + kAcc + XR * (CB + 1);          // [8][32] group sums of sq
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int n0 = blockIdx.x * CB;
@@ -286,18 +418,47 @@ __global__ void __launch_bounds__(kLinThreads) in_conv_xproj_kernel(const LinArg
         }
     }
 
+    // Row m's scale rsqrt(mean h^2 + eps) (normed input only): thread (row
+    // tid % 32, group g = tid / 32) adds tiles g, g + 8, ... in order, then
+    // the 8 group sums are added in group order.  The sq loads are issued
+    // ahead of the product's copies, so the first stage's wait covers them
+    // (loads return in order) and no round trip follows the product.
+    const int sm = min(tid & 31, a.M - 1), sg = tid >> 5;
+    float sv[kSqPerThread];
+    if (c.sq) {
+#pragma unroll
+        for (int i = 0; i < kSqPerThread; ++i) sv[i] = c.sq[(int64_t)min(sg + 8 * i, c.nsq - 1) * a.M + sm];
+    }
+
     skinny_tile<RB, MB, D>(a, ring, n0, 0);
+
+    // every thread calls it (normed input only)
+    auto row_scale = [&](int m) __attribute__((always_inline)) {
+        // opaque from here on: no part of the sum may move ahead of the product
+#pragma unroll
+        for (int i = 0; i < kSqPerThread; ++i) asm volatile("" : "+v"(sv[i]));
+        float s = 0.f;
+#pragma unroll
+        for (int i = 0; i < kSqPerThread; ++i)
+            if (sg + 8 * i < c.nsq) s += sv[i];
+        s_rs[sg * 32 + (tid & 31)] = s;
+        __syncthreads();
+        float tot = 0.f;
+#pragma unroll
+        for (int g = 0; g < 8; ++g) tot += s_rs[g * 32 + min(m, 31)];
+        return rsqrtf(tot / (float)a.K + c.eps);
+    };
 
     const int t = tid;                                 // this thread's output pair, if t < 64 RB MB
     const bool has_pair = t < RB * MB * 64;
     if (!xtile) {
-        if (has_pair) {
-            int m, nl;
-            F4v v = tile_sum<RB, MB>(ring, t, m, nl);
-            if (m < a.M) {
-                if (a.bias) v += ld4(a.bias + n0 + nl);
-                *reinterpret_cast<F4v*>(c.z + m * c.z_rs + (n0 + nl - c.D)) = v;
-            }
+        int m = 0, nl = 0;
+        F4v v = {0.f, 0.f, 0.f, 0.f};
+        if (has_pair) v = tile_sum<RB, MB>(ring, t, m, nl);
+        if (c.sq) v *= row_scale(m);
+        if (has_pair && m < a.M) {
+            if (a.bias) v += ld4(a.bias + n0 + nl);
+            *reinterpret_cast<F4v*>(c.z + m * c.z_rs + (n0 + nl - c.D)) = v;
         }
         return;
     }
@@ -308,12 +469,11 @@ __global__ void __launch_bounds__(kLinThreads) in_conv_xproj_kernel(const LinArg
     // kernel has copied into LDS)
     int m = 0, nl = 0, ch = 0;
     F4v xcv = {0.f, 0.f, 0.f, 0.f}, nh[K - 1];
+    F4v v = {0.f, 0.f, 0.f, 0.f}, hist[K - 1], cw[K], cb = {0.f, 0.f, 0.f, 0.f};
     if (has_pair) {
-        F4v v = tile_sum<RB, MB>(ring, t, m, nl);
-        if (a.bias) v += ld4(a.bias + n0 + nl);
+        v = tile_sum<RB, MB>(ring, t, m, nl);
         ch = n0 + nl;
         const int mm = min(m, a.M - 1);
-        F4v hist[K - 1], cw[K], cb = {0.f, 0.f, 0.f, 0.f};
         const F4v* sp = reinterpret_cast<const F4v*>(c.state + ((int64_t)mm * c.D + ch) * (K - 1));
 #pragma unroll
         for (int k = 0; k < K - 1; ++k) hist[k] = sp[k];
@@ -321,6 +481,10 @@ __global__ void __launch_bounds__(kLinThreads) in_conv_xproj_kernel(const LinArg
 #pragma unroll
         for (int k = 0; k < K; ++k) cw[k] = wp[k];
         if (c.conv_b) cb = ld4(c.conv_b + ch);
+    }
+    if (c.sq) v *= row_scale(m);
+    if (has_pair) {
+        if (a.bias) v += ld4(a.bias + n0 + nl);
         // channel q of the four: history tap k is float q (K - 1) + k of the
         // pair's history block, conv weight k float q K + k of its weight block
 #pragma unroll
@@ -581,12 +745,41 @@ extern "C" int mtl_in_proj_conv_prefill(const float* x, int64_t x_rs, const floa
     return check_launch("in_conv_prefill_kernel");
 }
 
-extern "C" int mtl_in_proj_conv_xproj(const float* x, int64_t x_rs, const float* W_in, const float* b_in,
-                                      float* conv_state, const float* conv_w, const float* conv_b, int32_t d_conv,
-                                      const float* W_xT, int32_t J, float* xc, float* z, int64_t z_rs, float* xpart,
-                                      int64_t batch, int64_t d_model, int64_t d_inner, int32_t channels_per_part,
-                                      mtl_stream_t stream) {
+extern "C" int mtl_linear_skinny_residual(const float* x, int64_t x_rs, const float* W, const float* bias,
+                                          float* parts, int64_t M, int64_t N, int64_t K, int32_t ksplit,
+                                          int32_t rows_per_block, float* h, const float* w_next, float* x_next,
+                                          float* sq, uint32_t* counters, mtl_stream_t stream) {
     clear_error();
+    MTL_REQUIRE(x && W && parts && h && w_next && x_next && sq && counters, "null required pointer");
+    MTL_REQUIRE(M >= 1 && M <= 32, "M (rows of x) must be in [1, 32]");
+    MTL_REQUIRE(rows_per_block == 16 || rows_per_block == 32, "rows_per_block must be 16 or 32");
+    MTL_REQUIRE(N >= rows_per_block && N % rows_per_block == 0 && N < (int64_t(1) << 30),
+                "N must be a positive multiple of rows_per_block");
+    MTL_REQUIRE(ksplit >= 1 && ksplit <= kResidMaxSplit, "ksplit must be in [1, 4]");
+    MTL_REQUIRE(K >= 1 && K % (int64_t(kKC) * ksplit) == 0 && K < (int64_t(1) << 31),
+                "K must be a positive multiple of 128 * ksplit");
+    MTL_REQUIRE(x_rs >= K && x_rs % 4 == 0, "x row stride must cover a row and be a multiple of 4");
+    MTL_REQUIRE((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(W) | reinterpret_cast<uintptr_t>(bias) |
+                 reinterpret_cast<uintptr_t>(parts) | reinterpret_cast<uintptr_t>(h) |
+                 reinterpret_cast<uintptr_t>(w_next) | reinterpret_cast<uintptr_t>(x_next)) % 16 == 0,
+                "x, W, bias, parts, h, w_next and x_next must be 16-byte aligned");
+    MTL_REQUIRE(x_next != h, "x_next must not alias h");
+    LinArgs a{x, W, bias, parts, x_rs, N, M * N, (int)M, (int)N, (int)K, (int)ksplit};
+    const ResidArgs r{h, w_next, x_next, sq, counters};
+    hipStream_t st = as_stream(stream);
+    if (rows_per_block == 32) {
+        if (M > 16) launch_resid<2, 2>(a, r, st); else launch_resid<2, 1>(a, r, st);
+    } else {
+        if (M > 16) launch_resid<1, 2>(a, r, st); else launch_resid<1, 1>(a, r, st);
+    }
+    return check_launch("linear_resid_kernel");
+}
+
+static int in_proj_conv_xproj(const float* x, int64_t x_rs, const float* W_in, const float* b_in, float* conv_state,
+                              const float* conv_w, const float* conv_b, int32_t d_conv, const float* W_xT, int32_t J,
+                              float* xc, float* z, int64_t z_rs, float* xpart, int64_t batch, int64_t d_model,
+                              int64_t d_inner, int32_t channels_per_part, const float* sq, int32_t sq_tiles, float eps,
+                              mtl_stream_t stream) {
     MTL_REQUIRE(x && W_in && conv_state && conv_w && W_xT && xc && z && xpart, "null required pointer");
     MTL_REQUIRE(batch >= 1 && batch <= 32, "batch must be in [1, 32]");
     MTL_REQUIRE(d_model >= 2 * kKC && d_model % kKC == 0 && d_model < (int64_t(1) << 30),
@@ -604,7 +797,7 @@ extern "C" int mtl_in_proj_conv_xproj(const float* x, int64_t x_rs, const float*
                  reinterpret_cast<uintptr_t>(z) | reinterpret_cast<uintptr_t>(W_xT)) % 16 == 0,
                 "x, W_in, b_in, conv_state, conv_w, conv_b, W_xT, xc and z must be 16-byte aligned");
     LinArgs a{x, W_in, b_in, nullptr, x_rs, 0, 0, (int)batch, (int)(2 * d_inner), (int)d_model, 1};
-    InConvArgs c{conv_state, conv_w, conv_b, W_xT, xc, z, xpart, z_rs, (int)d_inner, (int)J};
+    InConvArgs c{conv_state, conv_w, conv_b, W_xT, xc, z, xpart, sq, z_rs, (int)d_inner, (int)J, (int)sq_tiles, eps};
     hipStream_t st = as_stream(stream);
     const bool two_m = batch > 16;
     if (channels_per_part == 32) {
@@ -613,4 +806,28 @@ extern "C" int mtl_in_proj_conv_xproj(const float* x, int64_t x_rs, const float*
         if (two_m) dispatch_in_conv<1, 2>(d_conv, a, c, st); else dispatch_in_conv<1, 1>(d_conv, a, c, st);
     }
     return check_launch("in_conv_xproj_kernel");
+}
+
+extern "C" int mtl_in_proj_conv_xproj(const float* x, int64_t x_rs, const float* W_in, const float* b_in,
+                                      float* conv_state, const float* conv_w, const float* conv_b, int32_t d_conv,
+                                      const float* W_xT, int32_t J, float* xc, float* z, int64_t z_rs, float* xpart,
+                                      int64_t batch, int64_t d_model, int64_t d_inner, int32_t channels_per_part,
+                                      mtl_stream_t stream) {
+    clear_error();
+    return in_proj_conv_xproj(x, x_rs, W_in, b_in, conv_state, conv_w, conv_b, d_conv, W_xT, J, xc, z, z_rs, xpart,
+                              batch, d_model, d_inner, channels_per_part, nullptr, 0, 0.f, stream);
+}
+
+extern "C" int mtl_in_proj_conv_xproj_normed(const float* x, int64_t x_rs, const float* W_in, const float* b_in,
+                                             float* conv_state, const float* conv_w, const float* conv_b,
+                                             int32_t d_conv, const float* W_xT, int32_t J, float* xc, float* z,
+                                             int64_t z_rs, float* xpart, int64_t batch, int64_t d_model,
+                                             int64_t d_inner, int32_t channels_per_part, const float* sq,
+                                             int32_t sq_tiles, float eps, mtl_stream_t stream) {
+    clear_error();
+    MTL_REQUIRE(sq, "null sq");
+    MTL_REQUIRE(sq_tiles >= 1 && sq_tiles <= 8 * kSqPerThread, "sq_tiles must be in [1, 128]");
+    MTL_REQUIRE(eps >= 0.f, "eps must be >= 0");
+    return in_proj_conv_xproj(x, x_rs, W_in, b_in, conv_state, conv_w, conv_b, d_conv, W_xT, J, xc, z, z_rs, xpart,
+                              batch, d_model, d_inner, channels_per_part, sq, sq_tiles, eps, stream);
 }

@@ -129,6 +129,11 @@ SIGNATURES = {
                                                 _i64, _i64, _vp]),
     "mtl_in_proj_conv_xproj": (ctypes.c_int, [_fp, _i64, _fp, _fp, _fp, _fp, _fp, _i32, _fp, _i32, _fp, _fp, _i64, _fp,
                                               _i64, _i64, _i64, _i32, _vp]),
+    "mtl_in_proj_conv_xproj_normed": (ctypes.c_int, [_fp, _i64, _fp, _fp, _fp, _fp, _fp, _i32, _fp, _i32, _fp, _fp,
+                                                     _i64, _fp, _i64, _i64, _i64, _i32, _fp, _i32, ctypes.c_float,
+                                                     _vp]),
+    "mtl_linear_skinny_residual": (ctypes.c_int, [_fp, _i64, _fp, _fp, _fp, _i64, _i64, _i64, _i32, _i32, _fp, _fp,
+                                                  _fp, _fp, _vp, _vp]),
     "mtl_decode_norm_gemv": (ctypes.c_int, [_fp, _fp, ctypes.c_float, _fp, _fp, _fp, _i32, _i32, _i32, _vp]),
     "mtl_decode_ssm": (ctypes.c_int, [_fp, _i32, _fp, _fp, _fp, _fp, _fp, _fp, _fp, _fp, _i32, _i32, _i32, _i32,
                                       _vp]),

@@ -204,6 +204,23 @@ _XPROJ_PARTS = 4
 # against 475, 1.4b 1730 against 2343).
 FUSED_STEP_MAX_BATCH = 2
 
+# A batched fp32 step past FUSED_STEP_MAX_BATCH of at most
+# STEP_NORM_FOLD_MAX_ROWS rows adds each block's residual in its out_proj
+# launch, which also leaves the next block's norm inputs
+# (mtl_linear_skinny_residual); the next in_proj applies that norm to its dot
+# products (mtl_in_proj_conv_xproj_normed).  No add + norm launch runs
+# between two blocks.  The last workgroup of each out_proj tile waits on
+# three dependent memory round trips (its partial's stores, the count, the
+# other partials' loads): with two or more workgroups per CU (up to 16 rows)
+# other tiles' products hide them, at 32 rows (one per CU) they cost what the
+# launch saves.  Graph replays, fold off -> on: mamba-1.4b width 8 rows 2567-
+# 2571 -> 2501-2505 us, 32 rows 2302-2307 -> 2312-2341 us; mamba-130m width
+# 8 rows 551 -> 542 us, 32 rows 618 -> 621-629 us.  Eager steps gain 5-8%
+# at every size (the add + norm launch's host time).  The same rule holds
+# for eager and captured steps, so a graph replays the eager bits.
+STEP_NORM_FOLD = True
+STEP_NORM_FOLD_MAX_ROWS = 16
+
 
 def _f32(t: torch.Tensor | None) -> torch.Tensor | None:
     if t is None:
@@ -411,8 +428,11 @@ class MambaMixer(nn.Module):
             return None
         return ops.linear_skinny(y, w, self.out_proj.bias, ksplit=SKINNY_OUT_SPLIT)
 
-    def _step_y(self, x_t: torch.Tensor, cache: LayerCache) -> torch.Tensor:
-        """The step up to the gated SSM output y [b, d_inner] (before out_proj)."""
+    def _step_y(self, x_t: torch.Tensor, cache: LayerCache, sq: torch.Tensor | None = None,
+                eps: float = 0.0) -> torch.Tensor:
+        """The step up to the gated SSM output y [b, d_inner] (before out_proj).
+        With sq, x_t is h * norm weight and sq the per-tile sums of h^2 that
+        ops.linear_skinny_residual left: the in_proj input is RMSNorm(h)."""
         Dm, R = self.cfg.d_inner, self.cfg.dt_rank
         b = x_t.shape[0]
         J = R + 2 * self.cfg.d_state
@@ -423,9 +443,11 @@ class MambaMixer(nn.Module):
             # block in one launch (measured at the mamba-1.4b width, 32 tokens:
             # see in_proj_conv_xproj)
             xc, z, xpart = ops.in_proj_conv_xproj(x_t, w_in, self.in_proj.bias, cache.conv_state, conv_w, conv_b,
-                                                  self._xproj_t())
+                                                  self._xproj_t(), sq=sq, eps=eps)
             return ops.selective_state_update(cache.ssm_state, xc, z, ops.sum_parts(xpart), _f32(self.dt_proj.weight),
                                               _f32(self.dt_proj.bias), _f32(self.A_log), _f32(self.D), a_is_log=True)
+        if sq is not None:
+            raise ValueError("step: a normed input needs the in_proj_conv_xproj path")
         xz = self._in_proj_step(x_t)                             # [b, 2D]
         if xz.dtype == torch.float32 and b <= 32 and J <= 288 and cache.conv_state.dtype == torch.float32:
             # conv step and the x_proj partials of 32-channel blocks in one kernel
@@ -633,6 +655,8 @@ class MambaLM(nn.Module):
         if self._fused_step_ok(input_ids, cache):
             return self._step_fused(input_ids, cache)
         x = self.embedding(input_ids).squeeze(1)
+        if self._fold_ok(x, cache):
+            return self._step_folded(x, cache)
 
         def layer(i, xn):
             mx = self.layers[i].mixer
@@ -642,6 +666,65 @@ class MambaLM(nn.Module):
 
         xf = self._run(x, layer)
         return self.lm_head(xf).unsqueeze(1)
+
+    # ---- batched step with the residual add and norm folded into the projections ----
+    def _fold_ok(self, x, cache) -> bool:
+        """Whether the batched step takes _step_folded: STEP_NORM_FOLD, fp32
+        on the GPU, at most STEP_NORM_FOLD_MAX_ROWS (and 32) rows, two or more
+        layers, and every layer on the in_proj + conv + x_proj launch and the
+        split out_proj."""
+        cfg = self.cfg
+        if not STEP_NORM_FOLD or len(self.layers) < 2 or x.dim() != 2 or x.dtype != torch.float32 or not x.is_cuda:
+            return False
+        b, dm = x.shape
+        J = cfg.dt_rank + 2 * cfg.d_state
+        if b > min(32, STEP_NORM_FOLD_MAX_ROWS) or cfg.d_conv < 2 or cfg.d_inner % (128 * SKINNY_OUT_SPLIT) or \
+                len(cache.layers) != len(self.layers):
+            return False
+        rpb = ops.residual_rows_per_block(b, dm, SKINNY_OUT_SPLIT)
+        if dm % rpb or dm // rpb > 128:
+            return False
+        for blk, lc in zip(self.layers, cache.layers):
+            mx = blk.mixer
+            w = mx.out_proj.weight
+            if not ops.in_proj_conv_xproj_ok(x, mx.in_proj.weight, lc.conv_state, cfg.d_conv, J):
+                return False
+            if w.dtype != torch.float32 or not w.is_contiguous() or w.data_ptr() % 16 or \
+                    tuple(w.shape) != (dm, cfg.d_inner) or w.device != x.device:
+                return False
+        return True
+
+    def _step_folded(self, x, cache):
+        """MambaLM.step for b <= 32 fp32 rows with no add + norm launch between
+        blocks: layer 0's norm runs as mtl_add_rmsnorm; each out_proj but the
+        last adds the residual in place and leaves x_next = h * w_next and the
+        per-tile sums of h^2 (ops.linear_skinny_residual), from which the next
+        in_proj takes RMSNorm(h); the last out_proj's parts go to the final
+        add + norm as before.  The residual stream equals the per-op path's bit
+        for bit; each norm differs from it by float rounding (applied to the
+        dot products)."""
+        b, dm = x.shape
+        nl = len(self.layers)
+        rpb = ops.residual_rows_per_block(b, dm, SKINNY_OUT_SPLIT)
+        tiles = dm // rpb
+        h = x.float().contiguous()
+        inp = ops.add_rmsnorm(h, self._norm_weight(0), self._eps(0))
+        xn = torch.empty_like(h)
+        sq = torch.empty(tiles, b, device=h.device, dtype=torch.float32)
+        counters = torch.zeros(nl - 1, tiles, device=h.device, dtype=torch.int32)
+        parts = torch.empty(SKINNY_OUT_SPLIT, b, dm, device=h.device, dtype=torch.float32)
+        s = None
+        for i, blk in enumerate(self.layers):
+            mx = blk.mixer
+            y = mx._step_y(inp, cache.layers[i], sq=s, eps=self._eps(i))
+            if i + 1 < nl:
+                ops.linear_skinny_residual(y, mx.out_proj.weight, mx.out_proj.bias, h, self._norm_weight(i + 1), xn,
+                                           sq, counters[i], SKINNY_OUT_SPLIT, rpb, parts)
+                inp, s = xn, sq
+            else:
+                p = ops.linear_skinny(y, mx.out_proj.weight, mx.out_proj.bias, ksplit=SKINNY_OUT_SPLIT)
+                inp = ops.add_rmsnorm(h, self._norm_weight(nl), self._eps(nl), y_parts=p, x_out=h)
+        return self.lm_head(inp).unsqueeze(1)
 
     # ---- fused decode step ----
     def _fused_step_ok(self, input_ids, cache) -> bool:

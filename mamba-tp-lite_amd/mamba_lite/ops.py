@@ -344,12 +344,15 @@ def in_proj_conv_xproj_ok(x, W_in, conv_state, d_conv, J) -> bool:
             and tuple(conv_state.shape) == (b, D, d_conv - 1))
 
 
-def in_proj_conv_xproj(x, W_in, b_in, conv_state, conv_w, conv_b, W_xT, channels_per_part=None):
+def in_proj_conv_xproj(x, W_in, b_in, conv_state, conv_w, conv_b, W_xT, channels_per_part=None, sq=None, eps=0.0):
     """mtl_in_proj_conv_xproj: a batched step's in_proj (x [b, d_model] .
     W_in [2D, d_model]^T + b_in), the conv step + SiLU of its x half (conv
     history [b, D, K-1] updated in place) and the x_proj partials of each
     channel block, in one launch.  Returns (xc [b, D], z [b, D], xpart
-    [D / channels_per_part, b, J]); ops.sum_parts(xpart) is x_dbl."""
+    [D / channels_per_part, b, J]); ops.sum_parts(xpart) is x_dbl.
+    With sq [tiles, b] (mtl_in_proj_conv_xproj_normed): x is h * w and sq
+    the per-tile sums of h^2 that linear_skinny_residual left, and the
+    in_proj input is RMSNorm(h) with this eps."""
     b, M = x.shape
     D = W_in.shape[0] // 2
     w = conv_w.reshape(conv_w.shape[0], conv_w.shape[-1]) if conv_w.dim() == 3 else conv_w
@@ -369,12 +372,23 @@ def in_proj_conv_xproj(x, W_in, b_in, conv_state, conv_w, conv_b, W_xT, channels
     xc = torch.empty(b, D, device=x.device, dtype=torch.float32)
     z = torch.empty(b, D, device=x.device, dtype=torch.float32)
     xpart = torch.empty(D // channels_per_part, b, J, device=x.device, dtype=torch.float32)
-    _same_device(x, W_in, b_in, conv_state, w, conv_b, W_xT)
+    _same_device(x, W_in, b_in, conv_state, w, conv_b, W_xT, sq)
+    lib = _lib.load()
     with _dev_guard(x):
-        _lib.check(_lib.load().mtl_in_proj_conv_xproj(_ptr(x), x.stride(0), _ptr(W_in), _ptr(b_in), _ptr(conv_state),
-                                                      _ptr(w), _ptr(conv_b), K, _ptr(W_xT), J, _ptr(xc), _ptr(z),
-                                                      z.stride(0), _ptr(xpart), b, M, D, channels_per_part,
-                                                      _stream(x)), "in_proj_conv_xproj")
+        if sq is None:
+            _lib.check(lib.mtl_in_proj_conv_xproj(_ptr(x), x.stride(0), _ptr(W_in), _ptr(b_in), _ptr(conv_state),
+                                                  _ptr(w), _ptr(conv_b), K, _ptr(W_xT), J, _ptr(xc), _ptr(z),
+                                                  z.stride(0), _ptr(xpart), b, M, D, channels_per_part,
+                                                  _stream(x)), "in_proj_conv_xproj")
+        else:
+            _f32c(sq, "sq")
+            if sq.dim() != 2 or sq.shape[1] != b:
+                raise ValueError(f"in_proj_conv_xproj: sq must be [tiles, {b}], got {tuple(sq.shape)}")
+            _lib.check(lib.mtl_in_proj_conv_xproj_normed(_ptr(x), x.stride(0), _ptr(W_in), _ptr(b_in),
+                                                         _ptr(conv_state), _ptr(w), _ptr(conv_b), K, _ptr(W_xT), J,
+                                                         _ptr(xc), _ptr(z), z.stride(0), _ptr(xpart), b, M, D,
+                                                         channels_per_part, _ptr(sq), sq.shape[0], float(eps),
+                                                         _stream(x)), "in_proj_conv_xproj_normed")
     return xc, z, xpart
 
 
@@ -789,6 +803,48 @@ def linear_skinny(x, W, bias=None, out=None, ksplit=1, rows_per_block=None):
         _lib.check(_lib.load().mtl_linear_skinny(_ptr(x), x.stride(0), _ptr(W), _ptr(bias), _ptr(out), N, M * N,
                                                  M, N, K, ksplit, rows_per_block, _stream(x)), "linear_skinny")
     return out
+
+
+def residual_rows_per_block(M, N, ksplit) -> int:
+    """linear_skinny's tile choice for out_proj with ksplit parts."""
+    return 32 if 16 < M <= 32 and N % 32 == 0 and N // 32 * ksplit >= 256 else 16
+
+
+def linear_skinny_residual(y, W, bias, h, w_next, x_next, sq, counters, ksplit, rows_per_block=None, parts=None):
+    """mtl_linear_skinny_residual: out_proj of a batched step (y [M, K] .
+    W [N, K]^T + bias, as ksplit partial products) with the residual add h
+    += the parts in order (in place) and the next block's norm inputs:
+    x_next = h * w_next, sq [N / rows_per_block, M] = per-tile sums of h^2.
+    counters [N / rows_per_block] int32 must be zero (each call its own)."""
+    if not linear_skinny_ok(y, W):
+        raise ValueError("linear_skinny_residual: fp32 y [M<=32, K%128==0] and contiguous W [N, K] expected")
+    M, K = y.shape
+    N = W.shape[0]
+    if M > 32:
+        raise ValueError("linear_skinny_residual: at most 32 rows")
+    if rows_per_block is None:
+        rows_per_block = residual_rows_per_block(M, N, ksplit)
+    tiles = N // rows_per_block
+    for name, t, shape in (("h", h, (M, N)), ("x_next", x_next, (M, N)), ("sq", sq, (tiles, M))):
+        _f32c(t, name)
+        if tuple(t.shape) != shape:
+            raise ValueError(f"linear_skinny_residual: {name} must be {shape}, got {tuple(t.shape)}")
+    _f32_vec(w_next, N, "w_next")
+    if bias is not None:
+        _f32_vec(bias, N, "bias")
+    if counters.dtype != torch.int32 or not counters.is_contiguous() or counters.numel() != tiles:
+        raise ValueError(f"linear_skinny_residual: counters must be contiguous int32 [{tiles}]")
+    if parts is None:
+        parts = torch.empty(ksplit, M, N, device=y.device, dtype=torch.float32)
+    elif tuple(parts.shape) != (ksplit, M, N) or parts.dtype != torch.float32 or not parts.is_contiguous():
+        raise ValueError(f"linear_skinny_residual: parts must be contiguous float32 {(ksplit, M, N)}")
+    _same_device(y, W, bias, h, w_next, x_next, sq, counters, parts)
+    with _dev_guard(y):
+        _lib.check(_lib.load().mtl_linear_skinny_residual(_ptr(y), y.stride(0), _ptr(W), _ptr(bias), _ptr(parts), M,
+                                                          N, K, ksplit, rows_per_block, _ptr(h), _ptr(w_next),
+                                                          _ptr(x_next), _ptr(sq), _ptr(counters), _stream(y)),
+                   "linear_skinny_residual")
+    return h, x_next, sq
 
 
 def decode_gemv_parts(v, W, out_parts):

@@ -163,6 +163,18 @@ def test_invalid_arguments_are_rejected_without_a_gpu():
     ("mtl_in_proj_conv_xproj", dict(d_conv=5), b"d_conv"),
     ("mtl_in_proj_conv_xproj", dict(d_conv=1), b"d_conv"),
     ("mtl_in_proj_conv_xproj", dict(J=289), b"J (x_proj rows)"),
+    ("mtl_in_proj_conv_xproj_normed", dict(sq_tiles=129), b"sq_tiles must be in [1, 128]"),
+    ("mtl_in_proj_conv_xproj_normed", dict(sq_tiles=0), b"sq_tiles must be in [1, 128]"),
+    ("mtl_in_proj_conv_xproj_normed", dict(null_sq=True), b"null sq"),
+    ("mtl_in_proj_conv_xproj_normed", dict(eps=-1.0), b"eps"),
+    ("mtl_in_proj_conv_xproj_normed", dict(batch=33), b"batch must be in [1, 32]"),
+    ("mtl_linear_skinny_residual", dict(M=33), b"M (rows of x) must be in [1, 32]"),
+    ("mtl_linear_skinny_residual", dict(M=0), b"M (rows of x)"),
+    ("mtl_linear_skinny_residual", dict(N=48, rpb=32), b"multiple of rows_per_block"),
+    ("mtl_linear_skinny_residual", dict(rpb=8), b"rows_per_block must be 16 or 32"),
+    ("mtl_linear_skinny_residual", dict(K=256, ksplit=4), b"multiple of 128 * ksplit"),
+    ("mtl_linear_skinny_residual", dict(alias=True), b"x_next must not alias h"),
+    ("mtl_linear_skinny_residual", dict(null_cnt=True), b"null required pointer"),
 ])
 def test_entry_points_validate_sizes_on_the_host(case):
     """Each entry point rejects sizes its kernels do not cover, with a message,
@@ -293,6 +305,18 @@ def test_entry_points_validate_sizes_on_the_host(case):
         a.update(over)
         rc = lib.mtl_in_proj_conv_xproj(P, a["d_model"], P, None, P, P, None, a["d_conv"], P, a["J"], P, P,
                                         a["d_inner"], P, a["batch"], a["d_model"], a["d_inner"], a["cpp"], None)
+    elif name == "mtl_in_proj_conv_xproj_normed":
+        a = dict(batch=8, d_model=256, d_inner=64, cpp=16, d_conv=4, J=40, sq_tiles=16, null_sq=False, eps=1e-5)
+        a.update(over)
+        rc = lib.mtl_in_proj_conv_xproj_normed(P, a["d_model"], P, None, P, P, None, a["d_conv"], P, a["J"], P, P,
+                                               a["d_inner"], P, a["batch"], a["d_model"], a["d_inner"], a["cpp"],
+                                               None if a["null_sq"] else P, a["sq_tiles"], a["eps"], None)
+    elif name == "mtl_linear_skinny_residual":
+        a = dict(M=8, N=256, K=512, ksplit=4, rpb=16, alias=False, null_cnt=False)
+        a.update(over)
+        xn = P if a["alias"] else ctypes.c_void_p(64)
+        rc = lib.mtl_linear_skinny_residual(P, a["K"], P, None, P, a["M"], a["N"], a["K"], a["ksplit"], a["rpb"], P,
+                                            P, xn, P, None if a["null_cnt"] else P, None)
     else:
         a = dict(width=4)
         a.update(over)
