@@ -808,7 +808,7 @@ __global__ void __launch_bounds__(kLaneChannels * 64) scan_lanes_kernel(const Sc
 // rounding of the step-by-step loop.
 // It holds more registers (NS = 16: 214 VGPRs, one 8-wavefront workgroup per
 // CU), so it is taken where the grid is one workgroup per CU at most, for
-// sequences over 128 steps and more than 4 states.  Measured against the
+// sequences over 128 steps and 5 to 16 states.  Measured against the
 // kernel above (mixer layout, HIP events): D 1536, batch 1, 1024 steps 35.5
 // -> 28.6 us, 256 steps 11.0 -> 8.4 us; bf16 D 2048, 2048 steps 81.1 -> 59.9
 // us; at 512 workgroups (D 4096) 60.7 -> 58.8 us but 104.6 -> 111.2 us at
@@ -817,6 +817,7 @@ constexpr int kLaneSteps = 4;
 constexpr int kLanesLongMinSteps = 128;
 constexpr int64_t kLanesLongMaxWorkgroups = 256;
 constexpr int kLanesLongMinStates = 5;
+constexpr int kLanesLongMaxStates = 16;     // 32 states would spill (256 VGPRs and scratch)
 
 template <typename T, int NS>
 __global__ void __launch_bounds__(kLaneChannels * 64) scan_lanes_long_kernel(const ScanArgs a) {
@@ -1011,11 +1012,10 @@ template <typename T>
 void launch_scan_lanes(const ScanArgs& a, int64_t batch, hipStream_t st) {
     dim3 grid((unsigned)((a.D + kLaneChannels - 1) / kLaneChannels), (unsigned)batch);
     dim3 block(kLaneChannels * 64);
-    if (a.L > kLanesLongMinSteps && a.N >= kLanesLongMinStates &&
+    if (a.L > kLanesLongMinSteps && a.N >= kLanesLongMinStates && a.N <= kLanesLongMaxStates &&
         (int64_t)grid.x * grid.y <= kLanesLongMaxWorkgroups) {
         if (a.N <= 8) hipLaunchKernelGGL((scan_lanes_long_kernel<T, 8>), grid, block, 0, st, a);
-        else if (a.N <= 16) hipLaunchKernelGGL((scan_lanes_long_kernel<T, 16>), grid, block, 0, st, a);
-        else hipLaunchKernelGGL((scan_lanes_long_kernel<T, 32>), grid, block, 0, st, a);
+        else hipLaunchKernelGGL((scan_lanes_long_kernel<T, 16>), grid, block, 0, st, a);
         return;
     }
     if (a.N <= 4) hipLaunchKernelGGL((scan_lanes_kernel<T, 4>), grid, block, 0, st, a);

@@ -61,10 +61,12 @@ ALGOS = ["tiled", "chunked"]
 @pytest.mark.parametrize("layout", ["cm", "tm"])
 @pytest.mark.parametrize("b,D,L,N", [(2, 64, 16, 16), (2, 200, 70, 16), (1, 96, 33, 8), (3, 70, 5, 4),
                                      (1, 64, 40, 32), (1, 130, 129, 1), (2, 32, 64, 16), (1, 48, 65, 16),
-                                     (1, 20, 1000, 16), (2, 8, 191, 5)])
+                                     (1, 20, 1000, 16), (2, 8, 191, 5), (1, 24, 300, 32), (1, 16, 260, 12)])
 def test_scan_fp32_vs_oracle(algo, layout, b, D, L, N):
     """Chunk boundaries of the chunked kernel sit every 64 steps: lengths
-    below, at and past one chunk, and many chunks (1000 steps)."""
+    below, at and past one chunk, and many chunks (1000 steps).  Past 128
+    steps on these small grids, 5 to 16 states take its long form (256-step
+    chunks; 12 states: a partial group of four), 32 states the 64-step form."""
     print(f"scan fp32 {algo} {layout} b={b} D={D} L={L} N={N}", flush=True)
     c = scan_case(np.random.default_rng(b * 1000 + D + L + N), b, D, L, N)
     h0 = np.random.default_rng(7).standard_normal((b, D, N)).astype(np.float32)
