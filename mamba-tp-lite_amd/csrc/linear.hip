@@ -230,12 +230,17 @@ void launch_linear(const LinArgs& a, hipStream_t st) {
 // columns added in order).  The next in_proj adds the sq row of every tile
 // and scales its dot products by rsqrt(mean h^2 + eps).
 // The partials move between workgroups (and XCDs) as agent-scope atomic
-// stores and loads, which the L2 of either XCD does not hold back; each
-// wavefront waits for its stores (vmcnt(0)) before the workgroup counts its
-// arrival, and the last arrival loads them only after its count returned.
-// Agent-scope fences instead (an L2 write-back per wavefront and an L2
-// invalidate in the last arrival) took the launch from 10.9 to 27.8 us at
-// the mamba-1.4b width, 32 rows.  h and w come from earlier launches, so
+// stores and loads (sc1: coherent at agent scope once complete, never served
+// from a stale L2 line); each wavefront waits for its stores (vmcnt(0))
+// before the workgroup counts its arrival, and the last arrival issues its
+// loads only after its count returned.  That is the release/acquire pair for
+// data that is itself written and read atomically: the L2 write-back of a
+// release fence exists for plain stores, the L2 invalidate of an acquire
+// fence for plain loads, and neither is needed here.  They cost: a release
+// fence per wavefront and an acquire fence per wavefront of the last arrival
+// took the launch from 10.9 to 27.8 us at the mamba-1.4b width, 32 rows; a
+// release on the count and an acquire in the last arrival only (one each per
+// workgroup) still added 8.6 us per layer to the 8-row step (2494 -> 2906 us).  h and w come from earlier launches, so
 // every workgroup loads its pairs' h and w before it counts.  Counters start
 // at zero and each is taken by exactly KS workgroups of one launch; nothing
 // is reset, so a call needs its own zeroed counters.
