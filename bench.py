@@ -2,7 +2,8 @@
 
     python bench.py [--gpus 1] [--steps K] [--warmup W]
                    [--only scan|decode|quant|shard|prefill|prefill-short|prefill-long|copy|decode-counters|all]
-                   [--decode-shapes 130m,1.4b] [--decode-persist] [--no-cpu-baseline]
+                   [--decode-shapes 130m,1.4b] [--decode-batches B,...] [--decode-persist]
+                   [--no-step-fold] [--no-cpu-baseline]
 
 Headline (`value`): fused selective-scan prefill throughput, fp32, on the
 isolated-op workload u, delta, z [32, 1536, 1024], B, C [32, 16, 1024],
@@ -524,6 +525,11 @@ def main():
                              "copy", "decode-counters"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--decode-shapes", default="130m,1.4b", help="comma list of 130m, 1.4b")
+    ap.add_argument("--decode-batches", default="",
+                    help="comma list of batch sizes for every decode shape (default: 1 at 130m, 1 and 32 at 1.4b)")
+    ap.add_argument("--no-step-fold", action="store_true",
+                    help="batched steps of 3-16 rows keep the add + norm launch between blocks (MambaLM folds it "
+                         "into the projections by default)")
     ap.add_argument("--decode-persist", action="store_true",
                     help="decode batch 1 through the persistent single-launch step (off by default in MambaLM); "
                          "the shapes it does not take run their usual step")
@@ -645,6 +651,11 @@ def main():
             import mamba_lite.model as mm
             mm.DECODE_PERSIST = True
             extra["decode_persist"] = True
+        if args.no_step_fold:
+            import mamba_lite.model as mm
+            mm.STEP_NORM_FOLD = False
+            extra["step_fold"] = False
+        only_b = tuple(int(v) for v in args.decode_batches.split(",") if v) if args.decode_batches else None
         for name, cfg_kw, batches, prompt, ntok in (
                 ("130m", dict(d_model=768, n_layer=24, vocab_size=50280), (1,), 64, 256),
                 ("1.4b", dict(d_model=2048, n_layer=48, vocab_size=50280), (1, 32), 1024, 256)):
@@ -653,21 +664,21 @@ def main():
             try:
                 log(f"decode {name}: building model")
                 model = build_lm(MambaConfig(**cfg_kw), dev)
-                for bsz in batches:
+                for bsz in (only_b or batches):
                     us, ok = bench_decode(model, bsz, prompt, ntok, dev)
                     dec[f"{name}_b{bsz}"] = {"us_per_step": us, "us_per_token": us / bsz, "graph_equals_eager": ok,
                                              "prompt": prompt, "tokens_timed": ntok}
                     log(f"decode {name} b={bsz}: {us:.1f} us/step (graph==eager {ok})")
                 if name == "130m" and not args.no_cpu_baseline:
                     cb = cpu_baseline_decode(model, dev)
-                    dec["130m_b1"]["cpu_baseline"] = cb
+                    dec.setdefault("130m_b1", {})["cpu_baseline"] = cb
                     log(f"decode cpu baseline: {cb['value']:.0f} us/token; GPU step rel err vs oracle "
                         f"{cb['gpu_step_max_rel_err_vs_oracle_f64']:.2e}")
                 if name == "1.4b" and not args.no_cpu_baseline:
                     # reduced: a 16-token prompt (not 1024) and 8 timed steps at
                     # batch 1; the float64 parity of this shape is in the tests
                     cb = cpu_baseline_decode(model, dev, prompt=16, steps=8, name="1.4b", parity=False)
-                    dec["1.4b_b1"]["cpu_baseline"] = cb
+                    dec.setdefault("1.4b_b1", {})["cpu_baseline"] = cb
                     log(f"decode 1.4b cpu baseline: {cb['value']:.0f} us/token")
                 del model
                 torch.cuda.empty_cache()

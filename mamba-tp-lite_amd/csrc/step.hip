@@ -137,8 +137,10 @@ __global__ void __launch_bounds__(256) sum_parts4_kernel(const float* __restrict
 }
 
 // The same four-quarter order for any part count: each quarter's parts are
-// summed by a runtime-count loop (a load round trip per part, for the part
-// counts above 128 that only models wider than d_inner 4096 reach).
+// summed by a runtime-count loop (a load round trip per part), for more than
+// 512 parts.  Up to 512, sum_parts4_kernel loads a quarter in one batch: the
+// 256 x_proj blocks of a mamba-1.4b-width step at up to 16 rows (16-channel
+// blocks) took 16.8 us here at 8 rows.
 __global__ void __launch_bounds__(256) sum_parts4_any_kernel(const float* __restrict__ parts, int nparts, int64_t n,
                                                              float* __restrict__ out) {
     __shared__ float s_q[4][64];
@@ -653,6 +655,8 @@ extern "C" int mtl_sum_parts(const float* parts, int32_t nparts, int64_t n, floa
     else if (nparts <= 32) hipLaunchKernelGGL((sum_parts_kernel<32>), grid, dim3(256), 0, st, parts, nparts, n, out);
     else if (nparts <= 64) hipLaunchKernelGGL((sum_parts4_kernel<16>), grid4, dim3(256), 0, st, parts, nparts, n, out);
     else if (nparts <= 128) hipLaunchKernelGGL((sum_parts4_kernel<32>), grid4, dim3(256), 0, st, parts, nparts, n, out);
+    else if (nparts <= 256) hipLaunchKernelGGL((sum_parts4_kernel<64>), grid4, dim3(256), 0, st, parts, nparts, n, out);
+    else if (nparts <= 512) hipLaunchKernelGGL((sum_parts4_kernel<128>), grid4, dim3(256), 0, st, parts, nparts, n, out);
     else hipLaunchKernelGGL(sum_parts4_any_kernel, grid4, dim3(256), 0, st, parts, nparts, n, out);
     return check_launch("sum_parts");
 }

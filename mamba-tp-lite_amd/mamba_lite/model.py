@@ -213,9 +213,9 @@ FUSED_STEP_MAX_BATCH = 2
 # three dependent memory round trips (its partial's stores, the count, the
 # other partials' loads): with two or more workgroups per CU (up to 16 rows)
 # other tiles' products hide them, at 32 rows (one per CU) they cost what the
-# launch saves.  Graph replays, fold off -> on: mamba-1.4b width 8 rows 2567-
-# 2571 -> 2501-2505 us, 32 rows 2302-2307 -> 2312-2341 us; mamba-130m width
-# 8 rows 551 -> 542 us, 32 rows 618 -> 621-629 us.  Eager steps gain 5-8%
+# launch saves.  Graph replays, fold off -> on: mamba-1.4b width 8 rows 1945
+# -> 1885 us, 16 rows 2027 -> 1995 us, 32 rows 2302-2307 -> 2312-2341 us;
+# mamba-130m width 8 rows 550 -> 540 us, 32 rows 618 -> 621-629 us.  Eager steps gain 5-8%
 # at every size (the add + norm launch's host time).  The same rule holds
 # for eager and captured steps, so a graph replays the eager bits.
 STEP_NORM_FOLD = True

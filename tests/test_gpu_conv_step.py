@@ -242,7 +242,8 @@ def test_add_rmsnorm_parts(rows, cols, nparts):
 
 
 @pytest.mark.parametrize("nparts,n", [(1, 5), (3, 1000), (16, 5120), (32, 257), (33, 100), (64, 300), (97, 64),
-                                      (128, 5120)])
+                                      (128, 5120), (129, 70), (256, 1280), (320, 2560), (512, 64), (513, 100),
+                                      (700, 33)])
 def test_sum_parts_in_part_order(nparts, n):
     """mtl_sum_parts adds the parts in its documented fixed order (left to
     right up to 32 parts, four ordered quarters above), bit for bit."""
