@@ -690,7 +690,9 @@ def main():
     if want("prefill"):
         try:
             model = build_lm(MambaConfig(d_model=768, n_layer=24, vocab_size=50280), dev)
+            # 64 tokens: mtl_prefill_short; 256: mtl_prefill_long; 32 x 1024: the per-op path
             extra["prefill_tok_s"] = {"130m_b1_l64": bench_prefill(model, 1, 64, dev),
+                                      "130m_b1_l256": bench_prefill(model, 1, 256, dev),
                                       "130m_b32_l1024": bench_prefill(model, 32, 1024, dev)}
             log(f"prefill: {extra['prefill_tok_s']}")
             extra["prefill_graph_tok_s"] = {"130m_b1_l64": bench_prefill_graph(model, 1, 64, dev)}
@@ -699,6 +701,7 @@ def main():
             torch.cuda.empty_cache()
             # the 1.4b shape's 1024-token prompts (48 layers, d_inner 4096)
             model = build_lm(MambaConfig(d_model=2048, n_layer=48, vocab_size=50280), dev)
+            extra["prefill_tok_s"]["1p4b_b1_l128"] = bench_prefill(model, 1, 128, dev)
             extra["prefill_tok_s"]["1p4b_b1_l1024"] = bench_prefill(model, 1, 1024, dev, iters=5)
             extra["prefill_tok_s"]["1p4b_b32_l1024"] = bench_prefill(model, 32, 1024, dev, iters=2)
             log(f"prefill 1.4b: b=1 x 1024 {extra['prefill_tok_s']['1p4b_b1_l1024']:.0f} tok/s, "

@@ -405,6 +405,55 @@ typedef struct {
 
 int mtl_prefill_short(const mtl_prefill_short_args* args, const mtl_prefill_layer* layers, mtl_stream_t stream);
 
+/* ------------------------------------------------------------------------
+ * A prompt's whole layer stack in one call past the short-prompt limit:
+ * MambaLM.prefill (model.py:328-341) over MambaBlock.prefill (303-306) and
+ * MambaMixer.prefill (184-241), fp32, any number of token rows, with the
+ * per-op path's kernels launched from C++ (the projections as hipBLASLt
+ * GEMMs):
+ *   xn = RMSNorm_0(h);  per layer i:
+ *     xz = xn W_in^T + b_in;  u = SiLU(causal conv of xz's x half), the final
+ *     history into conv_state_out (mtl_causal_conv1d_fwd);
+ *     x_dbl = u W_x^T;  dt = x_dbl[:, :R] W_dt^T;
+ *     y = selective scan (dt_bias + softplus, D skip, gate SiLU(xz's z half);
+ *         h0 -> h_out, which may alias) (mtl_selective_scan_fwd);
+ *     h += y W_out^T + b_out;  xn = RMSNorm_{i+1}(h)  (norm_f into normed_out
+ *     after the last layer) (mtl_add_rmsnorm).
+ * h: [b l, d_model] (row m = token m % seqlen of batch row m / seqlen), the
+ * embedded tokens in, the final residual stream out.  The layers are
+ * mtl_prefill_layer entries as mtl_prefill_short takes them (conv_w [D, K],
+ * W_in [2D, M], W_x [R + 2N, D], W_dt [D, R], W_out [M, D], all contiguous;
+ * conv_state_in may be NULL for zeros; with d_conv 1 the conv states are not
+ * used).  Workspace (contiguous fp32): xn, out [b l, M]; xz [b l, 2D]; u, dt,
+ * y [b l, D]; x_dbl [b l, R + 2N]; blas_ws: blas_ws_bytes of GEMM workspace.
+ * The GEMM algorithm of each shape is hipBLASLt's first heuristic pick,
+ * looked up on the shape's first call on a device and kept; the handle is
+ * created on the first call on a device.  After that a call allocates no
+ * device memory and may be captured into a HIP graph.  Calls on one process
+ * are serialized inside the library.  d_state <= 32, 1 <= d_conv <= 8.
+ * ---------------------------------------------------------------------- */
+typedef struct {
+    float* h;
+    float* xn;
+    float* xz;
+    float* u;
+    float* x_dbl;
+    float* dt;
+    float* y;
+    float* out;
+    void* blas_ws;
+    int64_t blas_ws_bytes;
+    const float* norm_f;
+    float* normed_out;
+    float eps_f;
+    int32_t d_conv;
+    int32_t n_layers;
+    int32_t reserved;
+    int64_t batch, seqlen, d_model, d_inner, d_state, dt_rank;
+} mtl_prefill_long_args;
+
+int mtl_prefill_long(const mtl_prefill_long_args* args, const mtl_prefill_layer* layers, mtl_stream_t stream);
+
 int mtl_in_proj_conv_xproj(const float* x, int64_t x_rs, const float* W_in, const float* b_in, float* conv_state,
                            const float* conv_w, const float* conv_b, int32_t d_conv, const float* W_xT, int32_t J,
                            float* xc, float* z, int64_t z_rs, float* xpart, int64_t batch, int64_t d_model,

@@ -68,7 +68,7 @@ def build(jobs: int | None = None, verbose: bool = False) -> str:
         with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
             list(ex.map(lambda so: _compile(cc, so[0], so[1], verbose), zip(srcs, objs)))
         tmp_out = OUT + ".tmp"
-        cmd = [cc, "-shared", "-fPIC", f"--offload-arch={ARCH}", *objs, "-o", tmp_out]
+        cmd = [cc, "-shared", "-fPIC", f"--offload-arch={ARCH}", *objs, "-lhipblaslt", "-o", tmp_out]
         if verbose:
             print(" ".join(cmd), flush=True)
         r = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)

@@ -73,6 +73,17 @@ class PrefillShortArgs(ctypes.Structure):
     ]
 
 
+class PrefillLongArgs(ctypes.Structure):
+    """mirror of mtl_prefill_long_args"""
+    _fields_ = [
+        ("h", _vp), ("xn", _vp), ("xz", _vp), ("u", _vp), ("x_dbl", _vp), ("dt", _vp), ("y", _vp), ("out", _vp),
+        ("blas_ws", _vp), ("blas_ws_bytes", _i64), ("norm_f", _vp), ("normed_out", _vp),
+        ("eps_f", ctypes.c_float), ("d_conv", _i32), ("n_layers", _i32), ("reserved", _i32),
+        ("batch", _i64), ("seqlen", _i64), ("d_model", _i64), ("d_inner", _i64), ("d_state", _i64),
+        ("dt_rank", _i64),
+    ]
+
+
 class DecodeLayer(ctypes.Structure):
     """mirror of mtl_decode_layer"""
     _fields_ = [
@@ -108,6 +119,7 @@ SIGNATURES = {
     "mtl_sum_parts": (ctypes.c_int, [_fp, _i32, _i64, _fp, _vp]),
     "mtl_xproj_sum_dt": (ctypes.c_int, [_fp, _i32, _i64, _i32, _fp, _i32, _i64, _fp, _fp, _vp]),
     "mtl_prefill_short": (ctypes.c_int, [ctypes.POINTER(PrefillShortArgs), ctypes.POINTER(PrefillLayer), _vp]),
+    "mtl_prefill_long": (ctypes.c_int, [ctypes.POINTER(PrefillLongArgs), ctypes.POINTER(PrefillLayer), _vp]),
     "mtl_decode_step": (ctypes.c_int, [ctypes.POINTER(DecodeStepArgs), ctypes.POINTER(DecodeLayer), _vp]),
     "mtl_decode_persist_workspace_bytes": (ctypes.c_size_t, [_i32, _i32, _i32, _i32]),
     "mtl_decode_persist_grid": (_i32, [_i32, _i32, _i32, _i32, _i32, _i32, _i32]),

@@ -149,6 +149,20 @@ _SKINNY_PREFILL = True
 # Python per layer that bounds an eager short prefill goes away.
 SHORT_PREFILL_NATIVE = True
 
+# Longer prompts on an fp32 model run as one C call too (mtl_prefill_long),
+# with the projections as hipBLASLt GEMMs launched from C++, up to
+# LONG_PREFILL_MAX_ELEMS token-channels (b l d_inner): below it an eager
+# per-op prefill is bound by its ~160 us of Python per layer.  Measured per
+# prompt, one call against the per-op path: mamba-130m width 65 tokens 1.62
+# against 3.94 ms, 256 tokens 1.70 against 3.91 ms, 1024 tokens 3.55 against
+# 3.92 ms; mamba-1.4b width 128 tokens 4.82 against 8.10 ms, 512 tokens 12.87
+# against 12.85 ms.  Past it the GPU time dominates and the per-op path keeps
+# torch's GEMMs (and any tuned GEMM table: 1.4b 1024 tokens 23.4 against 23.9
+# ms with it).  The C call's GEMM picks differ from torch's, so its logits
+# differ from the per-op path's by float rounding.
+LONG_PREFILL_NATIVE = True
+LONG_PREFILL_MAX_ELEMS = 1 << 21
+
 # The fused decode step (fp32, batch 1 and 2) runs its whole layer stack as
 # one C call (mtl_decode_step) launching the same kernels with the same
 # arguments as the per-layer Python loop: the same bits, without the Python
@@ -559,7 +573,7 @@ class MambaLM(nn.Module):
         captured decode graph can serve the next prompt without re-capture."""
         if out_cache is not None and len(out_cache.layers) != len(self.layers):
             raise ValueError("out_cache has the wrong number of layers")
-        native = self._prefill_short(input_ids, cache, out_cache)
+        native = self._prefill_native(input_ids, cache, out_cache)
         if native is not None:
             return native
         x = self.embedding(input_ids)
@@ -601,17 +615,28 @@ class MambaLM(nn.Module):
         self._short_plan = (key, arr)
         return arr
 
-    def _prefill_short(self, input_ids, cache, out_cache):
-        """prefill() through mtl_prefill_short, or None where it does not
-        apply (more than 64 tokens, a layer shape or dtype it does not take,
-        caches that are not contiguous float32)."""
+    def _native_prefill_kind(self, b, l):
+        """'short' (mtl_prefill_short), 'long' (mtl_prefill_long) or None for
+        a prompt of b x l tokens of this model's shape."""
         cfg = self.cfg
-        if not (SHORT_PREFILL_NATIVE and _SKINNY_PREFILL) or input_ids.dim() != 2 or not input_ids.is_cuda:
+        D, N, K = cfg.d_inner, cfg.d_state, cfg.d_conv
+        if SHORT_PREFILL_NATIVE and _SKINNY_PREFILL and ops.prefill_short_ok(b * l, cfg.d_model, D, N, cfg.dt_rank, K):
+            return "short"
+        if LONG_PREFILL_NATIVE and b * l * D <= LONG_PREFILL_MAX_ELEMS and N <= 32 and 1 <= K <= 8:
+            return "long"
+        return None
+
+    def _prefill_native(self, input_ids, cache, out_cache):
+        """prefill() through mtl_prefill_short or mtl_prefill_long, or None
+        where neither applies (a size or layer shape they do not take, a
+        dtype other than float32, caches that are not contiguous float32)."""
+        cfg = self.cfg
+        if input_ids.dim() != 2 or not input_ids.is_cuda:
             return None
         b, l = input_ids.shape
         D, N, K = cfg.d_inner, cfg.d_state, cfg.d_conv
-        if not ops.prefill_short_ok(b * l, cfg.d_model, D, N, cfg.dt_rank, K) or \
-                self.embedding.weight.dtype != torch.float32:
+        kind = self._native_prefill_kind(b, l)
+        if kind is None or self.embedding.weight.dtype != torch.float32:
             return None
         for c in (cache, out_cache):
             if c is not None and not all(
@@ -643,7 +668,8 @@ class MambaLM(nn.Module):
             L.h0 = lc.ssm_state.data_ptr() if lc is not None else None   # h_out may be h0
             L.h_out = h_out.data_ptr()
         h = self.embedding(input_ids).contiguous()
-        normed = ops.prefill_short(h, arr, self.norm_f.weight, self.norm_f.eps, D, N, cfg.dt_rank, K)
+        run = ops.prefill_short if kind == "short" else ops.prefill_long
+        normed = run(h, arr, self.norm_f.weight, self.norm_f.eps, D, N, cfg.dt_rank, K)
         return self.lm_head(normed), (out_cache if out_cache is not None else MambaCache(new_layers))
 
     def step(self, input_ids: torch.Tensor, cache: MambaCache):

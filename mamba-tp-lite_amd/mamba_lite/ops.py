@@ -553,6 +553,41 @@ def prefill_short(h, layers, norm_f, eps_f, d_inner, d_state, dt_rank, d_conv):
     return normed
 
 
+PREFILL_LONG_BLAS_WS = 32 << 20     # bytes of hipBLASLt workspace per mtl_prefill_long call
+
+
+def prefill_long(h, layers, norm_f, eps_f, d_inner, d_state, dt_rank, d_conv):
+    """mtl_prefill_long: a prompt's whole layer stack in one call (any
+    length, the projections on hipBLASLt).  h [b, l, d_model] float32 holds
+    the embedded tokens and is overwritten with the final residual stream;
+    `layers` is a ctypes array of _lib.PrefillLayer (weights plus this call's
+    cache pointers).  Returns norm_f(h) [b, l, d_model]."""
+    _f32c(h, "h")
+    _f32c(norm_f, "norm_f")
+    b, l, M = h.shape
+    rows, J = b * l, dt_rank + 2 * d_state
+    # one workspace, every buffer on a 256-byte boundary
+    sizes = [rows * M, rows * 2 * d_inner, rows * d_inner, rows * J, rows * d_inner, rows * d_inner, rows * M,
+             PREFILL_LONG_BLAS_WS // 4]
+    offs, n = [], 0
+    for sz in sizes:
+        offs.append(n)
+        n += -(-sz // 64) * 64
+    ws = torch.empty(n + rows * M, device=h.device, dtype=torch.float32)
+    normed = ws[n:].view(b, l, M)
+    base = ws.data_ptr()
+    a = _lib.PrefillLongArgs()
+    a.h = h.data_ptr()
+    a.xn, a.xz, a.u, a.x_dbl, a.dt, a.y, a.out, a.blas_ws = [base + 4 * o for o in offs]
+    a.blas_ws_bytes = PREFILL_LONG_BLAS_WS
+    a.norm_f, a.normed_out, a.eps_f = norm_f.data_ptr(), normed.data_ptr(), float(eps_f)
+    a.d_conv, a.n_layers = d_conv, len(layers)
+    a.batch, a.seqlen, a.d_model, a.d_inner, a.d_state, a.dt_rank = b, l, M, d_inner, d_state, dt_rank
+    with _dev_guard(h):
+        _lib.check(_lib.load().mtl_prefill_long(ctypes.byref(a), layers, _stream(h)), "prefill_long")
+    return normed
+
+
 def decode_step(layers, ids, emb, norm_f, eps_f, logits, xc, gz, y, xs, xpart, cfg, channels_per_block, split_k,
                 xproj_parts):
     """mtl_decode_step: one fused decode step of every layer in one call.

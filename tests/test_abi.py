@@ -50,6 +50,9 @@ def test_struct_layouts_match_header():
     # mtl_prefill_short_args: 11 pointers, eps_f and three int32, six int64 sizes
     assert ctypes.sizeof(_lib.PrefillShortArgs) == 11 * 8 + 4 * 4 + 6 * 8
     assert _lib.PrefillShortArgs.batch.offset == 104
+    # mtl_prefill_long_args: 9 pointers, blas_ws_bytes, 2 pointers, eps_f and three int32, six int64 sizes
+    assert ctypes.sizeof(_lib.PrefillLongArgs) == 12 * 8 + 4 * 4 + 6 * 8
+    assert _lib.PrefillLongArgs.batch.offset == 112
     # mtl_decode_layer: norm_w, eps + reserved, 14 pointers
     assert ctypes.sizeof(_lib.DecodeLayer) == 8 + 4 + 4 + 14 * 8
     # mtl_decode_step_args: 11 pointers, eps_f, then eleven int32
@@ -163,6 +166,13 @@ def test_invalid_arguments_are_rejected_without_a_gpu():
     ("mtl_in_proj_conv_xproj", dict(d_conv=5), b"d_conv"),
     ("mtl_in_proj_conv_xproj", dict(d_conv=1), b"d_conv"),
     ("mtl_in_proj_conv_xproj", dict(J=289), b"J (x_proj rows)"),
+    ("mtl_prefill_long", dict(d_conv=9), b"d_conv"),
+    ("mtl_prefill_long", dict(d_state=33), b"d_state"),
+    ("mtl_prefill_long", dict(batch=1 << 12, seqlen=1 << 12), b"batch * seqlen"),
+    ("mtl_prefill_long", dict(n_layers=0), b"n_layers"),
+    ("mtl_prefill_long", dict(null_ws=True), b"null workspace"),
+    ("mtl_prefill_long", dict(null_layer=True), b"layer 1: null required pointer"),
+    ("mtl_prefill_long", dict(alias=True), b"layer 1: conv_state_out must not alias"),
     ("mtl_in_proj_conv_xproj_normed", dict(sq_tiles=129), b"sq_tiles must be in [1, 128]"),
     ("mtl_in_proj_conv_xproj_normed", dict(sq_tiles=0), b"sq_tiles must be in [1, 128]"),
     ("mtl_in_proj_conv_xproj_normed", dict(null_sq=True), b"null sq"),
@@ -259,6 +269,27 @@ def test_entry_points_validate_sizes_on_the_host(case):
             if a["misaligned_layer"] and i == 1:
                 L.W_out = 24
         rc = lib.mtl_prefill_short(ctypes.byref(args), layers, None)
+    elif name == "mtl_prefill_long":
+        a = dict(batch=1, seqlen=128, d_model=256, d_inner=512, d_state=16, d_conv=4, n_layers=2, null_ws=False,
+                 null_layer=False, alias=False)
+        a.update(over)
+        args = _lib.PrefillLongArgs()
+        for f in ("h", "xn", "xz", "u", "x_dbl", "dt", "y", "out", "blas_ws", "norm_f", "normed_out"):
+            setattr(args, f, None if a["null_ws"] and f == "y" else 16)
+        args.blas_ws_bytes = 1 << 20
+        args.eps_f, args.d_conv, args.n_layers = 1e-5, a["d_conv"], a["n_layers"]
+        args.batch, args.seqlen, args.d_model, args.d_inner = a["batch"], a["seqlen"], a["d_model"], a["d_inner"]
+        args.d_state, args.dt_rank = a["d_state"], 16
+        layers = (_lib.PrefillLayer * 2)()
+        for i, L in enumerate(layers):
+            for f, *_ in _lib.PrefillLayer._fields_:
+                if f not in ("eps", "reserved"):
+                    setattr(L, f, 16 * (len(f) + 1))
+            L.conv_state_out = 32
+            L.conv_state_in = 32 if a["alias"] and i == 1 else 48
+            if a["null_layer"] and i == 1:
+                L.W_dt = None
+        rc = lib.mtl_prefill_long(ctypes.byref(args), layers, None)
     elif name == "mtl_decode_step":
         a = dict(batch=1, cpb=8, n_layers=2, split_k=1, xproj_parts=1, null_ws=False, null_layer=False, d_state=16,
                  d_inner=512, d_conv=4, d_model=256, dt_rank=16, misaligned_layer=False, same_ws=False)

@@ -69,7 +69,7 @@ def test_c1_130m_64_token_prompt_then_32_steps(persist, monkeypatch):
     lm = lm.to(DEV).eval()
     ids = _t(c["ids"])
     with torch.no_grad():
-        assert lm._prefill_short(ids[:, :64], None, None) is not None     # the one-call short prefill
+        assert lm._native_prefill_kind(1, 64) == "short"                 # the one-call short prefill
         logits, cache = lm.prefill(ids[:, :64])
         assert_rel(_n(logits), c["prefill"], 1e-4, "prefill logits")
         assert lm._fused_step_ok(ids[:, :1], cache)

@@ -111,7 +111,7 @@ def test_random_config_prefill_continue_step_vs_oracle(seed):
     ref1, rc1 = om.lm_prefill(W, ids[:, l0:l0 + l1], cache=[(c.copy(), h.copy()) for c, h in rc0], dtype=np.float64)
     with torch.no_grad():
         if seed >= N_CASES:
-            assert lm._prefill_short(tids[:, :l0], None, None) is not None, "the one-call short prefill"
+            assert lm._native_prefill_kind(batch, l0) == "short", "the one-call short prefill"
         got0, c0 = lm.prefill(tids[:, :l0])
         assert_rel(got0.float().cpu().numpy(), ref0, 1e-4, "prefill logits")
         _check_cache(_cache_np(c0), rc0, "prefill")

@@ -474,6 +474,7 @@ def test_short_prefill_on_the_skinny_gemm_vs_oracle(b, l, monkeypatch):
     import mamba_lite.model as mm
     from mamba_lite import ops as mops
     monkeypatch.setattr(mm, "SHORT_PREFILL_NATIVE", False)    # the per-op launches themselves
+    monkeypatch.setattr(mm, "LONG_PREFILL_NATIVE", False)
     torch.manual_seed(11)
     cfg = MambaConfig(d_model=256, n_layer=2, vocab_size=384, d_state=16)
     with torch.device(DEV):
@@ -570,9 +571,13 @@ def test_bf16_lm_prefill_step_generate(d_model):
 def test_short_prefill_conv_widths_and_biases(d_conv, bias, b, l, monkeypatch):
     """The fused short-prefill path (in_proj with the conv epilogue, split
     x_proj with dt_proj, out_proj parts) at conv widths 2, 3, 4, with the
-    in_proj / out_proj biases, against the float64 oracle at 1e-4."""
+    in_proj / out_proj biases, against the float64 oracle at 1e-4.  At this
+    width the one-call short prefill does not apply; the one-call long
+    prefill, which would take the prompt, is switched off to reach the
+    per-op launches."""
     import mamba_lite.model as mm
     from mamba_lite import ops as mops
+    monkeypatch.setattr(mm, "LONG_PREFILL_NATIVE", False)
     torch.manual_seed(40 + d_conv)
     cfg = MambaConfig(d_model=128, n_layer=2, vocab_size=256, d_state=16, d_conv=d_conv, bias=bias)
     with torch.device(DEV):
@@ -627,6 +632,7 @@ def test_native_short_prefill_equals_the_per_op_path(d_conv, bias, b, l, monkeyp
     nat = run()
     assert len(calls) == 2
     monkeypatch.setattr(mm, "SHORT_PREFILL_NATIVE", False)
+    monkeypatch.setattr(mm, "LONG_PREFILL_NATIVE", False)
     per = run()
     assert len(calls) == 2
     for k, (x, y) in enumerate(zip(nat, per)):

@@ -1,0 +1,134 @@
+"""mtl_prefill_long: a prompt's whole layer stack in one C call past the
+short-prompt limit, on the GPU (model.py:184-241, 303-306, 328-341):
+
+  * logits and final states against the float64 oracle (1e-4, the fp32
+    tolerance) and against the per-op Python path (1e-5: the GEMM picks
+    differ, so the bits may), at the 130m and 1.4b widths and at small widths
+    with biases, d_conv 1 and 3, 8 and 32 states;
+  * continuation from a cache, written in place (h_out aliasing h0, the conv
+    history read and written in different runs), and into a separate
+    out_cache;
+  * a captured GraphedPrefill replays the eager bits, with eager work between
+    replays;
+  * which prompts take it (more than 64 tokens, or a shape the short path
+    does not take, up to LONG_PREFILL_MAX_ELEMS token-channels)."""
+import numpy as np
+import pytest
+import torch
+
+import _golden as G
+from _util import assert_rel
+from mamba_lite import ops
+from mamba_lite.cuda_graph import GraphedPrefill
+from mamba_lite.model import MambaCache, MambaConfig, MambaLM
+from oracle import mixer as om
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _n(t):
+    return t.detach().double().cpu().numpy()
+
+
+def _t(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(DEV)
+
+
+def _lm(seed, d_model, n_layer, vocab, **kw):
+    sd = G.lm_weights(seed, d_model, n_layer, vocab, **kw)
+    lm = MambaLM(MambaConfig(d_model=d_model, n_layer=n_layer, vocab_size=vocab, **kw))
+    lm.load_state_dict({k: torch.from_numpy(v) for k, v in sd.items()}, strict=True)
+    return lm.to(DEV).eval(), G.oracle_lm_dict(sd, n_layer)
+
+
+def _counting(monkeypatch):
+    calls = []
+    real = ops.prefill_long
+    monkeypatch.setattr(ops, "prefill_long", lambda *a, **k: calls.append(1) or real(*a, **k))
+    return calls
+
+
+@pytest.mark.parametrize("b,l,d_model,n_layer,kw", [
+    (1, 65, 768, 2, {}), (1, 300, 768, 2, {}), (2, 130, 256, 3, dict(bias=True)), (3, 40, 256, 2, {}),
+    (1, 200, 2048, 1, dict(dt_rank=128)), (2, 70, 128, 2, dict(d_conv=1)), (1, 90, 256, 2, dict(d_conv=3, d_state=8)),
+    (1, 100, 256, 2, dict(d_state=32)), (1, 9, 64, 2, {})])
+def test_long_prefill_vs_oracle_and_per_op(b, l, d_model, n_layer, kw, monkeypatch):
+    import mamba_lite.model as mm
+    print(f"\n[prefill long b={b} l={l} d_model={d_model} layers={n_layer} {kw}]", flush=True)
+    vocab = 512
+    lm, W = _lm(90 + b + l + d_model, d_model, n_layer, vocab, **kw)
+    calls = _counting(monkeypatch)
+    ids = np.random.default_rng(b * 7 + l).integers(0, vocab, (b, l), dtype=np.int64)
+    with torch.no_grad():
+        logits, cache = lm.prefill(_t(ids))
+        assert calls == [1], "the prompt did not take mtl_prefill_long"
+        monkeypatch.setattr(mm, "LONG_PREFILL_NATIVE", False)
+        ref_logits, ref_cache = lm.prefill(_t(ids))
+        monkeypatch.setattr(mm, "LONG_PREFILL_NATIVE", True)
+    o_logits, o_cache = om.lm_prefill(W, ids, dtype=np.float64)
+    assert_rel(_n(logits), o_logits, 1e-4, "logits vs oracle")
+    assert_rel(_n(logits), _n(ref_logits), 1e-5, "logits vs per-op path")
+    for i, (lc, rc, (oc, oh)) in enumerate(zip(cache.layers, ref_cache.layers, o_cache)):
+        assert_rel(_n(lc.ssm_state), oh, 1e-4, f"layer {i} ssm_state vs oracle")
+        assert_rel(_n(lc.conv_state), oc, 1e-4, f"layer {i} conv_state vs oracle")
+        assert_rel(_n(lc.ssm_state), _n(rc.ssm_state), 1e-5, f"layer {i} ssm_state vs per-op")
+
+
+@pytest.mark.parametrize("in_place", [True, False])
+def test_long_prefill_continues_a_cache(in_place, monkeypatch):
+    """A 100-token prompt, then 150 more tokens from its cache: into the same
+    cache (states rewritten in place) or into a separate out_cache; both
+    against the oracle's continuation."""
+    print(f"\n[prefill long continuation in_place={in_place}]", flush=True)
+    lm, W = _lm(95, 256, 2, 512, bias=True)
+    calls = _counting(monkeypatch)
+    rng = np.random.default_rng(95)
+    ids0, ids1 = rng.integers(0, 512, (2, 100)), rng.integers(0, 512, (2, 150))
+    with torch.no_grad():
+        _, cache = lm.prefill(_t(ids0))
+        out = cache if in_place else MambaCache.allocate(lm.cfg, 2, DEV, torch.float32)
+        before = [lc.ssm_state.clone() for lc in cache.layers]
+        logits, got = lm.prefill(_t(ids1), cache=cache, out_cache=out)
+    assert got is out and len(calls) == 2
+    if not in_place:
+        assert all(torch.equal(a, lc.ssm_state) for a, lc in zip(before, cache.layers)), "input cache changed"
+    _, oc = om.lm_prefill(W, ids0, dtype=np.float64)
+    o_logits, oc2 = om.lm_prefill(W, ids1, cache=oc, dtype=np.float64)
+    assert_rel(_n(logits), o_logits, 1e-4, "logits")
+    for i, (lc, (c, h)) in enumerate(zip(got.layers, oc2)):
+        assert_rel(_n(lc.ssm_state), h, 1e-4, f"layer {i} ssm_state")
+        assert_rel(_n(lc.conv_state), c, 1e-4, f"layer {i} conv_state")
+
+
+def test_graphed_long_prefill_replays_equal_eager(monkeypatch):
+    print("\n[prefill long: graph replay]", flush=True)
+    lm, _ = _lm(97, 768, 2, 512)
+    calls = _counting(monkeypatch)
+    rng = np.random.default_rng(97)
+    prompts = [_t(rng.integers(0, 512, (1, 128))) for _ in range(3)]
+    cache = MambaCache.allocate(lm.cfg, 1, DEV, torch.float32)
+    gp = GraphedPrefill(lm, cache, 1, 128, "cuda")
+    gp.capture()
+    with torch.no_grad():
+        for i, ids in enumerate(prompts):
+            got = gp.replay(ids).clone()
+            g_states = [lc.ssm_state.clone() for lc in cache.layers]
+            torch.cuda.synchronize()
+            ref, rcache = lm.prefill(ids)                       # eager work between replays
+            assert torch.equal(got, ref), f"replay {i} differs from eager"
+            assert all(torch.equal(a, lc.ssm_state) for a, lc in zip(g_states, rcache.layers))
+    assert calls, "the captured prefill did not take mtl_prefill_long"
+
+
+def test_native_prefill_kind():
+    import mamba_lite.model as mm
+    lm, _ = _lm(99, 768, 1, 512)
+    assert lm._native_prefill_kind(1, 64) == "short"
+    assert lm._native_prefill_kind(1, 65) == "long"
+    assert lm._native_prefill_kind(4, 256) == "long"
+    lim = mm.LONG_PREFILL_MAX_ELEMS // lm.cfg.d_inner
+    assert lm._native_prefill_kind(1, lim) == "long"
+    assert lm._native_prefill_kind(1, lim + 1) is None
+    small, _ = _lm(99, 64, 1, 512)
+    assert small._native_prefill_kind(1, 8) == "long"     # the short path takes d_model >= 256 only

@@ -256,12 +256,15 @@ def test_prefill_short_covers_the_sizes_its_kernels_take(rows, M, D, N, R, K, ok
     assert ops.prefill_short_ok(rows, M, D, N, R, K) is ok
 
 
-def test_prefill_short_is_not_taken_off_the_gpu():
-    """MambaLM._prefill_short declines CPU token ids and non-fp32 models
-    before touching the library, so prefill() keeps its other paths there."""
+def test_native_prefill_is_not_taken_off_the_gpu():
+    """MambaLM._prefill_native declines CPU token ids (short and long
+    prompts) before touching the library, so prefill() keeps its other paths
+    there."""
     cfg = MambaConfig(d_model=256, n_layer=1, vocab_size=64, d_state=16)
     model = MambaLM(cfg)
-    assert model._prefill_short(torch.zeros(1, 8, dtype=torch.long), None, None) is None
+    assert model._native_prefill_kind(1, 8) == "short" and model._native_prefill_kind(1, 300) == "long"
+    for l in (8, 300):
+        assert model._prefill_native(torch.zeros(1, l, dtype=torch.long), None, None) is None
     assert not hasattr(model, "_short_plan")
 
 
