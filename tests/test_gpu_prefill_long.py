@@ -11,7 +11,9 @@ short-prompt limit, on the GPU (model.py:184-241, 303-306, 328-341):
   * a captured GraphedPrefill replays the eager bits, with eager work between
     replays;
   * which prompts take it (more than 64 tokens, or a shape the short path
-    does not take, up to LONG_PREFILL_MAX_ELEMS token-channels)."""
+    does not take, up to LONG_PREFILL_MAX_ELEMS token-channels);
+  * two threads prefilling on their own streams at once get what each would
+    alone, bit for bit."""
 import numpy as np
 import pytest
 import torch
@@ -132,3 +134,34 @@ def test_native_prefill_kind():
     assert lm._native_prefill_kind(1, lim + 1) is None
     small, _ = _lm(99, 64, 1, 512)
     assert small._native_prefill_kind(1, 8) == "long"     # the short path takes d_model >= 256 only
+
+
+def test_concurrent_long_prefills_on_two_streams():
+    """Two threads prefill different prompts on their own streams at once
+    (the library serializes the calls and shares its GEMM plans); each gets
+    what a prefill on its own would give, bit for bit."""
+    import threading
+    print("\n[prefill long: two threads, two streams]", flush=True)
+    lm, _ = _lm(101, 256, 2, 512)
+    rng = np.random.default_rng(101)
+    prompts = [_t(rng.integers(0, 512, (1, 200))), _t(rng.integers(0, 512, (2, 90)))]
+    with torch.no_grad():
+        alone = [lm.prefill(p)[0] for p in prompts]
+    torch.cuda.synchronize()
+    got = [None, None]
+
+    def run(i):
+        s = torch.cuda.Stream()
+        with torch.no_grad(), torch.cuda.stream(s):
+            for _ in range(5):
+                got[i] = lm.prefill(prompts[i])[0]
+        s.synchronize()
+
+    threads = [threading.Thread(target=run, args=(i,)) for i in range(2)]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join()
+    torch.cuda.synchronize()
+    for i in range(2):
+        assert torch.equal(got[i], alone[i]), f"thread {i} differs"
