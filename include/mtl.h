@@ -38,7 +38,7 @@ typedef void* mtl_stream_t; /* hipStream_t */
 
 /* Thread-local text of the last failure ("" if none). */
 const char* mtl_last_error(void);
-/* ABI version, bumped on any signature change. */
+/* ABI version, bumped on any signature change or new entry point the Python layer binds. */
 int mtl_abi_version(void);
 
 /* ------------------------------------------------------------------------
@@ -612,6 +612,61 @@ typedef struct {
 } mtl_decode_step_args;
 
 int mtl_decode_step(const mtl_decode_step_args* args, const mtl_decode_layer* layers, mtl_stream_t stream);
+
+/* ------------------------------------------------------------------------
+ * mtl_decode_step_batched: a batched decode step of the whole layer stack in
+ * one call -- MambaLM.step (model.py:343-353) over MambaBlock.step (308-311)
+ * and MambaMixer.step (249-294) -- fp32, 1..32 rows, up to the lm_head's
+ * input.  Per layer: mtl_in_proj_conv_xproj (with fold, from layer 1 on,
+ * mtl_in_proj_conv_xproj_normed), mtl_sum_parts, mtl_selective_state_update,
+ * then out_proj as 4 split-K parts: with fold and before the last layer
+ * mtl_linear_skinny_residual, otherwise mtl_linear_skinny followed by
+ * mtl_add_rmsnorm_parts (the residual add and the next RMSNorm; norm_f after
+ * the last layer).  The tile choices are those of the Python layer's per-op
+ * step, so the results are the same bits as calling those entry points one
+ * by one.
+ *   h           [b, d_model] in: the embedding rows of the step's tokens;
+ *               out: the residual stream after the last layer
+ *   normed_out  [b, d_model] out: norm_f of it, the tied lm_head's input
+ *   workspace   inp, xn [b, d_model]; xc, z, y [b, d_inner]; xpart
+ *               [d_inner / 16, b, J]; x_dbl [b, J]; parts [4, b, d_model];
+ *               with fold also sq [d_model / 16, b] and counters
+ *               [n_layers - 1, d_model / 16], zero-filled before each call
+ *               (a call needs its own zeroed counters); xn, sq and counters
+ *               may be NULL without fold
+ *   layers      mtl_decode_layer with W_xT ([d_inner, J], x_proj transposed)
+ *               and conv_w [d_inner, d_conv]; W_x is not read.  Each layer's
+ *               conv_state [b, d_inner, d_conv - 1] and ssm_state
+ *               [b, d_inner, d_state] are updated in place.
+ * d_model a multiple of 128 (at least 256), d_inner a multiple of 512,
+ * d_state <= 16, dt_rank <= 256 with dt_rank + 2 d_state <= 288, d_conv
+ * 2..4.  Every layer's pointers, the sizes and the alignments the entry
+ * points take are checked before the first launch.
+ * ---------------------------------------------------------------------- */
+typedef struct {
+    float* h;
+    float* normed_out;
+    const float* norm_f;       /* [d_model] */
+    float* inp;
+    float* xn;
+    float* xc;
+    float* z;
+    float* y;
+    float* xpart;
+    float* x_dbl;
+    float* parts;
+    float* sq;
+    uint32_t* counters;
+    float eps_f;
+    int32_t n_layers;
+    int32_t batch;
+    int32_t d_model, d_inner, d_state, dt_rank, d_conv;
+    int32_t fold;              /* 1: residual add + norm folded into the projections */
+    int32_t reserved;
+} mtl_decode_step_batched_args;
+
+int mtl_decode_step_batched(const mtl_decode_step_batched_args* args, const mtl_decode_layer* layers,
+                            mtl_stream_t stream);
 
 /* ------------------------------------------------------------------------
  * mtl_decode_step_persist: the same step -- MambaLM.step (model.py:343-353)

@@ -26,4 +26,4 @@ int check_launch(const char* what) {
 }  // namespace mtl
 
 extern "C" const char* mtl_last_error(void) { return mtl::g_last_error.c_str(); }
-extern "C" int mtl_abi_version(void) { return 2; }
+extern "C" int mtl_abi_version(void) { return 3; }

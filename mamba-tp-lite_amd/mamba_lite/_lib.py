@@ -15,7 +15,7 @@ import os
 import torch  # noqa: F401  (must be loaded first, see module docstring)
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libmtl.so")
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 MTL_F32 = 0
 MTL_BF16 = 1
@@ -105,6 +105,16 @@ class DecodeStepArgs(ctypes.Structure):
     ]
 
 
+class DecodeStepBatchedArgs(ctypes.Structure):
+    """mirror of mtl_decode_step_batched_args"""
+    _fields_ = [
+        ("h", _vp), ("normed_out", _vp), ("norm_f", _vp), ("inp", _vp), ("xn", _vp), ("xc", _vp), ("z", _vp),
+        ("y", _vp), ("xpart", _vp), ("x_dbl", _vp), ("parts", _vp), ("sq", _vp), ("counters", _vp),
+        ("eps_f", ctypes.c_float), ("n_layers", _i32), ("batch", _i32), ("d_model", _i32), ("d_inner", _i32),
+        ("d_state", _i32), ("dt_rank", _i32), ("d_conv", _i32), ("fold", _i32), ("reserved", _i32),
+    ]
+
+
 # name -> (restype, argtypes); every symbol of include/mtl.h
 SIGNATURES = {
     "mtl_last_error": (ctypes.c_char_p, []),
@@ -121,6 +131,8 @@ SIGNATURES = {
     "mtl_prefill_short": (ctypes.c_int, [ctypes.POINTER(PrefillShortArgs), ctypes.POINTER(PrefillLayer), _vp]),
     "mtl_prefill_long": (ctypes.c_int, [ctypes.POINTER(PrefillLongArgs), ctypes.POINTER(PrefillLayer), _vp]),
     "mtl_decode_step": (ctypes.c_int, [ctypes.POINTER(DecodeStepArgs), ctypes.POINTER(DecodeLayer), _vp]),
+    "mtl_decode_step_batched": (ctypes.c_int, [ctypes.POINTER(DecodeStepBatchedArgs), ctypes.POINTER(DecodeLayer),
+                                               _vp]),
     "mtl_decode_persist_workspace_bytes": (ctypes.c_size_t, [_i32, _i32, _i32, _i32]),
     "mtl_decode_persist_grid": (_i32, [_i32, _i32, _i32, _i32, _i32, _i32, _i32]),
     "mtl_decode_step_persist": (ctypes.c_int, [ctypes.POINTER(DecodeStepArgs), ctypes.POINTER(DecodeLayer), _vp, _vp,

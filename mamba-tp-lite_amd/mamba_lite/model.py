@@ -169,6 +169,13 @@ LONG_PREFILL_MAX_ELEMS = 1 << 21
 # per launch that bounds an eager step.
 DECODE_STEP_NATIVE = True
 
+# The batched step (fp32, the rows the fused step does not take, up to 32)
+# runs its layer stack as one C call too (mtl_decode_step_batched) when
+# every layer takes the per-op path's in_proj + conv + x_proj launch and
+# split out_proj: the same launches with the same tile choices, so the same
+# bits, without the ~5 Python-launched ops per layer.
+BATCHED_STEP_NATIVE = True
+
 # With DECODE_PERSIST, the batch-1 fused decode of a model that fits its
 # register blocking (d_model <= 1024, d_inner <= 2 d_model, dt_rank <= 64,
 # d_conv <= 4, <= 64 layers) runs as one persistent launch,
@@ -681,7 +688,13 @@ class MambaLM(nn.Module):
         if self._fused_step_ok(input_ids, cache):
             return self._step_fused(input_ids, cache)
         x = self.embedding(input_ids).squeeze(1)
-        if self._fold_ok(x, cache):
+        fold = self._fold_ok(x, cache)
+        if BATCHED_STEP_NATIVE:
+            arr = self._batched_step_layers(x, cache)
+            if arr is not None:
+                normed = ops.decode_step_batched(arr, x, self.norm_f.weight, self.norm_f.eps, self.cfg, fold)
+                return self.lm_head(normed).unsqueeze(1)
+        if fold:
             return self._step_folded(x, cache)
 
         def layer(i, xn):
@@ -751,6 +764,55 @@ class MambaLM(nn.Module):
                 p = ops.linear_skinny(y, mx.out_proj.weight, mx.out_proj.bias, ksplit=SKINNY_OUT_SPLIT)
                 inp = ops.add_rmsnorm(h, self._norm_weight(nl), self._eps(nl), y_parts=p, x_out=h)
         return self.lm_head(inp).unsqueeze(1)
+
+    def _batched_step_layers(self, x, cache):
+        """ctypes array of mtl_decode_layer for mtl_decode_step_batched (this
+        call's cache pointers filled in), or None when some layer would not
+        take the per-op path's in_proj + conv + x_proj launch and split
+        out_proj, or a weight or cache tensor is not a contiguous float32
+        tensor of its shape on x's device (the step then runs op by op, with
+        that path's checks and errors)."""
+        cfg = self.cfg
+        if x.dim() != 2 or x.dtype != torch.float32 or not x.is_cuda or not x.is_contiguous() or \
+                x.data_ptr() % 16 or len(cache.layers) != len(self.layers):
+            return None
+        b, dm = x.shape
+        D, N, K = cfg.d_inner, cfg.d_state, cfg.d_conv
+        J = cfg.dt_rank + 2 * N
+        if b > ops.IN_CONV_MAX_ROWS or D % (128 * SKINNY_OUT_SPLIT) or N > 16 or cfg.dt_rank > 256:
+            return None
+        dev = x.device
+        ok = lambda t, shape: t is None or (t.device == dev and t.dtype == torch.float32 and t.is_contiguous()
+                                            and tuple(t.shape) == shape)
+        ws = []
+        for blk, lc in zip(self.layers, cache.layers):
+            mx = blk.mixer
+            if not ops.in_proj_conv_xproj_ok(x, mx.in_proj.weight, lc.conv_state, K, J):
+                return None
+            if not (ok(lc.ssm_state, (b, D, N)) and ok(mx.out_proj.weight, (dm, D)) and mx.out_proj.weight.data_ptr() % 16 == 0):
+                return None
+            conv_w = mx._conv_w()
+            tens = [blk.norm.weight, mx.in_proj.weight, mx.in_proj.bias, conv_w, mx.conv1d.bias, mx._xproj_t(),
+                    mx.dt_proj.weight, mx.dt_proj.bias, mx.A_log, mx.D, mx.out_proj.weight, mx.out_proj.bias]
+            shapes = [(dm,), (2 * D, dm), (2 * D,), (D, K), (D,), (D, J), (D, cfg.dt_rank), (D,), (D, N), (D,),
+                      (dm, D), (dm,)]
+            if not all(ok(t, s) for t, s in zip(tens, shapes)):
+                return None
+            ws.append(tens)
+        key = tuple(0 if t is None else t.data_ptr() for tens in ws for t in tens)
+        cached = getattr(self, "_batched_tmpl", None)
+        if cached is None or cached[0] != key or cached[2] != dev:
+            tmpl = (_lib.DecodeLayer * len(self.layers))()
+            for i, L in enumerate(tmpl):
+                (L.norm_w, L.W_in, L.b_in, L.conv_w, L.conv_b, L.W_xT, L.W_dt, L.dt_bias, L.A_log, L.Dv, L.W_out,
+                 L.b_out) = key[12 * i:12 * i + 12]
+                L.eps = self.layers[i].norm.eps
+            cached = (key, tmpl, dev)
+            self._batched_tmpl = cached
+        arr = type(cached[1]).from_buffer_copy(cached[1])   # per call: read by the library without the GIL
+        for L, lc in zip(arr, cache.layers):
+            L.conv_state, L.ssm_state = lc.conv_state.data_ptr(), lc.ssm_state.data_ptr()
+        return arr
 
     # ---- fused decode step ----
     def _fused_step_ok(self, input_ids, cache) -> bool:

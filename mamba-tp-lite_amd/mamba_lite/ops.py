@@ -616,6 +616,40 @@ def decode_step(layers, ids, emb, norm_f, eps_f, logits, xc, gz, y, xs, xpart, c
     return logits
 
 
+def decode_step_batched(layers, h, norm_f, eps_f, cfg, fold):
+    """mtl_decode_step_batched: a batched step of every layer in one call.
+    `layers` is a ctypes array of _lib.DecodeLayer (weights with W_xT, and
+    this call's cache pointers); h [b, d_model] float32 holds the step's
+    embedding rows and is left holding the final residual stream.  Returns
+    norm_f of it [b, d_model], the tied lm_head's input.  The workspace is
+    allocated here (one float32 tensor, and with fold the zeroed counters)."""
+    _f32c(h, "h")
+    _f32c(norm_f, "norm_f")
+    if h.dim() != 2 or h.data_ptr() % 16:
+        raise ValueError("decode_step_batched: h must be a 16-byte aligned [b, d_model] tensor")
+    b, M = h.shape
+    D, J = cfg.d_inner, cfg.dt_rank + 2 * cfg.d_state
+    nl = len(layers)
+    pad = lambda n: -(-n // 64) * 64                      # 256-byte aligned slices
+    sizes = {"normed_out": b * M, "inp": b * M, "xn": b * M, "xc": b * D, "z": b * D, "y": b * D,
+             "xpart": (D // 16) * b * J, "x_dbl": b * J, "parts": 4 * b * M, "sq": (M // 16) * b}
+    ws = torch.empty(sum(pad(n) for n in sizes.values()), device=h.device, dtype=torch.float32)
+    a = _lib.DecodeStepBatchedArgs()
+    off = 0
+    for name, n in sizes.items():
+        setattr(a, name, ws.data_ptr() + 4 * off)
+        off += pad(n)
+    counters = torch.zeros(max(nl - 1, 1), M // 16, device=h.device, dtype=torch.int32) if fold else None
+    a.h, a.norm_f = h.data_ptr(), norm_f.data_ptr()
+    a.counters = counters.data_ptr() if fold else None
+    a.eps_f, a.n_layers, a.batch = float(eps_f), nl, b
+    a.d_model, a.d_inner, a.d_state, a.dt_rank, a.d_conv = M, D, cfg.d_state, cfg.dt_rank, cfg.d_conv
+    a.fold = int(bool(fold))
+    with _dev_guard(h):
+        _lib.check(_lib.load().mtl_decode_step_batched(ctypes.byref(a), layers, _stream(h)), "decode_step_batched")
+    return ws[:b * M].view(b, M)
+
+
 def decode_persist_workspace(cfg, device) -> torch.Tensor:
     """A zero-filled workspace for mtl_decode_step_persist (its exchange slots,
     epoch and error word), to be kept and reused by every call on `device`."""

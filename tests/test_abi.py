@@ -58,6 +58,10 @@ def test_struct_layouts_match_header():
     # mtl_decode_step_args: 11 pointers, eps_f, then eleven int32
     assert ctypes.sizeof(_lib.DecodeStepArgs) == 11 * 8 + 4 + 11 * 4
     assert _lib.DecodeStepArgs.eps_f.offset == 88
+    # mtl_decode_step_batched_args: 13 pointers, eps_f, then nine int32
+    assert ctypes.sizeof(_lib.DecodeStepBatchedArgs) == 13 * 8 + 4 + 9 * 4
+    assert _lib.DecodeStepBatchedArgs.eps_f.offset == 104
+    assert _lib.DecodeStepBatchedArgs.fold.offset == 136
 
 
 def test_invalid_arguments_are_rejected_without_a_gpu():
@@ -158,6 +162,20 @@ def test_invalid_arguments_are_rejected_without_a_gpu():
     ("mtl_decode_step_persist", dict(null_xt=True), b"layer 1: null required pointer"),
     ("mtl_prefill_short", dict(misaligned_layer=True),
      b"layer 1: W_in, b_in, W_x, W_out and b_out must be 16-byte aligned"),
+    ("mtl_decode_step_batched", dict(batch=33), b"batch must be in [1, 32]"),
+    ("mtl_decode_step_batched", dict(n_layers=0), b"n_layers"),
+    ("mtl_decode_step_batched", dict(d_model=320), b"d_model"),
+    ("mtl_decode_step_batched", dict(d_inner=768), b"d_inner"),
+    ("mtl_decode_step_batched", dict(d_state=17), b"d_state"),
+    ("mtl_decode_step_batched", dict(dt_rank=260), b"dt_rank"),
+    ("mtl_decode_step_batched", dict(d_conv=5), b"d_conv"),
+    ("mtl_decode_step_batched", dict(null_ws=True), b"null workspace"),
+    ("mtl_decode_step_batched", dict(fold=1, null_fold=True), b"fold needs xn, sq and counters"),
+    ("mtl_decode_step_batched", dict(fold=1, xn_is_h=True), b"xn must not alias h or inp"),
+    ("mtl_decode_step_batched", dict(null_layer=True), b"layer 1: null required pointer"),
+    ("mtl_decode_step_batched", dict(misaligned_layer=True), b"layer 1: W_in, b_in, conv_state"),
+    ("mtl_decode_step_batched", dict(fold=1, misaligned_norm=True), b"layer 1: W_in, b_in, conv_state"),
+    ("mtl_decode_step_batched", dict(fold=1, d_model=2176), b"at most 128"),
     ("mtl_in_proj_conv_xproj", dict(batch=33), b"batch must be in [1, 32]"),
     ("mtl_in_proj_conv_xproj", dict(d_model=128), b"at least 256"),
     ("mtl_in_proj_conv_xproj", dict(d_model=320), b"multiple of 128"),
@@ -331,6 +349,36 @@ def test_entry_points_validate_sizes_on_the_host(case):
                 L.W_xT = None
         rc = lib.mtl_decode_step_persist(ctypes.byref(args), layers, ctypes.c_void_p(256), ctypes.c_void_p(256),
                                          a["ws_bytes"], a["blocking"], None)
+    elif name == "mtl_decode_step_batched":
+        a = dict(batch=8, n_layers=2, d_model=256, d_inner=512, d_state=16, dt_rank=16, d_conv=4, fold=0,
+                 null_ws=False, null_fold=False, xn_is_h=False, null_layer=False, misaligned_layer=False,
+                 misaligned_norm=False)
+        a.update(over)
+        args = _lib.DecodeStepBatchedArgs()
+        for k, (f, *_) in enumerate(_lib.DecodeStepBatchedArgs._fields_[:13]):
+            # distinct 16-byte aligned placeholders, never dereferenced
+            setattr(args, f, 16 * (k + 1))
+        if a["null_ws"]:
+            args.x_dbl = None
+        if a["null_fold"]:
+            args.sq = None
+        if a["xn_is_h"]:
+            args.xn = args.h
+        args.eps_f, args.n_layers, args.batch, args.fold = 1e-5, a["n_layers"], a["batch"], a["fold"]
+        args.d_model, args.d_inner, args.d_state, args.dt_rank, args.d_conv = a["d_model"], a["d_inner"], \
+            a["d_state"], a["dt_rank"], a["d_conv"]
+        layers = (_lib.DecodeLayer * 2)()
+        for i, L in enumerate(layers):
+            for f, *_ in _lib.DecodeLayer._fields_:
+                if f not in ("eps", "reserved", "W_x"):
+                    setattr(L, f, 16)
+            if a["null_layer"] and i == 1:
+                L.W_xT = None
+            if a["misaligned_layer"] and i == 1:
+                L.conv_state = 24
+            if a["misaligned_norm"] and i == 1:
+                L.norm_w = 20
+        rc = lib.mtl_decode_step_batched(ctypes.byref(args), layers, None)
     elif name == "mtl_in_proj_conv_xproj":
         a = dict(batch=8, d_model=256, d_inner=64, cpp=16, d_conv=4, J=40)
         a.update(over)

@@ -107,6 +107,7 @@ def test_folded_step_vs_oracle_and_unfolded(b, d_model, n_layer, kw, monkeypatch
     there); the limit is raised so the folded kernels are checked up to 32."""
     import mamba_lite.model as mm
     monkeypatch.setattr(mm, "STEP_NORM_FOLD_MAX_ROWS", 32)
+    monkeypatch.setattr(mm, "BATCHED_STEP_NATIVE", False)     # the Python launches, counted below
     print(f"\n[fold: lm step b={b} d_model={d_model} layers={n_layer} {kw}]", flush=True)
     vocab = 512
     lm, W = _lm(60 + b + d_model, d_model, n_layer, vocab, **kw)

@@ -212,7 +212,9 @@ def test_graph_replay_on_the_skinny_gemm_step(batch, monkeypatch):
     (4 split-K parts summed by the residual add): graph replays equal eager
     bit for bit, with eager work between replays, and the eager step matches
     the float64 oracle."""
+    import mamba_lite.model as mm
     from mamba_lite import ops as mops
+    monkeypatch.setattr(mm, "BATCHED_STEP_NATIVE", False)     # the Python launches, counted below
     calls = []
     real = mops.linear_skinny
     monkeypatch.setattr(mops, "linear_skinny", lambda *a, **k: calls.append(k.get("ksplit", 1)) or real(*a, **k))
