@@ -244,7 +244,9 @@ def bench_decode(model, batch, prompt, n_tokens, dev):
         st.capture()
         ok = all(torch.equal(st.replay(nxt), e) for e in eager)   # graph == eager, bit for bit
         ms = _timed(lambda: st.replay(nxt), n_tokens, 3)
-    return ms * 1000.0, ok
+        # eager steps (what generate() runs), launched from the host one step at a time
+        ms_eager = _timed(lambda: model.step(nxt, cache_e), 64, 3)
+    return ms * 1000.0, ok, ms_eager * 1000.0
 
 
 def _oracle_lm_weights(model):
@@ -665,10 +667,10 @@ def main():
                 log(f"decode {name}: building model")
                 model = build_lm(MambaConfig(**cfg_kw), dev)
                 for bsz in (only_b or batches):
-                    us, ok = bench_decode(model, bsz, prompt, ntok, dev)
+                    us, ok, us_eager = bench_decode(model, bsz, prompt, ntok, dev)
                     dec[f"{name}_b{bsz}"] = {"us_per_step": us, "us_per_token": us / bsz, "graph_equals_eager": ok,
-                                             "prompt": prompt, "tokens_timed": ntok}
-                    log(f"decode {name} b={bsz}: {us:.1f} us/step (graph==eager {ok})")
+                                             "prompt": prompt, "tokens_timed": ntok, "eager_us_per_step": us_eager}
+                    log(f"decode {name} b={bsz}: {us:.1f} us/step (graph==eager {ok}); eager {us_eager:.1f} us/step")
                 if name == "130m" and not args.no_cpu_baseline:
                     cb = cpu_baseline_decode(model, dev)
                     dec.setdefault("130m_b1", {})["cpu_baseline"] = cb

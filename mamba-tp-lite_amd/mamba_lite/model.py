@@ -511,6 +511,11 @@ class MambaMixer(nn.Module):
         return F.linear(xc, self.x_proj.weight)
 
 
+# field order of MambaLM._layer_tensors()
+(_LT_NORM, _LT_W_IN, _LT_B_IN, _LT_CONV_W, _LT_CONV_B, _LT_XPROJ, _LT_W_DT, _LT_B_DT, _LT_A_LOG, _LT_D, _LT_W_OUT,
+ _LT_B_OUT) = range(12)
+
+
 @dataclass
 class _Parts:
     """A mixer output given as split-K partial products [P, b, d_model],
@@ -685,16 +690,17 @@ class MambaLM(nn.Module):
         (FUSED_STEP_MAX_BATCH) take the fused decode path (3-4 launches per
         layer); others run the per-op path (the matrix-core skinny GEMMs or
         the library's, the conv-step and SSM-update kernels)."""
-        if self._fused_step_ok(input_ids, cache):
-            return self._step_fused(input_ids, cache)
+        lt = self._layer_tensors()
+        if self._fused_step_ok(input_ids, cache, lt=lt):
+            return self._step_fused(input_ids, cache, lt=lt)
         x = self.embedding(input_ids).squeeze(1)
-        fold = self._fold_ok(x, cache)
         if BATCHED_STEP_NATIVE:
-            arr = self._batched_step_layers(x, cache)
-            if arr is not None:
+            got = self._batched_step_layers(x, cache, lt)
+            if got is not None:
+                arr, fold = got
                 normed = ops.decode_step_batched(arr, x, self.norm_f.weight, self.norm_f.eps, self.cfg, fold)
                 return self.lm_head(normed).unsqueeze(1)
-        if fold:
+        if self._fold_ok(x, cache):
             return self._step_folded(x, cache)
 
         def layer(i, xn):
@@ -765,57 +771,84 @@ class MambaLM(nn.Module):
                 inp = ops.add_rmsnorm(h, self._norm_weight(nl), self._eps(nl), y_parts=p, x_out=h)
         return self.lm_head(inp).unsqueeze(1)
 
-    def _batched_step_layers(self, x, cache):
-        """ctypes array of mtl_decode_layer for mtl_decode_step_batched (this
-        call's cache pointers filled in), or None when some layer would not
-        take the per-op path's in_proj + conv + x_proj launch and split
-        out_proj, or a weight or cache tensor is not a contiguous float32
-        tensor of its shape on x's device (the step then runs op by op, with
-        that path's checks and errors)."""
+    def _batched_step_layers(self, x, cache, lt=None):
+        """(ctypes array of mtl_decode_layer for mtl_decode_step_batched with
+        this call's cache pointers, whether the residual add + norm fold),
+        or None when some layer would not take the per-op path's in_proj +
+        conv + x_proj launch and split out_proj, or a weight or cache tensor
+        is not a contiguous float32 tensor of its shape on x's device (the
+        step then runs op by op, with that path's checks and errors).  The
+        weights are checked when their addresses (or x_proj's version, which
+        its transposed copy follows) change; the cache tensors every call.
+        The fold follows _fold_ok's rule, which on these layers reduces to
+        the row count and the out_proj tile."""
         cfg = self.cfg
+        nl = len(self.layers)
         if x.dim() != 2 or x.dtype != torch.float32 or not x.is_cuda or not x.is_contiguous() or \
-                x.data_ptr() % 16 or len(cache.layers) != len(self.layers):
+                x.data_ptr() % 16 or len(cache.layers) != nl:
             return None
         b, dm = x.shape
-        D, N, K = cfg.d_inner, cfg.d_state, cfg.d_conv
-        J = cfg.dt_rank + 2 * N
-        if b > ops.IN_CONV_MAX_ROWS or D % (128 * SKINNY_OUT_SPLIT) or N > 16 or cfg.dt_rank > 256:
+        D, N, K, R = cfg.d_inner, cfg.d_state, cfg.d_conv, cfg.dt_rank
+        if not (1 <= b <= ops.IN_CONV_MAX_ROWS and dm >= 256 and dm % 128 == 0 and D % (128 * SKINNY_OUT_SPLIT) == 0
+                and N <= 16 and R <= 256 and 2 <= K <= 4 and R + 2 * N <= 288):
             return None
         dev = x.device
-        ok = lambda t, shape: t is None or (t.device == dev and t.dtype == torch.float32 and t.is_contiguous()
-                                            and tuple(t.shape) == shape)
-        ws = []
-        for blk, lc in zip(self.layers, cache.layers):
-            mx = blk.mixer
-            if not ops.in_proj_conv_xproj_ok(x, mx.in_proj.weight, lc.conv_state, K, J):
-                return None
-            if not (ok(lc.ssm_state, (b, D, N)) and ok(mx.out_proj.weight, (dm, D)) and mx.out_proj.weight.data_ptr() % 16 == 0):
-                return None
-            conv_w = mx._conv_w()
-            tens = [blk.norm.weight, mx.in_proj.weight, mx.in_proj.bias, conv_w, mx.conv1d.bias, mx._xproj_t(),
-                    mx.dt_proj.weight, mx.dt_proj.bias, mx.A_log, mx.D, mx.out_proj.weight, mx.out_proj.bias]
-            shapes = [(dm,), (2 * D, dm), (2 * D,), (D, K), (D,), (D, J), (D, cfg.dt_rank), (D,), (D, N), (D,),
-                      (dm, D), (dm,)]
-            if not all(ok(t, s) for t, s in zip(tens, shapes)):
-                return None
-            ws.append(tens)
-        key = tuple(0 if t is None else t.data_ptr() for tens in ws for t in tens)
+        lt = self._layer_tensors() if lt is None else lt
+        sig = (dev, dm, tuple(0 if t is None else t.data_ptr() for ts in lt for t in ts),
+               tuple(ts[_LT_XPROJ]._version for ts in lt))
         cached = getattr(self, "_batched_tmpl", None)
-        if cached is None or cached[0] != key or cached[2] != dev:
-            tmpl = (_lib.DecodeLayer * len(self.layers))()
-            for i, L in enumerate(tmpl):
-                (L.norm_w, L.W_in, L.b_in, L.conv_w, L.conv_b, L.W_xT, L.W_dt, L.dt_bias, L.A_log, L.Dv, L.W_out,
-                 L.b_out) = key[12 * i:12 * i + 12]
-                L.eps = self.layers[i].norm.eps
-            cached = (key, tmpl, dev)
+        if cached is None or cached[0] != sig:
+            cached = (sig, self._batched_template(lt, dev, dm))
             self._batched_tmpl = cached
-        arr = type(cached[1]).from_buffer_copy(cached[1])   # per call: read by the library without the GIL
+        tmpl = cached[1]
+        if tmpl is None:
+            return None
+        cs_shape, hs_shape = (b, D, K - 1), (b, D, N)
+        for lc in cache.layers:
+            cs, hs = lc.conv_state, lc.ssm_state
+            if cs.dtype != torch.float32 or hs.dtype != torch.float32 or cs.shape != cs_shape or \
+                    hs.shape != hs_shape or not cs.is_contiguous() or not hs.is_contiguous() or cs.device != dev or \
+                    hs.device != dev or cs.data_ptr() % 16:
+                return None
+        arr = type(tmpl).from_buffer_copy(tmpl)   # per call: read by the library without the GIL
         for L, lc in zip(arr, cache.layers):
             L.conv_state, L.ssm_state = lc.conv_state.data_ptr(), lc.ssm_state.data_ptr()
-        return arr
+        rpb = ops.residual_rows_per_block(b, dm, SKINNY_OUT_SPLIT)
+        fold = STEP_NORM_FOLD and nl >= 2 and b <= min(32, STEP_NORM_FOLD_MAX_ROWS) and dm % rpb == 0 and \
+            dm // rpb <= 128
+        return arr, fold
+
+    def _batched_template(self, lt, dev, dm):
+        """The weight half of _batched_step_layers: mtl_decode_layer records
+        (W_xT = x_proj transposed, conv weights as [D, K] views), or None when
+        a weight is not a contiguous float32 tensor of its shape on dev or
+        in_proj / out_proj is not 16-byte aligned."""
+        cfg = self.cfg
+        D, N, K, R = cfg.d_inner, cfg.d_state, cfg.d_conv, cfg.dt_rank
+        ok = lambda t, shape: t.device == dev and t.dtype == torch.float32 and t.is_contiguous() and \
+            tuple(t.shape) == shape
+        opt = lambda t, shape: t is None or ok(t, shape)
+        tmpl = (_lib.DecodeLayer * len(lt))()
+        for i, (ts, L) in enumerate(zip(lt, tmpl)):
+            if not (ok(ts[_LT_NORM], (dm,)) and ok(ts[_LT_W_IN], (2 * D, dm)) and opt(ts[_LT_B_IN], (2 * D,))
+                    and ok(ts[_LT_CONV_W], (D, 1, K)) and opt(ts[_LT_CONV_B], (D,))
+                    and ok(ts[_LT_XPROJ], (R + 2 * N, D)) and ok(ts[_LT_W_DT], (D, R)) and ok(ts[_LT_B_DT], (D,))
+                    and ok(ts[_LT_A_LOG], (D, N)) and opt(ts[_LT_D], (D,)) and ok(ts[_LT_W_OUT], (dm, D))
+                    and opt(ts[_LT_B_OUT], (dm,))):
+                return None
+            if ts[_LT_W_IN].data_ptr() % 16 or ts[_LT_W_OUT].data_ptr() % 16:
+                return None
+            w_xt = self.layers[i].mixer._xproj_t()
+            ptr = lambda t: 0 if t is None else t.data_ptr()
+            (L.norm_w, L.W_in, L.b_in, L.conv_w, L.conv_b, L.W_xT, L.W_dt, L.dt_bias, L.A_log, L.Dv, L.W_out,
+             L.b_out) = (ptr(ts[_LT_NORM]), ptr(ts[_LT_W_IN]), ptr(ts[_LT_B_IN]), ptr(ts[_LT_CONV_W]),
+                         ptr(ts[_LT_CONV_B]), w_xt.data_ptr(), ptr(ts[_LT_W_DT]), ptr(ts[_LT_B_DT]),
+                         ptr(ts[_LT_A_LOG]), ptr(ts[_LT_D]), ptr(ts[_LT_W_OUT]), ptr(ts[_LT_B_OUT]))
+            L.eps = self.layers[i].norm.eps
+        return tmpl
 
     # ---- fused decode step ----
-    def _fused_step_ok(self, input_ids, cache) -> bool:
+    def _fused_step_ok(self, input_ids, cache, lt=None) -> bool:
         cfg = self.cfg
         b = input_ids.shape[0]
         if b not in (1, 2, 4) or b > FUSED_STEP_MAX_BATCH or cfg.d_state > 16 or cfg.d_model % 4 or \
@@ -829,9 +862,9 @@ class MambaLM(nn.Module):
                 lc.conv_state.is_contiguous() and lc.ssm_state.is_contiguous()):
             return False
         if DECODE_STEP_NATIVE:
-            plan = self._decode_plan()
+            plan = self._decode_plan(lt)
             split_k = b <= plan["split_k_max_b"]
-            if self._decode_step_template(plan, split_k, input_ids.device) is None:
+            if self._decode_step_template(plan, split_k, input_ids.device, lt) is None:
                 return False
         return True
 
@@ -854,13 +887,31 @@ class MambaLM(nn.Module):
                 raise ValueError(f"step: layer {i} ssm_state must be contiguous float32 {h_shape} on {device}, "
                                  f"got {tuple(hs.shape)} {hs.dtype} on {hs.device}")
 
-    def _derived_key(self):
+    def _layer_tensors(self):
+        """Per layer, the parameters a one-call decode step reads, in the
+        order _LT_* names: looked up through the modules' own dicts, not
+        nn.Module attribute access (an eager step reads ~300 of them, and
+        each attribute lookup through nn.Module costs ~0.2 us)."""
+        out = []
+        for blk in self.layers._modules.values():
+            bm = blk._modules
+            mx = bm["mixer"]
+            sub, mp = mx._modules, mx._parameters
+            ip, cv = sub["in_proj"]._parameters, sub["conv1d"]._parameters
+            xp, dp, op = sub["x_proj"]._parameters, sub["dt_proj"]._parameters, sub["out_proj"]._parameters
+            out.append((bm["norm"]._parameters["weight"], ip["weight"], ip.get("bias"), cv["weight"], cv.get("bias"),
+                        xp["weight"], dp["weight"], dp.get("bias"), mp["A_log"], mp["D"], op["weight"],
+                        op.get("bias")))
+        return out
+
+    def _derived_key(self, lt=None):
         """(address, version) of the parameters that derived weight copies are
         built from: the fused decode plan and the per-op step's transposed
         x_proj.  A captured graph reads those copies, so it is stale once
         this key changes."""
-        return tuple((m.mixer.x_proj.weight.data_ptr(), m.mixer.x_proj.weight._version,
-                      m.mixer.conv1d.weight.data_ptr(), m.mixer.conv1d.weight._version) for m in self.layers)
+        lt = self._layer_tensors() if lt is None else lt
+        return tuple((t[_LT_XPROJ].data_ptr(), t[_LT_XPROJ]._version, t[_LT_CONV_W].data_ptr(),
+                      t[_LT_CONV_W]._version) for t in lt)
 
     def _derived_tensors(self):
         """The derived copies a step reads now (held by a captured graph so a
@@ -871,11 +922,11 @@ class MambaLM(nn.Module):
             held += [getattr(m.mixer, "_xproj_cache", None), getattr(m.mixer, "_unit_conv_w", None)]
         return held
 
-    def _decode_plan(self):
+    def _decode_plan(self, lt=None):
         """Per-layer tensors of the fused step: x_proj transposed [D, J] for the
         split-K partials, conv weights as [D, K].  Rebuilt whenever a source
         parameter changes (tracked by tensor version and address)."""
-        key = self._derived_key()
+        key = self._derived_key(lt)
         plan = getattr(self, "_plan", None)
         if plan is not None and plan["key"] == key:
             return plan
@@ -933,18 +984,17 @@ class MambaLM(nn.Module):
             self._persist_ws = ws
         return t
 
-    def _decode_step_template(self, plan, split_k, device):
+    def _decode_step_template(self, plan, split_k, device, lt=None):
         """ctypes array of mtl_decode_layer with every layer's weight pointers
         (x_proj transposed from the decode plan with split_k, as is without),
         or None when a weight is not a contiguous float32 tensor on `device`
         (the step then runs op by op).  Rebuilt whenever any of those
         tensors' addresses change."""
         ws = []
-        for blk, lp in zip(self.layers, plan["layers"]):
-            mx = blk.mixer
-            ws += [blk.norm.weight, mx.in_proj.weight, mx.in_proj.bias, lp["conv_w"], mx.conv1d.bias,
-                   lp["W_xT"] if split_k else None, None if split_k else mx.x_proj.weight, mx.dt_proj.weight,
-                   mx.dt_proj.bias, mx.A_log, mx.D, mx.out_proj.weight, mx.out_proj.bias]
+        for t, lp in zip(self._layer_tensors() if lt is None else lt, plan["layers"]):
+            ws += [t[_LT_NORM], t[_LT_W_IN], t[_LT_B_IN], lp["conv_w"], t[_LT_CONV_B],
+                   lp["W_xT"] if split_k else None, None if split_k else t[_LT_XPROJ], t[_LT_W_DT], t[_LT_B_DT],
+                   t[_LT_A_LOG], t[_LT_D], t[_LT_W_OUT], t[_LT_B_OUT]]
         key = tuple(0 if t is None else t.data_ptr() for t in ws)
         cached = getattr(self, "_step_tmpl", {}).get(split_k)
         if cached is not None and cached[0] == key and cached[2] == device:
@@ -961,9 +1011,9 @@ class MambaLM(nn.Module):
         self._step_tmpl[split_k] = (key, arr, device)
         return arr
 
-    def _step_fused(self, input_ids, cache):
+    def _step_fused(self, input_ids, cache, lt=None):
         cfg = self.cfg
-        plan = self._decode_plan()
+        plan = self._decode_plan(lt)
         b, M, D, J = input_ids.shape[0], cfg.d_model, cfg.d_inner, plan["J"]
         split_k = b <= plan["split_k_max_b"]
         dev = input_ids.device
@@ -986,7 +1036,7 @@ class MambaLM(nn.Module):
         # than its grid (a partitioned GPU) runs the three-kernel step
         if DECODE_STEP_NATIVE and DECODE_PERSIST and b == 1 and 0 < plan["persist"] <= _cu_count(dev):
             self._check_step_cache(cache, b, dev)
-            tmpl = self._decode_step_template(plan, True, dev)
+            tmpl = self._decode_step_template(plan, True, dev, lt)
             tab = self._persist_table(tmpl, dev) if tmpl is not None else None
             wsp = self._persist_workspace(dev) if tab is not None else None
             if wsp is not None:
@@ -1000,7 +1050,7 @@ class MambaLM(nn.Module):
         if DECODE_STEP_NATIVE:
             self._check_step_cache(cache, b, dev)
             logits = torch.empty(b, self.embedding.weight.shape[0], **f32)
-            tmpl = self._decode_step_template(plan, split_k, dev)
+            tmpl = self._decode_step_template(plan, split_k, dev, lt)
             arr = type(tmpl).from_buffer_copy(tmpl)     # per call: read by the library without the GIL
             for L, lc in zip(arr, cache.layers):
                 L.conv_state, L.ssm_state = lc.conv_state.data_ptr(), lc.ssm_state.data_ptr()

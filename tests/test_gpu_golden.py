@@ -107,7 +107,7 @@ def test_lm_matches_reference_vectors(case, monkeypatch):
     fused = lm._fused_step_ok(_t(f["ids"][:, :1]), MambaCache.allocate(lm.cfg, batch, DEV, torch.float32))
     assert fused == (batch in (1, 2, 4) and cfg.get("d_conv", 4) >= 2)
     _check_lm(lm, f, plen, steps, "fused step" if fused else "per-op step")
-    monkeypatch.setattr(MambaLM, "_fused_step_ok", lambda self, ids, cache: False)
+    monkeypatch.setattr(MambaLM, "_fused_step_ok", lambda self, ids, cache, **kw: False)
     _check_lm(lm, f, plen, steps, "per-op step")
 
 

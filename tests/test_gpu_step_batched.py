@@ -134,7 +134,7 @@ def test_batched_step_is_taken_only_where_the_per_op_kernels_apply(monkeypatch):
     with torch.no_grad():
         x = lm.embedding(ids).squeeze(1)
         good = MambaCache.allocate(lm.cfg, 4, DEV, torch.float32)
-        assert lm._batched_step_layers(x, good) is not None
+        assert lm._batched_step_layers(x, good) is not None and lm._batched_step_layers(x, good)[1]
         half = MambaCache([type(lc)(lc.conv_state.bfloat16(), lc.ssm_state) for lc in good.layers])
         assert lm._batched_step_layers(x, half) is None
         wrong = MambaCache.allocate(lm.cfg, 8, DEV, torch.float32)
