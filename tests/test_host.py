@@ -268,6 +268,29 @@ def test_native_prefill_is_not_taken_off_the_gpu():
     assert not hasattr(model, "_short_plan")
 
 
+@pytest.mark.parametrize("bias,conv_bias", [(False, True), (True, False)])
+def test_layer_tensors_are_the_step_parameters_in_order(bias, conv_bias):
+    """MambaLM._layer_tensors() reads each layer's parameters through the
+    modules' dicts: the very parameter objects attribute access gives, in the
+    order of the _LT_* indices (the one-call steps build their weight
+    records from it), with absent biases as None; a replaced weight is
+    seen at once."""
+    import mamba_lite.model as mm
+    model = MambaLM(MambaConfig(d_model=64, n_layer=2, vocab_size=64, bias=bias, conv_bias=conv_bias))
+    for blk, lt in zip(model.layers, model._layer_tensors()):
+        mx = blk.mixer
+        want = {mm._LT_NORM: blk.norm.weight, mm._LT_W_IN: mx.in_proj.weight, mm._LT_B_IN: mx.in_proj.bias,
+                mm._LT_CONV_W: mx.conv1d.weight, mm._LT_CONV_B: mx.conv1d.bias, mm._LT_XPROJ: mx.x_proj.weight,
+                mm._LT_W_DT: mx.dt_proj.weight, mm._LT_B_DT: mx.dt_proj.bias, mm._LT_A_LOG: mx.A_log,
+                mm._LT_D: mx.D, mm._LT_W_OUT: mx.out_proj.weight, mm._LT_B_OUT: mx.out_proj.bias}
+        assert len(lt) == len(want) == 12
+        for k, t in want.items():
+            assert lt[k] is t, k
+        assert (lt[mm._LT_B_IN] is None) == (not bias) and (lt[mm._LT_CONV_B] is None) == (not conv_bias)
+    model.layers[1].mixer.out_proj.weight = torch.nn.Parameter(torch.zeros(64, 128))
+    assert model._layer_tensors()[1][mm._LT_W_OUT] is model.layers[1].mixer.out_proj.weight
+
+
 def test_persistent_decode_grid_query():
     """mtl_decode_persist_grid: the 130m shape takes 64 workgroups with the
     first blocking and 128 with the second; shapes outside the kernel's
