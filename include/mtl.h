@@ -279,7 +279,8 @@ int mtl_quant_dequant_sum_fp16(const float* const* parts, int32_t nparts, int64_
  * in_proj (model.py:261), out_proj (model.py:293) and the tied lm_head
  * (model.py:326, 353) in MambaMixer.step / MambaLM.step -- and of a prefill
  * of at most 64 tokens (model.py:197, 214, 240, 339).
- *   x: [M, K], row stride x_rs (>= K, multiple of 4), 1 <= M <= 64;
+ *   x: [M, K], row stride x_rs (>= K, multiple of 4), M >= 1: up to 64 rows
+ *      per launch chunk (a prefill's longer row counts run as 64-row chunks);
  *   W: [N, K] contiguous, N a multiple of 4; bias: [N] or NULL;
  *   y: [M, N] with row stride y_rs (>= N, multiple of 4).
  * K must be a multiple of 128 * ksplit.  With ksplit > 1 the K range is cut
@@ -431,6 +432,14 @@ int mtl_prefill_short(const mtl_prefill_short_args* args, const mtl_prefill_laye
  * created on the first call on a device.  After that a call allocates no
  * device memory and may be captured into a HIP graph.  Calls on one process
  * are serialized inside the library.  d_state <= 32, 1 <= d_conv <= 8.
+ * With b l <= skinny_rows (0: never) the projections run on mtl_linear_skinny
+ * instead (in 64-row chunks; x_proj as split-K parts summed by
+ * mtl_xproj_sum_dt, which also applies dt_proj; out_proj as 4 parts summed by
+ * mtl_add_rmsnorm_parts), where every operand fits it: d_model a multiple of
+ * 128, d_inner of 512, R + 2N of 4, dt_rank <= 160, xn, xz, u, y, blas_ws and
+ * every layer's W_in, b_in, W_x, W_out, b_out 16-byte aligned, and blas_ws
+ * holding (xs (R + 2N) + 4 d_model) b l floats for the parts (xs: the x_proj
+ * split, at most 16); otherwise the hipBLASLt form runs.
  * ---------------------------------------------------------------------- */
 typedef struct {
     float* h;
@@ -448,7 +457,7 @@ typedef struct {
     float eps_f;
     int32_t d_conv;
     int32_t n_layers;
-    int32_t reserved;
+    int32_t skinny_rows;       /* the projections on mtl_linear_skinny up to this many b l rows; 0: never */
     int64_t batch, seqlen, d_model, d_inner, d_state, dt_rank;
 } mtl_prefill_long_args;
 

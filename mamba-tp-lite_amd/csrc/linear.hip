@@ -188,26 +188,36 @@ __device__ __forceinline__ F4v tile_sum(const float* ring, int t, int& m, int& n
 template <int RB, int MB, int D>
 constexpr int ring_floats() { return kLinWaves * D * (16 * RB + 16 * MB) * kKW; }
 
+// blockIdx.z: the chunk of 16 MB rows of x (and y) this workgroup takes;
+// one chunk (z = 0, all M <= 16 MB rows) unless M is larger.  A chunk's
+// workgroups are those of the z = 0 launch with x and y moved down, so the
+// n-tiles of every chunk share the tile order and land on the same XCD as
+// their z = 0 twins when the tiles per chunk are a multiple of 8.
 template <int RB, int MB, int D>
 __global__ void __launch_bounds__(kLinThreads) linear_skinny_kernel(const LinArgs a) {
     __shared__ __align__(16) float ring[ring_floats<RB, MB, D>()];
     static_assert(sizeof(ring) >= sizeof(F4v) * kLinWaves * RB * MB * 64, "reduction space");
     const int n0 = blockIdx.x * 16 * RB, ks = blockIdx.y;
-    skinny_tile<RB, MB, D>(a, ring, n0, ks);
+    const int r0 = blockIdx.z * 16 * MB;
+    LinArgs c = a;
+    c.x += (int64_t)r0 * a.x_rs;
+    c.y += (int64_t)r0 * a.y_rs;
+    c.M = min(16 * MB, a.M - r0);
+    skinny_tile<RB, MB, D>(c, ring, n0, ks);
     for (int t = threadIdx.x; t < RB * MB * 64; t += kLinThreads) {
         int m, nl;
         F4v sum = tile_sum<RB, MB>(ring, t, m, nl);
         const int n = n0 + nl;
-        if (m < a.M && n < a.N) {
-            if (a.bias && ks == 0) sum += ld4(a.bias + n);
-            *reinterpret_cast<F4v*>(a.y + ks * a.y_ks + (int64_t)m * a.y_rs + n) = sum;
+        if (m < c.M && n < c.N) {
+            if (c.bias && ks == 0) sum += ld4(c.bias + n);
+            *reinterpret_cast<F4v*>(c.y + ks * c.y_ks + (int64_t)m * c.y_rs + n) = sum;
         }
     }
 }
 
 template <int RB, int MB>
 void launch_linear(const LinArgs& a, hipStream_t st) {
-    dim3 grid((unsigned)((a.N + 16 * RB - 1) / (16 * RB)), (unsigned)a.KS);
+    dim3 grid((unsigned)((a.N + 16 * RB - 1) / (16 * RB)), (unsigned)a.KS, (unsigned)((a.M + 16 * MB - 1) / (16 * MB)));
     // 64 rows of x: a 2-stage ring (80 KB of LDS at 16 W rows, 96 KB at 32)
     if constexpr (MB > 2)
         hipLaunchKernelGGL((linear_skinny_kernel<RB, MB, 2>), grid, dim3(kLinThreads), 0, st, a);
@@ -697,7 +707,7 @@ extern "C" int mtl_linear_skinny(const float* x, int64_t x_rs, const float* W, c
                                  int32_t rows_per_block, mtl_stream_t stream) {
     clear_error();
     MTL_REQUIRE(x && W && y, "null pointer");
-    MTL_REQUIRE(M >= 1 && M <= 64, "M (rows of x) must be in [1, 64]");
+    MTL_REQUIRE(M >= 1 && M <= 64 * 65535, "M (rows of x) must be in [1, 4194240]");
     MTL_REQUIRE(N >= 1 && N % 4 == 0 && N < (int64_t(1) << 31), "N must be a positive multiple of 4");
     MTL_REQUIRE(ksplit >= 1 && ksplit <= 64, "ksplit must be in [1, 64]");
     MTL_REQUIRE(K >= 1 && K % (int64_t(kKC) * ksplit) == 0 && K < (int64_t(1) << 31),

@@ -17,6 +17,15 @@
 //   -> out_proj GEMM (+ bias)                       out [rows, M]
 // and after the last layer the residual add + norm_f.
 //
+// Up to skinny_rows token rows (and where every operand fits them) the
+// projections run on the library's matrix-core skinny GEMM instead, in
+// 64-row chunks (mtl_linear_skinny): in_proj with its bias; x_proj as split-K
+// parts whose ordered sum also applies dt_proj (mtl_xproj_sum_dt); out_proj
+// as 4 split-K parts that the residual add + norm sums (mtl_add_rmsnorm_parts)
+// -- the short prompt's launches with the conv as its own kernel, because a
+// conv over more than 64 rows crosses the in_proj tiles.  The parts live in
+// blas_ws, which the skinny form does not otherwise use.
+//
 // The GEMMs are hipBLASLt matmuls, fp32 in and out, fp32 compute.  For each
 // shape the heuristic's first algorithm is looked up once per device and
 // kept (descriptors and algorithm), so a call costs the launches only; the
@@ -126,6 +135,21 @@ int gemm(int dev, const float* W, int64_t ldw, const float* X, int64_t ldx, floa
     return MTL_OK;
 }
 
+// the largest split of K into whole 128-column granules, at most `most` parts
+int32_t split_of(int64_t K, int32_t most) {
+    const int64_t g = K / 128;
+    int32_t best = 1;
+    for (int32_t p = 1; p <= most && p <= g; ++p)
+        if (g % p == 0) best = p;
+    return best;
+}
+
+// rows_per_block of mtl_linear_skinny for M rows (the Python layer's rule):
+// 32-row weight tiles only at 17..32 rows of x where every CU still gets one
+int32_t rows_per_block_of(int64_t M, int64_t N, int32_t ksplit) {
+    return (M > 16 && M <= 32 && (N + 31) / 32 * ksplit >= 256) ? 32 : 16;
+}
+
 }  // namespace
 
 extern "C" int mtl_prefill_long(const mtl_prefill_long_args* a, const mtl_prefill_layer* layers,
@@ -154,6 +178,21 @@ extern "C" int mtl_prefill_long(const mtl_prefill_long_args* a, const mtl_prefil
         MTL_REQUIRE(K == 1 || L.conv_state_in != L.conv_state_out,
                     "layer " + std::to_string(i) + ": conv_state_out must not alias conv_state_in");
     }
+    // the skinny form: sizes and alignments the skinny GEMMs and the fused
+    // x_proj sum + dt_proj take, on every layer, and room for the parts
+    constexpr int32_t kOutSplit = 4;
+    const int32_t xs = split_of(D, 16);
+    auto al16 = [](const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; };
+    bool skinny = a->skinny_rows > 0 && rows <= a->skinny_rows && M % 128 == 0 && D % (128 * kOutSplit) == 0 &&
+                  J % 4 == 0 && R <= 160 && al16(a->xn) && al16(a->u) && al16(a->y) && al16(a->xz) &&
+                  al16(a->blas_ws) &&
+                  (int64_t)(xs * J + kOutSplit * M) * rows * (int64_t)sizeof(float) <= a->blas_ws_bytes;
+    for (int32_t i = 0; skinny && i < a->n_layers; ++i) {
+        const mtl_prefill_layer& L = layers[i];
+        skinny = al16(L.W_in) && al16(L.b_in) && al16(L.W_x) && al16(L.W_out) && al16(L.b_out);
+    }
+    float* x_parts = static_cast<float*>(a->blas_ws);                 // [xs, rows, J]
+    float* y_parts = x_parts + (int64_t)xs * rows * J;                 // [4, rows, M]
     hipStream_t st = as_stream(stream);
     int dev = 0;
     if (hipStreamGetDevice(st, &dev) != hipSuccess) {
@@ -167,7 +206,11 @@ extern "C" int mtl_prefill_long(const mtl_prefill_long_args* a, const mtl_prefil
     if (rc) return rc;
     for (int32_t i = 0; i < a->n_layers; ++i) {
         const mtl_prefill_layer& L = layers[i];
-        rc = gemm(dev, L.W_in, M, a->xn, M, a->xz, 2 * D, L.b_in, 2 * D, rows, M, ws, wsb, st);
+        if (skinny)
+            rc = mtl_linear_skinny(a->xn, M, L.W_in, L.b_in, a->xz, 2 * D, 0, rows, 2 * D, M, 1,
+                                   rows_per_block_of(rows, 2 * D, 1), stream);
+        else
+            rc = gemm(dev, L.W_in, M, a->xn, M, a->xz, 2 * D, L.b_in, 2 * D, rows, M, ws, wsb, st);
         if (rc) return rc;
         // [b, D, l] views of the [b l, 2D] and [b l, D] buffers
         mtl_conv_params c{};
@@ -179,27 +222,47 @@ extern "C" int mtl_prefill_long(const mtl_prefill_long_args* a, const mtl_prefil
         c.batch = b; c.seqlen = l; c.dim = D; c.width = K; c.dtype = MTL_F32; c.silu = 1;
         rc = mtl_causal_conv1d_fwd(&c, stream);
         if (rc) return rc;
-        rc = gemm(dev, L.W_x, D, a->u, D, a->x_dbl, J, nullptr, J, rows, D, ws, wsb, st);
-        if (rc) return rc;
-        rc = gemm(dev, L.W_dt, R, a->x_dbl, J, a->dt, D, nullptr, D, rows, R, ws, wsb, st);
-        if (rc) return rc;
+        const float* x_dbl = a->x_dbl;
+        if (skinny) {
+            rc = mtl_linear_skinny(a->u, D, L.W_x, nullptr, x_parts, J, rows * J, rows, J, D, xs,
+                                   rows_per_block_of(rows, J, xs), stream);
+            if (rc) return rc;
+            rc = mtl_xproj_sum_dt(x_parts, xs, rows, (int32_t)J, L.W_dt, (int32_t)R, D, xs > 1 ? a->x_dbl : nullptr,
+                                  a->dt, stream);
+            if (rc) return rc;
+            if (xs == 1) x_dbl = x_parts;
+        } else {
+            rc = gemm(dev, L.W_x, D, a->u, D, a->x_dbl, J, nullptr, J, rows, D, ws, wsb, st);
+            if (rc) return rc;
+            rc = gemm(dev, L.W_dt, R, a->x_dbl, J, a->dt, D, nullptr, D, rows, R, ws, wsb, st);
+            if (rc) return rc;
+        }
         mtl_scan_params p{};
         p.u = a->u;          p.u_sb = l * D;       p.u_sd = 1; p.u_sl = D;
         p.delta = a->dt;     p.delta_sb = l * D;   p.delta_sd = 1; p.delta_sl = D;
         p.z = a->xz + D;     p.z_sb = l * 2 * D;   p.z_sd = 1; p.z_sl = 2 * D;
-        p.B = a->x_dbl + R;  p.B_sb = l * J;       p.B_sn = 1; p.B_sl = J;
-        p.C = a->x_dbl + R + N; p.C_sb = l * J;    p.C_sn = 1; p.C_sl = J;
+        p.B = x_dbl + R;     p.B_sb = l * J;       p.B_sn = 1; p.B_sl = J;
+        p.C = x_dbl + R + N; p.C_sb = l * J;       p.C_sn = 1; p.C_sl = J;
         p.y = a->y;          p.y_sb = l * D;       p.y_sd = 1; p.y_sl = D;
         p.A = L.A_log; p.D = L.Dv; p.delta_bias = L.dt_bias; p.h0 = L.h0; p.h_out = L.h_out;
         p.batch = b; p.seqlen = l; p.dim = D; p.dstate = N;
         p.dtype = MTL_F32; p.delta_softplus = 1; p.a_is_log = 1; p.algo = 0;
         rc = mtl_selective_scan_fwd(&p, stream);
         if (rc) return rc;
-        rc = gemm(dev, L.W_out, D, a->y, D, a->out, M, L.b_out, M, rows, D, ws, wsb, st);
-        if (rc) return rc;
         const bool last = i + 1 == a->n_layers;
-        rc = mtl_add_rmsnorm(a->h, a->out, a->h, last ? a->norm_f : layers[i + 1].norm_w,
-                             last ? a->normed_out : a->xn, rows, M, last ? a->eps_f : layers[i + 1].eps, stream);
+        const float* w_next = last ? a->norm_f : layers[i + 1].norm_w;
+        float* normed = last ? a->normed_out : a->xn;
+        const float eps = last ? a->eps_f : layers[i + 1].eps;
+        if (skinny) {
+            rc = mtl_linear_skinny(a->y, D, L.W_out, L.b_out, y_parts, M, rows * M, rows, M, D, kOutSplit,
+                                   rows_per_block_of(rows, M, kOutSplit), stream);
+            if (rc) return rc;
+            rc = mtl_add_rmsnorm_parts(a->h, y_parts, kOutSplit, a->h, w_next, normed, rows, M, eps, stream);
+        } else {
+            rc = gemm(dev, L.W_out, D, a->y, D, a->out, M, L.b_out, M, rows, D, ws, wsb, st);
+            if (rc) return rc;
+            rc = mtl_add_rmsnorm(a->h, a->out, a->h, w_next, normed, rows, M, eps, stream);
+        }
         if (rc) return rc;
     }
     return MTL_OK;

@@ -78,7 +78,7 @@ class PrefillLongArgs(ctypes.Structure):
     _fields_ = [
         ("h", _vp), ("xn", _vp), ("xz", _vp), ("u", _vp), ("x_dbl", _vp), ("dt", _vp), ("y", _vp), ("out", _vp),
         ("blas_ws", _vp), ("blas_ws_bytes", _i64), ("norm_f", _vp), ("normed_out", _vp),
-        ("eps_f", ctypes.c_float), ("d_conv", _i32), ("n_layers", _i32), ("reserved", _i32),
+        ("eps_f", ctypes.c_float), ("d_conv", _i32), ("n_layers", _i32), ("skinny_rows", _i32),
         ("batch", _i64), ("seqlen", _i64), ("d_model", _i64), ("d_inner", _i64), ("d_state", _i64),
         ("dt_rank", _i64),
     ]

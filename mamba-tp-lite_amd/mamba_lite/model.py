@@ -162,6 +162,17 @@ SHORT_PREFILL_NATIVE = True
 # differ from the per-op path's by float rounding.
 LONG_PREFILL_NATIVE = True
 LONG_PREFILL_MAX_ELEMS = 1 << 21
+# Up to LONG_PREFILL_SKINNY_ROWS token rows, at widths up to
+# LONG_PREFILL_SKINNY_MAX_D_MODEL, the one-call long prefill runs its
+# projections on the library's skinny GEMM (64-row chunks) instead of
+# hipBLASLt.  Eager prompts, skinny against hipBLASLt, one run: mamba-130m
+# width 65 tokens 1199 against 1452 us, 128 tokens 1278 against 1498, 192
+# tokens 1566 against 1727, 256 tokens 1700 against 1679, 512 tokens 2738
+# against 2369; mamba-1.4b width 65 tokens 5978 against 4387 us, slower at
+# every length (each further 64-row chunk streams the 67 MB in_proj weight
+# again).
+LONG_PREFILL_SKINNY_ROWS = 192
+LONG_PREFILL_SKINNY_MAX_D_MODEL = 1024
 
 # The fused decode step (fp32, batch 1 and 2) runs its whole layer stack as
 # one C call (mtl_decode_step) launching the same kernels with the same
@@ -680,8 +691,12 @@ class MambaLM(nn.Module):
             L.h0 = lc.ssm_state.data_ptr() if lc is not None else None   # h_out may be h0
             L.h_out = h_out.data_ptr()
         h = self.embedding(input_ids).contiguous()
-        run = ops.prefill_short if kind == "short" else ops.prefill_long
-        normed = run(h, arr, self.norm_f.weight, self.norm_f.eps, D, N, cfg.dt_rank, K)
+        if kind == "short":
+            normed = ops.prefill_short(h, arr, self.norm_f.weight, self.norm_f.eps, D, N, cfg.dt_rank, K)
+        else:
+            skinny = LONG_PREFILL_SKINNY_ROWS if cfg.d_model <= LONG_PREFILL_SKINNY_MAX_D_MODEL else 0
+            normed = ops.prefill_long(h, arr, self.norm_f.weight, self.norm_f.eps, D, N, cfg.dt_rank, K,
+                                      skinny_rows=skinny)
         return self.lm_head(normed), (out_cache if out_cache is not None else MambaCache(new_layers))
 
     def step(self, input_ids: torch.Tensor, cache: MambaCache):

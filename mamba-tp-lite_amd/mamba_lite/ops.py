@@ -556,12 +556,14 @@ def prefill_short(h, layers, norm_f, eps_f, d_inner, d_state, dt_rank, d_conv):
 PREFILL_LONG_BLAS_WS = 32 << 20     # bytes of hipBLASLt workspace per mtl_prefill_long call
 
 
-def prefill_long(h, layers, norm_f, eps_f, d_inner, d_state, dt_rank, d_conv):
+def prefill_long(h, layers, norm_f, eps_f, d_inner, d_state, dt_rank, d_conv, skinny_rows=0):
     """mtl_prefill_long: a prompt's whole layer stack in one call (any
-    length, the projections on hipBLASLt).  h [b, l, d_model] float32 holds
-    the embedded tokens and is overwritten with the final residual stream;
-    `layers` is a ctypes array of _lib.PrefillLayer (weights plus this call's
-    cache pointers).  Returns norm_f(h) [b, l, d_model]."""
+    length, the projections on hipBLASLt; up to skinny_rows token rows on
+    the library's skinny GEMM where the shapes fit it).  h [b, l, d_model]
+    float32 holds the embedded tokens and is overwritten with the final
+    residual stream; `layers` is a ctypes array of _lib.PrefillLayer
+    (weights plus this call's cache pointers).  Returns norm_f(h)
+    [b, l, d_model]."""
     _f32c(h, "h")
     _f32c(norm_f, "norm_f")
     b, l, M = h.shape
@@ -581,7 +583,7 @@ def prefill_long(h, layers, norm_f, eps_f, d_inner, d_state, dt_rank, d_conv):
     a.xn, a.xz, a.u, a.x_dbl, a.dt, a.y, a.out, a.blas_ws = [base + 4 * o for o in offs]
     a.blas_ws_bytes = PREFILL_LONG_BLAS_WS
     a.norm_f, a.normed_out, a.eps_f = norm_f.data_ptr(), normed.data_ptr(), float(eps_f)
-    a.d_conv, a.n_layers = d_conv, len(layers)
+    a.d_conv, a.n_layers, a.skinny_rows = d_conv, len(layers), int(skinny_rows)
     a.batch, a.seqlen, a.d_model, a.d_inner, a.d_state, a.dt_rank = b, l, M, d_inner, d_state, dt_rank
     with _dev_guard(h):
         _lib.check(_lib.load().mtl_prefill_long(ctypes.byref(a), layers, _stream(h)), "prefill_long")
@@ -825,19 +827,21 @@ def decode_gemv(v, W, out, bias=None, x_in=None):
     return out
 
 
-SKINNY_MAX_ROWS = 64     # mtl_linear_skinny: rows of x
+SKINNY_MAX_ROWS = 64     # mtl_linear_skinny: rows of x per launch chunk
+SKINNY_CHUNKED_MAX_ROWS = 64 * 65535   # rows of x over all chunks
 IN_CONV_MAX_ROWS = 32    # mtl_in_proj_conv_xproj: batch rows
 
 
-def linear_skinny_ok(x, W) -> bool:
-    """Whether mtl_linear_skinny takes y = x W^T for these operands: fp32 on
-    the GPU, 1..64 rows of x, K a multiple of 128, W rows a multiple of 4,
-    16-byte aligned rows."""
+def linear_skinny_ok(x, W, max_rows=SKINNY_MAX_ROWS) -> bool:
+    """Whether mtl_linear_skinny takes y = x W^T for these operands in one
+    chunk (or, with max_rows, in 64-row chunks): fp32 on the GPU, 1..64
+    rows of x, K a multiple of 128, W rows a multiple of 4, 16-byte aligned
+    rows."""
     if x.dim() != 2 or W.dim() != 2 or x.dtype != torch.float32 or W.dtype != torch.float32:
         return False
     M, K = x.shape
     N = W.shape[0]
-    return (x.is_cuda and W.is_cuda and 1 <= M <= SKINNY_MAX_ROWS and W.shape[1] == K and K % 128 == 0
+    return (x.is_cuda and W.is_cuda and 1 <= M <= max_rows and W.shape[1] == K and K % 128 == 0
             and N % 4 == 0 and x.stride(1) == 1 and x.stride(0) % 4 == 0 and W.is_contiguous()
             and x.data_ptr() % 16 == 0 and W.data_ptr() % 16 == 0)
 
@@ -845,11 +849,11 @@ def linear_skinny_ok(x, W) -> bool:
 def linear_skinny(x, W, bias=None, out=None, ksplit=1, rows_per_block=None):
     """mtl_linear_skinny: out [M, N] = x [M, K] . W [N, K]^T (+ bias) on the
     matrix cores, for M <= 64 (the projections of a batched decode step,
-    and of a prefill of at most 64 tokens).
+    and of a prefill of at most 64 tokens), larger M in 64-row chunks.
     With ksplit > 1, out is [ksplit, M, N]: the partial products over K
     split into ksplit equal ranges (bias in part 0), to be added in order."""
-    if not linear_skinny_ok(x, W):
-        raise ValueError("linear_skinny: fp32 x [M<=64, K%128==0] (unit column stride, 16B rows) and contiguous "
+    if not linear_skinny_ok(x, W, SKINNY_CHUNKED_MAX_ROWS):
+        raise ValueError("linear_skinny: fp32 x [M, K%128==0] (unit column stride, 16B rows) and contiguous "
                          "W [N%4==0, K] expected")
     M, K = x.shape
     N = W.shape[0]

@@ -110,7 +110,7 @@ def test_invalid_arguments_are_rejected_without_a_gpu():
     ("mtl_decode_gemv_parts", dict(cols=4100, nparts=4), b"multiple of 4 * nparts"),
     ("mtl_decode_gemv_parts", dict(cols=8192 * 4, nparts=4), b"at most 4096"),
     ("mtl_decode_gemv_parts", dict(batch=3), b"batch must be 1, 2 or 4"),
-    ("mtl_linear_skinny", dict(M=65), b"M (rows of x)"),
+    ("mtl_linear_skinny", dict(M=64 * 65535 + 1), b"M (rows of x)"),
     ("mtl_in_proj_conv_prefill", dict(batch=5, seqlen=13), b"batch * seqlen"),
     ("mtl_in_proj_conv_prefill", dict(d_conv=5), b"d_conv"),
     ("mtl_in_proj_conv_prefill", dict(d_inner=40), b"multiple of 16"),

@@ -90,3 +90,31 @@ def test_xproj_sum_dt_vs_float64(P, rows, J, R, D):
     if P == 1:
         x1, dt1 = ops.xproj_sum_dt(parts, W_dt, write_x_dbl=False)
         assert x1.data_ptr() == parts.data_ptr() and torch.equal(dt1, dt)
+
+
+@pytest.mark.parametrize("M,N,K,ks", [(65, 3072, 768, 1), (128, 768, 1536, 4), (200, 80, 1536, 12),
+                                      (256, 8192, 2048, 1), (129, 2048, 4096, 4), (300, 160, 4096, 16),
+                                      (64 * 9 + 5, 1000, 384, 3)])
+@pytest.mark.parametrize("rows_per_block", [16, 32])
+def test_linear_skinny_row_chunks(M, N, K, ks, rows_per_block):
+    """Past 64 rows of x the rows run as 64-row chunks of one launch: each
+    chunk's outputs (every split-K part, bias in part 0) equal a launch over
+    that chunk's rows alone bit for bit, and the whole is within 1e-5 of the
+    float64 product.  x rows strided (a view of a wider tensor)."""
+    print(f"\n[linear_skinny chunks M={M} N={N} K={K} ksplit={ks} rpb={rows_per_block}]", flush=True)
+    g = torch.Generator(device=DEV).manual_seed(M + N + K + ks)
+    x = torch.randn(M, K + 64, device=DEV, generator=g)[:, 8:8 + K]
+    W = torch.randn(N, K, device=DEV, generator=g) / K ** 0.5
+    bias = torch.randn(N, device=DEV, generator=g)
+    y = ops.linear_skinny(x, W, bias, ksplit=ks, rows_per_block=rows_per_block)
+    parts = y.view(ks, M, N)
+    for r0 in range(0, M, 64):
+        xc = x[r0:r0 + 64]
+        rpb = rows_per_block if xc.shape[0] > 32 else 16   # 32-row tiles at <= 32 rows pick other MFMA blocks
+        alone = ops.linear_skinny(xc, W, bias, ksplit=ks, rows_per_block=rpb).view(ks, xc.shape[0], N)
+        if xc.shape[0] > 32:
+            assert torch.equal(parts[:, r0:r0 + 64], alone), f"chunk at row {r0}"
+        else:
+            assert_rel(parts[:, r0:r0 + 64].cpu().numpy(), alone.cpu().numpy(), TOL, f"chunk at row {r0}")
+    full = ops.sum_parts(parts) if ks > 1 else y
+    assert_rel(full.cpu().numpy(), _ref(x, W, bias), TOL, "y")

@@ -13,7 +13,9 @@ short-prompt limit, on the GPU (model.py:184-241, 303-306, 328-341):
   * which prompts take it (more than 64 tokens, or a shape the short path
     does not take, up to LONG_PREFILL_MAX_ELEMS token-channels);
   * two threads prefilling on their own streams at once get what each would
-    alone, bit for bit."""
+    alone, bit for bit;
+  * up to LONG_PREFILL_SKINNY_ROWS rows, the projections on the skinny GEMM
+    against the same call's hipBLASLt form and the oracle."""
 import numpy as np
 import pytest
 import torch
@@ -165,3 +167,39 @@ def test_concurrent_long_prefills_on_two_streams():
     torch.cuda.synchronize()
     for i in range(2):
         assert torch.equal(got[i], alone[i]), f"thread {i} differs"
+
+
+@pytest.mark.parametrize("b,l,d_model,n_layer,kw", [
+    (1, 65, 768, 2, {}), (1, 256, 768, 2, {}), (3, 50, 256, 3, dict(bias=True)), (1, 130, 2048, 1, dict(dt_rank=128)),
+    (2, 100, 256, 2, dict(d_conv=3, d_state=8)), (1, 200, 512, 2, dict(d_state=32))])
+def test_long_prefill_skinny_projections(b, l, d_model, n_layer, kw, monkeypatch):
+    """Up to LONG_PREFILL_SKINNY_ROWS token rows (raised here, and the width
+    limit with it, to reach every case) the one call runs its projections on
+    the skinny GEMM in 64-row chunks (x_proj as split-K parts
+    summed with dt_proj applied, out_proj as parts summed by the residual
+    norm): logits and states within 3e-5 of the same call's hipBLASLt form
+    and within 1e-4 of the float64 oracle; the two forms round differently,
+    so their logits differ in some bit (both forms ran)."""
+    import mamba_lite.model as mm
+    print(f"\n[prefill long skinny b={b} l={l} d_model={d_model} layers={n_layer} {kw}]", flush=True)
+    vocab = 512
+    lm, W = _lm(200 + b + l + d_model, d_model, n_layer, vocab, **kw)
+    calls = _counting(monkeypatch)
+    ids = np.random.default_rng(b * 11 + l).integers(0, vocab, (b, l), dtype=np.int64)
+    with torch.no_grad():
+        monkeypatch.setattr(mm, "LONG_PREFILL_SKINNY_ROWS", 4096)
+        monkeypatch.setattr(mm, "LONG_PREFILL_SKINNY_MAX_D_MODEL", 4096)
+        logits, cache = lm.prefill(_t(ids))
+        monkeypatch.setattr(mm, "LONG_PREFILL_SKINNY_ROWS", 0)
+        ref_logits, ref_cache = lm.prefill(_t(ids))
+    assert calls == [1, 1], "the prompt did not take mtl_prefill_long"
+    assert not torch.equal(logits, ref_logits), "the skinny form did not run"
+    o_logits, o_cache = om.lm_prefill(W, ids, dtype=np.float64)
+    assert_rel(_n(logits), o_logits, 1e-4, "logits vs oracle")
+    # two fp32 forms of the same sums, rounded differently and carried through
+    # the recurrence: 3e-5 between them, the oracle's 1e-4 for each
+    assert_rel(_n(logits), _n(ref_logits), 3e-5, "logits vs the hipBLASLt form")
+    for i, (lc, rc, (oc, oh)) in enumerate(zip(cache.layers, ref_cache.layers, o_cache)):
+        assert_rel(_n(lc.ssm_state), oh, 1e-4, f"layer {i} ssm_state vs oracle")
+        assert_rel(_n(lc.conv_state), oc, 1e-4, f"layer {i} conv_state vs oracle")
+        assert_rel(_n(lc.ssm_state), _n(rc.ssm_state), 3e-5, f"layer {i} ssm_state vs the hipBLASLt form")
