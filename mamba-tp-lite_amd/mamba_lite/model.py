@@ -810,7 +810,7 @@ class MambaLM(nn.Module):
         dev = x.device
         lt = self._layer_tensors() if lt is None else lt
         sig = (dev, dm, tuple(0 if t is None else t.data_ptr() for ts in lt for t in ts),
-               tuple(ts[_LT_XPROJ]._version for ts in lt))
+               tuple(ts[_LT_XPROJ]._version for ts in lt), self._norm_eps())
         cached = getattr(self, "_batched_tmpl", None)
         if cached is None or cached[0] != sig:
             cached = (sig, self._batched_template(lt, dev, dm))
@@ -919,6 +919,10 @@ class MambaLM(nn.Module):
                         op.get("bias")))
         return out
 
+    def _norm_eps(self):
+        """Every block norm's eps (the weight records carry them)."""
+        return tuple(blk._modules["norm"].eps for blk in self.layers._modules.values())
+
     def _derived_key(self, lt=None):
         """(address, version) of the parameters that derived weight copies are
         built from: the fused decode plan and the per-op step's transposed
@@ -1010,7 +1014,7 @@ class MambaLM(nn.Module):
             ws += [t[_LT_NORM], t[_LT_W_IN], t[_LT_B_IN], lp["conv_w"], t[_LT_CONV_B],
                    lp["W_xT"] if split_k else None, None if split_k else t[_LT_XPROJ], t[_LT_W_DT], t[_LT_B_DT],
                    t[_LT_A_LOG], t[_LT_D], t[_LT_W_OUT], t[_LT_B_OUT]]
-        key = tuple(0 if t is None else t.data_ptr() for t in ws)
+        key = tuple(0 if t is None else t.data_ptr() for t in ws) + self._norm_eps()
         cached = getattr(self, "_step_tmpl", {}).get(split_k)
         if cached is not None and cached[0] == key and cached[2] == device:
             return cached[1]

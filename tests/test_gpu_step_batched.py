@@ -142,3 +142,33 @@ def test_batched_step_is_taken_only_where_the_per_op_kernels_apply(monkeypatch):
         with pytest.raises(ValueError):
             lm.step(ids, wrong)
     assert calls == []
+
+
+@pytest.mark.parametrize("b", [1, 8])
+def test_a_changed_norm_eps_reaches_the_one_call_steps(b, monkeypatch):
+    """The one-call steps keep their weight records between calls (the fused
+    one at b = 1, the batched one at b = 8); a block norm's eps changed after
+    a step is in the next one: it equals the per-op step bit for bit."""
+    import mamba_lite.model as mm
+    print(f"\n[one-call steps: changed norm eps b={b}]", flush=True)
+    lm, _ = _lm(160 + b, 256, 2, 512)
+    rng = np.random.default_rng(b + 9)
+    ids = _t(rng.integers(0, 512, (b, 5), dtype=np.int64))
+    steps = [_t(rng.integers(0, 512, (b, 1), dtype=np.int64)) for _ in range(2)]
+
+    def per_op(s, cache):
+        monkeypatch.setattr(mm, "BATCHED_STEP_NATIVE", False)
+        monkeypatch.setattr(mm, "DECODE_STEP_NATIVE", False)
+        out = lm.step(s, cache)
+        monkeypatch.setattr(mm, "BATCHED_STEP_NATIVE", True)
+        monkeypatch.setattr(mm, "DECODE_STEP_NATIVE", True)
+        return out
+
+    with torch.no_grad():
+        _, c_nat = lm.prefill(ids)
+        _, c_per = lm.prefill(ids)
+        assert torch.equal(lm.step(steps[0], c_nat), per_op(steps[0], c_per))
+        lm.layers[1].norm.eps = 3e-2
+        got = lm.step(steps[1], c_nat)
+        want = per_op(steps[1], c_per)
+    assert torch.equal(got, want), "the changed eps did not reach the one-call step"
