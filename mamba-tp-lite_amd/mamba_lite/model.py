@@ -616,15 +616,11 @@ class MambaLM(nn.Module):
     def _short_prefill_plan(self):
         """ctypes array of mtl_prefill_layer holding every layer's weight
         pointers, or None when a weight is not a contiguous float32 GPU
-        tensor.  Rebuilt whenever any weight tensor's address changes."""
-        ws = []
-        for blk in self.layers:
-            mx = blk.mixer
-            ws += [blk.norm.weight, mx.in_proj.weight, mx.in_proj.bias, mx.conv1d.weight, mx.conv1d.bias,
-                   mx.x_proj.weight, mx.dt_proj.weight, mx.dt_proj.bias, mx.A_log, mx.D, mx.out_proj.weight,
-                   mx.out_proj.bias]
+        tensor.  Rebuilt whenever any weight tensor's address or a block
+        norm's eps changes."""
+        ws = [t for lt in self._layer_tensors() for t in lt]     # 12 per layer, in mtl_prefill_layer's order
         ws.append(self.norm_f.weight)
-        key = tuple(0 if t is None else t.data_ptr() for t in ws)
+        key = tuple(0 if t is None else t.data_ptr() for t in ws) + self._norm_eps()
         plan = getattr(self, "_short_plan", None)
         if plan is not None and plan[0] == key:
             return plan[1]

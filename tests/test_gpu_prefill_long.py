@@ -203,3 +203,26 @@ def test_long_prefill_skinny_projections(b, l, d_model, n_layer, kw, monkeypatch
         assert_rel(_n(lc.ssm_state), oh, 1e-4, f"layer {i} ssm_state vs oracle")
         assert_rel(_n(lc.conv_state), oc, 1e-4, f"layer {i} conv_state vs oracle")
         assert_rel(_n(lc.ssm_state), _n(rc.ssm_state), 3e-5, f"layer {i} ssm_state vs the hipBLASLt form")
+
+
+@pytest.mark.parametrize("l", [40, 100])
+def test_a_changed_norm_eps_reaches_the_one_call_prefill(l, monkeypatch):
+    """The one-call prefills (the short one at 40 tokens, the long one at
+    100) keep their weight records between calls; a block norm's eps changed
+    after a prompt is in the next one: it matches the per-op prefill with
+    the new eps (1e-5) and differs from the prompt before the change."""
+    import mamba_lite.model as mm
+    print(f"\n[prefill: changed norm eps l={l}]", flush=True)
+    lm, _ = _lm(170 + l, 256, 2, 512)
+    calls = _counting(monkeypatch)
+    ids = _t(np.random.default_rng(l).integers(0, 512, (1, l), dtype=np.int64))
+    with torch.no_grad():
+        before, _ = lm.prefill(ids)
+        lm.layers[1].norm.eps = 3e-2
+        logits, _ = lm.prefill(ids)
+        monkeypatch.setattr(mm, "SHORT_PREFILL_NATIVE", False)
+        monkeypatch.setattr(mm, "LONG_PREFILL_NATIVE", False)
+        ref, _ = lm.prefill(ids)
+    assert len(calls) == (2 if l > 64 else 0)
+    assert not torch.equal(logits, before)
+    assert_rel(_n(logits), _n(ref), 1e-5, "logits with the new eps vs per-op")
