@@ -10,6 +10,10 @@ and MambaMixer.step 249-294):
   * the same steps against the float64 oracle (1e-4, the fp32 tolerance);
   * a captured GraphedStepper replays the eager bits, with eager work
     between replays;
+  * 24 seeded random shapes it takes (widths 256-1024, d_inner multiples of
+    512, 1-16 states, d_conv 2-4, dt_rank, biases, 1-3 layers, 3-32 rows)
+    against the per-op step bit for bit and the oracle at 1e-4;
+  * a block norm's eps changed between steps reaches the next one;
   * the model takes it only where every layer runs the per-op step's in_proj
     + conv + x_proj launch and split out_proj; elsewhere the per-op path runs,
     with its own checks (a cache of the wrong batch still raises
@@ -172,3 +176,52 @@ def test_a_changed_norm_eps_reaches_the_one_call_steps(b, monkeypatch):
         got = lm.step(steps[1], c_nat)
         want = per_op(steps[1], c_per)
     assert torch.equal(got, want), "the changed eps did not reach the one-call step"
+
+
+def _draw(seed):
+    """A random model shape the one-call batched step takes: d_model a
+    multiple of 128 from 256, d_inner a multiple of 512, d_state up to 16,
+    d_conv 2..4, dt_rank with dt_rank + 2 d_state <= 288, biases on or off,
+    1-3 layers, 3-32 rows."""
+    r = np.random.default_rng(seed)
+    d_model = int(r.choice([256, 384, 512, 768, 1024]))
+    expand = int(r.choice([e for e in (1, 2, 3, 4) if (e * d_model) % 512 == 0]))
+    d_state = int(r.choice([1, 4, 8, 12, 16]))
+    cfg = dict(d_model=d_model, n_layer=int(r.integers(1, 4)), vocab_size=int(r.choice([64, 100])), d_state=d_state,
+               d_conv=int(r.integers(2, 5)), expand=expand, bias=bool(r.integers(0, 2)),
+               conv_bias=bool(r.integers(0, 2)))
+    if r.integers(0, 2):
+        cfg["dt_rank"] = int(r.integers(1, min(160, 288 - 2 * d_state) + 1))
+    return cfg, int(r.integers(3, 33))
+
+
+@pytest.mark.parametrize("seed", range(24))
+def test_random_shapes_batched_step_equals_per_op(seed, monkeypatch):
+    import mamba_lite.model as mm
+    cfg_kw, b = _draw(seed)
+    print(f"\n[batched step fuzz {seed}: {cfg_kw} batch={b}]", flush=True)
+    cfg = MambaConfig(**cfg_kw)
+    extra = {k: cfg_kw[k] for k in ("d_state", "d_conv", "expand", "dt_rank", "bias", "conv_bias") if k in cfg_kw}
+    sd = G.lm_weights(4000 + seed, cfg.d_model, cfg.n_layer, cfg.vocab_size, **extra)
+    lm = MambaLM(cfg)
+    lm.load_state_dict({k: torch.from_numpy(v) for k, v in sd.items()}, strict=True)
+    lm = lm.to(DEV).eval()
+    W = G.oracle_lm_dict(sd, cfg.n_layer)
+    calls = _counting(monkeypatch)
+    ids = np.random.default_rng(5000 + seed).integers(0, cfg.vocab_size, (b, 7), dtype=np.int64)
+    with torch.no_grad():
+        _, c_nat = lm.prefill(_t(ids[:, :4]))
+        _, c_per = lm.prefill(_t(ids[:, :4]))
+        _, rcache = om.lm_prefill(W, ids[:, :4], dtype=np.float64)
+        for k in range(3):
+            s = ids[:, 4 + k:5 + k]
+            got = lm.step(_t(s), c_nat)
+            monkeypatch.setattr(mm, "BATCHED_STEP_NATIVE", False)
+            per = lm.step(_t(s), c_per)
+            monkeypatch.setattr(mm, "BATCHED_STEP_NATIVE", True)
+            ref = om.lm_step(W, s, rcache, dtype=np.float64)
+            assert torch.equal(got, per), f"step {k}: logits differ from the per-op step"
+            assert_rel(_n(got), ref, 1e-4, f"step {k} logits vs oracle")
+    assert len(calls) == 3
+    for i, (ln, lp) in enumerate(zip(c_nat.layers, c_per.layers)):
+        assert torch.equal(ln.conv_state, lp.conv_state) and torch.equal(ln.ssm_state, lp.ssm_state), f"layer {i}"
