@@ -3,9 +3,9 @@
 This package restates, in numpy, the arithmetic of the reference
 (`mamba_lite/model.py`, `mamba_lite/tp_utils.py` of mamba-tp-lite) so the HIP
 kernels can be checked against it.  Only `tests/`, `__graft_entry__.smoke()`
-and the `cpu_baseline` leg of `bench.py` may import it, and only as the
-checker / the timed CPU baseline.  The product package never imports it and
-has no CPU fallback.
+and the `cpu_baseline` leg of `bench.py` may import it, and only to check
+results against or to time as the CPU baseline.  The product package never
+imports it and has no CPU fallback.
 
 Modules
 -------
