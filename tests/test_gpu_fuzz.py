@@ -166,7 +166,7 @@ def test_random_bf16_mixer_prefill_and_continuation_vs_oracle(seed, monkeypatch)
         assert_rel(_n(out), ro, 1e-2, "prefill out")
         assert_rel(_n(cs), rc, 1e-2, "prefill conv_state")
         assert_rel(_n(hs), rh, 1e-2, "prefill ssm_state")
-        # the continuation from this build's own states (bf16 history, fp32 state)
+        # the continuation from the HIP path's own states (bf16 history, fp32 state)
         ro1, rc1, rh1 = om.mixer_prefill(p, x1, conv_state=_n(cs), ssm_state=_n(hs), dtype=np.float64, act=bf16_round)
         out1, cs1, hs1 = m.prefill(torch.from_numpy(x1).to(DEV).bfloat16(), LayerCache(cs, hs))
         assert_rel(_n(out1), ro1, 1e-2, "continuation out")

@@ -360,7 +360,7 @@ def test_graph_serves_a_second_prompt_after_prefill_into_its_cache(b):
 @pytest.mark.parametrize("d_model,b", [(768, 32), (2048, 1), (2048, 32)])
 def test_tuned_gemm_table_loads_and_keeps_prefill_results(d_model, b):
     """mamba_lite.gemm_table: torch accepts the committed TunableOp table on
-    this build, and a mixer prefill of b x 1024 tokens at the 130m and 1.4b
+    this torch and ROCm, and a mixer prefill of b x 1024 tokens at the 130m and 1.4b
     widths (whose projection shapes are in the table: in_proj whole at 1 x
     1024, its halves at 32 x 1024, x_proj, dt_proj, out_proj) gives the same
     output and states within 1e-4 relative as the default GEMM paths."""

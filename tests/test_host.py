@@ -328,7 +328,7 @@ def test_from_pretrained_loads_in_proj_bias_of_a_bias_snapshot(tmp_path):
     """A `use_bias: true` snapshot: the in_proj and out_proj biases are both
     loaded.  (The reference's loader remaps out_proj.bias only, so its strict
     load of such a snapshot stops on the missing in_proj.bias, model.py:
-    392-396; loading it is this build's deliberate deviation.)"""
+    392-396; loading it is this library's deliberate deviation.)"""
     import _golden as G
     import torch
     from _util import write_hf_snapshot
