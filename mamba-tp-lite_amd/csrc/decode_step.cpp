@@ -161,6 +161,9 @@ extern "C" int mtl_decode_step_batched(const mtl_decode_step_batched_args* a, co
     MTL_REQUIRE(al16(a->h) && al16(a->inp) && al16(a->xc) && al16(a->z) && al16(a->y) && al16(a->parts) &&
                 (!fold || al16(a->xn)), "workspace h, inp, xn, xc, z, y and parts must be 16-byte aligned");
     MTL_REQUIRE(!fold || (a->xn != a->h && a->xn != a->inp), "xn must not alias h or inp");
+    // h carries the residual stream through every layer and out of the call
+    MTL_REQUIRE(a->inp != a->h && a->normed_out != a->h && a->normed_out != a->parts,
+                "inp and normed_out must not alias h (normed_out not parts either)");
     // every layer is checked before the first launch, so a bad layer leaves
     // no conv history or SSM state half stepped
     for (int32_t i = 0; i < nl; ++i) {
@@ -172,6 +175,7 @@ extern "C" int mtl_decode_step_batched(const mtl_decode_step_batched_args* a, co
                     al16(L.W_xT) && al16(L.W_out) && al16(L.b_out) && (!fold || al16(L.norm_w)),
                     at + "W_in, b_in, conv_state, conv_w, conv_b, W_xT, W_out, b_out and (folded) norm_w must be "
                          "16-byte aligned");
+        MTL_REQUIRE(!(L.eps < 0.f), at + "eps must be >= 0");
     }
     const int64_t bJ = (int64_t)b * J, bM = (int64_t)b * M;
     int rc = mtl_add_rmsnorm(a->h, nullptr, nullptr, layers[0].norm_w, a->inp, b, M, layers[0].eps, stream);

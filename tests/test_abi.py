@@ -176,6 +176,8 @@ def test_invalid_arguments_are_rejected_without_a_gpu():
     ("mtl_decode_step_batched", dict(misaligned_layer=True), b"layer 1: W_in, b_in, conv_state"),
     ("mtl_decode_step_batched", dict(fold=1, misaligned_norm=True), b"layer 1: W_in, b_in, conv_state"),
     ("mtl_decode_step_batched", dict(fold=1, d_model=2176), b"at most 128"),
+    ("mtl_decode_step_batched", dict(inp_is_h=True), b"must not alias h"),
+    ("mtl_decode_step_batched", dict(negative_eps=True), b"layer 1: eps must be >= 0"),
     ("mtl_in_proj_conv_xproj", dict(batch=33), b"batch must be in [1, 32]"),
     ("mtl_in_proj_conv_xproj", dict(d_model=128), b"at least 256"),
     ("mtl_in_proj_conv_xproj", dict(d_model=320), b"multiple of 128"),
@@ -352,7 +354,7 @@ def test_entry_points_validate_sizes_on_the_host(case):
     elif name == "mtl_decode_step_batched":
         a = dict(batch=8, n_layers=2, d_model=256, d_inner=512, d_state=16, dt_rank=16, d_conv=4, fold=0,
                  null_ws=False, null_fold=False, xn_is_h=False, null_layer=False, misaligned_layer=False,
-                 misaligned_norm=False)
+                 misaligned_norm=False, inp_is_h=False, negative_eps=False)
         a.update(over)
         args = _lib.DecodeStepBatchedArgs()
         for k, (f, *_) in enumerate(_lib.DecodeStepBatchedArgs._fields_[:13]):
@@ -364,6 +366,8 @@ def test_entry_points_validate_sizes_on_the_host(case):
             args.sq = None
         if a["xn_is_h"]:
             args.xn = args.h
+        if a["inp_is_h"]:
+            args.inp = args.h
         args.eps_f, args.n_layers, args.batch, args.fold = 1e-5, a["n_layers"], a["batch"], a["fold"]
         args.d_model, args.d_inner, args.d_state, args.dt_rank, args.d_conv = a["d_model"], a["d_inner"], \
             a["d_state"], a["dt_rank"], a["d_conv"]
@@ -378,6 +382,8 @@ def test_entry_points_validate_sizes_on_the_host(case):
                 L.conv_state = 24
             if a["misaligned_norm"] and i == 1:
                 L.norm_w = 20
+            if a["negative_eps"] and i == 1:
+                L.eps = -1.0
         rc = lib.mtl_decode_step_batched(ctypes.byref(args), layers, None)
     elif name == "mtl_in_proj_conv_xproj":
         a = dict(batch=8, d_model=256, d_inner=64, cpp=16, d_conv=4, J=40)
