@@ -875,8 +875,12 @@ class MambaLM(nn.Module):
         if DECODE_STEP_NATIVE:
             plan = self._decode_plan(lt)
             split_k = b <= plan["split_k_max_b"]
-            if self._decode_step_template(plan, split_k, input_ids.device, lt) is None:
+            tmpl = self._decode_step_template(plan, split_k, input_ids.device, lt)
+            if tmpl is None:
                 return False
+            # the step that follows in the same call reuses them (keyed on this
+            # call's parameter list, so no other call can pick them up)
+            self._fused_memo = (lt, plan, tmpl) if lt is not None else None
         return True
 
     def _check_step_cache(self, cache, b: int, device):
@@ -1028,7 +1032,10 @@ class MambaLM(nn.Module):
 
     def _step_fused(self, input_ids, cache, lt=None):
         cfg = self.cfg
-        plan = self._decode_plan(lt)
+        memo = getattr(self, "_fused_memo", None)
+        memo = memo if memo is not None and lt is not None and memo[0] is lt else None
+        self._fused_memo = None
+        plan = memo[1] if memo is not None else self._decode_plan(lt)
         b, M, D, J = input_ids.shape[0], cfg.d_model, cfg.d_inner, plan["J"]
         split_k = b <= plan["split_k_max_b"]
         dev = input_ids.device
@@ -1065,7 +1072,7 @@ class MambaLM(nn.Module):
         if DECODE_STEP_NATIVE:
             self._check_step_cache(cache, b, dev)
             logits = torch.empty(b, self.embedding.weight.shape[0], **f32)
-            tmpl = self._decode_step_template(plan, split_k, dev, lt)
+            tmpl = memo[2] if memo is not None else self._decode_step_template(plan, split_k, dev, lt)
             arr = type(tmpl).from_buffer_copy(tmpl)     # per call: read by the library without the GIL
             for L, lc in zip(arr, cache.layers):
                 L.conv_state, L.ssm_state = lc.conv_state.data_ptr(), lc.ssm_state.data_ptr()
