@@ -431,7 +431,8 @@ int mtl_prefill_short(const mtl_prefill_short_args* args, const mtl_prefill_laye
  * looked up on the shape's first call on a device and kept; the handle is
  * created on the first call on a device.  After that a call allocates no
  * device memory and may be captured into a HIP graph.  Calls on one process
- * are serialized inside the library.  d_state <= 32, 1 <= d_conv <= 8.
+ * are serialized inside the library.  b l <= 2^20 with b <= 65535,
+ * d_state <= 32, 1 <= d_conv <= 8.
  * With b l <= skinny_rows (0: never) the projections run on mtl_linear_skinny
  * instead (in 64-row chunks; x_proj as split-K parts summed by
  * mtl_xproj_sum_dt, which also applies dt_proj; out_proj as 4 parts summed by
@@ -439,7 +440,8 @@ int mtl_prefill_short(const mtl_prefill_short_args* args, const mtl_prefill_laye
  * 128, d_inner of 512, R + 2N of 4, dt_rank <= 160, xn, xz, u, y, blas_ws and
  * every layer's W_in, b_in, W_x, W_out, b_out 16-byte aligned, and blas_ws
  * holding (xs (R + 2N) + 4 d_model) b l floats for the parts (xs: the x_proj
- * split, at most 16); otherwise the hipBLASLt form runs.
+ * split, at most 16), xs (R + 2N) b l below 2^31; otherwise the hipBLASLt
+ * form runs.
  * ---------------------------------------------------------------------- */
 typedef struct {
     float* h;
@@ -649,8 +651,8 @@ int mtl_decode_step(const mtl_decode_step_args* args, const mtl_decode_layer* la
  *               [b, d_inner, d_state] are updated in place.
  * d_model a multiple of 128 (at least 256), d_inner a multiple of 512,
  * d_state <= 16, dt_rank <= 256 with dt_rank + 2 d_state <= 288, d_conv
- * 2..4.  Every layer's pointers, the sizes and the alignments the entry
- * points take are checked before the first launch.
+ * 2..4.  Every layer's pointers, its eps (>= 0, not NaN), the sizes and the
+ * alignments the entry points take are checked before the first launch.
  * ---------------------------------------------------------------------- */
 typedef struct {
     float* h;

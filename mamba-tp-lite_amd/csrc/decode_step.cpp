@@ -175,7 +175,7 @@ extern "C" int mtl_decode_step_batched(const mtl_decode_step_batched_args* a, co
                     al16(L.W_xT) && al16(L.W_out) && al16(L.b_out) && (!fold || al16(L.norm_w)),
                     at + "W_in, b_in, conv_state, conv_w, conv_b, W_xT, W_out, b_out and (folded) norm_w must be "
                          "16-byte aligned");
-        MTL_REQUIRE(!(L.eps < 0.f), at + "eps must be >= 0");
+        MTL_REQUIRE(L.eps >= 0.f, at + "eps must be >= 0 (not NaN)");
     }
     const int64_t bJ = (int64_t)b * J, bM = (int64_t)b * M;
     int rc = mtl_add_rmsnorm(a->h, nullptr, nullptr, layers[0].norm_w, a->inp, b, M, layers[0].eps, stream);

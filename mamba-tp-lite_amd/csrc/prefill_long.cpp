@@ -161,6 +161,7 @@ extern "C" int mtl_prefill_long(const mtl_prefill_long_args* a, const mtl_prefil
     const int64_t rows = b * l, J = R + 2 * N;
     const int32_t K = a->d_conv;
     MTL_REQUIRE(b >= 1 && l >= 1 && rows <= (int64_t(1) << 20), "batch * seqlen must be in [1, 2^20]");
+    MTL_REQUIRE(b <= 65535, "batch must be <= 65535");   // the conv and scan grids' row limit
     MTL_REQUIRE(a->n_layers >= 1, "n_layers must be >= 1");
     MTL_REQUIRE(M >= 1 && M <= (int64_t(1) << 16) && D >= 1 && D <= (int64_t(1) << 16),
                 "d_model and d_inner must be in [1, 65536]");
@@ -185,7 +186,7 @@ extern "C" int mtl_prefill_long(const mtl_prefill_long_args* a, const mtl_prefil
     auto al16 = [](const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; };
     bool skinny = a->skinny_rows > 0 && rows <= a->skinny_rows && M % 128 == 0 && D % (128 * kOutSplit) == 0 &&
                   J % 4 == 0 && R <= 160 && al16(a->xn) && al16(a->u) && al16(a->y) && al16(a->xz) &&
-                  al16(a->blas_ws) &&
+                  al16(a->blas_ws) && (int64_t)xs * J * rows < (int64_t(1) << 31) &&
                   (int64_t)(xs * J + kOutSplit * M) * rows * (int64_t)sizeof(float) <= a->blas_ws_bytes;
     for (int32_t i = 0; skinny && i < a->n_layers; ++i) {
         const mtl_prefill_layer& L = layers[i];

@@ -177,7 +177,10 @@ def test_invalid_arguments_are_rejected_without_a_gpu():
     ("mtl_decode_step_batched", dict(fold=1, misaligned_norm=True), b"layer 1: W_in, b_in, conv_state"),
     ("mtl_decode_step_batched", dict(fold=1, d_model=2176), b"at most 128"),
     ("mtl_decode_step_batched", dict(inp_is_h=True), b"must not alias h"),
-    ("mtl_decode_step_batched", dict(negative_eps=True), b"layer 1: eps must be >= 0"),
+    ("mtl_decode_step_batched", dict(layer1_eps=-1.0), b"layer 1: eps must be >= 0"),
+    # a NaN eps would pass a "not below zero" test and then fail in the folded
+    # in_proj of layer 1, after layer 0 has stepped its caches
+    ("mtl_decode_step_batched", dict(fold=1, layer1_eps=float("nan")), b"layer 1: eps must be >= 0"),
     ("mtl_in_proj_conv_xproj", dict(batch=33), b"batch must be in [1, 32]"),
     ("mtl_in_proj_conv_xproj", dict(d_model=128), b"at least 256"),
     ("mtl_in_proj_conv_xproj", dict(d_model=320), b"multiple of 128"),
@@ -190,6 +193,7 @@ def test_invalid_arguments_are_rejected_without_a_gpu():
     ("mtl_prefill_long", dict(d_state=33), b"d_state"),
     ("mtl_prefill_long", dict(batch=1 << 12, seqlen=1 << 12), b"batch * seqlen"),
     ("mtl_prefill_long", dict(n_layers=0), b"n_layers"),
+    ("mtl_prefill_long", dict(batch=65536, seqlen=1), b"batch must be <= 65535"),
     ("mtl_prefill_long", dict(null_ws=True), b"null workspace"),
     ("mtl_prefill_long", dict(null_layer=True), b"layer 1: null required pointer"),
     ("mtl_prefill_long", dict(alias=True), b"layer 1: conv_state_out must not alias"),
@@ -354,7 +358,7 @@ def test_entry_points_validate_sizes_on_the_host(case):
     elif name == "mtl_decode_step_batched":
         a = dict(batch=8, n_layers=2, d_model=256, d_inner=512, d_state=16, dt_rank=16, d_conv=4, fold=0,
                  null_ws=False, null_fold=False, xn_is_h=False, null_layer=False, misaligned_layer=False,
-                 misaligned_norm=False, inp_is_h=False, negative_eps=False)
+                 misaligned_norm=False, inp_is_h=False, layer1_eps=None)
         a.update(over)
         args = _lib.DecodeStepBatchedArgs()
         for k, (f, *_) in enumerate(_lib.DecodeStepBatchedArgs._fields_[:13]):
@@ -382,8 +386,8 @@ def test_entry_points_validate_sizes_on_the_host(case):
                 L.conv_state = 24
             if a["misaligned_norm"] and i == 1:
                 L.norm_w = 20
-            if a["negative_eps"] and i == 1:
-                L.eps = -1.0
+            if a["layer1_eps"] is not None and i == 1:
+                L.eps = a["layer1_eps"]
         rc = lib.mtl_decode_step_batched(ctypes.byref(args), layers, None)
     elif name == "mtl_in_proj_conv_xproj":
         a = dict(batch=8, d_model=256, d_inner=64, cpp=16, d_conv=4, J=40)
