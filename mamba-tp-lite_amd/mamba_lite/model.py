@@ -211,13 +211,13 @@ def _cu_count(device) -> int:
     return torch.cuda.get_device_properties(device).multi_processor_count
 
 
-def _skinny_rows(x: torch.Tensor, w: torch.Tensor, enabled: bool = True) -> torch.Tensor | None:
-    """x [..., K] as the [rows, K] operand of mtl_linear_skinny, or None
-    where it does not apply."""
+def _skinny_rows(x: torch.Tensor, w: torch.Tensor, enabled: bool = True, bias=None) -> torch.Tensor | None:
+    """x [..., K] as the [rows, K] operand of mtl_linear_skinny (with this
+    bias), or None where it does not apply."""
     if not (enabled and _SKINNY_PREFILL) or not x.is_contiguous():
         return None
     x2 = x.reshape(-1, x.shape[-1])
-    return x2 if ops.linear_skinny_ok(x2, w) else None
+    return x2 if ops.linear_skinny_ok(x2, w, bias=bias) else None
 
 
 def _skinny_split(K: int, most: int = 16) -> int:
@@ -346,7 +346,7 @@ class MambaMixer(nn.Module):
                     not out.ssm_state.is_contiguous():
                 raise ValueError(f"out.ssm_state must be contiguous float32 {(b, Dm, N)}")
         split = b * l >= SPLIT_PROJ_MIN_TOKENS
-        x2 = None if split else _skinny_rows(x, self.in_proj.weight, skinny)
+        x2 = None if split else _skinny_rows(x, self.in_proj.weight, skinny, self.in_proj.bias)
         # in_proj with the causal conv as its epilogue (<= 64 tokens)
         fused_conv = x2 is not None and ops.in_proj_conv_prefill_ok(x2, self.in_proj.weight, K)
         if fused_conv:
@@ -421,7 +421,7 @@ class MambaMixer(nn.Module):
         h = h if out is not None else h.to(_state_dtype(x.dtype))
         if parts_ok:
             w_out = self.out_proj.weight
-            y2 = _skinny_rows(y_store, w_out, skinny)
+            y2 = _skinny_rows(y_store, w_out, skinny, self.out_proj.bias)
             if y2 is not None and Dm % (128 * SKINNY_OUT_SPLIT) == 0:
                 parts = ops.linear_skinny(y2, w_out, self.out_proj.bias, ksplit=SKINNY_OUT_SPLIT)
                 return _Parts(parts.view(SKINNY_OUT_SPLIT, b, l, -1)), conv_state, h
@@ -444,7 +444,7 @@ class MambaMixer(nn.Module):
         weight cold in HBM, against the library's GEMM: the mamba-130m width
         9.8 -> 6.0 us, 1.4b 17.8-18.7 -> 15.6-15.8 us."""
         w = self.in_proj.weight
-        if ops.linear_skinny_ok(x_t, w):
+        if ops.linear_skinny_ok(x_t, w, bias=self.in_proj.bias):
             return ops.linear_skinny(x_t, w, self.in_proj.bias)
         return self.in_proj(x_t)
 
@@ -456,7 +456,7 @@ class MambaMixer(nn.Module):
         out_proj 16.7 -> 10.0 us, 130m 7.9 -> 3.7 us."""
         w = self.out_proj.weight
         K = w.shape[1]
-        if K % (128 * SKINNY_OUT_SPLIT) or not ops.linear_skinny_ok(y, w):
+        if K % (128 * SKINNY_OUT_SPLIT) or not ops.linear_skinny_ok(y, w, bias=self.out_proj.bias):
             return None
         return ops.linear_skinny(y, w, self.out_proj.bias, ksplit=SKINNY_OUT_SPLIT)
 
@@ -470,7 +470,8 @@ class MambaMixer(nn.Module):
         J = R + 2 * self.cfg.d_state
         conv_w, conv_b = self._step_conv()
         w_in = self.in_proj.weight
-        if ops.in_proj_conv_xproj_ok(x_t, w_in, cache.conv_state, conv_w.shape[-1], J):
+        if ops.in_proj_conv_xproj_ok(x_t, w_in, cache.conv_state, conv_w.shape[-1], J, self.in_proj.bias, conv_w,
+                                     conv_b):
             # in_proj, the conv step and the x_proj partials of each channel
             # block in one launch (measured at the mamba-1.4b width, 32 tokens:
             # see in_proj_conv_xproj)
@@ -740,13 +741,18 @@ class MambaLM(nn.Module):
         rpb = ops.residual_rows_per_block(b, dm, SKINNY_OUT_SPLIT)
         if dm % rpb or dm // rpb > 128:
             return False
-        for blk, lc in zip(self.layers, cache.layers):
+        nl = len(self.layers)
+        for i, (blk, lc) in enumerate(zip(self.layers, cache.layers)):
             mx = blk.mixer
             w = mx.out_proj.weight
-            if not ops.in_proj_conv_xproj_ok(x, mx.in_proj.weight, lc.conv_state, cfg.d_conv, J):
+            conv_w, conv_b = mx._step_conv()
+            if not ops.in_proj_conv_xproj_ok(x, mx.in_proj.weight, lc.conv_state, cfg.d_conv, J, mx.in_proj.bias,
+                                             conv_w, conv_b):
                 return False
-            if w.dtype != torch.float32 or not w.is_contiguous() or w.data_ptr() % 16 or \
-                    tuple(w.shape) != (dm, cfg.d_inner) or w.device != x.device:
+            if w.dtype != torch.float32 or not w.is_contiguous() or tuple(w.shape) != (dm, cfg.d_inner) or \
+                    w.device != x.device or not ops.aligned16(w, mx.out_proj.bias):
+                return False
+            if i + 1 < nl and not ops.aligned16(self._norm_weight(i + 1)):   # the next norm, read by out_proj
                 return False
         return True
 
@@ -832,8 +838,9 @@ class MambaLM(nn.Module):
     def _batched_template(self, lt, dev, dm):
         """The weight half of _batched_step_layers: mtl_decode_layer records
         (W_xT = x_proj transposed, conv weights as [D, K] views), or None when
-        a weight is not a contiguous float32 tensor of its shape on dev or
-        in_proj / out_proj is not 16-byte aligned."""
+        a weight is not a contiguous float32 tensor of its shape on dev or one
+        the library loads in 16-byte runs (norm, in_proj, conv, out_proj and
+        their biases) is not 16-byte aligned."""
         cfg = self.cfg
         D, N, K, R = cfg.d_inner, cfg.d_state, cfg.d_conv, cfg.dt_rank
         ok = lambda t, shape: t.device == dev and t.dtype == torch.float32 and t.is_contiguous() and \
@@ -847,7 +854,8 @@ class MambaLM(nn.Module):
                     and ok(ts[_LT_A_LOG], (D, N)) and opt(ts[_LT_D], (D,)) and ok(ts[_LT_W_OUT], (dm, D))
                     and opt(ts[_LT_B_OUT], (dm,))):
                 return None
-            if ts[_LT_W_IN].data_ptr() % 16 or ts[_LT_W_OUT].data_ptr() % 16:
+            if not ops.aligned16(ts[_LT_NORM], ts[_LT_W_IN], ts[_LT_B_IN], ts[_LT_CONV_W], ts[_LT_CONV_B],
+                                 ts[_LT_W_OUT], ts[_LT_B_OUT]):
                 return None
             w_xt = self.layers[i].mixer._xproj_t()
             ptr = lambda t: 0 if t is None else t.data_ptr()
@@ -866,7 +874,8 @@ class MambaLM(nn.Module):
                 cfg.d_inner % 4 or b * cfg.d_model > 15 * 1024 or cfg.d_inner > 4096 or cfg.dt_rank > 256 or \
                 not 2 <= cfg.d_conv <= 8:
             return False
-        if self.embedding.weight.dtype != torch.float32 or not input_ids.is_cuda:
+        if self.embedding.weight.dtype != torch.float32 or not input_ids.is_cuda or \
+                not ops.aligned16(self.embedding.weight):
             return False
         lc = cache.layers[0]
         if not (lc.conv_state.dtype == torch.float32 and lc.ssm_state.dtype == torch.float32 and
@@ -1007,7 +1016,8 @@ class MambaLM(nn.Module):
         """ctypes array of mtl_decode_layer with every layer's weight pointers
         (x_proj transposed from the decode plan with split_k, as is without),
         or None when a weight is not a contiguous float32 tensor on `device`
-        (the step then runs op by op).  Rebuilt whenever any of those
+        or in_proj, out_proj or (without split_k) x_proj is not 16-byte
+        aligned (the step then runs op by op).  Rebuilt whenever any of those
         tensors' addresses change."""
         ws = []
         for t, lp in zip(self._layer_tensors() if lt is None else lt, plan["layers"]):
@@ -1019,7 +1029,8 @@ class MambaLM(nn.Module):
         if cached is not None and cached[0] == key and cached[2] == device:
             return cached[1]
         arr = None
-        if all(t is None or (t.device == device and t.dtype == torch.float32 and t.is_contiguous()) for t in ws):
+        if all(t is None or (t.device == device and t.dtype == torch.float32 and t.is_contiguous()) for t in ws) \
+                and ops.aligned16(*ws[1::13], *ws[6::13], *ws[11::13]):   # W_in, W_x, W_out
             arr = (_lib.DecodeLayer * len(self.layers))()
             for i, L in enumerate(arr):
                 (L.norm_w, L.W_in, L.b_in, L.conv_w, L.conv_b, L.W_xT, L.W_x, L.W_dt, L.dt_bias, L.A_log, L.Dv,

@@ -329,10 +329,17 @@ def in_proj_conv_prefill(x2, W_in, b_in, conv_w, conv_b, conv_state_in, conv_sta
     return u, z
 
 
-def in_proj_conv_xproj_ok(x, W_in, conv_state, d_conv, J) -> bool:
+def aligned16(*ts) -> bool:
+    """Whether every tensor given (None skipped) starts on a 16-byte boundary,
+    as the library's 16-byte loads of weights, biases and histories need."""
+    return all(t is None or t.data_ptr() % 16 == 0 for t in ts)
+
+
+def in_proj_conv_xproj_ok(x, W_in, conv_state, d_conv, J, b_in=None, conv_w=None, conv_b=None) -> bool:
     """Whether mtl_in_proj_conv_xproj takes this batched step: fp32 on the
     GPU, 1..32 rows, d_model a multiple of 128 (at least 256), d_conv 2..4,
-    J <= 288, d_inner a multiple of 16."""
+    J <= 288, d_inner a multiple of 16, x, W_in, the conv history and the
+    given b_in, conv_w and conv_b 16-byte aligned."""
     if x.dim() != 2 or W_in.dim() != 2 or x.dtype != torch.float32 or W_in.dtype != torch.float32:
         return False
     b, M = x.shape
@@ -341,7 +348,7 @@ def in_proj_conv_xproj_ok(x, W_in, conv_state, d_conv, J) -> bool:
             and D % 16 == 0 and 2 <= d_conv <= 4 and 1 <= J <= 288 and x.stride(1) == 1 and x.stride(0) % 4 == 0
             and W_in.is_contiguous() and x.data_ptr() % 16 == 0 and W_in.data_ptr() % 16 == 0
             and conv_state.dtype == torch.float32 and conv_state.is_contiguous()
-            and tuple(conv_state.shape) == (b, D, d_conv - 1))
+            and tuple(conv_state.shape) == (b, D, d_conv - 1) and aligned16(conv_state, b_in, conv_w, conv_b))
 
 
 def in_proj_conv_xproj(x, W_in, b_in, conv_state, conv_w, conv_b, W_xT, channels_per_part=None, sq=None, eps=0.0):
@@ -358,9 +365,10 @@ def in_proj_conv_xproj(x, W_in, b_in, conv_state, conv_w, conv_b, W_xT, channels
     w = conv_w.reshape(conv_w.shape[0], conv_w.shape[-1]) if conv_w.dim() == 3 else conv_w
     K = w.shape[1]
     J = W_xT.shape[1]
-    if not in_proj_conv_xproj_ok(x, W_in, conv_state, K, J):
+    if not in_proj_conv_xproj_ok(x, W_in, conv_state, K, J, b_in, w, conv_b):
         raise ValueError("in_proj_conv_xproj: fp32 x [b<=32, d_model%128==0, >=256], contiguous W_in [2D, d_model] "
-                         "(D%16==0), conv_state [b, D, K-1] with K in 2..4, J <= 288")
+                         "(D%16==0), conv_state [b, D, K-1] with K in 2..4, J <= 288; x, W_in, b_in, conv_state, "
+                         "conv_w and conv_b 16-byte aligned")
     _f32_mat(w, (D, K), "conv_w")
     _f32_vec(conv_b, D, "conv_b")
     _f32_vec(b_in, 2 * D, "b_in")
@@ -832,18 +840,18 @@ SKINNY_CHUNKED_MAX_ROWS = 64 * 65535   # rows of x over all chunks
 IN_CONV_MAX_ROWS = 32    # mtl_in_proj_conv_xproj: batch rows
 
 
-def linear_skinny_ok(x, W, max_rows=SKINNY_MAX_ROWS) -> bool:
-    """Whether mtl_linear_skinny takes y = x W^T for these operands in one
-    chunk (or, with max_rows, in 64-row chunks): fp32 on the GPU, 1..64
-    rows of x, K a multiple of 128, W rows a multiple of 4, 16-byte aligned
-    rows."""
+def linear_skinny_ok(x, W, max_rows=SKINNY_MAX_ROWS, bias=None) -> bool:
+    """Whether mtl_linear_skinny takes y = x W^T (+ bias) for these operands
+    in one chunk (or, with max_rows, in 64-row chunks): fp32 on the GPU,
+    1..64 rows of x, K a multiple of 128, W rows a multiple of 4, 16-byte
+    aligned rows and bias."""
     if x.dim() != 2 or W.dim() != 2 or x.dtype != torch.float32 or W.dtype != torch.float32:
         return False
     M, K = x.shape
     N = W.shape[0]
     return (x.is_cuda and W.is_cuda and 1 <= M <= max_rows and W.shape[1] == K and K % 128 == 0
             and N % 4 == 0 and x.stride(1) == 1 and x.stride(0) % 4 == 0 and W.is_contiguous()
-            and x.data_ptr() % 16 == 0 and W.data_ptr() % 16 == 0)
+            and x.data_ptr() % 16 == 0 and W.data_ptr() % 16 == 0 and aligned16(bias))
 
 
 def linear_skinny(x, W, bias=None, out=None, ksplit=1, rows_per_block=None):
@@ -852,9 +860,9 @@ def linear_skinny(x, W, bias=None, out=None, ksplit=1, rows_per_block=None):
     and of a prefill of at most 64 tokens), larger M in 64-row chunks.
     With ksplit > 1, out is [ksplit, M, N]: the partial products over K
     split into ksplit equal ranges (bias in part 0), to be added in order."""
-    if not linear_skinny_ok(x, W, SKINNY_CHUNKED_MAX_ROWS):
-        raise ValueError("linear_skinny: fp32 x [M, K%128==0] (unit column stride, 16B rows) and contiguous "
-                         "W [N%4==0, K] expected")
+    if not linear_skinny_ok(x, W, SKINNY_CHUNKED_MAX_ROWS, bias):
+        raise ValueError("linear_skinny: fp32 x [M, K%128==0] (unit column stride, 16B rows), contiguous "
+                         "W [N%4==0, K] and a 16-byte aligned bias expected")
     M, K = x.shape
     N = W.shape[0]
     if bias is not None:

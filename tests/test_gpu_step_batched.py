@@ -14,6 +14,9 @@ and MambaMixer.step 249-294):
     512, 1-16 states, d_conv 2-4, dt_rank, biases, 1-3 layers, 3-32 rows)
     against the per-op step bit for bit and the oracle at 1e-4;
   * a block norm's eps changed between steps reaches the next one;
+  * biases, conv and norm weights that start off a 16-byte boundary send
+    the step down paths that read them a float at a time (no entry point
+    rejects them mid-step), matching the aligned model at 1e-4;
   * the model takes it only where every layer runs the per-op step's in_proj
     + conv + x_proj launch and split out_proj; elsewhere the per-op path runs,
     with its own checks (a cache of the wrong batch still raises
@@ -225,3 +228,48 @@ def test_random_shapes_batched_step_equals_per_op(seed, monkeypatch):
     assert len(calls) == 3
     for i, (ln, lp) in enumerate(zip(c_nat.layers, c_per.layers)):
         assert torch.equal(ln.conv_state, lp.conv_state) and torch.equal(ln.ssm_state, lp.ssm_state), f"layer {i}"
+
+
+def _unaligned(p):
+    """p's values in a parameter that starts 4 bytes past a 16-byte boundary
+    (a view into a larger buffer)."""
+    buf = torch.empty(p.numel() + 1, device=p.device, dtype=p.dtype)
+    v = buf[1:].view_as(p)
+    v.copy_(p.detach())
+    return torch.nn.Parameter(v, requires_grad=False)
+
+
+@pytest.mark.parametrize("b", [1, 4, 24])
+def test_unaligned_vector_parameters_take_another_path_instead_of_raising(b, monkeypatch):
+    """Biases, conv weights and norm weights that start off a 16-byte
+    boundary cannot go to the entry points that load them in 16-byte runs
+    (the one-call batched step, the folded step, the in_proj + conv + x_proj
+    launch, the skinny GEMMs), which reject them: the step takes the paths
+    that read them a float at a time (batch 1: the fused step, whose kernels
+    do), and its logits and caches match the aligned model's at the fp32
+    tolerance over three steps from a zero cache."""
+    calls = _counting(monkeypatch)
+    lm, _ = _lm(160, 256, 2, 512, bias=True)
+    odd, _ = _lm(160, 256, 2, 512, bias=True)
+    for blk in odd.layers:
+        mx = blk.mixer
+        mx.in_proj.bias = _unaligned(mx.in_proj.bias)
+        mx.out_proj.bias = _unaligned(mx.out_proj.bias)
+        mx.conv1d.weight = _unaligned(mx.conv1d.weight)
+        mx.conv1d.bias = _unaligned(mx.conv1d.bias)
+        blk.norm.weight = _unaligned(blk.norm.weight)
+    assert all(blk.norm.weight.data_ptr() % 16 == 4 for blk in odd.layers)
+    ids = _t(np.random.default_rng(160 + b).integers(0, 512, (b, 3), dtype=np.int64))
+    ca = MambaCache.allocate(lm.cfg, b, DEV, torch.float32)
+    co = MambaCache.allocate(odd.cfg, b, DEV, torch.float32)
+    with torch.no_grad():
+        for k in range(3):
+            la = lm.step(ids[:, k:k + 1], ca)
+            n = len(calls)
+            lo = odd.step(ids[:, k:k + 1], co)
+            assert len(calls) == n, "the unaligned model took the one-call batched step"
+            assert_rel(_n(lo), _n(la), 1e-4, f"step {k} logits")
+    assert len(calls) == (3 if b > 2 else 0)
+    for i, (a_, o_) in enumerate(zip(ca.layers, co.layers)):
+        assert_rel(_n(o_.conv_state), _n(a_.conv_state), 1e-4, f"layer {i} conv_state")
+        assert_rel(_n(o_.ssm_state), _n(a_.ssm_state), 1e-4, f"layer {i} ssm_state")

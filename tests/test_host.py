@@ -291,6 +291,34 @@ def test_layer_tensors_are_the_step_parameters_in_order(bias, conv_bias):
     assert model._layer_tensors()[1][mm._LT_W_OUT] is model.layers[1].mixer.out_proj.weight
 
 
+def test_unaligned_parameters_keep_the_native_step_records_out():
+    """The one-call steps' weight records (_batched_template,
+    _decode_step_template) are built only from parameters the library can
+    load in 16-byte runs; a parameter that starts 4 bytes off a 16-byte
+    boundary (a view into a larger buffer) makes them None, so the step runs
+    a path that takes it, instead of an entry point that rejects it."""
+    model = MambaLM(MambaConfig(d_model=256, n_layer=2, vocab_size=64, bias=True)).eval()
+    dev = torch.device("cpu")
+
+    def unaligned(p):
+        buf = torch.empty(p.numel() + 1, dtype=p.dtype)
+        v = buf[1:].view_as(p)
+        v.copy_(p.detach())
+        return torch.nn.Parameter(v, requires_grad=False)
+
+    assert model._batched_template(model._layer_tensors(), dev, 256) is not None
+    for split_k in (True, False):
+        assert model._decode_step_template(model._decode_plan(), split_k, dev) is not None
+    mx = model.layers[1].mixer
+    mx.out_proj.bias = unaligned(mx.out_proj.bias)
+    assert model._batched_template(model._layer_tensors(), dev, 256) is None
+    for split_k in (True, False):   # biases are read a float at a time there
+        assert model._decode_step_template(model._decode_plan(), split_k, dev) is not None
+    mx.in_proj.weight = unaligned(mx.in_proj.weight)
+    for split_k in (True, False):
+        assert model._decode_step_template(model._decode_plan(), split_k, dev) is None
+
+
 def test_persistent_decode_grid_query():
     """mtl_decode_persist_grid: the 130m shape takes 64 workgroups with the
     first blocking and 128 with the second; shapes outside the kernel's
