@@ -635,9 +635,11 @@ def decode_step_batched(layers, h, norm_f, eps_f, cfg, fold):
     allocated here (one float32 tensor, and with fold the zeroed counters)."""
     _f32c(h, "h")
     _f32c(norm_f, "norm_f")
-    if h.dim() != 2 or h.data_ptr() % 16:
-        raise ValueError("decode_step_batched: h must be a 16-byte aligned [b, d_model] tensor")
+    if h.dim() != 2 or h.data_ptr() % 16 or h.shape[1] != cfg.d_model:
+        raise ValueError(f"decode_step_batched: h must be a 16-byte aligned [b, {cfg.d_model}] tensor")
     b, M = h.shape
+    if norm_f.numel() != M or norm_f.device != h.device:
+        raise ValueError(f"decode_step_batched: norm_f must hold {M} floats on {h.device}")
     D, J = cfg.d_inner, cfg.dt_rank + 2 * cfg.d_state
     nl = len(layers)
     pad = lambda n: -(-n // 64) * 64                      # 256-byte aligned slices

@@ -72,6 +72,12 @@ def test_shape_validation_before_launch():
                            torch.randn(1, 4, 4))
     with pytest.raises(ValueError):
         ops.causal_conv1d(torch.randn(1, 8, 4), torch.randn(7, 4))
+    # the one-call batched step takes d_model from h: a row of another width
+    # or a norm_f of another length would stride the weights wrongly
+    cfg = MambaConfig(d_model=256, n_layer=2, vocab_size=64)
+    for h, nf in ((torch.zeros(4, 384), torch.ones(384)), (torch.zeros(4, 256), torch.ones(384))):
+        with pytest.raises(ValueError):
+            ops.decode_step_batched(None, h, nf, 1e-5, cfg, False)
 
 
 def test_graphed_stepper_rejects_cpu():
