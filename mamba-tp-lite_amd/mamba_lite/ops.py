@@ -540,6 +540,8 @@ def prefill_short(h, layers, norm_f, eps_f, d_inner, d_state, dt_rank, d_conv):
     rows, J = b * l, dt_rank + 2 * d_state
     if not prefill_short_ok(rows, M, d_inner, d_state, dt_rank, d_conv):
         raise ValueError("prefill_short: sizes outside mtl_prefill_short")
+    if norm_f.numel() != M or norm_f.device != h.device:
+        raise ValueError(f"prefill_short: norm_f must hold {M} floats on {h.device}")
     # one workspace, every buffer on a 256-byte boundary
     sizes = [rows * M, rows * d_inner, rows * d_inner, rows * d_inner, rows * d_inner, 16 * rows * J, rows * J,
              4 * rows * M]
@@ -576,6 +578,8 @@ def prefill_long(h, layers, norm_f, eps_f, d_inner, d_state, dt_rank, d_conv, sk
     _f32c(norm_f, "norm_f")
     b, l, M = h.shape
     rows, J = b * l, dt_rank + 2 * d_state
+    if norm_f.numel() != M or norm_f.device != h.device:
+        raise ValueError(f"prefill_long: norm_f must hold {M} floats on {h.device}")
     # one workspace, every buffer on a 256-byte boundary
     sizes = [rows * M, rows * 2 * d_inner, rows * d_inner, rows * J, rows * d_inner, rows * d_inner, rows * M,
              PREFILL_LONG_BLAS_WS // 4]

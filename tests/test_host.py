@@ -78,6 +78,10 @@ def test_shape_validation_before_launch():
     for h, nf in ((torch.zeros(4, 384), torch.ones(384)), (torch.zeros(4, 256), torch.ones(384))):
         with pytest.raises(ValueError):
             ops.decode_step_batched(None, h, nf, 1e-5, cfg, False)
+    # the one-call prefills: a final norm of another width than h's rows
+    for fn in (ops.prefill_short, ops.prefill_long):
+        with pytest.raises(ValueError, match="norm_f"):
+            fn(torch.zeros(1, 8, 256), None, torch.ones(384), 1e-5, 512, 16, 16, 4)
 
 
 def test_graphed_stepper_rejects_cpu():
