@@ -431,8 +431,8 @@ int mtl_prefill_short(const mtl_prefill_short_args* args, const mtl_prefill_laye
  * looked up on the shape's first call on a device and kept; the handle is
  * created on the first call on a device.  After that a call allocates no
  * device memory and may be captured into a HIP graph.  Calls on one process
- * are serialized inside the library.  b l <= 2^20 with b <= 65535,
- * d_state <= 32, 1 <= d_conv <= 8.
+ * are serialized inside the library.  b l <= 2^20 with b <= 65535 and
+ * l <= 1048560, d_state <= 32, 1 <= d_conv <= 8.
  * With b l <= skinny_rows (0: never) the projections run on mtl_linear_skinny
  * instead (in 64-row chunks; x_proj as split-K parts summed by
  * mtl_xproj_sum_dt, which also applies dt_proj; out_proj as 4 parts summed by

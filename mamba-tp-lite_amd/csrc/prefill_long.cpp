@@ -162,6 +162,7 @@ extern "C" int mtl_prefill_long(const mtl_prefill_long_args* a, const mtl_prefil
     const int32_t K = a->d_conv;
     MTL_REQUIRE(b >= 1 && l >= 1 && rows <= (int64_t(1) << 20), "batch * seqlen must be in [1, 2^20]");
     MTL_REQUIRE(b <= 65535, "batch must be <= 65535");   // the conv and scan grids' row limit
+    MTL_REQUIRE(l <= 65535 * 16, "seqlen must be <= 1048560");   // the conv grid's time tiles of 16 steps
     MTL_REQUIRE(a->n_layers >= 1, "n_layers must be >= 1");
     MTL_REQUIRE(M >= 1 && M <= (int64_t(1) << 16) && D >= 1 && D <= (int64_t(1) << 16),
                 "d_model and d_inner must be in [1, 65536]");

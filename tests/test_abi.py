@@ -194,6 +194,7 @@ def test_invalid_arguments_are_rejected_without_a_gpu():
     ("mtl_prefill_long", dict(batch=1 << 12, seqlen=1 << 12), b"batch * seqlen"),
     ("mtl_prefill_long", dict(n_layers=0), b"n_layers"),
     ("mtl_prefill_long", dict(batch=65536, seqlen=1), b"batch must be <= 65535"),
+    ("mtl_prefill_long", dict(batch=1, seqlen=1 << 20), b"seqlen must be <= 1048560"),
     ("mtl_prefill_long", dict(null_ws=True), b"null workspace"),
     ("mtl_prefill_long", dict(null_layer=True), b"layer 1: null required pointer"),
     ("mtl_prefill_long", dict(alias=True), b"layer 1: conv_state_out must not alias"),
