@@ -7,7 +7,7 @@ short-prompt limit, on the GPU (model.py:184-241, 303-306, 328-341):
     with biases, d_conv 1 and 3, 8 and 32 states;
   * continuation from a cache, written in place (h_out aliasing h0, the conv
     history read and written in different runs), and into a separate
-    out_cache;
+    out_cache, with the projections on hipBLASLt and on the skinny GEMM;
   * a captured GraphedPrefill replays the eager bits, with eager work between
     replays;
   * which prompts take it (more than 64 tokens, or a shape the short path
@@ -79,19 +79,25 @@ def test_long_prefill_vs_oracle_and_per_op(b, l, d_model, n_layer, kw, monkeypat
         assert_rel(_n(lc.ssm_state), _n(rc.ssm_state), 1e-5, f"layer {i} ssm_state vs per-op")
 
 
+@pytest.mark.parametrize("b", [2, 1])
 @pytest.mark.parametrize("in_place", [True, False])
-def test_long_prefill_continues_a_cache(in_place, monkeypatch):
+def test_long_prefill_continues_a_cache(in_place, b, monkeypatch):
     """A 100-token prompt, then 150 more tokens from its cache: into the same
     cache (states rewritten in place) or into a separate out_cache; both
-    against the oracle's continuation."""
-    print(f"\n[prefill long continuation in_place={in_place}]", flush=True)
+    against the oracle's continuation.  Two batch rows put both calls past
+    the skinny-projection limit (200 and 300 token rows, hipBLASLt); one
+    keeps both on the skinny GEMM (100 and 150 rows), whose second call reads
+    the carried conv history and SSM state."""
+    import mamba_lite.model as mm
+    print(f"\n[prefill long continuation b={b} in_place={in_place}]", flush=True)
+    assert (b * 150 <= mm.LONG_PREFILL_SKINNY_ROWS) == (b == 1) and 256 <= mm.LONG_PREFILL_SKINNY_MAX_D_MODEL
     lm, W = _lm(95, 256, 2, 512, bias=True)
     calls = _counting(monkeypatch)
     rng = np.random.default_rng(95)
-    ids0, ids1 = rng.integers(0, 512, (2, 100)), rng.integers(0, 512, (2, 150))
+    ids0, ids1 = rng.integers(0, 512, (b, 100)), rng.integers(0, 512, (b, 150))
     with torch.no_grad():
         _, cache = lm.prefill(_t(ids0))
-        out = cache if in_place else MambaCache.allocate(lm.cfg, 2, DEV, torch.float32)
+        out = cache if in_place else MambaCache.allocate(lm.cfg, b, DEV, torch.float32)
         before = [lc.ssm_state.clone() for lc in cache.layers]
         logits, got = lm.prefill(_t(ids1), cache=cache, out_cache=out)
     assert got is out and len(calls) == 2
@@ -171,7 +177,8 @@ def test_concurrent_long_prefills_on_two_streams():
 
 @pytest.mark.parametrize("b,l,d_model,n_layer,kw", [
     (1, 65, 768, 2, {}), (1, 256, 768, 2, {}), (3, 50, 256, 3, dict(bias=True)), (1, 130, 2048, 1, dict(dt_rank=128)),
-    (2, 100, 256, 2, dict(d_conv=3, d_state=8)), (1, 200, 512, 2, dict(d_state=32))])
+    (2, 100, 256, 2, dict(d_conv=3, d_state=8)), (1, 200, 512, 2, dict(d_state=32)),
+    (2, 80, 512, 2, dict(d_conv=2, conv_bias=False))])
 def test_long_prefill_skinny_projections(b, l, d_model, n_layer, kw, monkeypatch):
     """Up to LONG_PREFILL_SKINNY_ROWS token rows (raised here, and the width
     limit with it, to reach every case) the one call runs its projections on
