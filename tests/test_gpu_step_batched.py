@@ -6,7 +6,8 @@ and MambaMixer.step 249-294):
     step's bit for bit over three steps, with the residual add + norm folded
     (up to 16 rows) and not, at widths 256, 768 (mamba-130m) and 2048
     (mamba-1.4b), with and without projection and conv biases, d_conv 2 and
-    3, 8 states;
+    3, 1 and 8 states, dt_rank 256 (x_proj's 288 columns, the most the call
+    takes);
   * the same steps against the float64 oracle (1e-4, the fp32 tolerance);
   * a captured GraphedStepper replays the eager bits, with eager work
     between replays;
@@ -62,7 +63,10 @@ def _counting(monkeypatch):
     (3, 256, 3, {}), (4, 256, 2, dict(bias=True)), (8, 768, 2, {}), (8, 256, 2, dict(conv_bias=False)),
     (16, 256, 3, dict(bias=True)), (12, 256, 2, dict(d_state=8)), (17, 256, 2, {}), (24, 512, 2, dict(d_conv=3)),
     (32, 768, 2, {}), (32, 2048, 2, dict(dt_rank=128)), (8, 2048, 2, dict(dt_rank=128)),
-    (5, 256, 1, {}), (20, 256, 2, dict(d_conv=2, bias=True))])
+    (5, 256, 1, {}), (20, 256, 2, dict(d_conv=2, bias=True)),
+    # the largest x_proj width the call takes (dt_rank 256 + 2 x 16 states =
+    # 288 columns), and one state
+    (4, 256, 2, dict(dt_rank=256)), (6, 256, 2, dict(d_state=1))])
 def test_batched_step_equals_per_op_and_oracle(b, d_model, n_layer, kw, monkeypatch):
     import mamba_lite.model as mm
     print(f"\n[batched step b={b} d_model={d_model} layers={n_layer} {kw}]", flush=True)
