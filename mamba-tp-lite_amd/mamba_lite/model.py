@@ -642,7 +642,8 @@ class MambaLM(nn.Module):
         D, N, K = cfg.d_inner, cfg.d_state, cfg.d_conv
         if SHORT_PREFILL_NATIVE and _SKINNY_PREFILL and ops.prefill_short_ok(b * l, cfg.d_model, D, N, cfg.dt_rank, K):
             return "short"
-        if LONG_PREFILL_NATIVE and b * l * D <= LONG_PREFILL_MAX_ELEMS and N <= 32 and 1 <= K <= 8:
+        if LONG_PREFILL_NATIVE and b * l * D <= LONG_PREFILL_MAX_ELEMS and \
+                ops.prefill_long_ok(b, l, cfg.d_model, D, N, cfg.dt_rank, K):
             return "long"
         return None
 

@@ -566,6 +566,16 @@ def prefill_short(h, layers, norm_f, eps_f, d_inner, d_state, dt_rank, d_conv):
 PREFILL_LONG_BLAS_WS = 32 << 20     # bytes of hipBLASLt workspace per mtl_prefill_long call
 
 
+def prefill_long_ok(b, l, d_model, d_inner, d_state, dt_rank, d_conv) -> bool:
+    """Whether mtl_prefill_long takes a prompt of b x l tokens of this layer
+    shape (its size checks): b l <= 2^20, b <= 65535, l <= 1048560, d_model
+    and d_inner in [1, 65536], d_state in [1, 32], dt_rank in [1, d_inner],
+    d_conv in [1, 8]."""
+    return (b >= 1 and l >= 1 and b * l <= 1 << 20 and b <= 65535 and l <= 65535 * 16
+            and 1 <= d_model <= 1 << 16 and 1 <= d_inner <= 1 << 16 and 1 <= d_state <= 32
+            and 1 <= dt_rank <= d_inner and 1 <= d_conv <= 8)
+
+
 def prefill_long(h, layers, norm_f, eps_f, d_inner, d_state, dt_rank, d_conv, skinny_rows=0):
     """mtl_prefill_long: a prompt's whole layer stack in one call (any
     length, the projections on hipBLASLt; up to skinny_rows token rows on

@@ -175,11 +175,14 @@ def test_fused_step_out_of_range_id_gives_nan_row(b):
 
 @pytest.mark.parametrize("kw", [dict(d_state=8, d_conv=3, bias=True, conv_bias=False),
                                 dict(d_state=4, d_conv=2, dt_rank=5),
-                                dict(d_state=16, d_conv=8, bias=True)])
+                                dict(d_state=16, d_conv=8, bias=True),
+                                dict(d_state=16, dt_rank=256)])
 @pytest.mark.parametrize("b", [1, 4])
 def test_fused_step_config_variants(kw, b):
     """Fused step with in/out_proj biases, no conv bias, N < 16, d_conv 2, 3
-    and 8, and a dt_rank that is not a multiple of 16: vs the per-op step."""
+    and 8, a dt_rank that is not a multiple of 16, and dt_rank 256 (the
+    largest the fused step takes: x_proj's 288 columns, more (column, row)
+    pairs than a workgroup has threads): vs the per-op step."""
     print(f"fused decode variant {kw} b={b}", flush=True)
     torch.manual_seed(b)
     cfg = MambaConfig(d_model=96, n_layer=2, vocab_size=200, **kw)

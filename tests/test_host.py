@@ -266,6 +266,33 @@ def test_prefill_short_covers_the_sizes_its_kernels_take(rows, M, D, N, R, K, ok
     assert ops.prefill_short_ok(rows, M, D, N, R, K) is ok
 
 
+@pytest.mark.parametrize("b,l,M,D,N,R,K,ok", [
+    (1, 100, 256, 512, 16, 16, 4, True),
+    (1, 100, 256, 512, 16, 16, 1, True),           # d_conv 1
+    (1, 100, 96, 192, 16, 256, 4, False),          # dt_rank above d_inner
+    (65536, 1, 256, 512, 16, 16, 4, False),        # batch rows
+    (1, 1 << 20, 1, 1, 1, 1, 4, False),            # seqlen past the conv grid
+    (1, 65535 * 16, 1, 1, 1, 1, 4, True),
+    (4096, 257, 256, 512, 16, 16, 4, False),       # b l past 2^20
+    (1, 100, 256, 512, 33, 16, 4, False),          # d_state
+    (1, 100, 256, 512, 16, 16, 9, False),          # d_conv
+    (1, 100, 1 << 17, 512, 16, 16, 4, False),      # d_model
+])
+def test_prefill_long_covers_the_sizes_its_checks_take(b, l, M, D, N, R, K, ok):
+    """ops.prefill_long_ok admits exactly the sizes mtl_prefill_long checks
+    before its first launch (the C-ABI rejection tests hold the same
+    bounds), so MambaLM never hands it a prompt it rejects."""
+    assert ops.prefill_long_ok(b, l, M, D, N, R, K) is ok
+
+
+def test_a_dt_rank_above_d_inner_takes_the_per_op_prefill():
+    """The reference allows dt_rank > d_inner (dt_proj is a Linear(dt_rank,
+    d_inner)); neither one-call prefill takes it, so prefill() runs op by op
+    for every prompt length."""
+    model = MambaLM(MambaConfig(d_model=96, n_layer=1, vocab_size=64, dt_rank=256))
+    assert model._native_prefill_kind(1, 5) is None and model._native_prefill_kind(2, 300) is None
+
+
 def test_native_prefill_is_not_taken_off_the_gpu():
     """MambaLM._prefill_native declines CPU token ids (short and long
     prompts) before touching the library, so prefill() keeps its other paths
