@@ -563,6 +563,18 @@ def prefill_short(h, layers, norm_f, eps_f, d_inner, d_state, dt_rank, d_conv):
     return normed
 
 
+STEP_MAX_D_STATE = 16     # one state per lane of a 16-lane row in every step kernel
+
+
+def check_step_d_state(d_state) -> None:
+    """ValueError for a model whose single-token step the step kernels do not
+    take (more than STEP_MAX_D_STATE states), raised by the step entry points
+    before anything is launched, so no cache is left half stepped."""
+    if d_state > STEP_MAX_D_STATE:
+        raise ValueError(f"step: d_state {d_state} > {STEP_MAX_D_STATE}; selective_state_update supports "
+                         f"d_state <= {STEP_MAX_D_STATE}")
+
+
 PREFILL_LONG_BLAS_WS = 32 << 20     # bytes of hipBLASLt workspace per mtl_prefill_long call
 
 
