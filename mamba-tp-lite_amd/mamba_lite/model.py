@@ -465,7 +465,7 @@ class MambaMixer(nn.Module):
         """The step up to the gated SSM output y [b, d_inner] (before out_proj).
         With sq, x_t is h * norm weight and sq the per-tile sums of h^2 that
         ops.linear_skinny_residual left: the in_proj input is RMSNorm(h)."""
-        ops.check_step_d_state(self.cfg.d_state)   # before the conv history moves
+        ops.check_step_shape(self.cfg.d_state, self.cfg.dt_rank)   # before the conv history moves
         Dm, R = self.cfg.d_inner, self.cfg.dt_rank
         b = x_t.shape[0]
         J = R + 2 * self.cfg.d_state

@@ -413,8 +413,9 @@ def selective_state_update(ssm_state, x, z, x_dbl, W_dt, b_dt, A, D=None, a_is_l
     _f32_mat(A, (Dm, N), "A")
     _f32_vec(b_dt, Dm, "b_dt")
     _f32_vec(D, Dm, "D")
-    if N > 16:
-        raise ValueError("selective_state_update supports d_state <= 16")
+    if N > STEP_MAX_D_STATE or R > STEP_MAX_DT_RANK:
+        raise ValueError(f"selective_state_update supports d_state <= {STEP_MAX_D_STATE} and dt_rank <= "
+                         f"{STEP_MAX_DT_RANK}")
     if tuple(x_dbl.shape) != (b, R + 2 * N) or x_dbl.stride(1) != 1:
         raise ValueError(f"x_dbl must be {(b, R + 2 * N)} with unit column stride, got {tuple(x_dbl.shape)}")
     for name, t in (("x", x), ("z", z)):
@@ -564,15 +565,17 @@ def prefill_short(h, layers, norm_f, eps_f, d_inner, d_state, dt_rank, d_conv):
 
 
 STEP_MAX_D_STATE = 16     # one state per lane of a 16-lane row in every step kernel
+STEP_MAX_DT_RANK = 256    # dt_proj columns a step lane holds: 16 lanes x 16 registers
 
 
-def check_step_d_state(d_state) -> None:
+def check_step_shape(d_state, dt_rank) -> None:
     """ValueError for a model whose single-token step the step kernels do not
-    take (more than STEP_MAX_D_STATE states), raised by the step entry points
-    before anything is launched, so no cache is left half stepped."""
-    if d_state > STEP_MAX_D_STATE:
-        raise ValueError(f"step: d_state {d_state} > {STEP_MAX_D_STATE}; selective_state_update supports "
-                         f"d_state <= {STEP_MAX_D_STATE}")
+    take (more than STEP_MAX_D_STATE states or STEP_MAX_DT_RANK dt_proj
+    columns), raised by the step entry points before anything is launched,
+    so no cache is left half stepped."""
+    if d_state > STEP_MAX_D_STATE or dt_rank > STEP_MAX_DT_RANK:
+        raise ValueError(f"step: d_state {d_state}, dt_rank {dt_rank}; the step kernels take d_state <= "
+                         f"{STEP_MAX_D_STATE} and dt_rank <= {STEP_MAX_DT_RANK}")
 
 
 PREFILL_LONG_BLAS_WS = 32 << 20     # bytes of hipBLASLt workspace per mtl_prefill_long call

@@ -172,7 +172,7 @@ class LocalTPMixer:
         advances in place (tp_model.py:137-179)."""
         if not self.shards:
             raise RuntimeError("no shards loaded: call load_shard_from_dense or load_shards first")
-        ops.check_step_d_state(self.cfg.d_state)   # before any rank's conv history moves
+        ops.check_step_shape(self.cfg.d_state, self.cfg.dt_rank)   # before any rank's conv history moves
         s1 = [sh.step_stage1(x_t, c) for sh, c in zip(self.shards, caches)]
         x_dbl = self._reduce(self._ar_x, [part for part, _ in s1], s1[0][0].shape, x_t.dtype)  # AllReduce #1
         parts = [sh.step_stage2(x_dbl, saved, c) for sh, (_, saved), c in zip(self.shards, s1, caches)]

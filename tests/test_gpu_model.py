@@ -653,13 +653,15 @@ def test_native_short_prefill_equals_the_per_op_path(d_conv, bias, b, l, monkeyp
     assert len(calls) == 3 and torch.equal(ln, lp) and not torch.equal(ln, nat[0])
 
 
-@pytest.mark.parametrize("b", [1, 4])
-def test_a_step_past_16_states_raises_before_touching_the_cache(b):
-    """The step kernels hold one state per lane of a 16-lane row; a model with
-    32 states prefills (the scan takes up to 32) but its step raises
-    ValueError before any launch, leaving every layer's conv history and SSM
-    state as they were (the reference's torch step would run it)."""
-    cfg = MambaConfig(d_model=256, n_layer=2, vocab_size=64, d_state=32)
+@pytest.mark.parametrize("b,kw,what", [(1, dict(d_state=32), "d_state 32"), (4, dict(d_state=32), "d_state 32"),
+                                       (4, dict(dt_rank=300), "dt_rank 300")])
+def test_a_step_past_the_step_kernels_limits_raises_before_touching_the_cache(b, kw, what):
+    """The step kernels hold one state per lane of a 16-lane row and at most
+    256 dt_proj columns; a model with 32 states or dt_rank 300 prefills (the
+    scan takes up to 32 states, the per-op prefill any dt_rank) but its step
+    raises ValueError before any launch, leaving every layer's conv history
+    and SSM state as they were (the reference's torch step would run it)."""
+    cfg = MambaConfig(d_model=256, n_layer=2, vocab_size=64, **kw)
     torch.manual_seed(b)
     with torch.device(DEV):
         lm = MambaLM(cfg).eval()
@@ -667,7 +669,7 @@ def test_a_step_past_16_states_raises_before_touching_the_cache(b):
     with torch.no_grad():
         _, cache = lm.prefill(ids[:, :8])
         before = [(lc.conv_state.clone(), lc.ssm_state.clone()) for lc in cache.layers]
-        with pytest.raises(ValueError, match="d_state 32"):
+        with pytest.raises(ValueError, match=what):
             lm.step(ids[:, 8:], cache)
         torch.cuda.synchronize()
     for i, ((c, h), lc) in enumerate(zip(before, cache.layers)):
